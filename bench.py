@@ -1,0 +1,423 @@
+#!/usr/bin/env python3
+"""Throughput of the ntops hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops all|name,...]
+
+A step is one pass of an op over its full synthetic workload (the shapes
+below), inputs resident in HBM.  The headline line is rms_norm on bf16
+(16384, 4096) -- the configuration the metric is quoted on -- and the same
+JSON line carries every other workload under "ops".
+
+Timing: W eager warmup steps, then K steps captured in one HIP graph (so host
+launch overhead does not pad ~35 us kernels) and replayed between HIP events
+recorded on the launch stream; three input/output buffer sets rotate so the
+256 MB MALL cannot serve a step from the previous one.  Achieved bandwidth
+uses algorithmic bytes (every compulsory byte counted once); GEMMs report
+algorithmic flops.  cpu_baseline times PyTorch's CPU implementation of the
+same op (the reference the configs name) on a bounded sample of the workload
+on this host's cores.
+"""
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "achieved HBM GB/s (% peak) for norm/softmax/RoPE/eltwise; bf16 mm TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+NSETS = 3
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--ops", default="all")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    p.add_argument("--eager", action="store_true", help="time eager wrapper calls instead of a graph")
+    return p.parse_args()
+
+
+# ----------------------------------------------------------- workloads ----
+
+
+class Workload:
+    """name, description, algorithmic work per step, and callables that build
+    rotating GPU buffer sets, launch one step on a set, and time the torch
+    CPU reference on a sample."""
+
+    def __init__(self, name, desc, unit, bound, work, kernels_per_step, build, step, cpu, dtype):
+        self.name, self.desc, self.unit, self.bound = name, desc, unit, bound
+        self.work, self.kernels_per_step = work, kernels_per_step
+        self.build, self.step, self.cpu, self.dtype = build, step, cpu, dtype
+
+
+def _gen(seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return g
+
+
+def _cpu_gen(seed=0):
+    return torch.Generator().manual_seed(seed)
+
+
+def make_workloads():
+    import torch.nn.functional as F
+
+    import ntops_amd
+    from ntops_amd import _lib
+    from ntops_amd.torch._gemm import gemm
+    from ntops_amd.torch.utils import _unary
+
+    lib = _lib.load()
+
+    import ctypes
+
+    def stream():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def check(rc, what):
+        _lib.check(rc, what)
+
+    W = []
+
+    # silu fp32 (8192, 4096)
+    def silu_build(i):
+        x = torch.randn(8192, 4096, device="cuda", generator=_gen(i))
+        return {"x": x, "y": torch.empty_like(x)}
+
+    def silu_step(s):
+        _unary(_lib.UNARY_SILU, s["x"], s["y"], "silu")
+
+    def silu_cpu():
+        x = torch.randn(2048, 4096, generator=_cpu_gen())
+        return (lambda: F.silu(x)), 2 * x.numel() * 4, "F.silu fp32 (2048, 4096) = 1/4 of the workload"
+
+    W.append(Workload("silu", "silu fp32 (8192, 4096)", "GB/s", "hbm", 2 * 8192 * 4096 * 4, 1,
+                      silu_build, silu_step, silu_cpu, "f32"))
+
+    # rms_norm / layer_norm bf16 (16384, 4096)
+    R, C = 16384, 4096
+
+    def norm_build(i):
+        g = _gen(100 + i)
+        x = torch.randn(R, C, device="cuda", generator=g).bfloat16()
+        w = (1 + 0.02 * torch.randn(C, device="cuda", generator=g)).bfloat16()
+        b = (0.02 * torch.randn(C, device="cuda", generator=g)).bfloat16()
+        return {"x": x, "w": w, "b": b, "y": torch.empty_like(x)}
+
+    def rms_step(s):
+        check(lib.ntops_rms_norm(_lib.BF16, R, C, s["x"].data_ptr(), C, s["w"].data_ptr(), _lib.BF16, 1e-6,
+                                 s["y"].data_ptr(), C, stream()), "rms_norm")
+
+    def ln_step(s):
+        check(lib.ntops_layer_norm(_lib.BF16, R, C, s["x"].data_ptr(), C, s["w"].data_ptr(), s["b"].data_ptr(),
+                                   _lib.BF16, 1e-5, s["y"].data_ptr(), C, stream()), "layer_norm")
+
+    def norm_cpu_inputs():
+        g = _cpu_gen()
+        x = torch.randn(4096, C, generator=g).bfloat16()
+        w = (1 + 0.02 * torch.randn(C, generator=g)).bfloat16()
+        b = (0.02 * torch.randn(C, generator=g)).bfloat16()
+        return x, w, b
+
+    def rms_cpu():
+        x, w, _ = norm_cpu_inputs()
+        return (lambda: F.rms_norm(x, (C,), w, 1e-6)), 2 * x.numel() * 2 + C * 2, \
+            "F.rms_norm bf16 (4096, 4096) = 1/4 of the workload"
+
+    def ln_cpu():
+        x, w, b = norm_cpu_inputs()
+        return (lambda: F.layer_norm(x, (C,), w, b, 1e-5)), 2 * x.numel() * 2 + 2 * C * 2, \
+            "F.layer_norm bf16 (4096, 4096) = 1/4 of the workload"
+
+    W.append(Workload("rms_norm", "rms_norm bf16 (16384, 4096), weight (4096,), eps 1e-6", "GB/s", "hbm",
+                      2 * R * C * 2 + C * 2, 1, norm_build, rms_step, rms_cpu, "bf16"))
+    W.append(Workload("layer_norm", "layer_norm bf16 (16384, 4096), weight + bias (4096,), eps 1e-5", "GB/s",
+                      "hbm", 2 * R * C * 2 + 2 * C * 2, 1, norm_build, ln_step, ln_cpu, "bf16"))
+
+    # softmax bf16 (4, 32, 2048, 2048) causal
+    SB, SH, SS = 4, 32, 2048
+
+    def sm_build(i):
+        g = _gen(200 + i)
+        mask = torch.triu(torch.ones(SS, SS, dtype=torch.bool, device="cuda"), 1)
+        x = torch.empty(SB, SH, SS, SS, dtype=torch.bfloat16, device="cuda")
+        for b in range(SB):
+            x[b] = (torch.randn(SH, SS, SS, device="cuda", generator=g) / math.sqrt(128)).masked_fill(
+                mask, float("-inf")).bfloat16()
+        return {"x": x, "y": torch.empty_like(x)}
+
+    sm_strides = _lib.i64_array((SS, 1, 1))
+
+    def sm_step(s):
+        check(lib.ntops_softmax(_lib.BF16, _lib.BF16, SB * SH * SS, SS, 1, s["x"].data_ptr(), sm_strides,
+                                s["y"].data_ptr(), sm_strides, stream()), "softmax")
+
+    def sm_cpu():
+        g = _cpu_gen()
+        mask = torch.triu(torch.ones(SS, SS, dtype=torch.bool), 1)
+        x = (torch.randn(1, 4, SS, SS, generator=g) / math.sqrt(128)).masked_fill(mask, float("-inf")).bfloat16()
+        return (lambda: F.softmax(x, -1)), 2 * x.numel() * 2, "F.softmax bf16 (1, 4, 2048, 2048) = 1/32 of the workload"
+
+    W.append(Workload("softmax", "softmax bf16 (4, 32, 2048, 2048) dim=-1, causal -inf mask", "GB/s", "hbm",
+                      2 * SB * SH * SS * SS * 2, 1, sm_build, sm_step, sm_cpu, "bf16"))
+
+    # RoPE bf16 q and k (4, 4096, 32, 128), tables (4096, 128)
+    RB, RS, RH, RD = 4, 4096, 32, 128
+    # tables: theta_i = 10000^(-2i/128), positions 0..4095, built in fp32,
+    # duplicated to (4096, 128) (rotate_half convention), cast to bf16
+    theta = 10000.0 ** (-2 * (torch.arange(RD // 2, dtype=torch.float32) / RD))
+    ang = torch.arange(RS, dtype=torch.float32)[:, None] * theta[None, :]
+    sn = torch.cat([torch.sin(ang), torch.sin(ang)], -1)
+    cs = torch.cat([torch.cos(ang), torch.cos(ang)], -1)
+    sin_t = sn.bfloat16().cuda()
+    cos_t = cs.bfloat16().cuda()
+
+    def rope_build(i):
+        g = _gen(300 + i)
+        q = torch.randn(RB, RS, RH, RD, device="cuda", generator=g).bfloat16()
+        k = torch.randn(RB, RS, RH, RD, device="cuda", generator=g).bfloat16()
+        return {"q": q, "k": k, "qo": torch.empty_like(q), "ko": torch.empty_like(k),
+                "st": _lib.i64_array(q.stride())}
+
+    def rope_step(s):
+        for x, y in ((s["q"], s["qo"]), (s["k"], s["ko"])):
+            check(lib.ntops_rope(_lib.BF16, RB, RS, RH, RD, x.data_ptr(), s["st"], sin_t.data_ptr(),
+                                 cos_t.data_ptr(), RD, RD, 0, y.data_ptr(), s["st"], stream()), "rope")
+
+    def rope_cpu():
+        g = _cpu_gen()
+        q = torch.randn(1, RS, RH, RD, generator=g).bfloat16()
+        st, ct = sn.bfloat16(), cs.bfloat16()
+
+        def run():
+            rot = torch.cat((-q[..., RD // 2:], q[..., : RD // 2]), -1)
+            return q * ct[None, :, None, :] + rot * st[None, :, None, :]
+
+        return run, 2 * q.numel() * 2 + 2 * RS * RD * 2, \
+            "torch eager x*cos + rotate_half(x)*sin, bf16 q (1, 4096, 32, 128) = 1/8 of the workload"
+
+    W.append(Workload("rope", "rotary_position_embedding bf16 q and k (4, 4096, 32, 128), (4096, 128) tables, "
+                      "non-interleaved", "GB/s", "hbm", 2 * (2 * RB * RS * RH * RD * 2 + 2 * RS * RD * 2), 2,
+                      rope_build, rope_step, rope_cpu, "bf16"))
+
+    # GEMMs
+    M, N, K = 8192, 14336, 4096
+
+    def mm_build(i):
+        g = _gen(400 + i)
+        a = (0.02 * torch.randn(M, K, device="cuda", generator=g)).bfloat16()
+        b = (0.02 * torch.randn(K, N, device="cuda", generator=g)).bfloat16()
+        bias = (0.02 * torch.randn(N, device="cuda", generator=g)).bfloat16()
+        return {"a": a, "b": b, "bias": bias.expand(M, N), "out": torch.empty(M, N, dtype=torch.bfloat16, device="cuda")}
+
+    def mm_step(s):
+        gemm(s["a"], s["b"], s["out"])
+
+    def addmm_step(s):
+        gemm(s["a"], s["b"], s["out"], c=s["bias"], alpha=1.0, beta=1.0)
+
+    def mm_cpu_inputs():
+        g = _cpu_gen()
+        a = (0.02 * torch.randn(512, K, generator=g)).bfloat16()
+        b = (0.02 * torch.randn(K, N, generator=g)).bfloat16()
+        bias = (0.02 * torch.randn(N, generator=g)).bfloat16()
+        return a, b, bias
+
+    def mm_cpu():
+        a, b, _ = mm_cpu_inputs()
+        return (lambda: torch.mm(a, b)), 2 * 512 * K * N, "torch.mm bf16 (512 x 4096).(4096 x 14336) = 1/16 of the workload"
+
+    def addmm_cpu():
+        a, b, bias = mm_cpu_inputs()
+        return (lambda: torch.addmm(bias, a, b)), 2 * 512 * K * N, \
+            "torch.addmm bf16 bias + (512 x 4096).(4096 x 14336) = 1/16 of the workload"
+
+    W.append(Workload("mm", "mm bf16 (8192 x 4096).(4096 x 14336), fp32 accumulate", "TFLOP/s", "mfma",
+                      2 * M * N * K, 1, mm_build, mm_step, mm_cpu, "bf16"))
+    W.append(Workload("addmm", "addmm bf16 bias (14336,) + (8192 x 4096).(4096 x 14336), beta = alpha = 1",
+                      "TFLOP/s", "mfma", 2 * M * N * K, 1, mm_build, addmm_step, addmm_cpu, "bf16"))
+
+    BB, BM, BK, BN = 32, 2048, 128, 2048
+
+    def bmm_build(i):
+        g = _gen(500 + i)
+        a = (0.02 * torch.randn(BB, BM, BK, device="cuda", generator=g)).bfloat16()
+        b = (0.02 * torch.randn(BB, BK, BN, device="cuda", generator=g)).bfloat16()
+        return {"a": a, "b": b, "out": torch.empty(BB, BM, BN, dtype=torch.bfloat16, device="cuda")}
+
+    def bmm_step(s):
+        gemm(s["a"], s["b"], s["out"], what="bmm")
+
+    def bmm_cpu():
+        g = _cpu_gen()
+        a = (0.02 * torch.randn(4, BM, BK, generator=g)).bfloat16()
+        b = (0.02 * torch.randn(4, BK, BN, generator=g)).bfloat16()
+        return (lambda: torch.bmm(a, b)), (4 * BM * BK + 4 * BK * BN + 4 * BM * BN) * 2, \
+            "torch.bmm bf16 4 x (2048 x 128).(128 x 2048) = 1/8 of the workload"
+
+    # bmm is HBM-bound (114 flop/B < ridge): judged on bytes
+    W.append(Workload("bmm", "bmm bf16 32 x (2048 x 128).(128 x 2048), fp32 accumulate", "GB/s", "hbm",
+                      (BB * BM * BK + BB * BK * BN + BB * BM * BN) * 2, 1, bmm_build, bmm_step, bmm_cpu, "bf16"))
+    W[-1].flops = 2 * BB * BM * BN * BK
+    return {w.name: w for w in W}
+
+
+# -------------------------------------------------------------- timing ----
+
+
+def time_gpu(w, steps, warmup, eager):
+    sets = [w.build(i) for i in range(NSETS)]
+    torch.cuda.synchronize()
+    for i in range(max(1, warmup)):  # >= 1: one-time kernel attributes are set outside capture
+        w.step(sets[i % NSETS])
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    if eager:
+        torch.cuda.synchronize()
+        start.record()
+        for i in range(steps):
+            w.step(sets[i % NSETS])
+        end.record()
+        torch.cuda.synchronize()
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(steps):
+                w.step(sets[i % NSETS])
+        graph.replay()  # one untimed replay (the graph's first launch)
+        torch.cuda.synchronize()
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        del graph
+    ms = start.elapsed_time(end) / steps
+    del sets
+    torch.cuda.empty_cache()
+    return ms
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_cpu(w):
+    fn, work, sample = w.cpu()
+    reps = 2 if w.name in ("mm", "addmm") else 3
+    fn()  # warmup
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    sec = statistics.median(ts)
+    rate = work / sec / (1e12 if w.unit == "TFLOP/s" else 1e9)
+    return {"value": round(rate, 3), "unit": w.unit, "cores": torch.get_num_threads(), "kind": "reference",
+            "sample": f"{sample}; PyTorch {torch.__version__} CPU op, median of {reps} after 1 warmup, "
+                      f"{cpu_model()}"}
+
+
+def result_for(w, ms):
+    sec = ms / 1e3
+    if w.unit == "TFLOP/s":
+        value = w.work / sec / 1e12
+        peak, unit = MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        value = w.work / sec / 1e9
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+    per_kernel_ms = ms / w.kernels_per_step
+    achieved = (w.work / w.kernels_per_step) / (per_kernel_ms / 1e3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    out = {
+        "workload": w.desc,
+        "value": round(value, 3),
+        "unit": unit,
+        "ms_per_step": round(ms, 5),
+        "kernel_ms": round(per_kernel_ms, 5),
+        "roofline": {"bound": w.bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+                     "frac": round(achieved / peak, 4), "traffic": None},
+    }
+    if getattr(w, "flops", None):
+        out["tflops"] = round(w.flops / sec / 1e12, 3)
+    return out
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(every op runs on a single MI355X; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    torch.set_num_threads(cpu_threads())
+    workloads = make_workloads()
+    names = list(workloads) if args.ops == "all" else args.ops.split(",")
+    headline = "rms_norm" if "rms_norm" in names else names[0]
+    names = [headline] + [n for n in names if n != headline]
+
+    results = {}
+    for n in names:
+        w = workloads[n]
+        ms = time_gpu(w, args.steps, args.warmup, args.eager)
+        r = result_for(w, ms)
+        if not args.no_cpu:
+            r["cpu_baseline"] = time_cpu(w)
+        results[n] = r
+        print(f"# {n}: {r['value']} {r['unit']} ({r['kernel_ms'] * 1e3:.1f} us/kernel, "
+              f"{100 * r['roofline']['frac']:.1f}% of roofline)", file=sys.stderr, flush=True)
+
+    h = results[headline]
+    line = {
+        "metric": METRIC,
+        "value": h["value"],
+        "unit": h["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": h["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": workloads[headline].dtype,
+        "data": "synthetic (seeded torch.randn of the configured shapes, resident in HBM)",
+        "config": {"workload": h["workload"], "timing": "eager" if args.eager else "hip-graph of K steps",
+                   "buffer_sets": NSETS},
+        "roofline": h["roofline"],
+        "cpu_baseline": h.get("cpu_baseline"),
+        "ops": {n: r for n, r in results.items() if n != headline},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

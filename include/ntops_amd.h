@@ -1,0 +1,178 @@
+/*
+ * ntops_amd.h -- C ABI of the MI355X (gfx950) operator library behind
+ * ntops_amd.torch.<op>.
+ *
+ * Every entry point takes raw device pointers, element counts and element
+ * strides (int64, in elements, never bytes), scalar arguments as plain C
+ * values, and the HIP stream to launch on (a hipStream_t passed as void*;
+ * NULL is the null stream).  Nothing here allocates device memory, nothing
+ * synchronises, and no C++ exception crosses the boundary: each call returns
+ * NTOPS_OK or an error code, and ntops_last_error() returns the message of the
+ * calling thread's most recent failure.  Launches are asynchronous and stream
+ * ordered, exactly like the Triton launches they replace.
+ *
+ * Reference interface replaced by each entry point (paths relative to the
+ * mygitljf/ntops source tree):
+ *   ntops_unary       <- src/ntops/torch/{silu,gelu,exp,bitwise_not}.py:7-17
+ *                        (kernels/{silu,gelu,exp,bitwise_not}.py application)
+ *   ntops_binary      <- src/ntops/torch/{add,mul,bitwise_and,bitwise_or}.py:7-15
+ *   ntops_cast        <- no ntops counterpart; the dtype promotion / layout
+ *                        copy that torch's TensorIterator performs before the
+ *                        elementwise kernels (kept native so no op falls back
+ *                        to torch for data movement)
+ *   ntops_rms_norm    <- src/ntops/torch/rms_norm.py:9-31, kernels/rms_norm.py:10-20
+ *   ntops_layer_norm  <- src/ntops/torch/layer_norm.py:9-33, kernels/layer_norm.py:11-31
+ *   ntops_softmax     <- src/ntops/torch/softmax.py:7-16, kernels/softmax.py:9-29
+ *   ntops_rope        <- src/ntops/torch/rotary_position_embedding.py:7-29,
+ *                        kernels/rotary_position_embedding.py:6-47
+ *   ntops_gemm        <- src/ntops/torch/{mm,bmm,addmm}.py:7-18,
+ *                        kernels/mm.py:54-65, kernels/bmm.py:8-43,
+ *                        kernels/addmm.py:64-67
+ */
+#ifndef NTOPS_AMD_H
+#define NTOPS_AMD_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define NTOPS_API __attribute__((visibility("default")))
+#else
+#define NTOPS_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- element types ---------------------------------------------------- */
+enum ntops_dtype {
+  NTOPS_F32 = 0,
+  NTOPS_F16 = 1,
+  NTOPS_BF16 = 2,
+  NTOPS_F64 = 3,
+  NTOPS_BOOL = 4,
+  NTOPS_U8 = 5,
+  NTOPS_I8 = 6,
+  NTOPS_I16 = 7,
+  NTOPS_I32 = 8,
+  NTOPS_I64 = 9
+};
+
+/* ---- status codes ----------------------------------------------------- */
+enum ntops_status {
+  NTOPS_OK = 0,
+  NTOPS_ERR_INVALID = 1,     /* bad shape / stride / pointer / argument   */
+  NTOPS_ERR_UNSUPPORTED = 2, /* valid request this library does not serve */
+  NTOPS_ERR_HIP = 3          /* the HIP runtime reported an error         */
+};
+
+/* Maximum tensor rank accepted by the strided entry points (after adjacent
+ * dimensions that are contiguous in every operand have been merged). */
+#define NTOPS_MAX_DIMS 8
+
+/* ---- library ----------------------------------------------------------- */
+NTOPS_API int ntops_abi_version(void);
+/* Message of this thread's most recent failed call ("" if none). */
+NTOPS_API const char* ntops_last_error(void);
+
+/* ---- elementwise ------------------------------------------------------ */
+enum ntops_unary_op {
+  NTOPS_UNARY_SILU = 1,      /* x / (1 + exp(-x))                 silu.py:10  */
+  NTOPS_UNARY_GELU = 2,      /* x * 0.5 * (1 + erf(x / sqrt 2))   gelu.py:11  */
+  NTOPS_UNARY_GELU_TANH = 3, /* 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3)))
+                                                                  gelu.py:14-26 */
+  NTOPS_UNARY_EXP = 4,       /* exp(x)                            exp.py:10   */
+  NTOPS_UNARY_BITWISE_NOT = 5 /* ~x; logical not for bool   bitwise_not.py:9-14 */
+};
+
+/* y = op(x) over an ndim-dimensional index space `shape`.  x and y have the
+ * same dtype; floating ops accept F32/F16/BF16/F64, BITWISE_NOT accepts
+ * BOOL/U8/I8/I16/I32/I64.  y may alias x exactly (in-place). */
+NTOPS_API int ntops_unary(int op, int dtype, int ndim, const int64_t* shape,
+                const void* x, const int64_t* x_strides,
+                void* y, const int64_t* y_strides, void* stream);
+
+enum ntops_binary_op {
+  NTOPS_BINARY_ADD = 1,         /* a + alpha * b              add.py:10 */
+  NTOPS_BINARY_MUL = 2,         /* a * b                      mul.py:9  */
+  NTOPS_BINARY_BITWISE_AND = 3, /* a & b               bitwise_and.py:9 */
+  NTOPS_BINARY_BITWISE_OR = 4   /* a | b                bitwise_or.py:9 */
+};
+
+/* out = op(a, b) over `shape`.  a, b and out share `dtype` (the caller has
+ * already applied type promotion).  Broadcasting is expressed by stride 0.
+ * When b is NULL, b is the scalar (b_f for floating dtypes, b_i for integer
+ * and bool dtypes).  alpha (ADD only) follows the same split; it is rounded
+ * to `dtype` before use, as torch's CPU kernel does. */
+NTOPS_API int ntops_binary(int op, int dtype, int ndim, const int64_t* shape,
+                 const void* a, const int64_t* a_strides,
+                 const void* b, const int64_t* b_strides,
+                 double b_f, int64_t b_i, double alpha_f, int64_t alpha_i,
+                 void* out, const int64_t* out_strides, void* stream);
+
+/* y = (dst_dtype) x, elementwise, any strides (stride 0 allowed on x). */
+NTOPS_API int ntops_cast(int src_dtype, int dst_dtype, int ndim, const int64_t* shape,
+               const void* x, const int64_t* x_strides,
+               void* y, const int64_t* y_strides, void* stream);
+
+/* ---- row reductions --------------------------------------------------- */
+/* y[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * w   (fp32 accumulate,
+ * one rounding to dtype).  x and y are rows x cols with unit column stride
+ * and the given row strides; w (may be NULL = ones) is cols contiguous
+ * elements of w_dtype, which is dtype or F32.  dtype in {F32, F16, BF16}. */
+NTOPS_API int ntops_rms_norm(int dtype, int64_t rows, int64_t cols,
+                   const void* x, int64_t x_row_stride,
+                   const void* w, int w_dtype, double eps,
+                   void* y, int64_t y_row_stride, void* stream);
+
+/* y[r, :] = (x - mean) * rsqrt(var + eps) * w + b, biased variance, fp32
+ * moments.  w and b may each be NULL (ones / zeros). */
+NTOPS_API int ntops_layer_norm(int dtype, int64_t rows, int64_t cols,
+                     const void* x, int64_t x_row_stride,
+                     const void* w, const void* b, int wb_dtype, double eps,
+                     void* y, int64_t y_row_stride, void* stream);
+
+/* Softmax over the middle axis of an (outer, dim_size, inner) view.
+ * x_strides / y_strides are the three strides of that view.  The input is
+ * first converted to out_dtype (as torch does for the dtype= argument), then
+ * max/sum are accumulated in fp32 (fp64 when out_dtype is F64).  A row that
+ * is entirely -inf produces NaN. */
+NTOPS_API int ntops_softmax(int in_dtype, int out_dtype,
+                  int64_t outer, int64_t dim_size, int64_t inner,
+                  const void* x, const int64_t* x_strides,
+                  void* y, const int64_t* y_strides, void* stream);
+
+/* ---- rotary position embedding ---------------------------------------- */
+/* x, y: (B, S, H, D) with the given 4 strides; y may alias x.  sin/cos:
+ * (S, table_cols) tables with row stride table_row_stride and unit column
+ * stride; table_cols is D/2 (one angle per pair, as ntops expects) or D
+ * (one value per element, the rotate_half convention).  interleaved != 0
+ * rotates pairs (2i, 2i+1); otherwise pairs (i, i + D/2).  Every product and
+ * sum is rounded to dtype, matching torch eager evaluation of
+ * x*cos + rotate_half(x)*sin.  dtype in {F32, F16, BF16}; D even, <= 1024. */
+NTOPS_API int ntops_rope(int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
+               const void* x, const int64_t* x_strides,
+               const void* sin_table, const void* cos_table,
+               int64_t table_row_stride, int64_t table_cols, int interleaved,
+               void* y, const int64_t* y_strides, void* stream);
+
+/* ---- GEMM family ------------------------------------------------------ */
+/* For each batch index: out = alpha * (A @ B) + beta * C
+ *   A: M x K, B: K x N, out: M x N, all with 3 strides (batch, row, col).
+ *   C may be NULL (or beta == 0: C is not read); its 3 strides may contain
+ *   zeros to broadcast (e.g. a bias row: {0, 0, 1}).
+ * dtype in {BF16, F16, F32} for A, B, C and out.  Products accumulate in
+ * fp32 and round to dtype once.  bf16/fp16 run on MFMA matrix cores; fp32
+ * runs IEEE fp32 (no reduced-precision input path exists on gfx950). */
+NTOPS_API int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+               const void* A, const int64_t* a_strides,
+               const void* B, const int64_t* b_strides,
+               const void* C, const int64_t* c_strides,
+               double alpha, double beta,
+               void* out, const int64_t* out_strides, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NTOPS_AMD_H */

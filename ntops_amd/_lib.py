@@ -1,0 +1,124 @@
+"""ctypes binding of libntops_amd.so (the C ABI declared in include/ntops_amd.h).
+
+This module replaces the reference's kernel factory (`_cached_make`,
+src/ntops/torch/utils.py:46-64) and the NineToothed/Triton launch below it:
+every op is a direct call into the prebuilt gfx950 library, launched
+asynchronously on torch's current HIP stream.  There is no fallback: if the
+library is missing or a call fails, a RuntimeError is raised.
+"""
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libntops_amd.so")
+
+# enum ntops_dtype
+F32, F16, BF16, F64, BOOL, U8, I8, I16, I32, I64 = range(10)
+
+DTYPE_CODE = {
+    torch.float32: F32,
+    torch.float16: F16,
+    torch.bfloat16: BF16,
+    torch.float64: F64,
+    torch.bool: BOOL,
+    torch.uint8: U8,
+    torch.int8: I8,
+    torch.int16: I16,
+    torch.int32: I32,
+    torch.int64: I64,
+}
+
+# enum ntops_unary_op / ntops_binary_op
+UNARY_SILU, UNARY_GELU, UNARY_GELU_TANH, UNARY_EXP, UNARY_BITWISE_NOT = 1, 2, 3, 4, 5
+BINARY_ADD, BINARY_MUL, BINARY_BITWISE_AND, BINARY_BITWISE_OR = 1, 2, 3, 4
+
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_d = ctypes.c_double
+
+_SIGNATURES = {
+    "ntops_abi_version": (_i, []),
+    "ntops_last_error": (ctypes.c_char_p, []),
+    "ntops_unary": (_i, [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp]),
+    "ntops_binary": (
+        _i,
+        [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _i64, _d, _i64, _vp, _c_i64p, _vp],
+    ),
+    "ntops_cast": (_i, [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp]),
+    "ntops_rms_norm": (_i, [_i, _i64, _i64, _vp, _i64, _vp, _i, _d, _vp, _i64, _vp]),
+    "ntops_layer_norm": (_i, [_i, _i64, _i64, _vp, _i64, _vp, _vp, _i, _d, _vp, _i64, _vp]),
+    "ntops_softmax": (_i, [_i, _i, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp]),
+    "ntops_rope": (
+        _i,
+        [_i, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _vp, _i64, _i64, _i, _vp, _c_i64p, _vp],
+    ),
+    "ntops_gemm": (
+        _i,
+        [_i, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _d, _vp, _c_i64p, _vp],
+    ),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+_lib = None
+
+
+def load():
+    """Loads (once) and returns the CDLL; raises if the library is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"ntops_amd: native library {LIB_PATH} is missing; build it with "
+                "`make -C ntops_amd/csrc` (or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def i64_array(values):
+    values = tuple(int(v) for v in values)
+    return (ctypes.c_int64 * max(len(values), 1))(*values)
+
+
+def dtype_code(dtype):
+    try:
+        return DTYPE_CODE[dtype]
+    except KeyError:
+        raise TypeError(f"ntops_amd: unsupported dtype {dtype}") from None
+
+
+def stream_of(tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+
+
+def check(rc, what):
+    if rc != 0:
+        msg = load().ntops_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {msg} (status {rc})")
+
+
+def require_cuda(*tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                f"ntops_amd: expected a GPU tensor, got a tensor on {t.device}"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"ntops_amd: tensors on different devices ({dev} and {t.device})")
+    return dev

@@ -1,0 +1,331 @@
+// rms_norm and layer_norm over the trailing `cols` elements of each row.
+//
+// Math (fp32 accumulate, one rounding per output element):
+//   rms_norm   kernels/rms_norm.py:10-20 -- y = x * rsqrt(mean(x^2) + eps) * w
+//              (torch's fused CPU kernel applies the weight in fp32 before
+//              the single rounding; eps defaults are resolved by the caller)
+//   layer_norm kernels/layer_norm.py:11-31 -- mean, biased variance of
+//              (x - mean) (two passes over the register-resident row),
+//              rstd = 1 / sqrt(var + eps); written as torch's CPU kernel
+//              evaluates it: y = (x * rstd + (-mean * rstd)) * w + b.
+//
+// Vector path: one HBM read + one HBM write per element, row held in VGPRs
+// (see rowcommon.h).  Looped path (unaligned rows, or rows wider than 64K
+// 16-bit elements): one 256-thread block per row, scalar strided accesses,
+// re-reading the row from L2 for the second / third pass.
+#include "dispatch.h"
+#include "rowcommon.h"
+
+namespace ntops {
+namespace {
+
+template <typename T>
+__device__ __forceinline__ float to_f(T v) {
+  return static_cast<float>(v);
+}
+
+// -------------------------------------------------------------- rms_norm --
+template <typename T, typename W, int CHUNKS, int WPR>
+__global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_vec(
+    const T* __restrict__ x, int64_t xs, const W* __restrict__ w, T* __restrict__ y, int64_t ys,
+    int64_t rows, int cols, float eps) {
+  constexpr int V = Pack16<T>::N;
+  constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
+  __shared__ float red[RPB * WPR];
+  const RowPos p = row_pos<WPR>();
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + p.row_in_block;
+  const bool row_ok = row < rows;
+  const int npk = cols / V;
+  const T* xr = x + row * xs;
+
+  Pack16<T> r[CHUNKS];
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int pk = pack_of<WPR>(p, c);
+    if (row_ok && pk < npk)
+      r[c] = load16(xr + pk * V);
+    else
+#pragma unroll
+      for (int i = 0; i < V; ++i) r[c].v[i] = T(0);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float f = to_f(r[c].v[i]);
+      ss += f * f;
+    }
+  ss = row_sum<WPR>(ss, red, p);
+  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+
+  if (!row_ok) return;
+  T* yr = y + row * ys;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int pk = pack_of<WPR>(p, c);
+    if (pk < npk) {
+      float wv[V];
+      if (w != nullptr)
+        load_as_float<W, V>(w + pk * V, wv);
+      else
+#pragma unroll
+        for (int i = 0; i < V; ++i) wv[i] = 1.0f;
+      Pack16<T> o;
+#pragma unroll
+      for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(r[c].v[i]), rstd), wv[i]));
+      store16_nt(yr + pk * V, o);
+    }
+  }
+}
+
+template <typename T, typename W>
+__global__ __launch_bounds__(256) void k_rms_loop(const T* x, int64_t xs, const W* w, T* y,
+                                                   int64_t ys, int64_t cols, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * xs;
+  float ss = 0.f;
+  for (int64_t j = threadIdx.x; j < cols; j += 256) {
+    const float f = to_f(xr[j]);
+    ss += f * f;
+  }
+  ss = block_sum256(ss, red);
+  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+  T* yr = y + row * ys;
+  for (int64_t j = threadIdx.x; j < cols; j += 256) {
+    const float wv = w != nullptr ? static_cast<float>(w[j]) : 1.0f;
+    yr[j] = static_cast<T>(mul_nc(mul_nc(to_f(xr[j]), rstd), wv));
+  }
+}
+
+// ------------------------------------------------------------ layer_norm --
+template <typename T, typename W, int CHUNKS, int WPR>
+__global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_ln_vec(
+    const T* __restrict__ x, int64_t xs, const W* __restrict__ w, const W* __restrict__ b,
+    T* __restrict__ y, int64_t ys, int64_t rows, int cols, float eps) {
+  constexpr int V = Pack16<T>::N;
+  constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
+  __shared__ float red0[RPB * WPR];
+  __shared__ float red1[RPB * WPR];
+  const RowPos p = row_pos<WPR>();
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + p.row_in_block;
+  const bool row_ok = row < rows;
+  const int npk = cols / V;
+  const T* xr = x + row * xs;
+
+  Pack16<T> r[CHUNKS];
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int pk = pack_of<WPR>(p, c);
+    if (row_ok && pk < npk)
+      r[c] = load16(xr + pk * V);
+    else
+#pragma unroll
+      for (int i = 0; i < V; ++i) r[c].v[i] = T(0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+    for (int i = 0; i < V; ++i) s += to_f(r[c].v[i]);
+  const float mean = row_sum<WPR>(s, red0, p) / static_cast<float>(cols);
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const bool ok = pack_of<WPR>(p, c) < npk;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float d = ok ? to_f(r[c].v[i]) - mean : 0.f;
+      q += d * d;
+    }
+  }
+  const float var = row_sum<WPR>(q, red1, p) / static_cast<float>(cols);
+  const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
+  const float shift = -rstd * mean;
+
+  if (!row_ok) return;
+  T* yr = y + row * ys;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int pk = pack_of<WPR>(p, c);
+    if (pk < npk) {
+      float wv[V], bv[V];
+      if (w != nullptr)
+        load_as_float<W, V>(w + pk * V, wv);
+      else
+#pragma unroll
+        for (int i = 0; i < V; ++i) wv[i] = 1.0f;
+      if (b != nullptr)
+        load_as_float<W, V>(b + pk * V, bv);
+      else
+#pragma unroll
+        for (int i = 0; i < V; ++i) bv[i] = 0.0f;
+      Pack16<T> o;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float n = add_nc(mul_nc(to_f(r[c].v[i]), rstd), shift);
+        o.v[i] = static_cast<T>(add_nc(mul_nc(n, wv[i]), bv[i]));
+      }
+      store16_nt(yr + pk * V, o);
+    }
+  }
+}
+
+template <typename T, typename W>
+__global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W* w, const W* b,
+                                                  T* y, int64_t ys, int64_t cols, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * xs;
+  float s = 0.f;
+  for (int64_t j = threadIdx.x; j < cols; j += 256) s += to_f(xr[j]);
+  const float mean = block_sum256(s, red) / static_cast<float>(cols);
+  float q = 0.f;
+  for (int64_t j = threadIdx.x; j < cols; j += 256) {
+    const float d = to_f(xr[j]) - mean;
+    q += d * d;
+  }
+  const float var = block_sum256(q, red) / static_cast<float>(cols);
+  const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
+  const float shift = -rstd * mean;
+  T* yr = y + row * ys;
+  for (int64_t j = threadIdx.x; j < cols; j += 256) {
+    const float wv = w != nullptr ? static_cast<float>(w[j]) : 1.0f;
+    const float bv = b != nullptr ? static_cast<float>(b[j]) : 0.0f;
+    const float n = add_nc(mul_nc(to_f(xr[j]), rstd), shift);
+    yr[j] = static_cast<T>(add_nc(mul_nc(n, wv), bv));
+  }
+}
+
+// -------------------------------------------------------------- dispatch --
+// Picks (CHUNKS, WPR) so that WPR * 64 * CHUNKS * V >= cols with the fewest
+// waves per row that keep CHUNKS <= 8.  Returns false if no vector config
+// fits (then the looped kernel is used).
+struct VecCfg {
+  int chunks, wpr;
+};
+inline bool pick_cfg(int64_t cols, int V, VecCfg* cfg) {
+  const int64_t npk = cols / V;
+  static const VecCfg table[] = {{1, 1}, {2, 1}, {4, 1}, {8, 1}, {8, 2}, {8, 4}, {8, 8}, {8, 16}};
+  for (const VecCfg& c : table) {
+    if (static_cast<int64_t>(c.chunks) * c.wpr * 64 >= npk) {
+      *cfg = c;
+      return true;
+    }
+  }
+  return false;
+}
+
+#define NTOPS_ROW_CASES(MACRO) \
+  MACRO(1, 1)                  \
+  MACRO(2, 1)                  \
+  MACRO(4, 1)                  \
+  MACRO(8, 1)                  \
+  MACRO(8, 2)                  \
+  MACRO(8, 4)                  \
+  MACRO(8, 8)                  \
+  MACRO(8, 16)
+
+template <typename T, typename W>
+int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* wv, double eps,
+            void* yv, int64_t ys, hipStream_t st) {
+  const T* x = static_cast<const T*>(xv);
+  const W* w = static_cast<const W*>(wv);
+  T* y = static_cast<T*>(yv);
+  constexpr int V = Pack16<T>::N;
+  VecCfg cfg;
+  const bool vec = (cols % V == 0) && (xs % V == 0) && (ys % V == 0) && aligned16(x) &&
+                   aligned16(y) && (w == nullptr || aligned16(w)) && pick_cfg(cols, V, &cfg);
+  const float feps = static_cast<float>(eps);
+  if (vec) {
+#define NTOPS_RMS_CASE(CH, WP)                                                                \
+  if (cfg.chunks == CH && cfg.wpr == WP) {                                                    \
+    constexpr int RPB = RowShape<WP>::kRowsPerBlock;                                          \
+    hipLaunchKernelGGL((k_rms_vec<T, W, CH, WP>), dim3(ceil_div(rows, RPB)),                  \
+                       dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, y, ys, rows,            \
+                       static_cast<int>(cols), feps);                                         \
+    return check_launch("rms_norm");                                                          \
+  }
+    NTOPS_ROW_CASES(NTOPS_RMS_CASE)
+#undef NTOPS_RMS_CASE
+  }
+  hipLaunchKernelGGL((k_rms_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, y, ys, cols, feps);
+  return check_launch("rms_norm");
+}
+
+template <typename T, typename W>
+int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* wv,
+           const void* bv, double eps, void* yv, int64_t ys, hipStream_t st) {
+  const T* x = static_cast<const T*>(xv);
+  const W* w = static_cast<const W*>(wv);
+  const W* b = static_cast<const W*>(bv);
+  T* y = static_cast<T*>(yv);
+  constexpr int V = Pack16<T>::N;
+  VecCfg cfg;
+  const bool vec = (cols % V == 0) && (xs % V == 0) && (ys % V == 0) && aligned16(x) &&
+                   aligned16(y) && (w == nullptr || aligned16(w)) &&
+                   (b == nullptr || aligned16(b)) && pick_cfg(cols, V, &cfg);
+  const float feps = static_cast<float>(eps);
+  if (vec) {
+#define NTOPS_LN_CASE(CH, WP)                                                                 \
+  if (cfg.chunks == CH && cfg.wpr == WP) {                                                    \
+    constexpr int RPB = RowShape<WP>::kRowsPerBlock;                                          \
+    hipLaunchKernelGGL((k_ln_vec<T, W, CH, WP>), dim3(ceil_div(rows, RPB)),                   \
+                       dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, b, y, ys, rows,         \
+                       static_cast<int>(cols), feps);                                         \
+    return check_launch("layer_norm");                                                        \
+  }
+    NTOPS_ROW_CASES(NTOPS_LN_CASE)
+#undef NTOPS_LN_CASE
+  }
+  hipLaunchKernelGGL((k_ln_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, b, y, ys, cols,
+                     feps);
+  return check_launch("layer_norm");
+}
+
+int check_rows(const char* what, int64_t rows, int64_t cols, const void* x, const void* y) {
+  if (rows < 0 || cols < 0) return set_error(NTOPS_ERR_INVALID, "%s: negative size", what);
+  if (rows > 0 && cols > 0 && (x == nullptr || y == nullptr))
+    return set_error(NTOPS_ERR_INVALID, "%s: null pointer", what);
+  if (rows > 0x7fffffffLL) return set_error(NTOPS_ERR_INVALID, "%s: too many rows", what);
+  return NTOPS_OK;
+}
+
+}  // namespace
+}  // namespace ntops
+
+using namespace ntops;
+
+extern "C" int ntops_rms_norm(int dtype, int64_t rows, int64_t cols, const void* x,
+                              int64_t x_row_stride, const void* w, int w_dtype, double eps,
+                              void* y, int64_t y_row_stride, void* stream) {
+  if (int e = check_rows("rms_norm", rows, cols, x, y)) return e;
+  if (rows == 0 || cols == 0) return NTOPS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (w != nullptr && w_dtype != dtype && w_dtype != NTOPS_F32)
+    return set_error(NTOPS_ERR_UNSUPPORTED, "rms_norm: weight dtype must equal input dtype or be F32");
+  return dispatch_float16_32(dtype, "rms_norm", [&](auto tag) {
+    using T = decltype(tag);
+    if (w != nullptr && w_dtype == NTOPS_F32 && dtype != NTOPS_F32)
+      return run_rms<T, float>(rows, cols, x, x_row_stride, w, eps, y, y_row_stride, st);
+    return run_rms<T, T>(rows, cols, x, x_row_stride, w, eps, y, y_row_stride, st);
+  });
+}
+
+extern "C" int ntops_layer_norm(int dtype, int64_t rows, int64_t cols, const void* x,
+                                int64_t x_row_stride, const void* w, const void* b, int wb_dtype,
+                                double eps, void* y, int64_t y_row_stride, void* stream) {
+  if (int e = check_rows("layer_norm", rows, cols, x, y)) return e;
+  if (rows == 0 || cols == 0) return NTOPS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if ((w != nullptr || b != nullptr) && wb_dtype != dtype && wb_dtype != NTOPS_F32)
+    return set_error(NTOPS_ERR_UNSUPPORTED,
+                     "layer_norm: weight/bias dtype must equal input dtype or be F32");
+  return dispatch_float16_32(dtype, "layer_norm", [&](auto tag) {
+    using T = decltype(tag);
+    if ((w != nullptr || b != nullptr) && wb_dtype == NTOPS_F32 && dtype != NTOPS_F32)
+      return run_ln<T, float>(rows, cols, x, x_row_stride, w, b, eps, y, y_row_stride, st);
+    return run_ln<T, T>(rows, cols, x, x_row_stride, w, b, eps, y, y_row_stride, st);
+  });
+}

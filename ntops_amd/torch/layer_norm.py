@@ -1,0 +1,61 @@
+"""layer_norm -- mirror of src/ntops/torch/layer_norm.py:9-33
+(math: kernels/layer_norm.py:11-31; fp32 moments, biased variance)."""
+
+import math
+
+import torch
+
+from ntops_amd import _lib
+from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _to_dtype
+
+
+def layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
+    if isinstance(normalized_shape, int):
+        normalized_shape = (normalized_shape,)
+
+    normalized_shape = tuple(normalized_shape)
+    nd = len(normalized_shape)
+    if tuple(input.shape[input.dim() - nd :]) != normalized_shape or nd > input.dim():
+        raise RuntimeError(
+            f"layer_norm: normalized_shape {normalized_shape} does not match input shape {tuple(input.shape)}"
+        )
+    if input.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"layer_norm: unsupported dtype {input.dtype}")
+
+    dev = _lib.require_cuda(input, weight, bias)
+    cols = math.prod(normalized_shape)
+    rows = input.numel() // cols if cols else 0
+    x = _contiguous(input)
+    output = torch.empty_like(x)
+
+    # weight and bias share one dtype: the input's, or fp32 for both.
+    params = [p for p in (weight, bias) if p is not None]
+    for p in params:
+        if tuple(p.shape) != normalized_shape:
+            raise RuntimeError("layer_norm: weight/bias shape must equal normalized_shape")
+    wb_dtype = input.dtype
+    if params and all(p.dtype == torch.float32 for p in params):
+        wb_dtype = torch.float32
+    if weight is not None:
+        weight = _contiguous(_to_dtype(weight, wb_dtype))
+    if bias is not None:
+        bias = _contiguous(_to_dtype(bias, wb_dtype))
+
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        rc = lib.ntops_layer_norm(
+            _lib.dtype_code(input.dtype),
+            rows,
+            cols,
+            x.data_ptr(),
+            cols,
+            weight.data_ptr() if weight is not None else None,
+            bias.data_ptr() if bias is not None else None,
+            _lib.dtype_code(wb_dtype),
+            float(eps),
+            output.data_ptr(),
+            cols,
+            _lib.stream_of(output),
+        )
+    _lib.check(rc, "ntops_amd.layer_norm")
+    return output

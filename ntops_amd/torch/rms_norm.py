@@ -1,0 +1,64 @@
+"""rms_norm -- mirror of src/ntops/torch/rms_norm.py:9-31
+(math: kernels/rms_norm.py:10-20).
+
+Semantic deltas from ntops, following torch (the parity reference):
+`eps=None` uses torch.finfo(torch.float32).eps (what torch 2.10's fused CPU
+kernel uses for fp32/fp16/bf16 inputs), and the weight is applied in fp32
+before the single rounding of each output element."""
+
+import math
+
+import torch
+
+from ntops_amd import _lib
+from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _to_dtype
+
+
+def rms_norm(input, normalized_shape, weight=None, eps=None):
+    if isinstance(normalized_shape, int):
+        normalized_shape = (normalized_shape,)
+
+    normalized_shape = tuple(normalized_shape)
+    nd = len(normalized_shape)
+    if tuple(input.shape[input.dim() - nd :]) != normalized_shape or nd > input.dim():
+        raise RuntimeError(
+            f"rms_norm: normalized_shape {normalized_shape} does not match input shape {tuple(input.shape)}"
+        )
+    if input.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"rms_norm: unsupported dtype {input.dtype}")
+
+    if eps is None:
+        eps = torch.finfo(torch.float32).eps
+
+    dev = _lib.require_cuda(input, weight)
+    cols = math.prod(normalized_shape)
+    rows = input.numel() // cols if cols else 0
+    x = _contiguous(input)
+    output = torch.empty_like(x)
+
+    w_ptr, w_code = None, _lib.dtype_code(input.dtype)
+    if weight is not None:
+        if tuple(weight.shape) != normalized_shape:
+            raise RuntimeError("rms_norm: weight shape must equal normalized_shape")
+        if weight.dtype not in (input.dtype, torch.float32):
+            weight = _to_dtype(weight, input.dtype)
+        weight = _contiguous(weight)
+        w_ptr, w_code = weight.data_ptr(), _lib.dtype_code(weight.dtype)
+
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        rc = lib.ntops_rms_norm(
+            _lib.dtype_code(input.dtype),
+            rows,
+            cols,
+            x.data_ptr(),
+            cols,
+            w_ptr,
+            w_code,
+            float(eps),
+            output.data_ptr(),
+            cols,
+            _lib.stream_of(output),
+        )
+    _lib.check(rc, "ntops_amd.rms_norm")
+    return output

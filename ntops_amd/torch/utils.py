@@ -1,0 +1,233 @@
+"""Configuration knobs and shared launch helpers of ntops_amd.torch.
+
+The default-knob setters/getters keep the reference's public surface
+(src/ntops/torch/utils.py:10-43; tests/conftest.py:14 calls
+`set_default_max_num_configs`).  They tune NineToothed's Triton code
+generation in the reference; here every kernel is prebuilt for gfx950 with
+its launch shape chosen per call from the problem size, so the values are
+stored and returned but do not change any launch.
+"""
+
+import torch
+
+from ntops_amd import _lib
+from ntops_amd.kernels.mm import InputPrecisionVariant
+
+
+class _CachedMakeDefaultConfig:
+    def __init__(self, num_warps=None, num_stages=None, max_num_configs=None):
+        self.num_warps = num_warps
+        self.num_stages = num_stages
+        self.max_num_configs = max_num_configs
+
+
+_cached_make_default_config = _CachedMakeDefaultConfig()
+
+
+def get_default_num_warps():
+    return _cached_make_default_config.num_warps
+
+
+def set_default_num_warps(num_warps):
+    _cached_make_default_config.num_warps = num_warps
+
+
+def get_default_num_stages():
+    return _cached_make_default_config.num_stages
+
+
+def set_default_num_stages(num_stages):
+    _cached_make_default_config.num_stages = num_stages
+
+
+def get_default_max_num_configs():
+    return _cached_make_default_config.max_num_configs
+
+
+def set_default_max_num_configs(max_num_configs):
+    _cached_make_default_config.max_num_configs = max_num_configs
+
+
+def _get_matmul_input_precision():
+    """Mirror of src/ntops/torch/utils.py:218-222.
+
+    gfx950 has no reduced-precision (TF32/XF32) fp32 matrix path, so fp32
+    GEMMs always run IEEE fp32 whatever this returns."""
+    if torch.get_float32_matmul_precision() == "highest":
+        return InputPrecisionVariant.IEEE
+    return InputPrecisionVariant.TF32
+
+
+# --------------------------------------------------------------- helpers --
+
+
+class _DeviceGuard:
+    """Makes `device` current for the duration of a library call."""
+
+    def __init__(self, device):
+        self.device = device
+        self.prev = None
+
+    def __enter__(self):
+        idx = self.device.index if self.device.index is not None else 0
+        cur = torch.cuda.current_device()
+        if cur != idx:
+            self.prev = cur
+            torch.cuda.set_device(idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def _strides(t):
+    return _lib.i64_array(t.stride())
+
+
+def _cast_into(src, dst):
+    """dst[...] = src converted to dst.dtype (same shape; any strides)."""
+    lib = _lib.load()
+    rc = lib.ntops_cast(
+        _lib.dtype_code(src.dtype),
+        _lib.dtype_code(dst.dtype),
+        src.dim(),
+        _lib.i64_array(src.shape),
+        src.data_ptr(),
+        _strides(src),
+        dst.data_ptr(),
+        _strides(dst),
+        _lib.stream_of(dst),
+    )
+    _lib.check(rc, "ntops_amd cast")
+    return dst
+
+
+def _to_dtype(t, dtype):
+    """t converted to `dtype` by the native cast kernel (t itself if equal)."""
+    if t.dtype == dtype:
+        return t
+    out = torch.empty(t.shape, dtype=dtype, device=t.device)
+    return _cast_into(t, out)
+
+
+def _contiguous(t):
+    """A row-major copy of t made by the native copy kernel (t if already)."""
+    if t.is_contiguous():
+        return t
+    out = torch.empty(t.shape, dtype=t.dtype, device=t.device)
+    return _cast_into(t, out)
+
+
+def _prepare_out(out, shape, dtype, device, like=None):
+    """Output tensor for an elementwise result.
+
+    Returns (target, compute): `compute` has the compute dtype and is written
+    by the kernel; if it differs from `target` (an `out=` of another dtype),
+    the caller casts it into `target` afterwards."""
+    shape = torch.Size(shape)
+    if out is None:
+        if like is not None and like.shape == shape and like.dtype == dtype:
+            target = torch.empty_like(like)
+        else:
+            target = torch.empty(shape, dtype=dtype, device=device)
+        return target, target
+    _lib.require_cuda(out)
+    if out.shape != shape:
+        out.resize_(shape)
+    if out.dtype == dtype:
+        return out, out
+    if not torch.can_cast(dtype, out.dtype):
+        raise RuntimeError(f"result type {dtype} can't be cast to the desired output type {out.dtype}")
+    return out, torch.empty(shape, dtype=dtype, device=device)
+
+
+def _unary(op, input, output, what):
+    lib = _lib.load()
+    dev = _lib.require_cuda(input, output)
+    with _DeviceGuard(dev):
+        rc = lib.ntops_unary(
+            op,
+            _lib.dtype_code(input.dtype),
+            input.dim(),
+            _lib.i64_array(input.shape),
+            input.data_ptr(),
+            _strides(input),
+            output.data_ptr(),
+            _strides(output),
+            _lib.stream_of(output),
+        )
+    _lib.check(rc, what)
+    return output
+
+
+def _is_number(x):
+    return isinstance(x, (bool, int, float))
+
+
+def _binary(op, input, other, alpha, out, what):
+    """Shared body of add / mul / bitwise_and / bitwise_or with torch's
+    promotion (torch.result_type) and broadcasting rules."""
+    if not isinstance(input, torch.Tensor):
+        raise TypeError(f"{what}: input must be a tensor")
+    if isinstance(other, torch.Tensor) and other.dim() == 0 and not other.is_cuda:
+        other_is_tensor = False
+        result_dtype = torch.result_type(input, other)
+        other = other.item()
+    elif isinstance(other, torch.Tensor):
+        other_is_tensor = True
+        result_dtype = torch.result_type(input, other)
+    elif _is_number(other):
+        other_is_tensor = False
+        result_dtype = torch.result_type(input, other)
+    else:
+        raise TypeError(f"{what}: unsupported operand {type(other)}")
+
+    dev = _lib.require_cuda(input, other if other_is_tensor else None)
+    shape = torch.broadcast_shapes(input.shape, other.shape) if other_is_tensor else input.shape
+    target, res = _prepare_out(out, shape, result_dtype, dev, like=input)
+
+    a = _to_dtype(input, result_dtype).expand(shape)
+    is_float = result_dtype.is_floating_point
+    if alpha is None:
+        alpha_f, alpha_i = 1.0, 1
+    else:
+        if not is_float and isinstance(alpha, float):
+            raise RuntimeError(
+                "For integral input tensors, argument alpha must not be a floating point number."
+            )
+        if result_dtype == torch.bool and not isinstance(alpha, bool):
+            raise RuntimeError("Boolean alpha only supported for Boolean results.")
+        alpha_f, alpha_i = float(alpha), int(alpha) if not isinstance(alpha, float) else 0
+
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        if other_is_tensor:
+            b = _to_dtype(other, result_dtype).expand(shape)
+            b_ptr, b_strides, b_f, b_i = b.data_ptr(), _strides(b), 0.0, 0
+        else:
+            b_ptr, b_strides = None, None
+            b_f = float(other)
+            b_i = int(other) if not isinstance(other, float) else 0
+        rc = lib.ntops_binary(
+            op,
+            _lib.dtype_code(result_dtype),
+            len(shape),
+            _lib.i64_array(shape),
+            a.data_ptr(),
+            _strides(a),
+            b_ptr,
+            b_strides,
+            b_f,
+            b_i,
+            alpha_f,
+            alpha_i,
+            res.data_ptr(),
+            _strides(res),
+            _lib.stream_of(res),
+        )
+        _lib.check(rc, what)
+        if res is not target:
+            _cast_into(res, target)
+    return target

@@ -1,0 +1,359 @@
+"""CPU oracle for the ntops LLM hot path -- TEST INFRASTRUCTURE ONLY.
+
+A numpy restatement of each operator's algorithm, used by tests/, by
+__graft_entry__.smoke() and by bench.py's cpu_baseline leg as the checker of
+the HIP kernels.  Nothing in the product (ntops_amd/) imports it.
+
+Representation: arrays are numpy arrays in their storage dtype, with bf16
+carried as uint16 bit patterns and tagged by the dtype string "bf16"
+(numpy has no bfloat16).  dtype strings: "f32", "f16", "bf16", "f64",
+"bool", "u8", "i8", "i16", "i32", "i64".
+
+Each function cites the reference file it restates (paths relative to the
+mygitljf/ntops tree).  Where ntops and torch differ, the oracle follows torch's
+CPU kernels, which is the parity reference this build is held to; the
+deviation is stated in the docstring.
+
+Pinning (tests/test_oracle.py): every function is checked against golden
+vectors written by torch CPU (tests/golden/), against live torch CPU, and
+against closed forms / invariants / brute force chosen so that a dropped
+term, a wrong sign or a transposed operand fails.  No function is unpinned.
+"""
+
+import numpy as np
+
+FLOAT_DTYPES = ("f32", "f16", "bf16", "f64")
+INT_DTYPES = ("bool", "u8", "i8", "i16", "i32", "i64")
+
+_NP = {
+    "f32": np.float32,
+    "f16": np.float16,
+    "bf16": np.uint16,
+    "f64": np.float64,
+    "bool": np.bool_,
+    "u8": np.uint8,
+    "i8": np.int8,
+    "i16": np.int16,
+    "i32": np.int32,
+    "i64": np.int64,
+}
+
+
+def np_dtype(dt):
+    return _NP[dt]
+
+
+# ---------------------------------------------------------------- bf16 ----
+
+
+def bf16_to_f32(u):
+    """bf16 bit patterns -> float32 (exact)."""
+    u = np.asarray(u, dtype=np.uint16)
+    return (u.astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def f32_to_bf16(f):
+    """float32 -> bf16 bit patterns, round to nearest even; NaN -> 0x7FC0
+    (c10::BFloat16's round_to_nearest_even)."""
+    f = np.ascontiguousarray(np.asarray(f, dtype=np.float32))
+    u = f.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r = np.where(np.isnan(f), np.uint16(0x7FC0), r)
+    return r.astype(np.uint16)
+
+
+def compute_type(dt):
+    """Opmath type: fp32 for 16-bit floats and fp32, fp64 for fp64."""
+    return np.float64 if dt == "f64" else np.float32
+
+
+def to_compute(a, dt):
+    """Storage -> opmath value (exact)."""
+    if dt == "bf16":
+        return bf16_to_f32(a)
+    if dt == "f64":
+        return np.asarray(a, dtype=np.float64)
+    return np.asarray(a).astype(np.float32)
+
+
+def round_to(v, dt):
+    """Opmath value -> storage dtype with one rounding (RNE)."""
+    if dt == "bf16":
+        return f32_to_bf16(np.asarray(v, dtype=np.float32))
+    if dt == "f16":
+        return np.asarray(v, dtype=np.float32).astype(np.float16)
+    if dt == "f32":
+        return np.asarray(v, dtype=np.float32)
+    if dt == "f64":
+        return np.asarray(v, dtype=np.float64)
+    raise ValueError(dt)
+
+
+def rnd(v, dt):
+    """Round an opmath value to dt and return it as opmath again."""
+    return to_compute(round_to(v, dt), dt)
+
+
+def _fma32(a, b, c):
+    """fp32 fused multiply-add a*b + c with a single rounding, computed in
+    fp64 (a*b is exact in fp64 for fp32 operands) then rounded to fp32."""
+    return (a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)).astype(np.float32)
+
+
+def _with_errstate(fn):
+    def wrapped(*args, **kwargs):
+        with np.errstate(all="ignore"):
+            return fn(*args, **kwargs)
+
+    wrapped.__name__ = fn.__name__
+    wrapped.__doc__ = fn.__doc__
+    return wrapped
+
+
+# ------------------------------------------------------------ unary ops ---
+
+
+@_with_errstate
+def silu(x, dt):
+    """kernels/silu.py:10 -- output = input / (1 + exp(-fp32(input)))."""
+    c = to_compute(x, dt)
+    one = compute_type(dt)(1)
+    return round_to(c / (one + np.exp(-c)), dt)
+
+
+@_with_errstate
+def gelu(x, dt, approximate="none"):
+    """kernels/gelu.py:10-26.  "none": x * 0.5 * (1 + erf(x / sqrt 2)), the
+    division by sqrt 2 applied as a multiply by 1/sqrt 2 (torch's CPU form);
+    "tanh": 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 x^3)))."""
+    from scipy.special import erf
+
+    c = to_compute(x, dt)
+    T = compute_type(dt)
+    if approximate == "tanh":
+        beta = T(np.sqrt(2.0) * (2.0 / np.sqrt(np.pi)) * 0.5)
+        kappa = T(0.044715)
+        inner = beta * (c + kappa * (c * c * c))
+        return round_to(T(0.5) * c * (T(1) + np.tanh(inner)), dt)
+    y = c * T(0.5) * (T(1) + erf(c * T(1.0 / np.sqrt(2.0))).astype(T))
+    return round_to(y, dt)
+
+
+@_with_errstate
+def exp(x, dt):
+    """kernels/exp.py:10 -- exp(input) in opmath, rounded to dt."""
+    return round_to(np.exp(to_compute(x, dt)), dt)
+
+
+def bitwise_not(x, dt):
+    """kernels/bitwise_not.py:9-14 -- ~x; logical not for bool."""
+    x = np.asarray(x)
+    if dt == "bool":
+        return np.logical_not(x)
+    return np.invert(x)
+
+
+# ----------------------------------------------------------- binary ops ---
+
+
+def _int_wrap(v, dt):
+    """int64 arithmetic result -> dt with two's-complement wrap-around."""
+    if dt == "bool":
+        return v != 0
+    return v.astype(np.int64).astype(np_dtype(dt))
+
+
+@_with_errstate
+def add(a, b, dt, alpha=1):
+    """kernels/add.py:10 -- input + alpha * other.
+
+    Floating: alpha is first rounded to dt, then a single-rounding fma in
+    opmath (torch's CPU kernel: vec::fmadd(other, alpha, self)); `b` may be a
+    Python number, which torch's CPU add rounds to dt as well.  Integral:
+    modular arithmetic; bool: (a + alpha*b) != 0."""
+    if dt in FLOAT_DTYPES:
+        al = to_compute(round_to(np.asarray(alpha, dtype=np.float64), dt), dt)
+        ac = to_compute(a, dt)
+        if np.isscalar(b) or np.ndim(b) == 0 and not isinstance(b, np.ndarray):
+            bc = to_compute(round_to(np.asarray(float(b)), dt), dt)
+        else:
+            bc = to_compute(b, dt)
+        bc, ac = np.broadcast_arrays(bc, ac)
+        if dt == "f64":
+            return ac + bc * al  # exactness of the fp64 fma is not needed at fp64 tolerance
+        return round_to(_fma32(bc, np.broadcast_to(al, bc.shape), ac), dt)
+    av = np.asarray(a).astype(np.int64)
+    bv = np.asarray(b).astype(np.int64)
+    with np.errstate(over="ignore"):
+        return _int_wrap(av + np.int64(int(alpha)) * bv, dt)
+
+
+@_with_errstate
+def mul(a, b, dt):
+    """kernels/mul.py:9 -- input * other in opmath, one rounding.  A Python
+    number `b` stays in opmath (torch's CPU mul does not round it to dt)."""
+    if dt in FLOAT_DTYPES:
+        ac = to_compute(a, dt)
+        if np.isscalar(b):
+            bc = compute_type(dt)(b)
+        else:
+            bc = to_compute(b, dt)
+        return round_to(ac * bc, dt)
+    if dt == "bool":
+        return np.logical_and(a, b)
+    with np.errstate(over="ignore"):
+        return _int_wrap(np.asarray(a).astype(np.int64) * np.asarray(b).astype(np.int64), dt)
+
+
+def bitwise_and(a, b, dt):
+    """kernels/bitwise_and.py:9 -- input & other (logical for bool)."""
+    if dt == "bool":
+        return np.logical_and(a, b)
+    return np.bitwise_and(np.asarray(a), np.asarray(b)).astype(np_dtype(dt))
+
+
+def bitwise_or(a, b, dt):
+    """kernels/bitwise_or.py:9 -- input | other (logical for bool)."""
+    if dt == "bool":
+        return np.logical_or(a, b)
+    return np.bitwise_or(np.asarray(a), np.asarray(b)).astype(np_dtype(dt))
+
+
+# --------------------------------------------------------- row reductions -
+
+
+def _rows(x, cols):
+    return np.asarray(x).reshape(-1, cols)
+
+
+@_with_errstate
+def rms_norm(x, dt, cols, weight=None, eps=None, w_dt=None):
+    """kernels/rms_norm.py:10-20 -- per row: rms = sqrt(sum(x^2)/N + eps) with
+    fp32 accumulation; y = x / rms * w.
+
+    Follows torch's fused CPU kernel: eps=None means finfo(float32).eps and
+    the output is bf16/f16(x * (1/rms) * w) with x, 1/rms and w in fp32 and a
+    single rounding (ntops instead rounds x / rms to dt before the weight and
+    uses finfo(dt).eps)."""
+    shape = np.shape(x)
+    xf = _rows(to_compute(x, dt), cols).astype(np.float32)
+    if eps is None:
+        eps = float(np.finfo(np.float32).eps)
+    ss = np.sum(xf * xf, axis=1, dtype=np.float32)
+    rstd = np.float32(1) / np.sqrt(ss / np.float32(cols) + np.float32(eps))
+    y = xf * rstd[:, None]
+    if weight is not None:
+        y = y * to_compute(weight, w_dt or dt).reshape(1, cols).astype(np.float32)
+    return round_to(y, dt).reshape(shape)
+
+
+@_with_errstate
+def layer_norm(x, dt, cols, weight=None, bias=None, eps=1e-5, wb_dt=None):
+    """kernels/layer_norm.py:11-31 -- mean and biased variance of each row in
+    fp32 (two passes), rstd = 1 / sqrt(var + eps), y = (x - mean) * rstd * w + b,
+    evaluated in torch's CPU order (x * rstd + (-rstd * mean)) * w + b."""
+    shape = np.shape(x)
+    xf = _rows(to_compute(x, dt), cols).astype(np.float32)
+    mean = np.sum(xf, axis=1, dtype=np.float32) / np.float32(cols)
+    d = xf - mean[:, None]
+    var = np.sum(d * d, axis=1, dtype=np.float32) / np.float32(cols)
+    rstd = np.float32(1) / np.sqrt(np.maximum(var, np.float32(0)) + np.float32(eps))
+    y = xf * rstd[:, None] + (-rstd * mean)[:, None]
+    if weight is not None:
+        y = y * to_compute(weight, wb_dt or dt).reshape(1, cols).astype(np.float32)
+    if bias is not None:
+        y = y + to_compute(bias, wb_dt or dt).reshape(1, cols).astype(np.float32)
+    return round_to(y, dt).reshape(shape)
+
+
+@_with_errstate
+def softmax(x, dim, in_dt, out_dt=None):
+    """kernels/softmax.py:9-29 -- max, sum of exp(x - max), exp(x - max)/sum.
+
+    The input is rounded to the output dtype first; max/sum accumulate in
+    fp32 (fp64 for fp64 output) and the result is exp(x - max) * (1/sum)
+    rounded once -- torch's CPU kernel.  (ntops accumulates in the output
+    dtype.)  An all -inf row gives NaN."""
+    out_dt = out_dt or in_dt
+    xin = to_compute(x, in_dt)
+    xo = to_compute(round_to(xin, out_dt), out_dt)
+    T = compute_type(out_dt)
+    xo = xo.astype(T)
+    if xo.ndim == 0:
+        return round_to(np.ones((), dtype=T), out_dt)
+    m = np.max(xo, axis=dim, keepdims=True)
+    e = np.exp(xo - m)
+    s = np.sum(e, axis=dim, keepdims=True, dtype=T)
+    return round_to(e * (T(1) / s), out_dt)
+
+
+# ------------------------------------------------------------------ RoPE --
+
+
+@_with_errstate
+def rotary_position_embedding(x, sin_table, cos_table, dt, interleaved=True):
+    """kernels/rotary_position_embedding.py:6-47 on (B, S, H, D) input.
+
+    Pairs are (2i, 2i+1) when interleaved, else (i, i + D/2).  Tables are
+    (S, D/2) -- one angle per pair, ntops' form -- or (S, D), one value per
+    element (x*cos + rotate_half(x)*sin).  out0 = x0*c0 - x1*s0,
+    out1 = x1*c1 + x0*s1, with every product and sum rounded to dt (torch's
+    eager evaluation order)."""
+    xc = to_compute(x, dt)
+    B, S, H, D = xc.shape
+    sn = to_compute(sin_table, dt)[:S]
+    cs = to_compute(cos_table, dt)[:S]
+    half = D // 2
+    if interleaved:
+        i0 = np.arange(0, D, 2)
+        i1 = i0 + 1
+    else:
+        i0 = np.arange(half)
+        i1 = i0 + half
+    x0 = xc[..., i0]
+    x1 = xc[..., i1]
+    if sn.shape[1] == D:
+        c0, s0, c1, s1 = cs[:, i0], sn[:, i0], cs[:, i1], sn[:, i1]
+    else:
+        c0 = c1 = cs
+        s0 = s1 = sn
+    c0, s0, c1, s1 = (t[None, :, None, :] for t in (c0, s0, c1, s1))
+    o0 = rnd(rnd(x0 * c0, dt) - rnd(x1 * s0, dt), dt)
+    o1 = rnd(rnd(x1 * c1, dt) + rnd(x0 * s1, dt), dt)
+    out = np.empty_like(xc)
+    out[..., i0] = o0
+    out[..., i1] = o1
+    return round_to(out, dt)
+
+
+def rope_tables(seq_len, emb_dim, base=10000.0, full=False):
+    """fp32 sin/cos tables built like tests/test_rotary_position_embedding.py:
+    37-45: theta_i = base^(-2i/D), angles = positions * theta.  With
+    full=True the (S, D/2) tables are duplicated to (S, D) (rotate_half form)."""
+    i = np.arange(emb_dim // 2, dtype=np.float32)
+    theta = np.float32(base) ** (-np.float32(2) * (i / np.float32(emb_dim)))
+    pos = np.arange(seq_len, dtype=np.float32)[:, None]
+    ang = (pos * theta[None, :]).astype(np.float32)
+    s, c = np.sin(ang).astype(np.float32), np.cos(ang).astype(np.float32)
+    if full:
+        s = np.concatenate([s, s], axis=1)
+        c = np.concatenate([c, c], axis=1)
+    return s, c
+
+
+# ------------------------------------------------------------------ GEMM --
+
+
+def gemm(a, b, dt, c=None, alpha=1.0, beta=0.0):
+    """kernels/mm.py:54-65, kernels/bmm.py:26-39, kernels/addmm.py:64-67 --
+    acc = sum_k a[..., m, k] * b[..., k, n] accumulated at (at least) fp32
+    precision (here fp64, exact enough to bound the kernel's fp32 summation
+    error), out = alpha * acc + beta * c rounded once to dt.  beta == 0
+    ignores c."""
+    af = to_compute(a, dt).astype(np.float64)
+    bf = to_compute(b, dt).astype(np.float64)
+    acc = np.matmul(af, bf)
+    out = np.float64(alpha) * acc
+    if c is not None and beta != 0:
+        out = out + np.float64(beta) * to_compute(c, dt).astype(np.float64)
+    return round_to(out.astype(np.float32) if dt != "f64" else out, dt)

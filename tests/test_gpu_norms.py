@@ -1,0 +1,133 @@
+"""GPU parity: rms_norm and layer_norm against the oracle (and torch CPU).
+
+Mirrors tests/test_rms_norm.py:11-30 and tests/test_layer_norm.py:11-37 of
+the reference (eps sweeps, weight/bias None, random normalized_shape suffix)
+with bf16 added, every register-resident row configuration and the looped
+fallback, and the bf16 (16384, 4096) config at full size."""
+
+import random
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import ntops_amd
+from oracle import ops as O
+from tests.helpers import DT_NAME, TOL_REDUCTION, assert_close, from_np, random_shape, to_np
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+
+FLOATS = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def cases():
+    out = []
+    for ndim in range(1, 5):
+        for dtype in FLOATS:
+            out.append((random_shape(ndim), dtype))
+    return out
+
+
+@pytest.mark.parametrize("eps", (None, 0, 1e-5, 1e-3))
+@pytest.mark.parametrize("weight_is_none", (False, True))
+@pytest.mark.parametrize("shape, dtype", cases())
+def test_rms_norm(shape, dtype, weight_is_none, eps):
+    x = torch.randn(shape).to(dtype)
+    normalized_shape = shape[-random.randint(1, len(shape)) :]
+    w = None if weight_is_none else torch.randn(normalized_shape).to(dtype)
+    got = ntops_amd.torch.rms_norm(x.cuda(), normalized_shape, weight=None if w is None else w.cuda(), eps=eps)
+    dt = DT_NAME[dtype]
+    cols = int(np.prod(normalized_shape))
+    exp = from_np(O.rms_norm(to_np(x), dt, cols, None if w is None else to_np(w), eps), dt)
+    rtol, atol = TOL_REDUCTION[dt]
+    assert_close(got, exp, rtol, atol, "rms_norm vs oracle")
+    ref = F.rms_norm(x, normalized_shape, weight=w, eps=eps)
+    assert_close(got, ref, rtol, atol, "rms_norm vs torch cpu")
+
+
+@pytest.mark.parametrize("eps", (1e-8, 1e-5, 1e-3))
+@pytest.mark.parametrize("bias_is_none", (False, True))
+@pytest.mark.parametrize("weight_is_none", (False, True))
+@pytest.mark.parametrize("shape, dtype", cases())
+def test_layer_norm(shape, dtype, weight_is_none, bias_is_none, eps):
+    x = torch.randn(shape).to(dtype)
+    normalized_shape = shape[-random.randint(1, len(shape)) :]
+    w = None if weight_is_none else torch.randn(normalized_shape).to(dtype)
+    b = None if bias_is_none else torch.randn(normalized_shape).to(dtype)
+    got = ntops_amd.torch.layer_norm(
+        x.cuda(), normalized_shape, weight=None if w is None else w.cuda(), bias=None if b is None else b.cuda(), eps=eps
+    )
+    dt = DT_NAME[dtype]
+    cols = int(np.prod(normalized_shape))
+    exp = from_np(O.layer_norm(to_np(x), dt, cols, None if w is None else to_np(w), None if b is None else to_np(b), eps), dt)
+    rtol, atol = TOL_REDUCTION[dt]
+    assert_close(got, exp, rtol, atol, "layer_norm vs oracle")
+    ref = F.layer_norm(x, normalized_shape, weight=w, bias=b, eps=eps)
+    assert_close(got, ref, rtol, atol, "layer_norm vs torch cpu")
+
+
+# Widths that hit every (chunks, waves-per-row) configuration of the vector
+# path for 16-bit and fp32 rows, plus widths that force the looped kernel
+# (not a multiple of the 16-byte pack, and wider than the register budget).
+WIDTHS = [8, 40, 512, 1000, 1024, 2048, 4096, 8192, 12288, 16384, 32768, 65536, 4100, 4099, 70000]
+
+
+@pytest.mark.parametrize("cols", WIDTHS)
+@pytest.mark.parametrize("dtype", FLOATS)
+def test_norm_widths(cols, dtype):
+    rows = 5
+    x = torch.randn(rows, cols).to(dtype)
+    w = (1 + 0.02 * torch.randn(cols)).to(dtype)
+    b = (0.02 * torch.randn(cols)).to(dtype)
+    dt = DT_NAME[dtype]
+    rtol, atol = TOL_REDUCTION[dt]
+    got = ntops_amd.torch.rms_norm(x.cuda(), (cols,), w.cuda(), 1e-6)
+    assert_close(got, from_np(O.rms_norm(to_np(x), dt, cols, to_np(w), 1e-6), dt), rtol, atol, f"rms {cols}")
+    got = ntops_amd.torch.layer_norm(x.cuda(), (cols,), w.cuda(), b.cuda(), 1e-5)
+    assert_close(got, from_np(O.layer_norm(to_np(x), dt, cols, to_np(w), to_np(b), 1e-5), dt), rtol, atol, f"ln {cols}")
+
+
+def test_norm_noncontiguous_input_and_fp32_weight():
+    x = torch.randn(64, 96).bfloat16()
+    xg = x.cuda().t()  # (96, 64) non-contiguous
+    w32 = 1 + 0.02 * torch.randn(64)
+    got = ntops_amd.torch.rms_norm(xg, (64,), w32.cuda(), 1e-6)
+    exp = from_np(O.rms_norm(to_np(x.t()), "bf16", 64, w32.numpy(), 1e-6, w_dt="f32"), "bf16")
+    assert_close(got, exp, 1.6e-2, 1.6e-2, "rms fp32 weight")
+    got = ntops_amd.torch.layer_norm(xg, (64,), w32.cuda(), w32.cuda() - 1, 1e-5)
+    exp = from_np(O.layer_norm(to_np(x.t()), "bf16", 64, w32.numpy(), (w32 - 1).numpy(), 1e-5, wb_dt="f32"), "bf16")
+    assert_close(got, exp, 1.6e-2, 1.6e-2, "ln fp32 weight")
+
+
+def _config_inputs():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(16384, 4096, generator=g).bfloat16()
+    w = (1 + 0.02 * torch.randn(4096, generator=g)).bfloat16()
+    b = (0.02 * torch.randn(4096, generator=g)).bfloat16()
+    return x, w, b
+
+
+def test_rms_norm_config_full_size():
+    """bf16 (16384, 4096), w ~N(1, 0.02), eps = 1e-6: every element against
+    the oracle; the output RMS of every row is 1 up to the weight."""
+    x, w, _ = _config_inputs()
+    got = ntops_amd.torch.rms_norm(x.cuda(), (4096,), w.cuda(), 1e-6)
+    exp = from_np(O.rms_norm(to_np(x), "bf16", 4096, to_np(w), 1e-6), "bf16")
+    assert_close(got, exp, 1.6e-2, 1.6e-2, "rms_norm config")
+    mism = (got.cpu() != exp).float().mean().item()
+    assert mism < 1e-3, f"bit mismatch fraction {mism}"
+    unweighted = (got.float() / w.cuda().float()).pow(2).mean(-1).sqrt()
+    assert torch.allclose(unweighted, torch.ones_like(unweighted), atol=2e-2)
+
+
+def test_layer_norm_config_full_size():
+    x, w, b = _config_inputs()
+    got = ntops_amd.torch.layer_norm(x.cuda(), (4096,), w.cuda(), b.cuda(), 1e-5)
+    exp = from_np(O.layer_norm(to_np(x), "bf16", 4096, to_np(w), to_np(b), 1e-5), "bf16")
+    assert_close(got, exp, 1.6e-2, 1.6e-2, "layer_norm config")
+    mism = (got.cpu() != exp).float().mean().item()
+    assert mism < 1e-3, f"bit mismatch fraction {mism}"
