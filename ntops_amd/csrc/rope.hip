@@ -61,8 +61,10 @@ __global__ __launch_bounds__(256) void k_rope_half_vec(const T* x, const T* sn, 
   const int64_t b = r / a.S;
   const int64_t xo = b * a.xs[0] + s * a.xs[1] + h * a.xs[2] + j * V;
   const int64_t yo = b * a.ys[0] + s * a.ys[1] + h * a.ys[2] + j * V;
-  const Pack16<T> x0 = load16(x + xo);
-  const Pack16<T> x1 = load16(x + xo + half);
+  // x and y stream through once (non-temporal); the tables stay cacheable
+  // because every head of a position re-reads them.
+  const Pack16<T> x0 = load16_nt(x + xo);
+  const Pack16<T> x1 = load16_nt(x + xo + half);
   const T* ct = cs + s * a.trs + j * V;
   const T* st = sn + s * a.trs + j * V;
   const Pack16<T> c0 = load16(ct);
@@ -82,8 +84,8 @@ __global__ __launch_bounds__(256) void k_rope_half_vec(const T* x, const T* sn, 
     o0.v[i] = static_cast<T>(r0);
     o1.v[i] = static_cast<T>(r1);
   }
-  store16(y + yo, o0);
-  store16(y + yo + half, o1);
+  store16_nt(y + yo, o0);
+  store16_nt(y + yo + half, o1);
 }
 
 // Interleaved, vector path.  Work item = (row, pack j over the whole row);
@@ -103,7 +105,7 @@ __global__ __launch_bounds__(256) void k_rope_inter_vec(const T* x, const T* sn,
   const int64_t b = r / a.S;
   const int64_t xo = b * a.xs[0] + s * a.xs[1] + h * a.xs[2] + j * V;
   const int64_t yo = b * a.ys[0] + s * a.ys[1] + h * a.ys[2] + j * V;
-  const Pack16<T> xv = load16(x + xo);
+  const Pack16<T> xv = load16_nt(x + xo);
   float c[V], sv[V];
   if (a.tcols == a.D) {
     const Pack16<T> cp = load16(cs + s * a.trs + j * V);
@@ -131,7 +133,7 @@ __global__ __launch_bounds__(256) void k_rope_inter_vec(const T* x, const T* sn,
     o.v[2 * i] = static_cast<T>(r0);
     o.v[2 * i + 1] = static_cast<T>(r1);
   }
-  store16(y + yo, o);
+  store16_nt(y + yo, o);
 }
 
 // Generic path: one thread per pair, any strides.

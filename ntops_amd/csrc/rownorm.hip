@@ -43,7 +43,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_vec(
   for (int c = 0; c < CHUNKS; ++c) {
     const int pk = pack_of<WPR>(p, c);
     if (row_ok && pk < npk)
-      r[c] = load16(xr + pk * V);
+      r[c] = load16_nt(xr + pk * V);
     else
 #pragma unroll
       for (int i = 0; i < V; ++i) r[c].v[i] = T(0);
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_ln_vec(
   for (int c = 0; c < CHUNKS; ++c) {
     const int pk = pack_of<WPR>(p, c);
     if (row_ok && pk < npk)
-      r[c] = load16(xr + pk * V);
+      r[c] = load16_nt(xr + pk * V);
     else
 #pragma unroll
       for (int i = 0; i < V; ++i) r[c].v[i] = T(0);
@@ -199,34 +199,6 @@ __global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W
 }
 
 // -------------------------------------------------------------- dispatch --
-// Picks (CHUNKS, WPR) so that WPR * 64 * CHUNKS * V >= cols with the fewest
-// waves per row that keep CHUNKS <= 8.  Returns false if no vector config
-// fits (then the looped kernel is used).
-struct VecCfg {
-  int chunks, wpr;
-};
-inline bool pick_cfg(int64_t cols, int V, VecCfg* cfg) {
-  const int64_t npk = cols / V;
-  static const VecCfg table[] = {{1, 1}, {2, 1}, {4, 1}, {8, 1}, {8, 2}, {8, 4}, {8, 8}, {8, 16}};
-  for (const VecCfg& c : table) {
-    if (static_cast<int64_t>(c.chunks) * c.wpr * 64 >= npk) {
-      *cfg = c;
-      return true;
-    }
-  }
-  return false;
-}
-
-#define NTOPS_ROW_CASES(MACRO) \
-  MACRO(1, 1)                  \
-  MACRO(2, 1)                  \
-  MACRO(4, 1)                  \
-  MACRO(8, 1)                  \
-  MACRO(8, 2)                  \
-  MACRO(8, 4)                  \
-  MACRO(8, 8)                  \
-  MACRO(8, 16)
-
 template <typename T, typename W>
 int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* wv, double eps,
             void* yv, int64_t ys, hipStream_t st) {
@@ -236,7 +208,7 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
   constexpr int V = Pack16<T>::N;
   VecCfg cfg;
   const bool vec = (cols % V == 0) && (xs % V == 0) && (ys % V == 0) && aligned16(x) &&
-                   aligned16(y) && (w == nullptr || aligned16(w)) && pick_cfg(cols, V, &cfg);
+                   aligned16(y) && (w == nullptr || aligned16(w)) && pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
   if (vec) {
 #define NTOPS_RMS_CASE(CH, WP)                                                                \
@@ -265,7 +237,7 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
   VecCfg cfg;
   const bool vec = (cols % V == 0) && (xs % V == 0) && (ys % V == 0) && aligned16(x) &&
                    aligned16(y) && (w == nullptr || aligned16(w)) &&
-                   (b == nullptr || aligned16(b)) && pick_cfg(cols, V, &cfg);
+                   (b == nullptr || aligned16(b)) && pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
   if (vec) {
 #define NTOPS_LN_CASE(CH, WP)                                                                 \

@@ -46,7 +46,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_softmax_vec(
   for (int c = 0; c < CHUNKS; ++c) {
     const int pk = pack_of<WPR>(p, c);
     if (row_ok && pk < npk) {
-      const Pack16<T> r = load16(xr + pk * V);
+      const Pack16<T> r = load16_nt(xr + pk * V);
 #pragma unroll
       for (int i = 0; i < V; ++i) v[c][i] = static_cast<C>(r.v[i]);
     } else {
@@ -132,31 +132,6 @@ __global__ __launch_bounds__(256) void k_softmax_col(const Ti* x, int64_t xs0, i
   }
 }
 
-struct VecCfg {
-  int chunks, wpr;
-};
-inline bool pick_cfg(int64_t cols, int V, VecCfg* cfg) {
-  const int64_t npk = cols / V;
-  static const VecCfg table[] = {{1, 1}, {2, 1}, {4, 1}, {8, 1}, {8, 2}, {8, 4}, {8, 8}, {8, 16}};
-  for (const VecCfg& c : table) {
-    if (static_cast<int64_t>(c.chunks) * c.wpr * 64 >= npk) {
-      *cfg = c;
-      return true;
-    }
-  }
-  return false;
-}
-
-#define NTOPS_ROW_CASES(MACRO) \
-  MACRO(1, 1)                  \
-  MACRO(2, 1)                  \
-  MACRO(4, 1)                  \
-  MACRO(8, 1)                  \
-  MACRO(8, 2)                  \
-  MACRO(8, 4)                  \
-  MACRO(8, 8)                  \
-  MACRO(8, 16)
-
 template <typename Ti, typename To>
 int run_softmax(int64_t outer, int64_t dim, int64_t inner, const void* xv, const int64_t* xs,
                 void* yv, const int64_t* ys, hipStream_t st) {
@@ -168,7 +143,7 @@ int run_softmax(int64_t outer, int64_t dim, int64_t inner, const void* xv, const
       constexpr int V = Pack16<To>::N;
       VecCfg cfg;
       const bool vec = xs[1] == 1 && ys[1] == 1 && dim % V == 0 && xs[0] % V == 0 &&
-                       ys[0] % V == 0 && aligned16(x) && aligned16(y) && pick_cfg(dim, V, &cfg) &&
+                       ys[0] % V == 0 && aligned16(x) && aligned16(y) && pick_row_cfg(dim / V, &cfg) &&
                        outer <= 0x7fffffffLL * 4;
       if (vec) {
 #define NTOPS_SM_CASE(CH, WP)                                                                  \
