@@ -45,7 +45,137 @@ def parse_args():
     p.add_argument("--ops", default="all")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     p.add_argument("--eager", action="store_true", help="time eager wrapper calls instead of a graph")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="run 10 plain 128 MiB copies (ntops_cast f32->f32) for byte-counter calibration")
+    p.add_argument("--rocprof-summary", metavar="DB", help="print kernel-duration stats of a rocprofv3 database")
+    p.add_argument("--traffic", metavar="DIR",
+                   help="print calibrated HBM bytes per launch (JSON) from rocprofv3 --pmc databases in "
+                        "DIR/<workload>_{FETCH,WRITE}_SIZE/ and DIR/cal_{FETCH,WRITE}_SIZE/")
+    p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic.json"),
+                   help="measured HBM bytes per launch used to fill roofline.traffic")
     return p.parse_args()
+
+
+# ------------------------------------------------- rocprofv3 post-processing
+
+
+def _db_rows(db, sql):
+    import sqlite3
+
+    con = sqlite3.connect(db)
+    try:
+        return con.execute(sql).fetchall()
+    finally:
+        con.close()
+
+
+def _kernel_key(name):
+    """Short stable key of a kernel symbol (template arguments kept)."""
+    import re
+
+    n = re.sub(r"\(anonymous namespace\)::", "", name)
+    n = n.replace("ntops::", "")
+    return n[:160]
+
+
+def rocprof_summary(db):
+    rows = _db_rows(db, "select name, duration from kernels")
+    by = {}
+    for n, d in rows:
+        by.setdefault(_kernel_key(n), []).append(d / 1e3)
+    print("| kernel | calls | mean us | median us | min us | max us |")
+    print("|---|---|---|---|---|---|")
+    for n, ds in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{n}` | {len(ds)} | {statistics.mean(ds):.2f} | {statistics.median(ds):.2f} | "
+              f"{min(ds):.2f} | {max(ds):.2f} |")
+
+
+def _counter_means(db):
+    rows = _db_rows(db, "select kernel_name, counter_name, value, dispatch_id from counters_collection")
+    per = {}
+    for n, c, v, d in rows:
+        per.setdefault((_kernel_key(n), c), {}).setdefault(d, 0.0)
+        per[(_kernel_key(n), c)][d] += v
+    return {k: statistics.mean(v.values()) for k, v in per.items()}
+
+
+COPY_CAL_BYTES = 128 << 20
+
+
+def _one_db(d):
+    import glob
+
+    dbs = sorted(glob.glob(os.path.join(d, "*.db")))
+    assert dbs, f"no rocprofv3 database in {d}"
+    return dbs[0]
+
+
+def _counter_for(db, counter, pattern):
+    vals = [v for (k, c), v in _counter_means(db).items() if c == counter and pattern in k]
+    return statistics.mean(vals) if vals else None
+
+
+def traffic(directory):
+    """HBM bytes per launch of each workload's kernel: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch) each scaled by true_bytes / counter_bytes of
+    a plain 128 MiB copy kernel (the calibration run)."""
+    cal_f = _counter_for(_one_db(os.path.join(directory, "cal_FETCH_SIZE")), "FETCH_SIZE", "k_cast_dense")
+    cal_w = _counter_for(_one_db(os.path.join(directory, "cal_WRITE_SIZE")), "WRITE_SIZE", "k_cast_dense")
+    fetch_factor = COPY_CAL_BYTES / (cal_f * 1024)
+    write_factor = COPY_CAL_BYTES / (cal_w * 1024)
+    out = {"fetch_factor": round(fetch_factor, 4), "write_factor": round(write_factor, 4), "kernels": {}}
+    for name, pattern in KERNEL_OF.items():
+        fd, wd = os.path.join(directory, f"{name}_FETCH_SIZE"), os.path.join(directory, f"{name}_WRITE_SIZE")
+        if not (os.path.isdir(fd) and os.path.isdir(wd)):
+            continue
+        f = _counter_for(_one_db(fd), "FETCH_SIZE", pattern)
+        w = _counter_for(_one_db(wd), "WRITE_SIZE", pattern)
+        if f is None or w is None:
+            continue
+        rd, wr = f * 1024 * fetch_factor, w * 1024 * write_factor
+        out["kernels"][name] = {"kernel": pattern, "read_bytes": round(rd), "write_bytes": round(wr),
+                                "bytes": round(rd + wr)}
+    print(json.dumps(out, indent=1))
+
+
+# kernel symbol fragment of each workload's dominant kernel
+KERNEL_OF = {
+    "silu": "k_unary_dense",
+    "rms_norm": "k_rms_vec",
+    "layer_norm": "k_ln_vec",
+    "softmax": "k_softmax_vec",
+    "rope": "k_rope_half_vec",
+    "mm": "k_gemm_mfma",
+    "addmm": "k_gemm_mfma",
+    "bmm": "k_gemm_mfma",
+}
+
+
+def copy_calibration():
+    import ctypes
+
+    from ntops_amd import _lib
+
+    lib = _lib.load()
+    n = COPY_CAL_BYTES // 4
+    xs = [torch.randn(n, device="cuda") for _ in range(NSETS)]
+    ys = [torch.empty(n, device="cuda") for _ in range(NSETS)]
+    shape, st = _lib.i64_array((n,)), _lib.i64_array((1,))
+    torch.cuda.synchronize()
+    for i in range(10):
+        _lib.check(lib.ntops_cast(_lib.F32, _lib.F32, 1, shape, xs[i % NSETS].data_ptr(), st,
+                                  ys[i % NSETS].data_ptr(), st,
+                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "copy")
+    torch.cuda.synchronize()
+    print(f"copy calibration: 10 x {COPY_CAL_BYTES} B (ntops_cast f32 -> f32, k_cast_dense<float, float>)")
+
+
+def load_traffic(path):
+    try:
+        with open(path) as f:
+            return json.load(f).get("kernels", {})
+    except (OSError, ValueError):
+        return {}
 
 
 # ----------------------------------------------------------- workloads ----
@@ -247,8 +377,10 @@ def make_workloads():
 
     W.append(Workload("mm", "mm bf16 (8192 x 4096).(4096 x 14336), fp32 accumulate", "TFLOP/s", "mfma",
                       2 * M * N * K, 1, mm_build, mm_step, mm_cpu, "bf16"))
+    W[-1].bytes = (M * K + K * N + M * N) * 2
     W.append(Workload("addmm", "addmm bf16 bias (14336,) + (8192 x 4096).(4096 x 14336), beta = alpha = 1",
                       "TFLOP/s", "mfma", 2 * M * N * K, 1, mm_build, addmm_step, addmm_cpu, "bf16"))
+    W[-1].bytes = (M * K + K * N + M * N + N) * 2
 
     BB, BM, BK, BN = 32, 2048, 128, 2048
 
@@ -346,7 +478,7 @@ def time_cpu(w):
                       f"{cpu_model()}"}
 
 
-def result_for(w, ms):
+def result_for(w, ms, measured_traffic):
     sec = ms / 1e3
     if w.unit == "TFLOP/s":
         value = w.work / sec / 1e12
@@ -365,6 +497,12 @@ def result_for(w, ms):
         "roofline": {"bound": w.bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4), "traffic": None},
     }
+    t = measured_traffic.get(w.name)
+    if t:
+        # HBM bytes per launch measured by rocprofv3 (profiles/traffic.json)
+        out["roofline"]["traffic"] = t["bytes"]
+        out["roofline"]["algorithmic_bytes_per_launch"] = (
+            w.work // w.kernels_per_step if unit == "GB/s" else getattr(w, "bytes", None))
     if getattr(w, "flops", None):
         out["tflops"] = round(w.flops / sec / 1e12, 3)
     return out
@@ -372,6 +510,12 @@ def result_for(w, ms):
 
 def main():
     args = parse_args()
+    if args.rocprof_summary:
+        rocprof_summary(args.rocprof_summary)
+        return
+    if args.traffic:
+        traffic(args.traffic)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(every op runs on a single MI355X; see the sharding notes in DESIGN.md)", file=sys.stderr)
@@ -379,7 +523,11 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     torch.set_num_threads(cpu_threads())
+    measured_traffic = load_traffic(args.traffic_file)
     workloads = make_workloads()
     names = list(workloads) if args.ops == "all" else args.ops.split(",")
     headline = "rms_norm" if "rms_norm" in names else names[0]
@@ -389,7 +537,7 @@ def main():
     for n in names:
         w = workloads[n]
         ms = time_gpu(w, args.steps, args.warmup, args.eager)
-        r = result_for(w, ms)
+        r = result_for(w, ms, measured_traffic)
         if not args.no_cpu:
             r["cpu_baseline"] = time_cpu(w)
         results[n] = r

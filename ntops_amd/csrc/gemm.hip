@@ -4,25 +4,33 @@
 // rounded to the input dtype), kernels/bmm.py:26-39 (batch tile of 1),
 // kernels/addmm.py:64-67 (beta * input + alpha * mm).
 //
-// MFMA path (bf16 / fp16 with 16-byte aligned, unit-stride operands):
-//  * macro tile BM x BN x 64, WM x WN wavefronts, each wave owns a
-//    (BM/WM) x (BN/WN) sub-tile built from 32x32 v_mfma_f32_32x32x16_{bf16,f16}
+// MFMA path (bf16 / fp16 operands with one unit-stride axis each):
+//  * macro tile BM x BN x 64, WM x WN wavefronts; each wave owns a
+//    (BM/WM) x (BN/WN) sub-tile of 32x32 v_mfma_f32_32x32x16_{bf16,f16}
 //    tiles with fp32 accumulators;
-//  * both operands are staged in LDS as [row][k] (row = m for A, n for B),
-//    128 B per row, 16-byte chunks XOR-swizzled by ((row>>1)+(row>>4))&7 so
-//    fragment reads (ds_read_b128) are conflict-free;
-//  * a K-major operand is copied chunk-for-chunk; an M/N-major operand (e.g.
-//    B of a row-major K x N matrix) is loaded as 4(k) x 8(n) blocks and
-//    transposed in registers on its way into LDS;
-//  * two LDS stages: global loads of tile k+1 are in flight while tile k is
-//    multiplied; one barrier per K tile;
-//  * the MFMA is issued with B as its first operand, so each lane ends up
-//    holding 4 consecutive output columns of one row: the epilogue applies
-//    alpha / beta in fp32, rounds once and writes 8-byte stores;
-//  * tiles are assigned XCD-aware: consecutive workgroups land on different
-//    XCDs (round-robin dispatch), so the tile order is remapped to give each
-//    XCD a contiguous, M-grouped range of tiles sharing A and B panels in its
-//    own L2.
+//  * operands go global -> LDS directly (buffer_load_dwordx4 ... lds): no
+//    VGPR staging, no LDS write instructions.  A lane's LDS destination is
+//    fixed (M0 + 16 * lane), so the swizzle is applied on the global side:
+//    each lane fetches the chunk that belongs at its LDS slot;
+//  * K-major operand tile: [row][64 k], 128 B per row, 16-byte chunk c of
+//    row r stored at chunk slot c ^ (((r >> 1) + (r >> 4)) & 7), so the
+//    fragment reads (ds_read_b128) are bank-conflict free;
+//  * M/N-major operand tile: [64 k][R], R * 2 bytes per row, chunk c of row k
+//    at slot c ^ (4 * (k % 4)); fragments are read with ds_read_b64_tr_b16,
+//    which transposes 4(k) x 16 blocks inside each 16-lane group so every
+//    lane receives 4 consecutive k of one column (two reads per 32x32x16
+//    operand); the swizzle makes those reads conflict free;
+//  * two LDS stages: the loads of tile k+1 are in flight while tile k is
+//    multiplied; fragment reads of k-step s+1 are issued before the MFMAs of
+//    k-step s; one barrier per K tile;
+//  * B is the MFMA's first operand, so each lane ends up holding 4
+//    consecutive output columns of one row: the epilogue applies alpha / beta
+//    in fp32, rounds once and writes 8-byte stores;
+//  * tiles are assigned XCD-aware: workgroup ids are dispatched round-robin
+//    over the 8 XCDs, so ids are remapped to give each XCD a contiguous,
+//    M-grouped range of tiles that share A and B panels in its L2;
+//  * edges: buffer loads with a per-tile resource; out-of-range chunks get an
+//    offset past the resource's extent and read as zero.
 // Generic path (fp32, or any other strides): 64x64 LDS-tiled FMA kernel with
 // fp32 accumulation (IEEE; gfx950 has no reduced-precision fp32 MFMA input).
 #include "dispatch.h"
@@ -34,6 +42,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 
 template <typename T>
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -59,19 +70,62 @@ struct GemmArgs {
   int use_c;
 };
 
-constexpr int kBK = 64;
-constexpr int kRowBytes = kBK * 2;  // one LDS row of 64 16-bit k values
+constexpr uint32_t kOOB = 0x80000000u;  // past every resource extent (< 2 GiB)
 
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) + (row >> 4)) & 7; }
-__device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * kRowBytes + ((chunk ^ swz(row)) << 4);
+// Chunk slot of 16-byte chunk `c` of row `r` in a K-major tile whose rows
+// hold BK k values (BK / 8 chunks); conflict-free for the fragment reads
+// (16 lanes per pass, rows r .. r + 15).
+template <int BK>
+__device__ __forceinline__ int kslot(int r, int c) {
+  if constexpr (BK == 64)
+    return c ^ (((r >> 1) + (r >> 4)) & 7);
+  else
+    return c ^ ((r >> 2) & 3);
+}
+// Chunk slot of chunk `c` of k-row `k` in an M/N-major tile.
+__device__ __forceinline__ int mnslot(int k, int c) { return c ^ ((k & 3) << 2); }
+
+// s_waitcnt with only the vector-memory counter constrained (<= n).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+}
+
+// s_waitcnt lgkmcnt(0) (LDS reads returned), other counters unconstrained.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
+// Waits until at most `younger` tiles' worth of this wave's DMA loads
+// (loads_per_tile each) are still in flight.
+__device__ __forceinline__ void wait_tile(int younger, int loads_per_tile) {
+  const int n = younger * loads_per_tile;
+  if (n >= 12)
+    wait_vmcnt<12>();
+  else if (n >= 8)
+    wait_vmcnt<8>();
+  else if (n >= 6)
+    wait_vmcnt<6>();
+  else if (n >= 4)
+    wait_vmcnt<4>();
+  else if (n >= 2)
+    wait_vmcnt<2>();
+  else
+    wait_vmcnt<0>();
+}
+
+// Workgroup barrier without a memory fence (the kernel orders its LDS DMA
+// with explicit vmcnt waits); also a scheduling fence for the compiler.
+__device__ __forceinline__ void block_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // Maps a linear workgroup id to (batch, tile_m, tile_n).
 __device__ __forceinline__ void tile_of(int pid, int nblocks, int tm_count, int tn_count,
                                         int& bat, int& tm, int& tn) {
-  // Workgroups are dispatched round-robin over the 8 XCDs; make the ids an
-  // XCD sees consecutive in tile order.
   if ((nblocks & 7) == 0) pid = (pid & 7) * (nblocks >> 3) + (pid >> 3);
   const int per_batch = tm_count * tn_count;
   bat = pid / per_batch;
@@ -86,129 +140,175 @@ __device__ __forceinline__ void tile_of(int pid, int nblocks, int tm_count, int 
   tn = r / gm;
 }
 
-// ---- global -> register staging ------------------------------------------
-// K-major operand: R rows x 64 k, 16-byte chunks (8 per row).
-template <int R, int NT, bool EVEN>
-struct KMajorLoader {
-  static constexpr int kChunks = R * 8 / NT;
-  u32x4 v[kChunks];
-  __device__ __forceinline__ void load(const uint16_t* base, int64_t s_row, int row0, int rows,
-                                       int k0, int K, int t) {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = t + i * NT;
-      const int r = c >> 3, kc = c & 7;
-      const int gr = row0 + r, gk = k0 + kc * 8;
-      if (EVEN || (gr < rows && gk < K))
-        v[i] = *reinterpret_cast<const u32x4*>(base + gr * s_row + gk);
-      else
-        v[i] = u32x4{0, 0, 0, 0};
-    }
-  }
-  __device__ __forceinline__ void store(char* lds, int t) const {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = t + i * NT;
-      const int r = c >> 3, kc = c & 7;
-      *reinterpret_cast<u32x4*>(lds + lds_off(r, kc)) = v[i];
-    }
-  }
-};
+// 16-byte global -> LDS copy per lane: lane l's 16 bytes land at LDS byte
+// address lds_dst + 16 * l.  Written as inline assembly so the compiler does
+// not see an LDS store it would have to order against every later LDS read
+// (it would wait for all outstanding loads before each K tile's first
+// fragment read); the kernel orders it explicitly with vmcnt waits and the
+// per-tile barrier.
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_dst, uint32_t voffset) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "{m0}"(lds_dst)
+               : "memory");
+}
 
-// M/N-major operand: 64 k x R (contiguous) columns, loaded as 4(k) x 8(col)
-// blocks and transposed to [col][k] in registers.
-template <int R, int NT, bool EVEN>
-struct MNMajorLoader {
-  static constexpr int kItems = 16 * (R / 8) / NT;
-  u32x4 v[kItems][4];
-  __device__ __forceinline__ static void item(int it, int& ng, int& kg) {
-    ng = (it & 7) + 8 * ((it >> 3) >> 4);
-    kg = (it >> 3) & 15;
+// One operand's global -> LDS stream for a tile of R rows/columns x BK k.
+// The tile is R * BK * 2 bytes: R * BK / 512 one-KiB load instructions,
+// spread evenly over the NW waves of the block.
+template <int R, bool KMAJ, int NW, bool EVEN, int BK>
+struct TileLoader {
+  static constexpr int kInst = R * BK / 512 / NW;
+  static_assert(kInst * NW * 512 == R * BK, "tile must split evenly over the waves");
+  static constexpr int kCprK = BK / 8;  // chunks per row (K-major)
+  static constexpr int kCprMN = R / 8;  // chunks per k-row (M/N-major)
+  u32x4 rsrc;             // buffer resource (V#) of the operand tile
+  uint32_t voff[kInst];   // byte offset of this lane's chunk at k0 = 0
+  int lim_row[kInst];     // K-major: tile row; M/N-major: k-row
+  int lim_col[kInst];     // K-major: k of the chunk; M/N-major: column of the chunk
+  uint32_t k_stride_bytes;
+  int lds_base;           // first instruction's LDS offset inside the operand tile
+
+  // base: element pointer at the tile origin; ld: row stride (K-major) or
+  // k-row stride (M/N-major), in elements; extent_bytes: readable bytes.
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, int64_t extent_bytes,
+                                       int wave, int lane) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    rsrc.x = static_cast<uint32_t>(addr);
+    rsrc.y = static_cast<uint32_t>(addr >> 32) & 0xffffu;  // stride 0, no swizzle
+    rsrc.z = static_cast<uint32_t>(extent_bytes);           // num_records (bytes)
+    rsrc.w = 0x00020000u;                                   // 32-bit data format
+    rsrc.x = __builtin_amdgcn_readfirstlane(rsrc.x);
+    rsrc.y = __builtin_amdgcn_readfirstlane(rsrc.y);
+    rsrc.z = __builtin_amdgcn_readfirstlane(rsrc.z);
+    lds_base = wave * kInst * 1024;
+    if constexpr (KMAJ) {
+      k_stride_bytes = 2;
+      constexpr int rows_per_inst = 1024 / (BK * 2);
+#pragma unroll
+      for (int i = 0; i < kInst; ++i) {
+        const int q = wave * kInst + i;
+        const int row = q * rows_per_inst + lane / kCprK;
+        const int c = kslot<BK>(row, lane % kCprK);
+        voff[i] = static_cast<uint32_t>(row * ld * 2 + c * 16);
+        lim_row[i] = row;
+        lim_col[i] = c * 8;
+      }
+    } else {
+      k_stride_bytes = static_cast<uint32_t>(ld * 2);
+      constexpr int rows_per_inst = 64 / kCprMN;
+#pragma unroll
+      for (int i = 0; i < kInst; ++i) {
+        const int q = wave * kInst + i;
+        const int krow = q * rows_per_inst + lane / kCprMN;
+        const int c = mnslot(krow, lane % kCprMN);
+        voff[i] = static_cast<uint32_t>(krow * ld * 2 + c * 16);
+        lim_row[i] = krow;
+        lim_col[i] = c * 8;
+      }
+    }
   }
-  __device__ __forceinline__ void load(const uint16_t* base, int64_t s_k, int col0, int cols,
-                                       int k0, int K, int t) {
+
+  // Issues the loads of the K tile starting at k0 into `lds` (this operand's
+  // tile in one LDS stage).  `valid` is the number of valid tile rows
+  // (K-major) or tile columns (M/N-major); K bounds the k axis.
+  __device__ __forceinline__ void issue(char* lds, int k0, int valid, int K) const {
 #pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-      int ng, kg;
-      item(t + i * NT, ng, kg);
-      const int gc = col0 + ng * 8;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int gk = k0 + kg * 4 + r;
-        if (EVEN || (gc < cols && gk < K))
-          v[i][r] = *reinterpret_cast<const u32x4*>(base + gk * s_k + gc);
+    for (int i = 0; i < kInst; ++i) {
+      uint32_t off = voff[i] + static_cast<uint32_t>(k0) * k_stride_bytes;
+      if constexpr (!EVEN) {
+        bool ok;
+        if constexpr (KMAJ)
+          ok = lim_row[i] < valid && k0 + lim_col[i] < K;
         else
-          v[i][r] = u32x4{0, 0, 0, 0};
+          ok = k0 + lim_row[i] < K && lim_col[i] < valid;
+        off = ok ? off : kOOB;
       }
-    }
-  }
-  __device__ __forceinline__ void store(char* lds, int t) const {
-#pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-      int ng, kg;
-      item(t + i * NT, ng, kg);
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        // column 2d takes the low halves, column 2d+1 the high halves.
-        u32x2 lo, hi;
-        lo.x = (v[i][0][d] & 0xffffu) | (v[i][1][d] << 16);
-        lo.y = (v[i][2][d] & 0xffffu) | (v[i][3][d] << 16);
-        hi.x = (v[i][0][d] >> 16) | (v[i][1][d] & 0xffff0000u);
-        hi.y = (v[i][2][d] >> 16) | (v[i][3][d] & 0xffff0000u);
-        const int c0 = ng * 8 + 2 * d;
-        const int kb = kg * 8;  // byte offset of these 4 k values in the row
-        *reinterpret_cast<u32x2*>(lds + lds_off(c0, kb >> 4) + (kb & 8)) = lo;
-        *reinterpret_cast<u32x2*>(lds + lds_off(c0 + 1, kb >> 4) + (kb & 8)) = hi;
-      }
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(
+          static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds + lds_base + i * 1024))));
+      dma16(rsrc, dst, off);
     }
   }
 };
 
-template <int R, int NT, bool KMAJ, bool EVEN>
-using Loader = typename std::conditional<KMAJ, KMajorLoader<R, NT, EVEN>, MNMajorLoader<R, NT, EVEN>>::type;
+// Fragment of one 32-row (m or n) x 16 k operand slice for lane `lane`:
+// lane l holds row (l & 31), k = 8 * (l >> 5) + 0..7.
+template <int R, bool KMAJ, int BK>
+__device__ __forceinline__ u32x4 load_frag(const char* tile, int row0, int ks, int lane) {
+  if constexpr (KMAJ) {
+    const int r = row0 + (lane & 31);
+    const int c = ks * 2 + (lane >> 5);
+    return *reinterpret_cast<const u32x4*>(tile + r * (BK * 2) + kslot<BK>(r, c) * 16);
+  } else {
+    // ds_read_b64_tr_b16: within each 16-lane group, source lane i reads
+    // 4 elements of k-row kb + i/4 at columns nb + 4 (i % 4) .. +3; output
+    // lane j receives column nb + j at k-rows kb .. kb + 3.
+    const int i = lane & 15;
+    const int n = row0 + ((lane >> 4) & 1) * 16 + (i & 3) * 4;
+    const int c = n >> 3, half = (n >> 2) & 1;
+    s16x4 v[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = ks * 16 + (lane >> 5) * 8 + h * 4 + (i >> 2);
+      const char* p = tile + k * (R * 2) + mnslot(k, c) * 16 + half * 8;
+      v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p));
+    }
+    u32x4 r;
+    r.x = static_cast<uint16_t>(v[0][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][1])) << 16);
+    r.y = static_cast<uint16_t>(v[0][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][3])) << 16);
+    r.z = static_cast<uint16_t>(v[1][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][1])) << 16);
+    r.w = static_cast<uint16_t>(v[1][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][3])) << 16);
+    return r;
+  }
+}
 
 // ---- MFMA kernel -----------------------------------------------------------
-template <typename T, int BM, int BN, int WM, int WN, bool AK, bool BK_, bool EVEN>
+// STAGES LDS stages, prefetch distance STAGES - 1: the loads of tile
+// kt + STAGES - 1 are issued right after the barrier that opens tile kt, so
+// an operand fetch that misses L2 has STAGES - 1 tiles of MFMA work to land.
+template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN>
 __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
-  constexpr int NT = WM * WN * 64;
+  constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
   constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
-  constexpr int kStage = (BM + BN) * kRowBytes;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int kATile = BM * BK * 2, kBTile = BN * BK * 2;
+  constexpr int kStage = kATile + kBTile;
+  using LA = TileLoader<BM, AK, NW, EVEN, BK>;
+  using LB = TileLoader<BN, BKM, NW, EVEN, BK>;
+  constexpr int kLoadsPerTile = LA::kInst + LB::kInst;  // per wave
+  static_assert(STAGES >= 2 && STAGES <= 5, "stages");
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
 
-  const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
 
   const int tm_count = (g.M + BM - 1) / BM, tn_count = (g.N + BN - 1) / BN;
   int bat, tmi, tni;
   tile_of(blockIdx.x, gridDim.x, tm_count, tn_count, bat, tmi, tni);
   const int m0 = tmi * BM, n0 = tni * BN;
+  const int m_valid = min(g.M - m0, BM), n_valid = min(g.N - n0, BN);
 
   const uint16_t* A = static_cast<const uint16_t*>(g.A) + bat * g.sa_b;
   const uint16_t* B = static_cast<const uint16_t*>(g.B) + bat * g.sb_b;
-  // Pointers at the tile origin (row/col offsets folded in).
-  const uint16_t* Ab = AK ? A + static_cast<int64_t>(m0) * g.sa_m : A + m0;
-  const uint16_t* Bb = BK_ ? B + static_cast<int64_t>(n0) * g.sb_n : B + n0;
-  const int a_rows = g.M - m0, b_cols = g.N - n0;
 
-  Loader<BM, NT, AK, EVEN> la;
-  Loader<BN, NT, BK_, EVEN> lb;
+  LA la;
+  LB lb;
+  if constexpr (AK)
+    la.init(A + static_cast<int64_t>(m0) * g.sa_m, g.sa_m,
+            (static_cast<int64_t>(m_valid - 1) * g.sa_m + g.K) * 2, wave, lane);
+  else
+    la.init(A + m0, g.sa_k, (static_cast<int64_t>(g.K - 1) * g.sa_k + m_valid) * 2, wave, lane);
+  if constexpr (BKM)
+    lb.init(B + static_cast<int64_t>(n0) * g.sb_n, g.sb_n,
+            (static_cast<int64_t>(n_valid - 1) * g.sb_n + g.K) * 2, wave, lane);
+  else
+    lb.init(B + n0, g.sb_k, (static_cast<int64_t>(g.K - 1) * g.sb_k + n_valid) * 2, wave, lane);
 
-  auto load_tile = [&](int k0) {
-    if constexpr (AK)
-      la.load(Ab, g.sa_m, 0, a_rows, k0, g.K, t);
-    else
-      la.load(Ab, g.sa_k, 0, a_rows, k0, g.K, t);
-    if constexpr (BK_)
-      lb.load(Bb, g.sb_n, 0, b_cols, k0, g.K, t);
-    else
-      lb.load(Bb, g.sb_k, 0, b_cols, k0, g.K, t);
-  };
-  auto store_tile = [&](int stage) {
+  auto issue = [&](int stage, int k0) {
     char* base = smem + stage * kStage;
-    la.store(base, t);
-    lb.store(base + BM * kRowBytes, t);
+    la.issue(base, k0, m_valid, g.K);
+    lb.issue(base + kATile, k0, n_valid, g.K);
   };
 
   f32x16 acc[TM][TN];
@@ -219,35 +319,57 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int ktiles = (g.K + kBK - 1) / kBK;
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
+  const int ktiles = (g.K + BK - 1) / BK;
+  constexpr int KS = BK / 16;
+  // Ping-pong: the block's waves form two groups with one wave per SIMD in
+  // each (waves are placed round-robin over the 4 SIMDs).  In every phase one
+  // group reads a K tile's fragments from LDS and issues the DMA of a later
+  // tile while the other group runs the MFMAs of the tile it read in the
+  // previous phase; a block barrier separates phases.  Group 1 runs one phase
+  // behind group 0, so each SIMD always has one wave feeding the matrix core.
+  const int grp = wave / (NW / 2);
 
-  const int frow = lane & 31, fchunk = lane >> 5;
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int stage = kt & 1;
-    const bool more = kt + 1 < ktiles;
-    if (more) load_tile((kt + 1) * kBK);
-    const char* sa = smem + stage * kStage;
-    const char* sb = sa + BM * kRowBytes;
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      u32x4 af[TM], bf[TN];
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < ktiles) issue(s, s * BK);
+  wait_tile(min(STAGES - 2, ktiles - 1), kLoadsPerTile);
+  block_barrier();
+
+  // Group 1 starts one phase late: its first barrier pairs with the barrier
+  // group 0 reaches after reading tile 0.  Both groups then run the same
+  // loop (read tile k | barrier | MFMAs of tile k | barrier); group 0 ends
+  // with one extra barrier so every wave executes the same number.
+  if (grp == 1) block_barrier();
+  u32x4 af[KS][TM], bf[KS][TN];
+  for (int k = 0; k < ktiles; ++k) {
+    // memory phase: refill the stage of tile k - 1 with tile k + STAGES - 1,
+    // then read all of tile k's fragments.
+    if (k + STAGES - 1 < ktiles) issue((k + STAGES - 1) % STAGES, (k + STAGES - 1) * BK);
+    const char* sa = smem + (k % STAGES) * kStage;
+    const char* sb = sa + kATile;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const u32x4*>(sa + lds_off(wm * WTM + i * 32 + frow, ks * 2 + fchunk));
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const u32x4*>(sb + lds_off(wn * WTN + j * 32 + frow, ks * 2 + fchunk));
+      for (int i = 0; i < TM; ++i) af[ks][i] = load_frag<BM, AK, BK>(sa, wm * WTM + i * 32, ks, lane);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[j], af[i], acc[i][j]);
+      for (int j = 0; j < TN; ++j) bf[ks][j] = load_frag<BN, BKM, BK>(sb, wn * WTN + j * 32, ks, lane);
     }
-    if (more) store_tile(stage ^ 1);
-    __syncthreads();
+    // The fragments are in registers before the stage can be refilled, and
+    // this wave's share of tile k + 1 has landed before the barrier that
+    // opens the next memory phase of either group.
+    wait_lgkmcnt0();
+    if (k + 1 < ktiles) wait_tile(min(STAGES - 2, ktiles - 2 - k), kLoadsPerTile);
+    block_barrier();
+    // MFMA phase.
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[ks][j], af[ks][i], acc[i][j]);
+    block_barrier();
   }
+  if (grp == 0) block_barrier();
 
   // Epilogue.  With B as the first MFMA operand, lane l of tile (i, j) holds
   // output row  m = l & 31  and columns  n = 8q + 4(l >> 5) + 0..3  in
@@ -348,11 +470,11 @@ __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
 }
 
 // ---- host dispatch ---------------------------------------------------------
-template <typename T, int BM, int BN, int WM, int WN, bool AK, bool BKM, bool EVEN>
+template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN>
 int launch_mfma(const GemmArgs& g, hipStream_t st) {
   constexpr int NT = WM * WN * 64;
-  constexpr int kLds = 2 * (BM + BN) * kRowBytes;
-  auto kern = k_gemm_mfma<T, BM, BN, WM, WN, AK, BKM, EVEN>;
+  constexpr int kLds = STAGES * (BM + BN) * BK * 2;
+  auto kern = k_gemm_mfma<T, BM, BN, WM, WN, BK, STAGES, AK, BKM, EVEN>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -369,14 +491,15 @@ int launch_mfma(const GemmArgs& g, hipStream_t st) {
 template <typename T, bool AK, bool BKM>
 int pick_tile(const GemmArgs& g, hipStream_t st) {
   const int64_t big_tiles = static_cast<int64_t>((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
+  constexpr int kBK = 32, kStages = 4;
   if (big_tiles >= 240) {
     const bool even = g.M % 256 == 0 && g.N % 256 == 0 && g.K % kBK == 0;
-    if (even) return launch_mfma<T, 256, 256, 2, 4, AK, BKM, true>(g, st);
-    return launch_mfma<T, 256, 256, 2, 4, AK, BKM, false>(g, st);
+    if (even) return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, AK, BKM, true>(g, st);
+    return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, AK, BKM, false>(g, st);
   }
   const bool even = g.M % 128 == 0 && g.N % 128 == 0 && g.K % kBK == 0;
-  if (even) return launch_mfma<T, 128, 128, 2, 2, AK, BKM, true>(g, st);
-  return launch_mfma<T, 128, 128, 2, 2, AK, BKM, false>(g, st);
+  if (even) return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, AK, BKM, true>(g, st);
+  return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, AK, BKM, false>(g, st);
 }
 
 template <typename T>
@@ -391,14 +514,11 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     const bool d_ok = g.sd_n == 1 && g.sd_m % 4 == 0 && g.sd_b % 4 == 0 &&
                       (reinterpret_cast<uintptr_t>(g.D) & 7u) == 0 && g.N % 4 == 0;
     const bool batch_ok = (g.batch == 1) || (g.sa_b % 8 == 0 && g.sb_b % 8 == 0);
-    const bool fits = static_cast<int64_t>(g.M) * g.sd_m < (int64_t(1) << 31) &&
-                      static_cast<int64_t>(g.M) * (a_k ? g.sa_m : 1) < (int64_t(1) << 31) &&
-                      static_cast<int64_t>(g.K) * (a_k ? 1 : g.sa_k) < (int64_t(1) << 31) &&
-                      static_cast<int64_t>(g.N) * (b_k ? g.sb_n : 1) < (int64_t(1) << 31) &&
-                      static_cast<int64_t>(g.K) * (b_k ? 1 : g.sb_k) < (int64_t(1) << 31) &&
-                      (!g.use_c || (static_cast<int64_t>(g.M) * (g.sc_m < 0 ? -g.sc_m : g.sc_m) +
-                                        static_cast<int64_t>(g.N) * (g.sc_n < 0 ? -g.sc_n : g.sc_n) <
-                                    (int64_t(1) << 31)));
+    // Every operand byte offset inside a tile's buffer resource must stay
+    // below 2 GiB (out-of-range chunks use offset 2^31).
+    const int64_t lim = int64_t(1) << 31;
+    const bool fits = (a_k ? (256 * g.sa_m + g.K) : (static_cast<int64_t>(g.K) * g.sa_k + 256)) * 2 < lim &&
+                      (b_k ? (256 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 256)) * 2 < lim;
     if ((a_k || a_m) && (b_k || b_n) && d_ok && batch_ok && fits && al(g.A) && al(g.B)) {
       if (a_k && b_n) return pick_tile<T, true, false>(g, st);
       if (a_k && b_k) return pick_tile<T, true, true>(g, st);
