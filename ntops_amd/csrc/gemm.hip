@@ -5,27 +5,33 @@
 // kernels/addmm.py:64-67 (beta * input + alpha * mm).
 //
 // MFMA path (bf16 / fp16 operands with one unit-stride axis each):
-//  * macro tile BM x BN x 64, WM x WN wavefronts; each wave owns a
-//    (BM/WM) x (BN/WN) sub-tile of 32x32 v_mfma_f32_32x32x16_{bf16,f16}
-//    tiles with fp32 accumulators;
+//  * macro tile BM x BN x BK (256 x 256 x 32 for large problems, 128 x 128 x
+//    32 otherwise), WM x WN wavefronts; each wave owns a (BM/WM) x (BN/WN)
+//    sub-tile of 32x32 v_mfma_f32_32x32x16_{bf16,f16} tiles with fp32
+//    accumulators;
 //  * operands go global -> LDS directly (buffer_load_dwordx4 ... lds): no
 //    VGPR staging, no LDS write instructions.  A lane's LDS destination is
 //    fixed (M0 + 16 * lane), so the swizzle is applied on the global side:
 //    each lane fetches the chunk that belongs at its LDS slot;
-//  * K-major operand tile: [row][64 k], 128 B per row, 16-byte chunk c of
-//    row r stored at chunk slot c ^ (((r >> 1) + (r >> 4)) & 7), so the
-//    fragment reads (ds_read_b128) are bank-conflict free;
-//  * M/N-major operand tile: [64 k][R], R * 2 bytes per row, chunk c of row k
-//    at slot c ^ (4 * (k % 4)); fragments are read with ds_read_b64_tr_b16,
-//    which transposes 4(k) x 16 blocks inside each 16-lane group so every
-//    lane receives 4 consecutive k of one column (two reads per 32x32x16
-//    operand); the swizzle makes those reads conflict free;
-//  * two LDS stages: the loads of tile k+1 are in flight while tile k is
-//    multiplied; fragment reads of k-step s+1 are issued before the MFMAs of
-//    k-step s; one barrier per K tile;
-//  * B is the MFMA's first operand, so each lane ends up holding 4
-//    consecutive output columns of one row: the epilogue applies alpha / beta
-//    in fp32, rounds once and writes 8-byte stores;
+//  * K-major operand tile: [row][BK k], 16-byte chunks XOR-swizzled per row
+//    (kslot) so the fragment reads (ds_read_b128) are bank-conflict free;
+//  * M/N-major operand tile: [BK k][R], chunk c of row k at slot
+//    c ^ (4 * (k % 4)); fragments are read with ds_read_b64_tr_b16, which
+//    transposes 4(k) x 16 blocks inside each 16-lane group so every lane
+//    receives 4 consecutive k of one column (two reads per 32x32x16 operand);
+//    the swizzle makes those reads conflict free;
+//  * STAGES LDS stages with prefetch distance STAGES - 1, ordered by explicit
+//    vmcnt waits and raw s_barrier (the DMA is issued from inline assembly so
+//    the compiler does not serialise every LDS read behind it);
+//  * ping-pong schedule: the two waves that share a SIMD are in opposite
+//    phases -- one reads a K tile's fragments and issues DMA while the other
+//    runs the MFMAs of the tile it read before -- so the matrix core is fed
+//    across the per-tile barriers;
+//  * B is the MFMA's first operand, so each lane holds 4 consecutive output
+//    columns of one row; the epilogue applies alpha / beta in fp32, rounds
+//    once, stages the wave's tile in LDS and writes full 128-byte row
+//    segments with 16-byte stores (8-byte direct stores when the output is
+//    not 16-byte aligned);
 //  * tiles are assigned XCD-aware: workgroup ids are dispatched round-robin
 //    over the 8 XCDs, so ids are remapped to give each XCD a contiguous,
 //    M-grouped range of tiles that share A and B panels in its L2;
@@ -68,6 +74,7 @@ struct GemmArgs {
   int M, N, K, batch;
   float alpha, beta;
   int use_c;
+  int staged;  // out is 16-byte aligned with unit column stride and N % 8 == 0
 };
 
 constexpr uint32_t kOOB = 0x80000000u;  // past every resource extent (< 2 GiB)
@@ -373,9 +380,57 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
 
   // Epilogue.  With B as the first MFMA operand, lane l of tile (i, j) holds
   // output row  m = l & 31  and columns  n = 8q + 4(l >> 5) + 0..3  in
-  // acc[i][j][4q .. 4q+3].
+  // acc[i][j][4q .. 4q+3].  alpha / beta are applied in fp32 and each value
+  // is rounded once.
   T* D = static_cast<T*>(g.D) + bat * g.sd_b;
   const T* Cp = g.use_c ? static_cast<const T*>(g.C) + bat * g.sc_b : nullptr;
+  auto final_value = [&](int i, int j, int q, int e, int m, int n) {
+    float v = g.alpha * acc[i][j][4 * q + e];
+    if (Cp != nullptr) v += g.beta * static_cast<float>(Cp[m * g.sc_m + (n + e) * g.sc_n]);
+    return v;
+  };
+  if (g.staged) {
+    // Staged through LDS (free once the loop is done): each wave writes its
+    // rounded WTM x WTN tile into its own LDS region (rows of WTN * 2 bytes,
+    // 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7)), then streams it
+    // out row by row with 16-byte stores, 8 lanes per 128-byte row segment,
+    // so every L2 write request is a full line instead of 16 bytes.
+    static_assert(WTN * 2 == 128, "staged epilogue assumes 64-column wave tiles");
+    char* ep = smem + wave * (WTM * WTN * 2);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = i * 32 + (lane & 31);
+      const int m = m0 + wm * WTM + r;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = j * 32 + q * 8 + (lane >> 5) * 4;
+          const int n = n0 + wn * WTN + col;
+          T o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = EVEN || (m < g.M && n + e < g.N);
+            o[e] = static_cast<T>(ok ? final_value(i, j, q, e, m, n) : 0.f);
+          }
+          const int c = col >> 3, half = (col >> 2) & 1;
+          *reinterpret_cast<u32x2*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + half * 8) =
+              __builtin_bit_cast(u32x2, o);
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int r0 = 0; r0 < WTM; r0 += 8) {
+      const int r = r0 + (lane >> 3), c = lane & 7;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+      const int m = m0 + wm * WTM + r;
+      const int n = n0 + wn * WTN + c * 8;
+      if (EVEN || (m < g.M && n < g.N))
+        *reinterpret_cast<u32x4*>(D + static_cast<int64_t>(m) * g.sd_m + n) = v;
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int m = m0 + wm * WTM + i * 32 + (lane & 31);
@@ -384,29 +439,17 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wn * WTN + j * 32 + q * 8 + (lane >> 5) * 4;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = g.alpha * acc[i][j][4 * q + e];
         if (EVEN || (m < g.M && n + 3 < g.N)) {
-          if (Cp != nullptr) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              v[e] += g.beta * static_cast<float>(Cp[m * g.sc_m + (n + e) * g.sc_n]);
-          }
           T o[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = static_cast<T>(v[e]);
+          for (int e = 0; e < 4; ++e) o[e] = static_cast<T>(final_value(i, j, q, e, m, n));
           *reinterpret_cast<u32x2*>(D + static_cast<int64_t>(m) * g.sd_m + n) =
               __builtin_bit_cast(u32x2, o);
         } else if (m < g.M) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (n + e < g.N) {
-              float r = v[e];
-              if (Cp != nullptr) r += g.beta * static_cast<float>(Cp[m * g.sc_m + (n + e) * g.sc_n]);
-              D[static_cast<int64_t>(m) * g.sd_m + n + e] = static_cast<T>(r);
-            }
-          }
+          for (int e = 0; e < 4; ++e)
+            if (n + e < g.N)
+              D[static_cast<int64_t>(m) * g.sd_m + n + e] = static_cast<T>(final_value(i, j, q, e, m, n));
         }
       }
     }
@@ -492,12 +535,19 @@ template <typename T, bool AK, bool BKM>
 int pick_tile(const GemmArgs& g, hipStream_t st) {
   const int64_t big_tiles = static_cast<int64_t>((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
   constexpr int kBK = 32, kStages = 4;
-  if (big_tiles >= 240) {
+  if (big_tiles >= 240 && g.K > 256) {
     const bool even = g.M % 256 == 0 && g.N % 256 == 0 && g.K % kBK == 0;
     if (even) return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, AK, BKM, true>(g, st);
     return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, AK, BKM, false>(g, st);
   }
   const bool even = g.M % 128 == 0 && g.N % 128 == 0 && g.K % kBK == 0;
+  if (g.K <= 256) {
+    // Short K: a tile's life is operand latency + a few MFMAs + its
+    // epilogue; 2 stages (32 KiB of LDS) let 4-5 tiles share a CU and
+    // overlap those phases.
+    if (even) return launch_mfma<T, 128, 128, 2, 2, kBK, 2, AK, BKM, true>(g, st);
+    return launch_mfma<T, 128, 128, 2, 2, kBK, 2, AK, BKM, false>(g, st);
+  }
   if (even) return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, AK, BKM, true>(g, st);
   return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, AK, BKM, false>(g, st);
 }
@@ -569,6 +619,10 @@ extern "C" int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_
   g.alpha = static_cast<float>(alpha);
   g.beta = static_cast<float>(beta);
   g.use_c = (C != nullptr && beta != 0.0) ? 1 : 0;
+  g.staged = (out_strides[2] == 1 && out_strides[1] % 8 == 0 && (batch == 1 || out_strides[0] % 8 == 0) &&
+              N % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0)
+                 ? 1
+                 : 0;
   g.C = C;
   if (g.use_c) {
     if (c_strides == nullptr) return set_error(NTOPS_ERR_INVALID, "gemm: null C strides");
