@@ -239,6 +239,10 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
                    aligned16(y) && (w == nullptr || aligned16(w)) &&
                    (b == nullptr || aligned16(b)) && pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
+  // layer_norm carries two dependent reductions and twice the per-element
+  // VALU work of rms_norm; for rows of 257..512 packs (e.g. 4096 bf16) four
+  // packs per lane over two waves measured ~4% faster than two over four.
+  if (vec && cfg.chunks == 2 && cfg.wpr == 4) cfg = VecCfg{4, 2};
   if (vec) {
 #define NTOPS_LN_CASE(CH, WP)                                                                 \
   if (cfg.chunks == CH && cfg.wpr == WP) {                                                    \
@@ -249,6 +253,7 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
     return check_launch("layer_norm");                                                        \
   }
     NTOPS_ROW_CASES(NTOPS_LN_CASE)
+    NTOPS_LN_CASE(4, 2)
 #undef NTOPS_LN_CASE
   }
   hipLaunchKernelGGL((k_ln_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, b, y, ys, cols,

@@ -1,9 +1,9 @@
 // softmax over one axis, viewed as (outer, dim_size, inner).
 //
-// Math follows kernels/softmax.py:9-29 (max, sum of exp(x - max), then
-// exp(x - max) / sum) with torch's accumulation rule, which the build keeps:
-// max and sum in fp32 (fp64 for fp64 output) and a single rounding of
-// exp(x - max) * (1 / sum) to the output dtype.  The input is first rounded to
+// Math follows kernels/softmax.py:9-29 (an online max / sum of
+// exp(x - max), then exp(x - max) / sum) with torch's accumulation rule,
+// which the build keeps: max and sum in fp32 (fp64 for fp64 output) and a
+// single rounding of each output to the output dtype.  The input is first rounded to
 // the output dtype, as torch does for softmax(..., dtype=).  A row that is all
 // -inf yields NaN (exp(-inf - -inf) = NaN), like torch.
 //
@@ -27,13 +27,41 @@ __device__ __forceinline__ C cmax(C a, C b) {
   return (a > b || a != a) ? a : b;
 }
 
+// exp(d) for the register-resident path: fp32 uses the hardware base-2
+// exponential, exp(d) = 2^(d * log2 e) (v_exp_f32), keeping the kernel under
+// the HBM bound (an accurate expf costs ~3x the VALU work per element, which
+// at 4 bytes per bf16 element is the same order as the memory time).  The
+// argument is <= 0 here, so the product's rounding changes the result by
+// less than |d| * 2^-24 relative.  fp64 keeps the accurate exp.
+__device__ __forceinline__ float row_exp(float d) {
+  return __builtin_amdgcn_exp2f(d * 1.44269504088896340736f);
+}
+__device__ __forceinline__ double row_exp(double d) { return exp(d); }
+
+// Merges the (max, sum of exp(x - max)) summary of another part of the row
+// into (m, s).  Parts whose max is -inf (no finite element) contribute 0; a
+// NaN max propagates.
+template <typename C>
+__device__ __forceinline__ void merge_max_sum(C& m, C& s, C m2, C s2) {
+  const C ninf = -__builtin_huge_val();
+  const C mn = cmax(m, m2);
+  const C ta = m == ninf ? C(0) : s * row_exp(m - mn);
+  const C tb = m2 == ninf ? C(0) : s2 * row_exp(m2 - mn);
+  m = mn;
+  s = ta + tb;
+}
+
+// One pass over the register-resident row: each lane reduces its own
+// elements to (max, sum of exp(x - max)), the lanes' summaries are merged
+// (64-lane butterfly, then one LDS exchange across the row's waves), and
+// every output is exp(x - lane max) * (exp(lane max - row max) / row sum).
 template <typename T, typename C, int CHUNKS, int WPR>
 __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_softmax_vec(
     const T* __restrict__ x, int64_t xs, T* __restrict__ y, int64_t ys, int64_t rows, int cols) {
   constexpr int V = Pack16<T>::N;
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
-  __shared__ C red0[RPB * WPR];
-  __shared__ C red1[RPB * WPR];
+  __shared__ C red_m[RPB * WPR];
+  __shared__ C red_s[RPB * WPR];
   const RowPos p = row_pos<WPR>();
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + p.row_in_block;
   const bool row_ok = row < rows;
@@ -54,25 +82,39 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_softmax_vec(
       for (int i = 0; i < V; ++i) v[c][i] = ninf;
     }
   }
-  C m = ninf;
+  // lane summary
+  C ml = ninf;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
-    for (int i = 0; i < V; ++i) m = cmax(m, v[c][i]);
-  m = row_max<WPR>(m, red0, p);
-  C s = 0;
+    for (int i = 0; i < V; ++i) ml = cmax(ml, v[c][i]);
+  C sl = 0;
+  const bool lane_empty = ml == ninf;  // every element -inf (or padding)
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const bool ok = pack_of<WPR>(p, c) < npk;
+  for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-      v[c][i] = ex(v[c][i] - m);
-      if (ok) s += v[c][i];
+      v[c][i] = lane_empty ? C(0) : row_exp(v[c][i] - ml);
+      sl += v[c][i];  // padding is -inf, so it adds exp(-inf) = 0
     }
+  // row summary
+  C m = ml, s = sl;
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) merge_max_sum(m, s, __shfl_xor(m, k, 64), __shfl_xor(s, k, 64));
+  if constexpr (WPR > 1) {
+    if (p.lane == 0) {
+      red_m[p.row_in_block * WPR + p.wave_in_row] = m;
+      red_s[p.row_in_block * WPR + p.wave_in_row] = s;
+    }
+    __syncthreads();
+    m = red_m[p.row_in_block * WPR];
+    s = red_s[p.row_in_block * WPR];
+#pragma unroll
+    for (int w = 1; w < WPR; ++w)
+      merge_max_sum(m, s, red_m[p.row_in_block * WPR + w], red_s[p.row_in_block * WPR + w]);
   }
-  s = row_sum<WPR>(s, red1, p);
-  const C inv = C(1) / s;
   if (!row_ok) return;
+  const C f = (lane_empty ? C(0) : row_exp(ml - m)) / s;
   T* yr = y + row * ys;
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
@@ -80,7 +122,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_softmax_vec(
     if (pk < npk) {
       Pack16<T> o;
 #pragma unroll
-      for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(v[c][i] * inv);
+      for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(v[c][i] * f);
       store16_nt(yr + pk * V, o);
     }
   }
