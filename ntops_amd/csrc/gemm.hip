@@ -84,7 +84,9 @@ constexpr uint32_t kOOB = 0x80000000u;  // past every resource extent (< 2 GiB)
 // (16 lanes per pass, rows r .. r + 15).
 template <int BK>
 __device__ __forceinline__ int kslot(int r, int c) {
-  if constexpr (BK == 64)
+  if constexpr (BK == 128)
+    return c ^ (r & 15);
+  else if constexpr (BK == 64)
     return c ^ (((r >> 1) + (r >> 4)) & 7);
   else
     return c ^ ((r >> 2) & 3);
@@ -216,6 +218,14 @@ struct TileLoader {
     }
   }
 
+  // Moves the resource to another tile origin with the same leading
+  // dimension and extent (the per-lane offsets stay valid).
+  __device__ __forceinline__ void rebase(const uint16_t* base) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    rsrc.x = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
+    rsrc.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32) & 0xffffu);
+  }
+
   // Issues the loads of the K tile starting at k0 into `lds` (this operand's
   // tile in one LDS stage).  `valid` is the number of valid tile rows
   // (K-major) or tile columns (M/N-major); K bounds the k axis.
@@ -268,6 +278,107 @@ __device__ __forceinline__ u32x4 load_frag(const char* tile, int row0, int ks, i
     return r;
   }
 }
+
+// ---- epilogue --------------------------------------------------------------
+// With B as the first MFMA operand, lane l of 32x32 tile (i, j) holds output
+// row  m = l & 31  and columns  n = 8q + 4(l >> 5) + 0..3  in
+// acc[i][j][4q .. 4q+3].  alpha / beta are applied in fp32 and each value is
+// rounded once.  (mw, nw) is the wave tile's origin in the output; D and Cp
+// already point at the batch's matrices.  HAS_C is a template parameter so
+// the C test is not a branch per element.
+template <typename T, bool HAS_C, int TM, int TN>
+__device__ __forceinline__ float final_value(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
+                                             const T* Cp, int i, int j, int q, int e, int m,
+                                             int n) {
+  float v = g.alpha * acc[i][j][4 * q + e];
+  if constexpr (HAS_C) v += g.beta * static_cast<float>(Cp[m * g.sc_m + (n + e) * g.sc_n]);
+  return v;
+}
+
+// Staged store: the wave writes its rounded WTM x WTN tile into its own LDS
+// region `ep` (rows of WTN * 2 bytes, 16-byte chunk c of row r at slot
+// c ^ ((r >> 1) & 7)), then streams it out row by row with 16-byte stores,
+// 8 lanes per 128-byte row segment, so every L2 write request is a full line
+// instead of 16 bytes.  Issues exactly WTM / 8 store instructions when EVEN.
+template <typename T, bool HAS_C, int TM, int TN, int WTM, int WTN, bool EVEN, bool NT>
+__device__ __forceinline__ void store_tile_staged(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
+                                                  char* ep, T* D, const T* Cp, int mw, int nw,
+                                                  int lane) {
+  static_assert(WTN * 2 == 128, "staged epilogue assumes 64-column wave tiles");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int r = i * 32 + (lane & 31);
+    const int m = mw + r;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = j * 32 + q * 8 + (lane >> 5) * 4;
+        const int n = nw + col;
+        T o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool ok = EVEN || (m < g.M && n + e < g.N);
+          o[e] = static_cast<T>(ok ? final_value<T, HAS_C>(g, acc, Cp, i, j, q, e, m, n) : 0.f);
+        }
+        const int c = col >> 3, half = (col >> 2) & 1;
+        *reinterpret_cast<u32x2*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + half * 8) =
+            __builtin_bit_cast(u32x2, o);
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int r0 = 0; r0 < WTM; r0 += 8) {
+    const int r = r0 + (lane >> 3), c = lane & 7;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+    const int m = mw + r;
+    const int n = nw + c * 8;
+    if (EVEN || (m < g.M && n < g.N)) {
+      u32x4* dst = reinterpret_cast<u32x4*>(D + static_cast<int64_t>(m) * g.sd_m + n);
+      if constexpr (NT)
+        __builtin_nontemporal_store(v, dst);
+      else
+        *dst = v;
+    }
+  }
+}
+
+// Direct store: 8-byte stores of each lane's 4 consecutive columns (any
+// output row stride that keeps 8-byte alignment), element stores at the edge.
+template <typename T, bool HAS_C, int TM, int TN, bool EVEN>
+__device__ __forceinline__ void store_tile_direct(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
+                                                  T* D, const T* Cp, int mw, int nw, int lane) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = mw + i * 32 + (lane & 31);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = nw + j * 32 + q * 8 + (lane >> 5) * 4;
+        if (EVEN || (m < g.M && n + 3 < g.N)) {
+          T o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[e] = static_cast<T>(final_value<T, HAS_C>(g, acc, Cp, i, j, q, e, m, n));
+          *reinterpret_cast<u32x2*>(D + static_cast<int64_t>(m) * g.sd_m + n) =
+              __builtin_bit_cast(u32x2, o);
+        } else if (m < g.M) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < g.N)
+              D[static_cast<int64_t>(m) * g.sd_m + n + e] =
+                  static_cast<T>(final_value<T, HAS_C>(g, acc, Cp, i, j, q, e, m, n));
+        }
+      }
+    }
+  }
+}
+
+// Output stores marked non-temporal (streamed past L2) per kernel.
+constexpr bool kStreamOutMfma = false;
+constexpr bool kStreamOutPanel = true;
 
 // ---- MFMA kernel -----------------------------------------------------------
 // STAGES LDS stages, prefetch distance STAGES - 1: the loads of tile
@@ -378,81 +489,152 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
   }
   if (grp == 0) block_barrier();
 
-  // Epilogue.  With B as the first MFMA operand, lane l of tile (i, j) holds
-  // output row  m = l & 31  and columns  n = 8q + 4(l >> 5) + 0..3  in
-  // acc[i][j][4q .. 4q+3].  alpha / beta are applied in fp32 and each value
-  // is rounded once.
   T* D = static_cast<T*>(g.D) + bat * g.sd_b;
   const T* Cp = g.use_c ? static_cast<const T*>(g.C) + bat * g.sc_b : nullptr;
-  auto final_value = [&](int i, int j, int q, int e, int m, int n) {
-    float v = g.alpha * acc[i][j][4 * q + e];
-    if (Cp != nullptr) v += g.beta * static_cast<float>(Cp[m * g.sc_m + (n + e) * g.sc_n]);
-    return v;
-  };
+  const int mw = m0 + wm * WTM, nw = n0 + wn * WTN;
+  char* ep = smem + wave * (WTM * WTN * 2);
   if (g.staged) {
-    // Staged through LDS (free once the loop is done): each wave writes its
-    // rounded WTM x WTN tile into its own LDS region (rows of WTN * 2 bytes,
-    // 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7)), then streams it
-    // out row by row with 16-byte stores, 8 lanes per 128-byte row segment,
-    // so every L2 write request is a full line instead of 16 bytes.
-    static_assert(WTN * 2 == 128, "staged epilogue assumes 64-column wave tiles");
-    char* ep = smem + wave * (WTM * WTN * 2);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int r = i * 32 + (lane & 31);
-      const int m = m0 + wm * WTM + r;
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int col = j * 32 + q * 8 + (lane >> 5) * 4;
-          const int n = n0 + wn * WTN + col;
-          T o[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const bool ok = EVEN || (m < g.M && n + e < g.N);
-            o[e] = static_cast<T>(ok ? final_value(i, j, q, e, m, n) : 0.f);
-          }
-          const int c = col >> 3, half = (col >> 2) & 1;
-          *reinterpret_cast<u32x2*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + half * 8) =
-              __builtin_bit_cast(u32x2, o);
-        }
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int r0 = 0; r0 < WTM; r0 += 8) {
-      const int r = r0 + (lane >> 3), c = lane & 7;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
-      const int m = m0 + wm * WTM + r;
-      const int n = n0 + wn * WTN + c * 8;
-      if (EVEN || (m < g.M && n < g.N))
-        *reinterpret_cast<u32x4*>(D + static_cast<int64_t>(m) * g.sd_m + n) = v;
-    }
-    return;
+    if (Cp != nullptr)
+      store_tile_staged<T, true, TM, TN, WTM, WTN, EVEN, kStreamOutMfma>(g, acc, ep, D, Cp, mw, nw, lane);
+    else
+      store_tile_staged<T, false, TM, TN, WTM, WTN, EVEN, kStreamOutMfma>(g, acc, ep, D, Cp, mw, nw, lane);
+  } else {
+    if (Cp != nullptr)
+      store_tile_direct<T, true, TM, TN, EVEN>(g, acc, D, Cp, mw, nw, lane);
+    else
+      store_tile_direct<T, false, TM, TN, EVEN>(g, acc, D, Cp, mw, nw, lane);
   }
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = m0 + wm * WTM + i * 32 + (lane & 31);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * WTN + j * 32 + q * 8 + (lane >> 5) * 4;
-        if (EVEN || (m < g.M && n + 3 < g.N)) {
-          T o[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = static_cast<T>(final_value(i, j, q, e, m, n));
-          *reinterpret_cast<u32x2*>(D + static_cast<int64_t>(m) * g.sd_m + n) =
-              __builtin_bit_cast(u32x2, o);
-        } else if (m < g.M) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < g.N)
-              D[static_cast<int64_t>(m) * g.sd_m + n + e] = static_cast<T>(final_value(i, j, q, e, m, n));
-        }
-      }
+}
+
+// ---- short-K persistent kernel ---------------------------------------------
+// For K <= 128 (bmm with a head-sized K) a tile's whole K panel is one DMA
+// of 2 x 32 KiB, and the kernel is bound by writing the output, not by the
+// MFMAs.  One 4-wave block per CU walks its tiles with the two 64 KiB LDS
+// stages alternating: the operand panels of tile t + 1 are in flight while
+// tile t runs its MFMAs and stores, and stores are never waited for except
+// through the in-order vmcnt counter (which also retires the loads they
+// precede).  Requires M % 128 == 0, N % 128 == 0, K % 8 == 0 and the staged
+// (16-byte aligned, unit column stride) output; k >= K reads as zero.
+constexpr int kPanelK = 128;
+
+template <typename T, bool AK, bool BKM>
+__global__ __launch_bounds__(256) void k_gemm_panel(GemmArgs g) {
+  constexpr int BM = 128, BN = 128, WN = 2, NW = 4;
+  constexpr int WTM = 64, WTN = 64, TM = 2, TN = 2, KS = kPanelK / 16;
+  constexpr int kATile = BM * kPanelK * 2, kStage = (BM + BN) * kPanelK * 2;
+  using LA = TileLoader<BM, AK, NW, false, kPanelK>;
+  using LB = TileLoader<BN, BKM, NW, false, kPanelK>;
+  constexpr int kLoads = LA::kInst + LB::kInst;  // DMA instructions per wave per tile
+  constexpr int kStores = WTM / 8;                // store instructions per wave per tile
+  static_assert(kLoads + kStores < 64, "vmcnt range");
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int tm_count = g.M / BM, tn_count = g.N / BN;
+  const int total = tm_count * tn_count * g.batch;
+  const int G = gridDim.x;
+
+  const uint16_t* A0 = static_cast<const uint16_t*>(g.A);
+  const uint16_t* B0 = static_cast<const uint16_t*>(g.B);
+  // Every tile has the same leading dimensions and extents: set the per-lane
+  // offsets once, move only the scalar base address per tile.
+  LA la;
+  LB lb;
+  if constexpr (AK)
+    la.init(A0, g.sa_m, (static_cast<int64_t>(BM - 1) * g.sa_m + g.K) * 2, wave, lane);
+  else
+    la.init(A0, g.sa_k, (static_cast<int64_t>(g.K - 1) * g.sa_k + BM) * 2, wave, lane);
+  if constexpr (BKM)
+    lb.init(B0, g.sb_n, (static_cast<int64_t>(BN - 1) * g.sb_n + g.K) * 2, wave, lane);
+  else
+    lb.init(B0, g.sb_k, (static_cast<int64_t>(g.K - 1) * g.sb_k + BN) * 2, wave, lane);
+
+  struct Coord {
+    int bat, m0, n0;
+  };
+  auto coord = [&](int t) {
+    Coord c;
+    int tmi, tni;
+    tile_of(t, total, tm_count, tn_count, c.bat, tmi, tni);
+    c.m0 = tmi * BM;
+    c.n0 = tni * BN;
+    return c;
+  };
+  // Issues a tile's operand panels into `stage`; ordered by the caller's
+  // vmcnt waits.
+  auto issue = [&](const Coord& c, int stage) {
+    la.rebase(A0 + c.bat * g.sa_b + (AK ? static_cast<int64_t>(c.m0) * g.sa_m : c.m0));
+    lb.rebase(B0 + c.bat * g.sb_b + (BKM ? static_cast<int64_t>(c.n0) * g.sb_n : c.n0));
+    char* base = smem + stage * kStage;
+    la.issue(base, 0, BM, g.K);
+    lb.issue(base + kATile, 0, BN, g.K);
+  };
+
+  int t = blockIdx.x;
+  if (t >= total) return;
+  Coord cur_c = coord(t);
+  issue(cur_c, 0);
+  for (int it = 0; t < total; t += G, ++it) {
+    const int cur = it & 1;
+    const bool has_next = t + G < total;
+    const Coord next_c = has_next ? coord(t + G) : cur_c;
+    // Every wave has finished reading stage cur ^ 1 (fragments two tiles
+    // back, staged output of the previous tile) before it is refilled.
+    block_barrier();
+    if (has_next) issue(next_c, cur ^ 1);
+    // In flight, oldest first: this tile's loads, the previous tile's
+    // stores (none on the first tile), the next tile's loads (if any).
+    if (it == 0) {
+      if (has_next)
+        wait_vmcnt<kLoads>();
+      else
+        wait_vmcnt<0>();
+    } else {
+      if (has_next)
+        wait_vmcnt<kLoads + kStores>();
+      else
+        wait_vmcnt<kStores>();
     }
+    block_barrier();
+
+    const char* sa = smem + cur * kStage;
+    const char* sb = sa + kATile;
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = load_frag<BM, AK, kPanelK>(sa, wm * WTM + i * 32, ks, lane);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = load_frag<BN, BKM, kPanelK>(sb, wn * WTN + j * 32, ks, lane);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[j], af[i], acc[i][j]);
+    }
+    // All fragment reads of stage cur are done before any wave overwrites
+    // it with its staged output.
+    wait_lgkmcnt0();
+    block_barrier();
+
+    T* D = static_cast<T*>(g.D) + cur_c.bat * g.sd_b;
+    char* ep = smem + cur * kStage + wave * (WTM * WTN * 2);
+    const int mw = cur_c.m0 + wm * WTM, nw = cur_c.n0 + wn * WTN;
+    if (g.use_c)
+      store_tile_staged<T, true, TM, TN, WTM, WTN, true, kStreamOutPanel>(
+          g, acc, ep, D, static_cast<const T*>(g.C) + cur_c.bat * g.sc_b, mw, nw, lane);
+    else
+      store_tile_staged<T, false, TM, TN, WTM, WTN, true, kStreamOutPanel>(g, acc, ep, D, nullptr,
+                                                                          mw, nw, lane);
+    cur_c = next_c;
   }
 }
 
@@ -531,8 +713,45 @@ int launch_mfma(const GemmArgs& g, hipStream_t st) {
   return check_launch("gemm");
 }
 
+// Number of CUs of the current device (queried once per device).
+int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+template <typename T, bool AK, bool BKM>
+int launch_panel(const GemmArgs& g, hipStream_t st) {
+  constexpr int kLds = 2 * (128 + 128) * kPanelK * 2;
+  auto kern = k_gemm_panel<T, AK, BKM>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLds) != hipSuccess)
+      return set_error(NTOPS_ERR_HIP, "gemm: cannot reserve %d bytes of LDS", kLds);
+    attr_set = true;
+  }
+  const int64_t tiles = static_cast<int64_t>(g.M / 128) * (g.N / 128) * g.batch;
+  // One block per CU (the two stages fill most of its LDS); a multiple of 8
+  // keeps each block on one XCD for the whole walk.
+  int64_t grid = (cu_count() / 8) * 8;
+  if (grid <= 0) grid = 256;
+  if (grid > tiles) grid = tiles;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(256), kLds, st, g);
+  return check_launch("gemm");
+}
+
 template <typename T, bool AK, bool BKM>
 int pick_tile(const GemmArgs& g, hipStream_t st) {
+  if (g.K <= kPanelK && g.M % 128 == 0 && g.N % 128 == 0 && g.staged &&
+      static_cast<int64_t>(g.M / 128) * (g.N / 128) * g.batch <= 0x7fffffffLL)
+    return launch_panel<T, AK, BKM>(g, st);
   const int64_t big_tiles = static_cast<int64_t>((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
   constexpr int kBK = 32, kStages = 4;
   if (big_tiles >= 240 && g.K > 256) {
@@ -569,7 +788,9 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     const int64_t lim = int64_t(1) << 31;
     const bool fits = (a_k ? (256 * g.sa_m + g.K) : (static_cast<int64_t>(g.K) * g.sa_k + 256)) * 2 < lim &&
                       (b_k ? (256 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 256)) * 2 < lim;
-    if ((a_k || a_m) && (b_k || b_n) && d_ok && batch_ok && fits && al(g.A) && al(g.B)) {
+    // K == 0 goes to the generic kernel, which never touches A or B (they may
+    // be null, and an empty M/N-major operand has no valid buffer extent).
+    if (g.K > 0 && (a_k || a_m) && (b_k || b_n) && d_ok && batch_ok && fits && al(g.A) && al(g.B)) {
       if (a_k && b_n) return pick_tile<T, true, false>(g, st);
       if (a_k && b_k) return pick_tile<T, true, true>(g, st);
       if (a_m && b_n) return pick_tile<T, false, false>(g, st);

@@ -108,6 +108,56 @@ def test_addmm_bias_and_beta_zero(dtype):
     assert_close(got, from_np(O.gemm(to_np(x), to_np(y), dt, None, 2.0, 0.0), dt), *TOL_GEMM[dt], "beta=0")
 
 
+# Short-K shapes (K <= 128, M and N multiples of 128): the persistent panel
+# kernel.  Tile counts below, at and above one block per CU, divisible by 8
+# or not (XCD remap on / off), K below the 128-wide panel (zero-filled tail),
+# all four operand layouts, and an addmm bias read in its epilogue.
+SHORT_K = [
+    (1, 128, 128, 8),
+    (3, 384, 256, 64),
+    (7, 384, 640, 120),
+    (11, 640, 640, 128),
+    (5, 1024, 896, 96),
+    (2, 2048, 2048, 128),
+]
+
+
+@pytest.mark.parametrize("layout", ("NN", "NT", "TN", "TT"))
+@pytest.mark.parametrize("bsz, m, n, k", SHORT_K)
+def test_bmm_short_k(bsz, m, n, k, layout):
+    dtype = torch.bfloat16 if (bsz + k) % 2 else torch.float16
+    a = (0.1 * torch.randn(bsz, m, k)).to(dtype)
+    b = (0.1 * torch.randn(bsz, k, n)).to(dtype)
+    ag = a.cuda() if layout[0] == "N" else a.transpose(1, 2).contiguous().cuda().transpose(1, 2)
+    bg = b.cuda() if layout[1] == "N" else b.transpose(1, 2).contiguous().cuda().transpose(1, 2)
+    got = ntops_amd.torch.bmm(ag, bg)
+    dt = DT_NAME[dtype]
+    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), dt), dt), 1.6e-2, 1.6e-2, f"bmm short-k {layout}")
+
+
+def test_addmm_short_k_bias():
+    m, n, k = 512, 768, 64
+    bias = torch.randn(n).bfloat16()
+    x = (0.1 * torch.randn(m, k)).bfloat16()
+    y = (0.1 * torch.randn(k, n)).bfloat16()
+    got = ntops_amd.torch.addmm(bias.cuda(), x.cuda(), y.cuda(), beta=0.5, alpha=2.0)
+    exp = from_np(O.gemm(to_np(x), to_np(y), "bf16", to_np(bias), 2.0, 0.5), "bf16")
+    assert_close(got, exp, 1.6e-2, 1.6e-2, "addmm short-k bias")
+
+
+def test_gemm_k_zero_strided_views():
+    """K == 0 through operand views whose strides would select the MFMA
+    layouts: the result is beta * C (zeros for mm)."""
+    big_a = torch.randn(256, 64).bfloat16().cuda()
+    big_b = torch.randn(64, 512).bfloat16().cuda()
+    a, b = big_a[:, :0], big_b[:0, :]
+    got = ntops_amd.torch.mm(a, b)
+    assert got.shape == (256, 512) and (got == 0).all()
+    bias = torch.randn(512).bfloat16()
+    got = ntops_amd.torch.addmm(bias.cuda(), a, b, beta=2.0)
+    assert torch.equal(got.cpu(), (2.0 * bias.float()).bfloat16().expand(256, 512))
+
+
 @pytest.mark.parametrize("b", (None, 1, 2, 3))
 @pytest.mark.parametrize("m, n, k, dtype", rand_sizes())
 def test_matmul(b, m, n, k, dtype):
