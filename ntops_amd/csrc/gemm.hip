@@ -507,34 +507,42 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
 }
 
 // ---- short-K persistent kernel ---------------------------------------------
-// For K <= 128 (bmm with a head-sized K) a tile's whole K panel is one DMA
-// of 2 x 32 KiB, and the kernel is bound by writing the output, not by the
-// MFMAs.  One 4-wave block per CU walks its tiles with the two 64 KiB LDS
-// stages alternating: the operand panels of tile t + 1 are in flight while
-// tile t runs its MFMAs and stores, and stores are never waited for except
-// through the in-order vmcnt counter (which also retires the loads they
-// precede).  Requires M % 128 == 0, N % 128 == 0, K % 8 == 0 and the staged
-// (16-byte aligned, unit column stride) output; k >= K reads as zero.
+// For K <= 128 (bmm with a head-sized K) a 128 x 128 tile's whole K panel is
+// one DMA of 2 x 32 KiB, and the kernel is bound by writing the output, not
+// by the MFMAs.  One 8-wave block per CU walks its tiles as two groups of
+// four waves (one wave per SIMD in each group) that take alternate tiles
+// and run in opposite phases: in phase p, the group owning tile p runs its
+// MFMAs (fragments from its own 64 KiB operand stage) while the other group
+// issues the DMA of its next tile into its stage, rounds and stages its
+// previous tile through a shared 32 KiB area and stores it as full 128-byte
+// lines.  Each SIMD thus has one wave feeding the matrix core and one
+// driving LDS and the store path; one block barrier ends each phase.  LDS:
+// 2 x 64 KiB stages + 32 KiB staging = 160 KiB.  Requires M % 128 == 0,
+// N % 128 == 0, K % 8 == 0 and the staged (16-byte aligned, unit column
+// stride) output; k >= K reads as zero.
 constexpr int kPanelK = 128;
+constexpr int kPanelLds = 2 * (128 + 128) * kPanelK * 2 + 4 * 64 * 64 * 2;  // 160 KiB
 
 template <typename T, bool AK, bool BKM>
-__global__ __launch_bounds__(256) void k_gemm_panel(GemmArgs g) {
-  constexpr int BM = 128, BN = 128, WN = 2, NW = 4;
+__global__ __launch_bounds__(512) void k_gemm_panel(GemmArgs g) {
+  constexpr int BM = 128, BN = 128, NWG = 4;  // waves per group
   constexpr int WTM = 64, WTN = 64, TM = 2, TN = 2, KS = kPanelK / 16;
   constexpr int kATile = BM * kPanelK * 2, kStage = (BM + BN) * kPanelK * 2;
-  using LA = TileLoader<BM, AK, NW, false, kPanelK>;
-  using LB = TileLoader<BN, BKM, NW, false, kPanelK>;
-  constexpr int kLoads = LA::kInst + LB::kInst;  // DMA instructions per wave per tile
-  constexpr int kStores = WTM / 8;                // store instructions per wave per tile
-  static_assert(kLoads + kStores < 64, "vmcnt range");
+  using LA = TileLoader<BM, AK, NWG, false, kPanelK>;
+  using LB = TileLoader<BN, BKM, NWG, false, kPanelK>;
+  constexpr int kStores = WTM / 8;  // store instructions per wave per tile
   extern __shared__ __attribute__((aligned(1024))) char smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN, wn = wave % WN;
+  const int grp = wave >> 2, gw = wave & 3;
+  const int wm = gw >> 1, wn = gw & 1;
   const int tm_count = g.M / BM, tn_count = g.N / BN;
   const int total = tm_count * tn_count * g.batch;
   const int G = gridDim.x;
+  const int t0 = blockIdx.x;
+  if (t0 >= total) return;
+  const int n = (total - 1 - t0) / G + 1;  // tiles of this block: t0 + i * G
 
   const uint16_t* A0 = static_cast<const uint16_t*>(g.A);
   const uint16_t* B0 = static_cast<const uint16_t*>(g.B);
@@ -543,27 +551,26 @@ __global__ __launch_bounds__(256) void k_gemm_panel(GemmArgs g) {
   LA la;
   LB lb;
   if constexpr (AK)
-    la.init(A0, g.sa_m, (static_cast<int64_t>(BM - 1) * g.sa_m + g.K) * 2, wave, lane);
+    la.init(A0, g.sa_m, (static_cast<int64_t>(BM - 1) * g.sa_m + g.K) * 2, gw, lane);
   else
-    la.init(A0, g.sa_k, (static_cast<int64_t>(g.K - 1) * g.sa_k + BM) * 2, wave, lane);
+    la.init(A0, g.sa_k, (static_cast<int64_t>(g.K - 1) * g.sa_k + BM) * 2, gw, lane);
   if constexpr (BKM)
-    lb.init(B0, g.sb_n, (static_cast<int64_t>(BN - 1) * g.sb_n + g.K) * 2, wave, lane);
+    lb.init(B0, g.sb_n, (static_cast<int64_t>(BN - 1) * g.sb_n + g.K) * 2, gw, lane);
   else
-    lb.init(B0, g.sb_k, (static_cast<int64_t>(g.K - 1) * g.sb_k + BN) * 2, wave, lane);
+    lb.init(B0, g.sb_k, (static_cast<int64_t>(g.K - 1) * g.sb_k + BN) * 2, gw, lane);
 
   struct Coord {
     int bat, m0, n0;
   };
-  auto coord = [&](int t) {
+  auto coord = [&](int i) {
     Coord c;
     int tmi, tni;
-    tile_of(t, total, tm_count, tn_count, c.bat, tmi, tni);
+    tile_of(t0 + i * G, total, tm_count, tn_count, c.bat, tmi, tni);
     c.m0 = tmi * BM;
     c.n0 = tni * BN;
     return c;
   };
-  // Issues a tile's operand panels into `stage`; ordered by the caller's
-  // vmcnt waits.
+  // Tile i lives in stage i % 2 (its group's stage).
   auto issue = [&](const Coord& c, int stage) {
     la.rebase(A0 + c.bat * g.sa_b + (AK ? static_cast<int64_t>(c.m0) * g.sa_m : c.m0));
     lb.rebase(B0 + c.bat * g.sb_b + (BKM ? static_cast<int64_t>(c.n0) * g.sb_n : c.n0));
@@ -572,69 +579,70 @@ __global__ __launch_bounds__(256) void k_gemm_panel(GemmArgs g) {
     lb.issue(base + kATile, 0, BN, g.K);
   };
 
-  int t = blockIdx.x;
-  if (t >= total) return;
-  Coord cur_c = coord(t);
-  issue(cur_c, 0);
-  for (int it = 0; t < total; t += G, ++it) {
-    const int cur = it & 1;
-    const bool has_next = t + G < total;
-    const Coord next_c = has_next ? coord(t + G) : cur_c;
-    // Every wave has finished reading stage cur ^ 1 (fragments two tiles
-    // back, staged output of the previous tile) before it is refilled.
-    block_barrier();
-    if (has_next) issue(next_c, cur ^ 1);
-    // In flight, oldest first: this tile's loads, the previous tile's
-    // stores (none on the first tile), the next tile's loads (if any).
-    if (it == 0) {
-      if (has_next)
-        wait_vmcnt<kLoads>();
-      else
-        wait_vmcnt<0>();
+  // Prologue: group 0's first tile lands before phase 0.
+  if (grp == 0) {
+    issue(coord(0), 0);
+    wait_vmcnt<0>();
+  }
+  block_barrier();
+
+  f32x16 acc[TM][TN];
+  Coord done_c = {0, 0, 0};  // this group's tile whose MFMAs are done
+  for (int p = 0; p <= n; ++p) {
+    if ((p & 1) == grp) {
+      // MFMA phase of tile p.
+      if (p < n) {
+        const char* sa = smem + grp * kStage;
+        const char* sb = sa + kATile;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          u32x4 af[TM], bf[TN];
+#pragma unroll
+          for (int i = 0; i < TM; ++i) af[i] = load_frag<BM, AK, kPanelK>(sa, wm * WTM + i * 32, ks, lane);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) bf[j] = load_frag<BN, BKM, kPanelK>(sb, wn * WTN + j * 32, ks, lane);
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[j], af[i], acc[i][j]);
+        }
+        // The stage is refilled only after the barrier ending this phase.
+        wait_lgkmcnt0();
+        done_c = coord(p);
+      }
     } else {
-      if (has_next)
-        wait_vmcnt<kLoads + kStores>();
-      else
-        wait_vmcnt<kStores>();
+      // Epilogue phase of tile p - 1 (this group's previous tile), after
+      // issuing the DMA of this group's next tile p + 1 so those loads are
+      // queued ahead of the stores.
+      const bool load_next = p + 1 < n;
+      if (load_next) issue(coord(p + 1), grp);
+      if (p >= 1) {
+        T* D = static_cast<T*>(g.D) + done_c.bat * g.sd_b;
+        char* ep = smem + 2 * kStage + gw * (WTM * WTN * 2);
+        const int mw = done_c.m0 + wm * WTM, nw = done_c.n0 + wn * WTN;
+        if (g.use_c)
+          store_tile_staged<T, true, TM, TN, WTM, WTN, true, kStreamOutPanel>(
+              g, acc, ep, D, static_cast<const T*>(g.C) + done_c.bat * g.sc_b, mw, nw, lane);
+        else
+          store_tile_staged<T, false, TM, TN, WTM, WTN, true, kStreamOutPanel>(g, acc, ep, D, nullptr,
+                                                                              mw, nw, lane);
+      }
+      // The next tile's operands have landed (only the stores just issued
+      // may still be in flight) before the barrier that opens its MFMA phase.
+      if (load_next) {
+        if (p >= 1)
+          wait_vmcnt<kStores>();
+        else
+          wait_vmcnt<0>();
+      }
     }
     block_barrier();
-
-    const char* sa = smem + cur * kStage;
-    const char* sb = sa + kATile;
-    f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      u32x4 af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = load_frag<BM, AK, kPanelK>(sa, wm * WTM + i * 32, ks, lane);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = load_frag<BN, BKM, kPanelK>(sb, wn * WTN + j * 32, ks, lane);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[j], af[i], acc[i][j]);
-    }
-    // All fragment reads of stage cur are done before any wave overwrites
-    // it with its staged output.
-    wait_lgkmcnt0();
-    block_barrier();
-
-    T* D = static_cast<T*>(g.D) + cur_c.bat * g.sd_b;
-    char* ep = smem + cur * kStage + wave * (WTM * WTN * 2);
-    const int mw = cur_c.m0 + wm * WTM, nw = cur_c.n0 + wn * WTN;
-    if (g.use_c)
-      store_tile_staged<T, true, TM, TN, WTM, WTN, true, kStreamOutPanel>(
-          g, acc, ep, D, static_cast<const T*>(g.C) + cur_c.bat * g.sc_b, mw, nw, lane);
-    else
-      store_tile_staged<T, false, TM, TN, WTM, WTN, true, kStreamOutPanel>(g, acc, ep, D, nullptr,
-                                                                          mw, nw, lane);
-    cur_c = next_c;
   }
 }
 
@@ -728,7 +736,7 @@ int cu_count() {
 
 template <typename T, bool AK, bool BKM>
 int launch_panel(const GemmArgs& g, hipStream_t st) {
-  constexpr int kLds = 2 * (128 + 128) * kPanelK * 2;
+  constexpr int kLds = kPanelLds;
   auto kern = k_gemm_panel<T, AK, BKM>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -738,12 +746,12 @@ int launch_panel(const GemmArgs& g, hipStream_t st) {
     attr_set = true;
   }
   const int64_t tiles = static_cast<int64_t>(g.M / 128) * (g.N / 128) * g.batch;
-  // One block per CU (the two stages fill most of its LDS); a multiple of 8
+  // One 8-wave block per CU (it takes all of the CU's LDS); a multiple of 8
   // keeps each block on one XCD for the whole walk.
   int64_t grid = (cu_count() / 8) * 8;
   if (grid <= 0) grid = 256;
   if (grid > tiles) grid = tiles;
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(256), kLds, st, g);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(512), kLds, st, g);
   return check_launch("gemm");
 }
 
