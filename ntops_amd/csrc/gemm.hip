@@ -297,13 +297,14 @@ __device__ __forceinline__ float final_value(const GemmArgs& g, const f32x16 (&a
 
 // Staged store: the wave writes its rounded WTM x WTN tile into its own LDS
 // region `ep` (rows of WTN * 2 bytes, 16-byte chunk c of row r at slot
-// c ^ ((r >> 1) & 7)), then streams it out row by row with 16-byte stores,
-// 8 lanes per 128-byte row segment, so every L2 write request is a full line
-// instead of 16 bytes.  Issues exactly WTM / 8 store instructions when EVEN.
-template <typename T, bool HAS_C, int TM, int TN, int WTM, int WTN, bool EVEN, bool NT>
-__device__ __forceinline__ void store_tile_staged(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
-                                                  char* ep, T* D, const T* Cp, int mw, int nw,
-                                                  int lane) {
+// c ^ ((r >> 1) & 7)), reads it back row by row (stage_tile), then streams
+// it out with 16-byte stores, 8 lanes per 128-byte row segment, so every L2
+// write request is a full line instead of 16 bytes (store_rows: exactly
+// WTM / 8 store instructions when EVEN).
+template <typename T, bool HAS_C, int TM, int TN, int WTM, int WTN, bool EVEN>
+__device__ __forceinline__ void stage_tile(const GemmArgs& g, const f32x16 (&acc)[TM][TN], char* ep,
+                                           const T* Cp, int mw, int nw, int lane,
+                                           u32x4 (&rows)[WTM / 8]) {
   static_assert(WTN * 2 == 128, "staged epilogue assumes 64-column wave tiles");
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -331,17 +332,35 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& g, const f32x1
 #pragma unroll
   for (int r0 = 0; r0 < WTM; r0 += 8) {
     const int r = r0 + (lane >> 3), c = lane & 7;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+    rows[r0 / 8] = *reinterpret_cast<const u32x4*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+  }
+}
+
+template <typename T, int WTM, bool EVEN, bool NT>
+__device__ __forceinline__ void store_rows(const GemmArgs& g, const u32x4 (&rows)[WTM / 8], T* D,
+                                           int mw, int nw, int lane) {
+#pragma unroll
+  for (int r0 = 0; r0 < WTM; r0 += 8) {
+    const int r = r0 + (lane >> 3), c = lane & 7;
     const int m = mw + r;
     const int n = nw + c * 8;
     if (EVEN || (m < g.M && n < g.N)) {
       u32x4* dst = reinterpret_cast<u32x4*>(D + static_cast<int64_t>(m) * g.sd_m + n);
       if constexpr (NT)
-        __builtin_nontemporal_store(v, dst);
+        __builtin_nontemporal_store(rows[r0 / 8], dst);
       else
-        *dst = v;
+        *dst = rows[r0 / 8];
     }
   }
+}
+
+template <typename T, bool HAS_C, int TM, int TN, int WTM, int WTN, bool EVEN, bool NT>
+__device__ __forceinline__ void store_tile_staged(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
+                                                  char* ep, T* D, const T* Cp, int mw, int nw,
+                                                  int lane) {
+  u32x4 rows[WTM / 8];
+  stage_tile<T, HAS_C, TM, TN, WTM, WTN, EVEN>(g, acc, ep, Cp, mw, nw, lane, rows);
+  store_rows<T, WTM, EVEN, NT>(g, rows, D, mw, nw, lane);
 }
 
 // Direct store: 8-byte stores of each lane's 4 consecutive columns (any
@@ -508,29 +527,39 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
 
 // ---- short-K persistent kernel ---------------------------------------------
 // For K <= 128 (bmm with a head-sized K) a 128 x 128 tile's whole K panel is
-// one DMA of 2 x 32 KiB, and the kernel is bound by writing the output, not
-// by the MFMAs.  One 8-wave block per CU walks its tiles as two groups of
-// four waves (one wave per SIMD in each group) that take alternate tiles
-// and run in opposite phases: in phase p, the group owning tile p runs its
-// MFMAs (fragments from its own 64 KiB operand stage) while the other group
-// issues the DMA of its next tile into its stage, rounds and stages its
-// previous tile through a shared 32 KiB area and stores it as full 128-byte
-// lines.  Each SIMD thus has one wave feeding the matrix core and one
-// driving LDS and the store path; one block barrier ends each phase.  LDS:
-// 2 x 64 KiB stages + 32 KiB staging = 160 KiB.  Requires M % 128 == 0,
-// N % 128 == 0, K % 8 == 0 and the staged (16-byte aligned, unit column
-// stride) output; k >= K reads as zero.
+// one DMA per operand (32 KiB each), and the kernel is bound by writing the
+// output, not by the MFMAs.
+//
+// Work is walked in units of `seg` consecutive tiles along one tile row
+// (same batch and 128-row block of A): the unit's A panel is loaded once
+// into one of two A buffers (alternating per unit) and only the B panel is
+// loaded per tile, which halves the operand traffic through the CU's memory
+// queue, where loads otherwise wait behind the output stores.
+//
+// One 8-wave block per CU runs two groups of four waves (one wave per SIMD
+// in each group) that take alternate tiles in opposite phases: in phase p
+// the group owning tile p runs its MFMAs while the other group issues the
+// DMA of its next tile, rounds and stages its previous tile through a
+// shared 32 KiB area and stores it as full 128-byte lines; one block barrier
+// ends each phase.  Each SIMD thus has one wave feeding the matrix core and
+// one driving LDS and the store path.  LDS: 2 x 32 KiB A + 2 x 32 KiB B
+// (one per group) + 32 KiB staging = 160 KiB.
+//
+// Requires M % 128 == 0, N % 128 == 0, K % 8 == 0, seg | N / 128 and the
+// staged (16-byte aligned, unit column stride) output; k >= K reads as zero.
 constexpr int kPanelK = 128;
-constexpr int kPanelLds = 2 * (128 + 128) * kPanelK * 2 + 4 * 64 * 64 * 2;  // 160 KiB
+constexpr int kPanelTile = 128 * kPanelK * 2;                     // one operand panel
+constexpr int kPanelLds = 4 * kPanelTile + 4 * 64 * 64 * 2;       // 160 KiB
 
 template <typename T, bool AK, bool BKM>
-__global__ __launch_bounds__(512) void k_gemm_panel(GemmArgs g) {
+__global__ __launch_bounds__(512) void k_gemm_panel(GemmArgs g, int seg) {
   constexpr int BM = 128, BN = 128, NWG = 4;  // waves per group
   constexpr int WTM = 64, WTN = 64, TM = 2, TN = 2, KS = kPanelK / 16;
-  constexpr int kATile = BM * kPanelK * 2, kStage = (BM + BN) * kPanelK * 2;
   using LA = TileLoader<BM, AK, NWG, false, kPanelK>;
   using LB = TileLoader<BN, BKM, NWG, false, kPanelK>;
   constexpr int kStores = WTM / 8;  // store instructions per wave per tile
+  // LDS map: A buffers 0/1, B stages 0/1 (group), staging.
+  constexpr int kOffA = 0, kOffB = 2 * kPanelTile, kOffStage = 4 * kPanelTile;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
 
   const int lane = threadIdx.x & 63;
@@ -538,16 +567,17 @@ __global__ __launch_bounds__(512) void k_gemm_panel(GemmArgs g) {
   const int grp = wave >> 2, gw = wave & 3;
   const int wm = gw >> 1, wn = gw & 1;
   const int tm_count = g.M / BM, tn_count = g.N / BN;
-  const int total = tm_count * tn_count * g.batch;
+  const int ups = tn_count / seg;                    // units per tile row
+  const int units = g.batch * tm_count * ups;
   const int G = gridDim.x;
-  const int t0 = blockIdx.x;
-  if (t0 >= total) return;
-  const int n = (total - 1 - t0) / G + 1;  // tiles of this block: t0 + i * G
+  const int u0 = blockIdx.x;
+  if (u0 >= units) return;
+  const int n = ((units - 1 - u0) / G + 1) * seg;   // tiles of this block
 
   const uint16_t* A0 = static_cast<const uint16_t*>(g.A);
   const uint16_t* B0 = static_cast<const uint16_t*>(g.B);
-  // Every tile has the same leading dimensions and extents: set the per-lane
-  // offsets once, move only the scalar base address per tile.
+  // Every panel has the same leading dimension and extent: set the per-lane
+  // offsets once, move only the scalar base address per panel.
   LA la;
   LB lb;
   if constexpr (AK)
@@ -561,22 +591,32 @@ __global__ __launch_bounds__(512) void k_gemm_panel(GemmArgs g) {
 
   struct Coord {
     int bat, m0, n0;
+    int abuf;    // A buffer of the tile's unit
+    bool first;  // first tile of its unit: loads the unit's A panel
   };
+  // Tile i of this block: unit k = i / seg (global unit u0 + k * G, remapped
+  // so each XCD walks a contiguous range of units), tile j = i % seg of it.
   auto coord = [&](int i) {
     Coord c;
-    int tmi, tni;
-    tile_of(t0 + i * G, total, tm_count, tn_count, c.bat, tmi, tni);
-    c.m0 = tmi * BM;
-    c.n0 = tni * BN;
+    const int k = i / seg, j = i - k * seg;
+    int u = u0 + k * G;
+    if ((units & 7) == 0 && (G & 7) == 0) u = (u & 7) * (units >> 3) + (u >> 3);
+    const int row = u / ups, s = u - row * ups;
+    c.bat = row / tm_count;
+    c.m0 = (row - c.bat * tm_count) * BM;
+    c.n0 = (s * seg + j) * BN;
+    c.abuf = k & 1;
+    c.first = j == 0;
     return c;
   };
-  // Tile i lives in stage i % 2 (its group's stage).
+  // Issues tile c's B panel into `stage` (and its unit's A panel first).
   auto issue = [&](const Coord& c, int stage) {
-    la.rebase(A0 + c.bat * g.sa_b + (AK ? static_cast<int64_t>(c.m0) * g.sa_m : c.m0));
+    if (c.first) {
+      la.rebase(A0 + c.bat * g.sa_b + (AK ? static_cast<int64_t>(c.m0) * g.sa_m : c.m0));
+      la.issue(smem + kOffA + c.abuf * kPanelTile, 0, BM, g.K);
+    }
     lb.rebase(B0 + c.bat * g.sb_b + (BKM ? static_cast<int64_t>(c.n0) * g.sb_n : c.n0));
-    char* base = smem + stage * kStage;
-    la.issue(base, 0, BM, g.K);
-    lb.issue(base + kATile, 0, BN, g.K);
+    lb.issue(smem + kOffB + stage * kPanelTile, 0, BN, g.K);
   };
 
   // Prologue: group 0's first tile lands before phase 0.
@@ -587,13 +627,14 @@ __global__ __launch_bounds__(512) void k_gemm_panel(GemmArgs g) {
   block_barrier();
 
   f32x16 acc[TM][TN];
-  Coord done_c = {0, 0, 0};  // this group's tile whose MFMAs are done
+  Coord done_c = {0, 0, 0, 0, false};  // this group's tile whose MFMAs are done
   for (int p = 0; p <= n; ++p) {
     if ((p & 1) == grp) {
-      // MFMA phase of tile p.
+      // MFMA phase of tile p (this group's; B in stage grp).
       if (p < n) {
-        const char* sa = smem + grp * kStage;
-        const char* sb = sa + kATile;
+        done_c = coord(p);
+        const char* sa = smem + kOffA + done_c.abuf * kPanelTile;
+        const char* sb = smem + kOffB + grp * kPanelTile;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -612,19 +653,20 @@ __global__ __launch_bounds__(512) void k_gemm_panel(GemmArgs g) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[j], af[i], acc[i][j]);
         }
-        // The stage is refilled only after the barrier ending this phase.
+        // Buffers are refilled only after the barrier ending this phase.
         wait_lgkmcnt0();
-        done_c = coord(p);
       }
     } else {
       // Epilogue phase of tile p - 1 (this group's previous tile), after
       // issuing the DMA of this group's next tile p + 1 so those loads are
-      // queued ahead of the stores.
+      // queued ahead of the stores.  B stage grp was last read by tile
+      // p - 1 (previous phase); an A buffer is refilled two units after its
+      // last use.
       const bool load_next = p + 1 < n;
       if (load_next) issue(coord(p + 1), grp);
       if (p >= 1) {
         T* D = static_cast<T*>(g.D) + done_c.bat * g.sd_b;
-        char* ep = smem + 2 * kStage + gw * (WTM * WTN * 2);
+        char* ep = smem + kOffStage + gw * (WTM * WTN * 2);
         const int mw = done_c.m0 + wm * WTM, nw = done_c.n0 + wn * WTN;
         if (g.use_c)
           store_tile_staged<T, true, TM, TN, WTM, WTN, true, kStreamOutPanel>(
@@ -745,13 +787,25 @@ int launch_panel(const GemmArgs& g, hipStream_t st) {
       return set_error(NTOPS_ERR_HIP, "gemm: cannot reserve %d bytes of LDS", kLds);
     attr_set = true;
   }
-  const int64_t tiles = static_cast<int64_t>(g.M / 128) * (g.N / 128) * g.batch;
+  // Units of `seg` tiles along a tile row: the longest divisor of the row's
+  // tile count that still leaves a unit for every CU.
+  const int cus = cu_count() > 0 ? cu_count() : 256;
+  const int tn = g.N / 128;
+  const int64_t rows = static_cast<int64_t>(g.M / 128) * g.batch;
+  int seg = 1;
+  for (int d = tn; d >= 1; --d) {
+    if (tn % d == 0 && rows * (tn / d) >= cus) {
+      seg = d;
+      break;
+    }
+  }
+  const int64_t units = rows * (tn / seg);
   // One 8-wave block per CU (it takes all of the CU's LDS); a multiple of 8
   // keeps each block on one XCD for the whole walk.
-  int64_t grid = (cu_count() / 8) * 8;
+  int64_t grid = (cus / 8) * 8;
   if (grid <= 0) grid = 256;
-  if (grid > tiles) grid = tiles;
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(512), kLds, st, g);
+  if (grid > units) grid = units;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(512), kLds, st, g, seg);
   return check_launch("gemm");
 }
 
