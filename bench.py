@@ -147,7 +147,7 @@ KERNEL_OF = {
     "rope": "k_rope_half_vec",
     "mm": "k_gemm_mfma",
     "addmm": "k_gemm_mfma",
-    "bmm": "k_gemm_mfma",
+    "bmm": "k_gemm_panel",
 }
 
 
