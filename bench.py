@@ -141,6 +141,9 @@ def traffic(directory):
 # kernel symbol fragment of each workload's dominant kernel
 KERNEL_OF = {
     "silu": "k_unary_dense",
+    "div": "k_binary_dense",
+    "eq": "k_binary_dense",
+    "clamp": "k_clamp_dense",
     "rms_norm": "k_rms_vec",
     "layer_norm": "k_ln_vec",
     "softmax": "k_softmax_vec",
@@ -236,6 +239,50 @@ def make_workloads():
 
     W.append(Workload("silu", "silu fp32 (8192, 4096)", "GB/s", "hbm", 2 * 8192 * 4096 * 4, 1,
                       silu_build, silu_step, silu_cpu, "f32"))
+
+    # the rest of the elementwise family: one workload per kernel shape --
+    # two tensors in (div floor), bool out (eq), four operands (clamp)
+    EN = (8192, 4096)
+    en_shape, en_strides = _lib.i64_array(EN), _lib.i64_array((EN[1], 1))
+
+    def ew_build(i, n_in):
+        g = _gen(50 + i)
+        ts = [torch.randn(*EN, device="cuda", generator=g) for _ in range(n_in)]
+        return {"in": ts, "y": torch.empty(*EN, device="cuda"), "yb": torch.empty(*EN, dtype=torch.bool, device="cuda")}
+
+    def div_step(s):
+        a, b = s["in"]
+        check(lib.ntops_binary(_lib.BINARY_DIV_FLOOR, _lib.F32, 2, en_shape, a.data_ptr(), en_strides, b.data_ptr(),
+                               en_strides, 0.0, 0, 1.0, 1, s["y"].data_ptr(), en_strides, stream()), "div")
+
+    def eq_step(s):
+        a, b = s["in"]
+        check(lib.ntops_compare(_lib.CMP_EQ, _lib.F32, 2, en_shape, a.data_ptr(), en_strides, b.data_ptr(),
+                                en_strides, 0.0, 0, s["yb"].data_ptr(), en_strides, stream()), "eq")
+
+    def clamp_step(s):
+        x, lo, hi = s["in"]
+        check(lib.ntops_clamp(_lib.F32, 2, en_shape, x.data_ptr(), en_strides, lo.data_ptr(), en_strides, 0.0, 0, 1,
+                              hi.data_ptr(), en_strides, 0.0, 0, 1, s["y"].data_ptr(), en_strides, stream()), "clamp")
+
+    def ew_cpu(fn, n_in, bytes_per_el, desc):
+        def make():
+            g = _cpu_gen()
+            ts = [torch.randn(2048, 4096, generator=g) for _ in range(n_in)]
+            return (lambda: fn(*ts)), 2048 * 4096 * bytes_per_el, desc
+        return make
+
+    W.append(Workload("div", "div fp32 (8192, 4096) / (8192, 4096), rounding_mode='floor'", "GB/s", "hbm",
+                      12 * EN[0] * EN[1], 1, lambda i: ew_build(i, 2), div_step,
+                      ew_cpu(lambda a, b: torch.div(a, b, rounding_mode="floor"), 2, 12,
+                             "torch.div(rounding_mode='floor') fp32 (2048, 4096) = 1/4 of the workload"), "f32"))
+    W.append(Workload("eq", "eq fp32 (8192, 4096) == (8192, 4096) -> bool", "GB/s", "hbm",
+                      9 * EN[0] * EN[1], 1, lambda i: ew_build(i, 2), eq_step,
+                      ew_cpu(torch.eq, 2, 9, "torch.eq fp32 (2048, 4096) = 1/4 of the workload"), "f32"))
+    W.append(Workload("clamp", "clamp fp32 (8192, 4096) with tensor min and max", "GB/s", "hbm",
+                      16 * EN[0] * EN[1], 1, lambda i: ew_build(i, 3), clamp_step,
+                      ew_cpu(torch.clamp, 3, 16, "torch.clamp fp32 (2048, 4096), tensor bounds = 1/4 of the workload"),
+                      "f32"))
 
     # rms_norm / layer_norm bf16 (16384, 4096)
     R, C = 16384, 4096

@@ -13,9 +13,14 @@
  *
  * Reference interface replaced by each entry point (paths relative to the
  * mygitljf/ntops source tree):
- *   ntops_unary       <- src/ntops/torch/{silu,gelu,exp,bitwise_not}.py:7-17
- *                        (kernels/{silu,gelu,exp,bitwise_not}.py application)
- *   ntops_binary      <- src/ntops/torch/{add,mul,bitwise_and,bitwise_or}.py:7-15
+ *   ntops_unary       <- src/ntops/torch/{silu,gelu,exp,bitwise_not}.py:7-17,
+ *                        {relu,sigmoid,tanh,neg,abs,rsqrt,sin,cos}.py:7-17
+ *                        (kernels/<op>.py application)
+ *   ntops_binary      <- src/ntops/torch/{add,mul,bitwise_and,bitwise_or}.py:7-15,
+ *                        {sub,div,pow}.py:7-15
+ *   ntops_compare     <- src/ntops/torch/{eq,ne,gt,ge,lt,le}.py:7-15
+ *   ntops_classify    <- src/ntops/torch/{isinf,isnan}.py:7-14
+ *   ntops_clamp       <- src/ntops/torch/clamp.py:7-15
  *   ntops_cast        <- no ntops counterpart; the dtype promotion / layout
  *                        copy that torch's TensorIterator performs before the
  *                        elementwise kernels (kept native so no op falls back
@@ -82,11 +87,21 @@ enum ntops_unary_op {
   NTOPS_UNARY_GELU_TANH = 3, /* 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3)))
                                                                   gelu.py:14-26 */
   NTOPS_UNARY_EXP = 4,       /* exp(x)                            exp.py:10   */
-  NTOPS_UNARY_BITWISE_NOT = 5 /* ~x; logical not for bool   bitwise_not.py:9-14 */
+  NTOPS_UNARY_BITWISE_NOT = 5, /* ~x; logical not for bool  bitwise_not.py:9-14 */
+  NTOPS_UNARY_RELU = 6,      /* max(0, x), NaN kept               relu.py:9   */
+  NTOPS_UNARY_SIGMOID = 7,   /* 1 / (1 + exp(-x))                 sigmoid.py:10 */
+  NTOPS_UNARY_TANH = 8,      /* tanh(x)                           tanh.py:10-13 */
+  NTOPS_UNARY_NEG = 9,       /* -x (two's complement wrap)        neg.py:9    */
+  NTOPS_UNARY_ABS = 10,      /* |x|                               abs.py:10   */
+  NTOPS_UNARY_RSQRT = 11,    /* 1 / sqrt(x), each op IEEE         rsqrt.py:10 */
+  NTOPS_UNARY_SIN = 12,      /* sin(x)                            sin.py:10   */
+  NTOPS_UNARY_COS = 13       /* cos(x)                            cos.py:10   */
 };
 
 /* y = op(x) over an ndim-dimensional index space `shape`.  x and y have the
- * same dtype; floating ops accept F32/F16/BF16/F64, BITWISE_NOT accepts
+ * same dtype; SILU/GELU/EXP/SIGMOID/TANH/RSQRT/SIN/COS accept F32/F16/BF16/F64
+ * (16-bit types compute in fp32 and round once), RELU/NEG/ABS accept the
+ * floating and the signed/unsigned integer types, BITWISE_NOT accepts
  * BOOL/U8/I8/I16/I32/I64.  y may alias x exactly (in-place). */
 NTOPS_API int ntops_unary(int op, int dtype, int ndim, const int64_t* shape,
                 const void* x, const int64_t* x_strides,
@@ -96,19 +111,71 @@ enum ntops_binary_op {
   NTOPS_BINARY_ADD = 1,         /* a + alpha * b              add.py:10 */
   NTOPS_BINARY_MUL = 2,         /* a * b                      mul.py:9  */
   NTOPS_BINARY_BITWISE_AND = 3, /* a & b               bitwise_and.py:9 */
-  NTOPS_BINARY_BITWISE_OR = 4   /* a | b                bitwise_or.py:9 */
+  NTOPS_BINARY_BITWISE_OR = 4,  /* a | b                bitwise_or.py:9 */
+  NTOPS_BINARY_SUB = 5,         /* a - alpha * b              sub.py:10 */
+  NTOPS_BINARY_DIV = 6,         /* a / b (floating only)      div.py:10 */
+  NTOPS_BINARY_DIV_TRUNC = 7,   /* trunc(a / b)               div.py:14 */
+  NTOPS_BINARY_DIV_FLOOR = 8,   /* floor(a / b), Python's floor division
+                                                              div.py:18 */
+  NTOPS_BINARY_POW = 9          /* a ** b                     pow.py:10 */
 };
 
 /* out = op(a, b) over `shape`.  a, b and out share `dtype` (the caller has
  * already applied type promotion).  Broadcasting is expressed by stride 0.
  * When b is NULL, b is the scalar (b_f for floating dtypes, b_i for integer
- * and bool dtypes).  alpha (ADD only) follows the same split; it is rounded
- * to `dtype` before use, as torch's CPU kernel does. */
+ * and bool dtypes).  alpha (ADD, SUB) follows the same split; it is rounded
+ * to `dtype` before use, as torch's CPU kernel does.  A scalar b of ADD/SUB
+ * and of POW is rounded to `dtype`; of MUL/DIV* it stays in fp32 (fp64 for
+ * F64) opmath -- torch's CPU conventions.  DIV_TRUNC / DIV_FLOOR on integer
+ * dtypes give 0 where b == 0 (torch's CPU kernel raises instead).  POW on
+ * integer dtypes uses torch's rule for negative exponents (1 for base 1,
+ * +-1 for base -1, else 0). */
 NTOPS_API int ntops_binary(int op, int dtype, int ndim, const int64_t* shape,
                  const void* a, const int64_t* a_strides,
                  const void* b, const int64_t* b_strides,
                  double b_f, int64_t b_i, double alpha_f, int64_t alpha_i,
                  void* out, const int64_t* out_strides, void* stream);
+
+enum ntops_compare_op {
+  NTOPS_CMP_EQ = 1, /* a == b   eq.py:9 */
+  NTOPS_CMP_NE = 2, /* a != b   ne.py:9 */
+  NTOPS_CMP_GT = 3, /* a >  b   gt.py:9 */
+  NTOPS_CMP_GE = 4, /* a >= b   ge.py:9 */
+  NTOPS_CMP_LT = 5, /* a <  b   lt.py:9 */
+  NTOPS_CMP_LE = 6  /* a <= b   le.py:9 */
+};
+
+/* out (BOOL) = op(a, b) over `shape`; a and b share `dtype` (any dtype),
+ * broadcasting by stride 0.  When b is NULL it is the scalar b_f / b_i,
+ * first rounded to `dtype` (the comparison runs in the common dtype, as in
+ * torch).  NaN compares unequal to everything. */
+NTOPS_API int ntops_compare(int op, int dtype, int ndim, const int64_t* shape,
+                  const void* a, const int64_t* a_strides,
+                  const void* b, const int64_t* b_strides,
+                  double b_f, int64_t b_i,
+                  void* out, const int64_t* out_strides, void* stream);
+
+enum ntops_classify_op {
+  NTOPS_CLASSIFY_ISINF = 1, /* x == +inf or x == -inf   isinf.py:9-11 */
+  NTOPS_CLASSIFY_ISNAN = 2  /* x != x                   isnan.py:9    */
+};
+
+/* out (BOOL) = op(x) over `shape`; x of any dtype (integer and bool inputs
+ * give false everywhere). */
+NTOPS_API int ntops_classify(int op, int dtype, int ndim, const int64_t* shape,
+                   const void* x, const int64_t* x_strides,
+                   void* out, const int64_t* out_strides, void* stream);
+
+/* out = min(max(x, lo), hi) over `shape` (clamp.py:9).  lo / hi are each
+ * absent (has_lo / has_hi = 0), a tensor (lo / hi non-NULL, strides with 0
+ * for broadcast) or the scalar lo_f / lo_i (hi_f / hi_i), rounded to
+ * `dtype`.  Floating: a NaN in x, then in lo, then in hi, is the result
+ * (torch's rule); lo > hi gives hi.  dtype: any but BOOL. */
+NTOPS_API int ntops_clamp(int dtype, int ndim, const int64_t* shape,
+                const void* x, const int64_t* x_strides,
+                const void* lo, const int64_t* lo_strides, double lo_f, int64_t lo_i, int has_lo,
+                const void* hi, const int64_t* hi_strides, double hi_f, int64_t hi_i, int has_hi,
+                void* out, const int64_t* out_strides, void* stream);
 
 /* y = (dst_dtype) x, elementwise, any strides (stride 0 allowed on x). */
 NTOPS_API int ntops_cast(int src_dtype, int dst_dtype, int ndim, const int64_t* shape,

@@ -31,9 +31,13 @@ DTYPE_CODE = {
     torch.int64: I64,
 }
 
-# enum ntops_unary_op / ntops_binary_op
+# enum ntops_unary_op / ntops_binary_op / ntops_compare_op / ntops_classify_op
 UNARY_SILU, UNARY_GELU, UNARY_GELU_TANH, UNARY_EXP, UNARY_BITWISE_NOT = 1, 2, 3, 4, 5
+UNARY_RELU, UNARY_SIGMOID, UNARY_TANH, UNARY_NEG, UNARY_ABS, UNARY_RSQRT, UNARY_SIN, UNARY_COS = range(6, 14)
 BINARY_ADD, BINARY_MUL, BINARY_BITWISE_AND, BINARY_BITWISE_OR = 1, 2, 3, 4
+BINARY_SUB, BINARY_DIV, BINARY_DIV_TRUNC, BINARY_DIV_FLOOR, BINARY_POW = 5, 6, 7, 8, 9
+CMP_EQ, CMP_NE, CMP_GT, CMP_GE, CMP_LT, CMP_LE = 1, 2, 3, 4, 5, 6
+CLASSIFY_ISINF, CLASSIFY_ISNAN = 1, 2
 
 _c_i64p = ctypes.POINTER(ctypes.c_int64)
 _vp = ctypes.c_void_p
@@ -48,6 +52,16 @@ _SIGNATURES = {
     "ntops_binary": (
         _i,
         [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _i64, _d, _i64, _vp, _c_i64p, _vp],
+    ),
+    "ntops_compare": (
+        _i,
+        [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _i64, _vp, _c_i64p, _vp],
+    ),
+    "ntops_classify": (_i, [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp]),
+    "ntops_clamp": (
+        _i,
+        [_i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _i64, _i, _vp, _c_i64p, _d, _i64, _i,
+         _vp, _c_i64p, _vp],
     ),
     "ntops_cast": (_i, [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp]),
     "ntops_rms_norm": (_i, [_i, _i64, _i64, _vp, _i64, _vp, _i, _d, _vp, _i64, _vp]),

@@ -1,30 +1,39 @@
 // Elementwise family for gfx950: silu, gelu (erf / tanh), exp, bitwise_not,
-// add, mul, bitwise_and, bitwise_or.
+// relu, sigmoid, tanh, neg, abs, rsqrt, sin, cos; add, sub, mul, div (true /
+// trunc / floor), pow, bitwise_and, bitwise_or; the comparisons eq ne gt ge
+// lt le; isinf, isnan; clamp.
 //
 // Per-element math follows the reference applications
 //   kernels/silu.py:10, kernels/gelu.py:11,14-26, kernels/exp.py:10,
-//   kernels/bitwise_not.py:9-14, kernels/add.py:10, kernels/mul.py:9,
-//   kernels/bitwise_and.py:9, kernels/bitwise_or.py:9
+//   kernels/bitwise_not.py:9-14, kernels/relu.py:9, kernels/sigmoid.py:10,
+//   kernels/tanh.py:10-13, kernels/neg.py:9, kernels/abs.py:10,
+//   kernels/rsqrt.py:10, kernels/sin.py:10, kernels/cos.py:10,
+//   kernels/add.py:10, kernels/sub.py:10, kernels/mul.py:9,
+//   kernels/div.py:9-18, kernels/pow.py:10, kernels/bitwise_and.py:9,
+//   kernels/bitwise_or.py:9, kernels/{eq,ne,gt,ge,lt,le}.py:9,
+//   kernels/isinf.py:9-11, kernels/isnan.py:9, kernels/clamp.py:9
 // with torch's CPU conventions where ntops leaves them open (16-bit floats
 // compute in fp32 and round once; add's alpha is rounded to the tensor dtype
 // and applied with a fused multiply-add).
 //
 // Two launch shapes:
-//  * dense: every operand is one contiguous, 16-byte aligned run.  Each
-//    thread moves UNROLL 16-byte packs per operand, all loads issued before
-//    the first use so that ~UNROLL*16 B per lane are in flight; packs of a
+//  * dense: every operand is one contiguous, aligned run.  Each thread moves
+//    one 16-byte pack of every input (V elements) and writes the V results
+//    with one store (16 bytes, or V bytes for a bool result); packs of a
 //    block are consecutive 4 KiB runs (fully coalesced).
 //  * strided: any strides (0 = broadcast) over up to 8 merged dims, 32-bit
 //    index math whenever every offset fits.
+// The output element type is the functor's result type (bool for the
+// comparisons and isinf / isnan).
 #include "dispatch.h"
 
 namespace ntops {
 namespace {
 
+// One 16-byte pack per operand per thread and many 256-thread workgroups: on
+// MI355X this streams at ~6.3 TB/s on 128 MiB copies, ahead of deeper
+// per-thread unrolls.
 constexpr int kThreads = 256;
-// One 16-byte pack per operand per thread and many workgroups: on MI355X this
-// streams at ~6.3 TB/s on 128 MiB copies, ahead of deeper per-thread unrolls.
-constexpr int kUnroll = 1;
 
 __device__ __forceinline__ float ex(float v) { return expf(v); }
 __device__ __forceinline__ double ex(double v) { return exp(v); }
@@ -34,6 +43,47 @@ __device__ __forceinline__ float th(float v) { return tanhf(v); }
 __device__ __forceinline__ double th(double v) { return tanh(v); }
 __device__ __forceinline__ float fm(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 __device__ __forceinline__ double fm(double a, double b, double c) { return __builtin_fma(a, b, c); }
+__device__ __forceinline__ float sn(float v) { return sinf(v); }
+__device__ __forceinline__ double sn(double v) { return sin(v); }
+__device__ __forceinline__ float cs(float v) { return cosf(v); }
+__device__ __forceinline__ double cs(double v) { return cos(v); }
+__device__ __forceinline__ float sq(float v) { return __builtin_sqrtf(v); }  // IEEE (correctly rounded)
+__device__ __forceinline__ double sq(double v) { return __builtin_sqrt(v); }
+__device__ __forceinline__ float pw(float a, float b) { return powf(a, b); }
+__device__ __forceinline__ double pw(double a, double b) { return pow(a, b); }
+__device__ __forceinline__ float fmd(float a, float b) { return fmodf(a, b); }
+__device__ __forceinline__ double fmd(double a, double b) { return fmod(a, b); }
+__device__ __forceinline__ float flr(float v) { return floorf(v); }
+__device__ __forceinline__ double flr(double v) { return floor(v); }
+__device__ __forceinline__ float trc(float v) { return truncf(v); }
+__device__ __forceinline__ double trc(double v) { return trunc(v); }
+__device__ __forceinline__ float cpsgn(float a, float b) { return copysignf(a, b); }
+__device__ __forceinline__ double cpsgn(double a, double b) { return copysign(a, b); }
+
+// Two's complement negation without signed overflow.
+template <typename T>
+__device__ __forceinline__ T wrap_neg(T v) {
+  return static_cast<T>(static_cast<uint64_t>(0) - static_cast<uint64_t>(static_cast<int64_t>(v)));
+}
+
+// clamp.py:9 with torch's rule: a NaN in x, then in lo, then in hi, is the
+// result; otherwise min(max(x, lo), hi) (so lo > hi gives hi).  The result
+// is always one of the three values, so no rounding happens.
+template <typename T>
+__device__ __forceinline__ T clamp_value(T x, T lo, T hi) {
+  if constexpr (IsFloat<T>::v) {
+    using C = opmath_t<T>;
+    const C xv = convert<C>(x), l = convert<C>(lo), h = convert<C>(hi);
+    if (xv != xv) return x;
+    if (l != l) return lo;
+    if (h != h) return hi;
+    const T r = xv < l ? lo : x;
+    return h < convert<C>(r) ? hi : r;
+  } else {
+    const T r = x < lo ? lo : x;
+    return hi < r ? hi : r;
+  }
+}
 
 // ------------------------------------------------------------ unary ops --
 // silu.py:10   output = input / (1 + exp(-fp32(input)))
@@ -85,6 +135,93 @@ struct NotF {
     else
       return static_cast<T>(~v);
   }
+};
+
+// relu.py:9  max(0, x) as torch's clamp_min: NaN stays NaN, -0 stays -0.
+struct ReluF {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T v) const {
+    if constexpr (IsFloat<T>::v) {
+      using C = opmath_t<T>;
+      return convert<C>(v) < C(0) ? T(0) : v;
+    } else if constexpr (std::is_signed<T>::value) {
+      return v < T(0) ? T(0) : v;
+    } else {
+      return v;
+    }
+  }
+};
+// sigmoid.py:10  1 / (1 + exp(-x)) in opmath, one rounding.
+struct SigmoidF {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T v) const {
+    using C = opmath_t<T>;
+    return convert<T>(C(1) / (C(1) + ex(-convert<C>(v))));
+  }
+};
+// tanh.py:10-13 (the reference spells tanh out through exp, which overflows
+// to NaN for |x| > 88; the library tanh is used, as torch does).
+struct TanhF {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T v) const {
+    using C = opmath_t<T>;
+    return convert<T>(th(convert<C>(v)));
+  }
+};
+// neg.py:9
+struct NegF {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T v) const {
+    if constexpr (IsFloat<T>::v)
+      return -v;
+    else
+      return wrap_neg(v);
+  }
+};
+// abs.py:10  (sign bit cleared for floats; integer minimum wraps)
+struct AbsF {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T v) const {
+    if constexpr (std::is_same<T, double>::value) {
+      return __builtin_fabs(v);
+    } else if constexpr (IsFloat<T>::v) {
+      return convert<T>(__builtin_fabsf(convert<float>(v)));
+    } else if constexpr (std::is_signed<T>::value) {
+      return v < T(0) ? wrap_neg(v) : v;
+    } else {
+      return v;
+    }
+  }
+};
+// rsqrt.py:10  1 / sqrt(x): IEEE square root, then IEEE division (bit-exact
+// with torch's CPU kernel).
+struct RsqrtF {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T v) const {
+    using C = opmath_t<T>;
+    return convert<T>(C(1) / sq(convert<C>(v)));
+  }
+};
+// sin.py:10 / cos.py:10
+struct SinF {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T v) const {
+    using C = opmath_t<T>;
+    return convert<T>(sn(convert<C>(v)));
+  }
+};
+struct CosF {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T v) const {
+    using C = opmath_t<T>;
+    return convert<T>(cs(convert<C>(v)));
+  }
+};
+// clamp with scalar (or absent) bounds, already rounded to T.
+template <typename T>
+struct ClampSF {
+  T lo, hi;
+  __device__ __forceinline__ T operator()(T v) const { return clamp_value(v, lo, hi); }
 };
 
 // ----------------------------------------------------------- binary ops --
@@ -187,31 +324,258 @@ struct BitF {
   }
 };
 
+// div.py:9-18.  Floating: in opmath, one rounding (trunc of two 16-bit
+// tensors truncates the quotient after rounding it to T, as torch's CPU
+// kernel does).  A Python-number divisor stays in opmath (not rounded to T).
+// MODE 0 = true division, 1 = trunc,
+// 2 = floor (Python's floor division: the quotient of (a - fmod(a, b)) / b,
+// corrected by the sign of the remainder and rounded to the nearest integer,
+// so that e.g. 7.5 // -inf = -1 and 0 // -3 = -0).
+template <typename C>
+__device__ __forceinline__ C floor_divide(C a, C b) {
+  if (b == C(0)) return a / b;
+  const C mod = fmd(a, b);
+  C div = (a - mod) / b;
+  if (mod != C(0) && ((b < C(0)) != (mod < C(0)))) div -= C(1);
+  if (div == C(0)) return cpsgn(C(0), a / b);
+  C fl = flr(div);
+  if (div - fl > C(0.5)) fl += C(1);
+  return fl;
+}
+template <int MODE, typename T, bool F = IsFloat<T>::v>
+struct DivF;
+template <int MODE, typename T>
+struct DivF<MODE, T, true> {
+  using C = opmath_t<T>;
+  // ROUNDQ: round a 16-bit trunc quotient to T before truncating (torch's
+  // tensor / tensor path; its tensor / number path truncates in opmath).
+  template <bool ROUNDQ>
+  __device__ __forceinline__ static C apply(C a, C b) {
+    if constexpr (MODE == 0)
+      return a / b;
+    else if constexpr (MODE == 1)
+      return ROUNDQ ? trc(convert<C>(convert<T>(a / b))) : trc(a / b);
+    else
+      return floor_divide(a, b);
+  }
+  __device__ __forceinline__ T operator()(T a, T b) const {
+    return convert<T>(apply<true>(convert<C>(a), convert<C>(b)));
+  }
+  __device__ __forceinline__ C scalar_b(double b) const { return static_cast<C>(b); }
+  __device__ __forceinline__ T with_scalar(T a, C b) const {
+    return convert<T>(apply<false>(convert<C>(a), b));
+  }
+};
+// Integer trunc / floor division in int64; division by zero gives 0 (torch's
+// CPU kernel raises), b = -1 negates with wraparound.
+template <int MODE, typename T>
+struct DivF<MODE, T, false> {
+  __device__ __forceinline__ static int64_t apply(int64_t a, int64_t b) {
+    if (b == 0) return 0;
+    if (b == -1) return static_cast<int64_t>(static_cast<uint64_t>(0) - static_cast<uint64_t>(a));
+    int64_t q = a / b;
+    if constexpr (MODE == 2)
+      if ((a % b != 0) && ((a < 0) != (b < 0))) q -= 1;
+    return q;
+  }
+  __device__ __forceinline__ T operator()(T a, T b) const {
+    return static_cast<T>(apply(static_cast<int64_t>(a), static_cast<int64_t>(b)));
+  }
+  __device__ __forceinline__ int64_t scalar_b(int64_t b) const { return b; }
+  __device__ __forceinline__ T with_scalar(T a, int64_t b) const {
+    return static_cast<T>(apply(static_cast<int64_t>(a), b));
+  }
+};
+
+// pow.py:10.  Floating tensor ** tensor: the library pow in opmath, one
+// rounding.  A Python-number exponent follows torch's CPU dispatch per dtype:
+//  * f32 / f64: 0.5 -> sqrt, -0.5 -> 1/sqrt, -1 -> 1/x, 2 -> x*x,
+//    3 -> x*x*x, -2 -> 1/(x*x); any other exponent (kept in double) -> pow
+//    evaluated in double and rounded once;
+//  * bf16: the exponent is rounded to bf16; the same special cases, the
+//    products rounded to bf16 after every multiply (x^3 = (x*x)*x,
+//    x^-2 = 1/(x*x)); other exponents -> powf, one rounding;
+//  * f16: the exponent is rounded to f16, always powf (no special cases, so
+//    e.g. (-inf)^0.5 = +inf).
+template <typename T, bool F = IsFloat<T>::v>
+struct PowF;
+template <typename T>
+struct PowF<T, true> {
+  using C = opmath_t<T>;
+  static constexpr bool kF16 = std::is_same<T, _Float16>::value;
+  static constexpr bool kBF16 = std::is_same<T, __bf16>::value;
+  __device__ __forceinline__ T operator()(T a, T b) const {
+    return convert<T>(pw(convert<C>(a), convert<C>(b)));
+  }
+  __device__ __forceinline__ double scalar_b(double b) const {
+    if constexpr (kF16 || kBF16)
+      return static_cast<double>(convert<float>(convert<T>(b)));
+    else
+      return b;
+  }
+  __device__ __forceinline__ T with_scalar(T a, double e) const {
+    const C x = convert<C>(a);
+    if constexpr (!kF16) {
+      if (e == 0.5) return convert<T>(sq(x));
+      if (e == -0.5) return convert<T>(C(1) / sq(x));
+      if (e == -1.0) return convert<T>(C(1) / x);
+      if (e == 2.0) return convert<T>(x * x);
+      if (e == 3.0) {
+        if constexpr (kBF16) return convert<T>(convert<C>(convert<T>(x * x)) * x);
+        return convert<T>(x * x * x);
+      }
+      if (e == -2.0) {
+        if constexpr (kBF16) return convert<T>(C(1) / convert<C>(convert<T>(x * x)));
+        return convert<T>(C(1) / (x * x));
+      }
+    }
+    if constexpr (std::is_same<T, float>::value)
+      return static_cast<float>(pow(static_cast<double>(x), e));
+    else if constexpr (std::is_same<T, double>::value)
+      return pow(x, e);
+    else
+      return convert<T>(pw(x, static_cast<float>(e)));
+  }
+};
+// Integer powers by squaring with wraparound; negative exponents follow
+// torch: base 1 -> 1, base -1 -> +-1 by parity, anything else -> 0.
+template <typename T>
+struct PowF<T, false> {
+  __device__ __forceinline__ static T apply(int64_t a, int64_t e) {
+    if (e < 0) {
+      if (a == 1) return T(1);
+      if (a == -1) return static_cast<T>((e & 1) ? -1 : 1);
+      return T(0);
+    }
+    uint64_t base = static_cast<uint64_t>(a), r = 1;
+    while (e) {
+      if (e & 1) r *= base;
+      base *= base;
+      e >>= 1;
+    }
+    return static_cast<T>(r);
+  }
+  __device__ __forceinline__ T operator()(T a, T b) const {
+    return apply(static_cast<int64_t>(a), static_cast<int64_t>(b));
+  }
+  __device__ __forceinline__ int64_t scalar_b(int64_t b) const { return b; }
+  __device__ __forceinline__ T with_scalar(T a, int64_t b) const { return apply(static_cast<int64_t>(a), b); }
+};
+
+// {eq,ne,gt,ge,lt,le}.py:9 -> bool.  Floats compare in opmath (exact for the
+// 16-bit types); a Python-number operand is first rounded to T (the common
+// dtype), integers compare as int64.
+template <int OP, typename T>
+struct CmpF {
+  static constexpr bool kBoolOut = true;
+  using K = typename std::conditional<IsFloat<T>::v, opmath_t<T>, int64_t>::type;
+  __device__ __forceinline__ static bool apply(K a, K b) {
+    if constexpr (OP == NTOPS_CMP_EQ)
+      return a == b;
+    else if constexpr (OP == NTOPS_CMP_NE)
+      return a != b;
+    else if constexpr (OP == NTOPS_CMP_GT)
+      return a > b;
+    else if constexpr (OP == NTOPS_CMP_GE)
+      return a >= b;
+    else if constexpr (OP == NTOPS_CMP_LT)
+      return a < b;
+    else
+      return a <= b;
+  }
+  __device__ __forceinline__ bool operator()(T a, T b) const {
+    return apply(static_cast<K>(convert<K>(a)), static_cast<K>(convert<K>(b)));
+  }
+  template <typename S>
+  __device__ __forceinline__ K scalar_b(S b) const {
+    if constexpr (IsFloat<T>::v)
+      return convert<K>(convert<T>(static_cast<double>(b)));
+    else
+      return static_cast<K>(b);
+  }
+  __device__ __forceinline__ bool with_scalar(T a, K b) const { return apply(convert<K>(a), b); }
+};
+
+// isinf.py:9-11 / isnan.py:9 -> bool (always false for integers)
+template <bool NAN_TEST>
+struct ClassifyF {
+  static constexpr bool kBoolOut = true;
+  template <typename T>
+  __device__ __forceinline__ bool operator()(T v) const {
+    if constexpr (IsFloat<T>::v) {
+      using C = opmath_t<T>;
+      const C x = convert<C>(v);
+      if constexpr (NAN_TEST)
+        return x != x;
+      else
+        return x == C(__builtin_huge_val()) || x == -C(__builtin_huge_val());
+    } else {
+      return false;
+    }
+  }
+};
+
 // Scalar-operand type of a functor for element type T.
 template <typename T>
 using scalar_arg_t = typename std::conditional<IsFloat<T>::v, opmath_t<T>, int64_t>::type;
 
 // ------------------------------------------------------------- kernels --
-template <typename T, typename F>
-__global__ __launch_bounds__(kThreads) void k_unary_dense(const T* x, T* y, int64_t npack,
+// Result element type of functor F on element type T: bool for functors that
+// declare `kBoolOut`, T otherwise.
+template <typename F, typename = void>
+struct BoolOut : std::false_type {};
+template <typename F>
+struct BoolOut<F, std::void_t<decltype(F::kBoolOut)>> : std::true_type {};
+template <typename F, typename T>
+using out1_t = typename std::conditional<BoolOut<F>::value, bool, T>::type;
+template <typename F, typename T>
+using out2_t = out1_t<F, T>;
+
+// Stores V results of type O with one non-temporal store of V * sizeof(O)
+// bytes (the caller guarantees that alignment).
+template <typename O, int V>
+__device__ __forceinline__ void store_out(O* p, const O (&v)[V]) {
+  constexpr int B = V * static_cast<int>(sizeof(O));
+  if constexpr (std::is_same<O, bool>::value || B != 16) {
+    if constexpr (B == 16) {
+      u32x4 w;
+      __builtin_memcpy(&w, v, 16);
+      __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+    } else if constexpr (B == 8) {
+      uint64_t w;
+      __builtin_memcpy(&w, v, 8);
+      __builtin_nontemporal_store(w, reinterpret_cast<uint64_t*>(p));
+    } else if constexpr (B == 4) {
+      uint32_t w;
+      __builtin_memcpy(&w, v, 4);
+      __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(p));
+    } else if constexpr (B == 2) {
+      uint16_t w;
+      __builtin_memcpy(&w, v, 2);
+      __builtin_nontemporal_store(w, reinterpret_cast<uint16_t*>(p));
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) p[i] = v[i];
+    }
+  } else {
+    Pack16<O> o;
+#pragma unroll
+    for (int i = 0; i < V; ++i) o.v[i] = v[i];
+    store16_nt(p, o);
+  }
+}
+
+template <typename T, typename O, typename F>
+__global__ __launch_bounds__(kThreads) void k_unary_dense(const T* x, O* y, int64_t npack,
                                                           int64_t n, F f) {
   constexpr int V = Pack16<T>::N;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnroll) + threadIdx.x;
-  Pack16<T> r[kUnroll];
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (p < npack) {
+    const Pack16<T> r = load16_nt(x + p * V);
+    O o[V];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + u * kThreads;
-    if (p < npack) r[u] = load16_nt(x + p * V);
-  }
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + u * kThreads;
-    if (p < npack) {
-      Pack16<T> o;
-#pragma unroll
-      for (int i = 0; i < V; ++i) o.v[i] = f(r[u].v[i]);
-      store16_nt(y + p * V, o);
-    }
+    for (int i = 0; i < V; ++i) o[i] = f(r.v[i]);
+    store_out<O, V>(y + p * V, o);
   }
   if (blockIdx.x == 0) {
     const int64_t i = npack * V + threadIdx.x;
@@ -219,8 +583,8 @@ __global__ __launch_bounds__(kThreads) void k_unary_dense(const T* x, T* y, int6
   }
 }
 
-template <typename T, typename F, typename I>
-__global__ __launch_bounds__(kThreads) void k_unary_strided(KSpace<2, I> sp, const T* x, T* y,
+template <typename T, typename O, typename F, typename I>
+__global__ __launch_bounds__(kThreads) void k_unary_strided(KSpace<2, I> sp, const T* x, O* y,
                                                             I n, F f) {
   for (I i = static_cast<I>(blockIdx.x) * kThreads + threadIdx.x; i < n;
        i += static_cast<I>(gridDim.x) * kThreads) {
@@ -230,29 +594,18 @@ __global__ __launch_bounds__(kThreads) void k_unary_strided(KSpace<2, I> sp, con
   }
 }
 
-template <typename T, typename F>
-__global__ __launch_bounds__(kThreads) void k_binary_dense(const T* a, const T* b, T* y,
+template <typename T, typename O, typename F>
+__global__ __launch_bounds__(kThreads) void k_binary_dense(const T* a, const T* b, O* y,
                                                            int64_t npack, int64_t n, F f) {
   constexpr int V = Pack16<T>::N;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnroll) + threadIdx.x;
-  Pack16<T> ra[kUnroll], rb[kUnroll];
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (p < npack) {
+    const Pack16<T> ra = load16_nt(a + p * V);
+    const Pack16<T> rb = load16_nt(b + p * V);
+    O o[V];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + u * kThreads;
-    if (p < npack) {
-      ra[u] = load16_nt(a + p * V);
-      rb[u] = load16_nt(b + p * V);
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + u * kThreads;
-    if (p < npack) {
-      Pack16<T> o;
-#pragma unroll
-      for (int i = 0; i < V; ++i) o.v[i] = f(ra[u].v[i], rb[u].v[i]);
-      store16_nt(y + p * V, o);
-    }
+    for (int i = 0; i < V; ++i) o[i] = f(ra.v[i], rb.v[i]);
+    store_out<O, V>(y + p * V, o);
   }
   if (blockIdx.x == 0) {
     const int64_t i = npack * V + threadIdx.x;
@@ -260,27 +613,18 @@ __global__ __launch_bounds__(kThreads) void k_binary_dense(const T* a, const T* 
   }
 }
 
-template <typename T, typename F, typename S>
-__global__ __launch_bounds__(kThreads) void k_binary_scalar_dense(const T* a, S braw, T* y,
+template <typename T, typename O, typename F, typename S>
+__global__ __launch_bounds__(kThreads) void k_binary_scalar_dense(const T* a, S braw, O* y,
                                                                   int64_t npack, int64_t n, F f) {
   constexpr int V = Pack16<T>::N;
   const auto bs = f.scalar_b(braw);
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kUnroll) + threadIdx.x;
-  Pack16<T> ra[kUnroll];
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (p < npack) {
+    const Pack16<T> ra = load16_nt(a + p * V);
+    O o[V];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + u * kThreads;
-    if (p < npack) ra[u] = load16_nt(a + p * V);
-  }
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t p = base + u * kThreads;
-    if (p < npack) {
-      Pack16<T> o;
-#pragma unroll
-      for (int i = 0; i < V; ++i) o.v[i] = f.with_scalar(ra[u].v[i], bs);
-      store16_nt(y + p * V, o);
-    }
+    for (int i = 0; i < V; ++i) o[i] = f.with_scalar(ra.v[i], bs);
+    store_out<O, V>(y + p * V, o);
   }
   if (blockIdx.x == 0) {
     const int64_t i = npack * V + threadIdx.x;
@@ -288,9 +632,9 @@ __global__ __launch_bounds__(kThreads) void k_binary_scalar_dense(const T* a, S 
   }
 }
 
-template <typename T, typename F, typename I>
+template <typename T, typename O, typename F, typename I>
 __global__ __launch_bounds__(kThreads) void k_binary_strided(KSpace<3, I> sp, const T* a,
-                                                             const T* b, T* y, I n, F f) {
+                                                             const T* b, O* y, I n, F f) {
   for (I i = static_cast<I>(blockIdx.x) * kThreads + threadIdx.x; i < n;
        i += static_cast<I>(gridDim.x) * kThreads) {
     I off[3];
@@ -299,9 +643,9 @@ __global__ __launch_bounds__(kThreads) void k_binary_strided(KSpace<3, I> sp, co
   }
 }
 
-template <typename T, typename F, typename S, typename I>
+template <typename T, typename O, typename F, typename S, typename I>
 __global__ __launch_bounds__(kThreads) void k_binary_scalar_strided(KSpace<2, I> sp, const T* a,
-                                                                    S braw, T* y, I n, F f) {
+                                                                    S braw, O* y, I n, F f) {
   const auto bs = f.scalar_b(braw);
   for (I i = static_cast<I>(blockIdx.x) * kThreads + threadIdx.x; i < n;
        i += static_cast<I>(gridDim.x) * kThreads) {
@@ -311,9 +655,47 @@ __global__ __launch_bounds__(kThreads) void k_binary_scalar_strided(KSpace<2, I>
   }
 }
 
+// clamp with at least one tensor bound: operands x, lo, hi, y.  A scalar
+// bound is passed as a value (its pointer is unused and its strides are 0).
+template <typename T, bool LO_T, bool HI_T>
+__global__ __launch_bounds__(kThreads) void k_clamp_dense(const T* x, const T* lo, const T* hi,
+                                                          T lo_s, T hi_s, T* y, int64_t npack,
+                                                          int64_t n) {
+  constexpr int V = Pack16<T>::N;
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (p < npack) {
+    const Pack16<T> rx = load16_nt(x + p * V);
+    Pack16<T> rl, rh;
+    if constexpr (LO_T) rl = load16_nt(lo + p * V);
+    if constexpr (HI_T) rh = load16_nt(hi + p * V);
+    T o[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) o[i] = clamp_value(rx.v[i], LO_T ? rl.v[i] : lo_s, HI_T ? rh.v[i] : hi_s);
+    store_out<T, V>(y + p * V, o);
+  }
+  if (blockIdx.x == 0) {
+    const int64_t i = npack * V + threadIdx.x;
+    if (threadIdx.x < V && i < n) y[i] = clamp_value(x[i], LO_T ? lo[i] : lo_s, HI_T ? hi[i] : hi_s);
+  }
+}
+
+template <typename T, bool LO_T, bool HI_T, typename I>
+__global__ __launch_bounds__(kThreads) void k_clamp_strided(KSpace<4, I> sp, const T* x,
+                                                            const T* lo, const T* hi, T lo_s,
+                                                            T hi_s, T* y, I n) {
+  for (I i = static_cast<I>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<I>(gridDim.x) * kThreads) {
+    I off[4];
+    strided_offsets<4, I>(sp, i, off);
+    const T l = LO_T ? lo[off[1]] : lo_s;
+    const T h = HI_T ? hi[off[2]] : hi_s;
+    y[off[3]] = clamp_value(x[off[0]], l, h);
+  }
+}
+
 // ------------------------------------------------------------ launchers --
 inline int64_t dense_blocks(int64_t npack) {
-  return ceil_div(npack > 0 ? npack : 1, static_cast<int64_t>(kThreads) * kUnroll);
+  return ceil_div(npack > 0 ? npack : 1, static_cast<int64_t>(kThreads));
 }
 inline unsigned strided_blocks(int64_t n) {
   int64_t b = ceil_div(n, kThreads);
@@ -330,9 +712,19 @@ bool space_is_dense(const StridedSpace<NOPS>& sp) {
   return true;
 }
 
+// Dense-path alignment of an output run of type O written V at a time.
+template <typename O, int V>
+bool out_aligned(const O* p) {
+  constexpr int B = V * static_cast<int>(sizeof(O));
+  const uintptr_t a = static_cast<uintptr_t>(B < 16 ? B : 16);
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
 template <typename T, typename F>
 int launch_unary(const F& f, int ndim, const int64_t* shape, const void* xv, const int64_t* xs,
                  void* yv, const int64_t* ys, hipStream_t st, const char* what) {
+  using O = out1_t<F, T>;
+  constexpr int V = Pack16<T>::N;
   const int64_t* strides[2] = {xs, ys};
   StridedSpace<2> sp;
   int64_t n = 0;
@@ -340,17 +732,18 @@ int launch_unary(const F& f, int ndim, const int64_t* shape, const void* xv, con
     return set_error(NTOPS_ERR_INVALID, "%s: more than %d non-mergeable dims", what, NTOPS_MAX_DIMS);
   if (n == 0) return NTOPS_OK;
   const T* x = static_cast<const T*>(xv);
-  T* y = static_cast<T*>(yv);
-  if (space_is_dense(sp) && aligned16(x) && aligned16(y)) {
-    const int64_t npack = n / Pack16<T>::N;
-    hipLaunchKernelGGL((k_unary_dense<T, F>), dim3(dense_blocks(npack)), dim3(kThreads), 0, st, x,
-                       y, npack, n, f);
+  O* y = static_cast<O*>(yv);
+  if (space_is_dense(sp) && aligned16(x) && out_aligned<O, V>(y)) {
+    const int64_t npack = n / V;
+    hipLaunchKernelGGL((k_unary_dense<T, O, F>), dim3(dense_blocks(npack)), dim3(kThreads), 0, st,
+                       x, y, npack, n, f);
   } else if (fits_int32(sp, n)) {
-    hipLaunchKernelGGL((k_unary_strided<T, F, int32_t>), dim3(strided_blocks(n)), dim3(kThreads),
-                       0, st, to_kspace<2, int32_t>(sp), x, y, static_cast<int32_t>(n), f);
+    hipLaunchKernelGGL((k_unary_strided<T, O, F, int32_t>), dim3(strided_blocks(n)),
+                       dim3(kThreads), 0, st, to_kspace<2, int32_t>(sp), x, y,
+                       static_cast<int32_t>(n), f);
   } else {
-    hipLaunchKernelGGL((k_unary_strided<T, F, int64_t>), dim3(strided_blocks(n)), dim3(kThreads),
-                       0, st, to_kspace<2, int64_t>(sp), x, y, n, f);
+    hipLaunchKernelGGL((k_unary_strided<T, O, F, int64_t>), dim3(strided_blocks(n)),
+                       dim3(kThreads), 0, st, to_kspace<2, int64_t>(sp), x, y, n, f);
   }
   return check_launch(what);
 }
@@ -359,9 +752,11 @@ template <typename T, typename F>
 int launch_binary(const F& f, int ndim, const int64_t* shape, const void* av, const int64_t* as,
                   const void* bv, const int64_t* bs, double b_f, int64_t b_i, void* yv,
                   const int64_t* ys, hipStream_t st, const char* what) {
+  using O = out2_t<F, T>;
+  constexpr int V = Pack16<T>::N;
   const T* a = static_cast<const T*>(av);
   const T* b = static_cast<const T*>(bv);
-  T* y = static_cast<T*>(yv);
+  O* y = static_cast<O*>(yv);
   using S = typename std::conditional<IsFloat<T>::v, double, int64_t>::type;
   S braw;
   if constexpr (IsFloat<T>::v) {
@@ -378,16 +773,16 @@ int launch_binary(const F& f, int ndim, const int64_t* shape, const void* av, co
     if (!build_space<2>(ndim, shape, strides, &sp, &n))
       return set_error(NTOPS_ERR_INVALID, "%s: more than %d non-mergeable dims", what, NTOPS_MAX_DIMS);
     if (n == 0) return NTOPS_OK;
-    if (space_is_dense(sp) && aligned16(a) && aligned16(y)) {
-      const int64_t npack = n / Pack16<T>::N;
-      hipLaunchKernelGGL((k_binary_scalar_dense<T, F, S>), dim3(dense_blocks(npack)),
+    if (space_is_dense(sp) && aligned16(a) && out_aligned<O, V>(y)) {
+      const int64_t npack = n / V;
+      hipLaunchKernelGGL((k_binary_scalar_dense<T, O, F, S>), dim3(dense_blocks(npack)),
                          dim3(kThreads), 0, st, a, braw, y, npack, n, f);
     } else if (fits_int32(sp, n)) {
-      hipLaunchKernelGGL((k_binary_scalar_strided<T, F, S, int32_t>), dim3(strided_blocks(n)),
+      hipLaunchKernelGGL((k_binary_scalar_strided<T, O, F, S, int32_t>), dim3(strided_blocks(n)),
                          dim3(kThreads), 0, st, to_kspace<2, int32_t>(sp), a, braw, y,
                          static_cast<int32_t>(n), f);
     } else {
-      hipLaunchKernelGGL((k_binary_scalar_strided<T, F, S, int64_t>), dim3(strided_blocks(n)),
+      hipLaunchKernelGGL((k_binary_scalar_strided<T, O, F, S, int64_t>), dim3(strided_blocks(n)),
                          dim3(kThreads), 0, st, to_kspace<2, int64_t>(sp), a, braw, y, n, f);
     }
     return check_launch(what);
@@ -398,18 +793,53 @@ int launch_binary(const F& f, int ndim, const int64_t* shape, const void* av, co
   if (!build_space<3>(ndim, shape, strides, &sp, &n))
     return set_error(NTOPS_ERR_INVALID, "%s: more than %d non-mergeable dims", what, NTOPS_MAX_DIMS);
   if (n == 0) return NTOPS_OK;
-  if (space_is_dense(sp) && aligned16(a) && aligned16(b) && aligned16(y)) {
-    const int64_t npack = n / Pack16<T>::N;
-    hipLaunchKernelGGL((k_binary_dense<T, F>), dim3(dense_blocks(npack)), dim3(kThreads), 0, st, a,
-                       b, y, npack, n, f);
+  if (space_is_dense(sp) && aligned16(a) && aligned16(b) && out_aligned<O, V>(y)) {
+    const int64_t npack = n / V;
+    hipLaunchKernelGGL((k_binary_dense<T, O, F>), dim3(dense_blocks(npack)), dim3(kThreads), 0, st,
+                       a, b, y, npack, n, f);
   } else if (fits_int32(sp, n)) {
-    hipLaunchKernelGGL((k_binary_strided<T, F, int32_t>), dim3(strided_blocks(n)), dim3(kThreads),
-                       0, st, to_kspace<3, int32_t>(sp), a, b, y, static_cast<int32_t>(n), f);
+    hipLaunchKernelGGL((k_binary_strided<T, O, F, int32_t>), dim3(strided_blocks(n)),
+                       dim3(kThreads), 0, st, to_kspace<3, int32_t>(sp), a, b, y,
+                       static_cast<int32_t>(n), f);
   } else {
-    hipLaunchKernelGGL((k_binary_strided<T, F, int64_t>), dim3(strided_blocks(n)), dim3(kThreads),
-                       0, st, to_kspace<3, int64_t>(sp), a, b, y, n, f);
+    hipLaunchKernelGGL((k_binary_strided<T, O, F, int64_t>), dim3(strided_blocks(n)),
+                       dim3(kThreads), 0, st, to_kspace<3, int64_t>(sp), a, b, y, n, f);
   }
   return check_launch(what);
+}
+
+// clamp: scalar-only bounds take the unary path; a tensor bound takes the
+// four-operand kernel (scalar bounds ride along as values).
+template <typename T, bool LO_T, bool HI_T>
+int launch_clamp_t(int ndim, const int64_t* shape, const T* x, const int64_t* xs, const T* lo,
+                   const int64_t* los, const T* hi, const int64_t* his, T lo_s, T hi_s, T* y,
+                   const int64_t* ys, hipStream_t st) {
+  int64_t zeros[64] = {0};
+  const int64_t* strides[4] = {xs, LO_T ? los : zeros, HI_T ? his : zeros, ys};
+  StridedSpace<4> sp;
+  int64_t n = 0;
+  if (!build_space<4>(ndim, shape, strides, &sp, &n))
+    return set_error(NTOPS_ERR_INVALID, "clamp: more than %d non-mergeable dims", NTOPS_MAX_DIMS);
+  if (n == 0) return NTOPS_OK;
+  bool dense = sp.ndim <= 1 && aligned16(x) && aligned16(y) && (!LO_T || aligned16(lo)) &&
+               (!HI_T || aligned16(hi));
+  if (sp.ndim == 1)
+    dense = dense && sp.stride[0][0] == 1 && sp.stride[3][0] == 1 &&
+            (!LO_T || sp.stride[1][0] == 1) && (!HI_T || sp.stride[2][0] == 1);
+  if (dense) {
+    const int64_t npack = n / Pack16<T>::N;
+    hipLaunchKernelGGL((k_clamp_dense<T, LO_T, HI_T>), dim3(dense_blocks(npack)), dim3(kThreads),
+                       0, st, x, lo, hi, lo_s, hi_s, y, npack, n);
+  } else if (fits_int32(sp, n)) {
+    hipLaunchKernelGGL((k_clamp_strided<T, LO_T, HI_T, int32_t>), dim3(strided_blocks(n)),
+                       dim3(kThreads), 0, st, to_kspace<4, int32_t>(sp), x, lo, hi, lo_s, hi_s, y,
+                       static_cast<int32_t>(n));
+  } else {
+    hipLaunchKernelGGL((k_clamp_strided<T, LO_T, HI_T, int64_t>), dim3(strided_blocks(n)),
+                       dim3(kThreads), 0, st, to_kspace<4, int64_t>(sp), x, lo, hi, lo_s, hi_s, y,
+                       n);
+  }
+  return check_launch("clamp");
 }
 
 // Validates the index space; pointers are only required when it is not
@@ -465,6 +895,45 @@ extern "C" int ntops_unary(int op, int dtype, int ndim, const int64_t* shape, co
         using T = decltype(tag);
         return launch_unary<T>(NotF{}, ndim, shape, x, x_strides, y, y_strides, st, "bitwise_not");
       });
+    case NTOPS_UNARY_SIGMOID:
+      return dispatch_float(dtype, "sigmoid", [&](auto tag) {
+        using T = decltype(tag);
+        return launch_unary<T>(SigmoidF{}, ndim, shape, x, x_strides, y, y_strides, st, "sigmoid");
+      });
+    case NTOPS_UNARY_TANH:
+      return dispatch_float(dtype, "tanh", [&](auto tag) {
+        using T = decltype(tag);
+        return launch_unary<T>(TanhF{}, ndim, shape, x, x_strides, y, y_strides, st, "tanh");
+      });
+    case NTOPS_UNARY_RSQRT:
+      return dispatch_float(dtype, "rsqrt", [&](auto tag) {
+        using T = decltype(tag);
+        return launch_unary<T>(RsqrtF{}, ndim, shape, x, x_strides, y, y_strides, st, "rsqrt");
+      });
+    case NTOPS_UNARY_SIN:
+      return dispatch_float(dtype, "sin", [&](auto tag) {
+        using T = decltype(tag);
+        return launch_unary<T>(SinF{}, ndim, shape, x, x_strides, y, y_strides, st, "sin");
+      });
+    case NTOPS_UNARY_COS:
+      return dispatch_float(dtype, "cos", [&](auto tag) {
+        using T = decltype(tag);
+        return launch_unary<T>(CosF{}, ndim, shape, x, x_strides, y, y_strides, st, "cos");
+      });
+    case NTOPS_UNARY_RELU:
+    case NTOPS_UNARY_NEG:
+    case NTOPS_UNARY_ABS: {
+      const char* name = op == NTOPS_UNARY_RELU ? "relu" : op == NTOPS_UNARY_NEG ? "neg" : "abs";
+      if (dtype == NTOPS_BOOL) return set_error(NTOPS_ERR_UNSUPPORTED, "%s: bool input is not supported", name);
+      return dispatch_all(dtype, name, [&](auto tag) {
+        using T = decltype(tag);
+        if (op == NTOPS_UNARY_RELU)
+          return launch_unary<T>(ReluF{}, ndim, shape, x, x_strides, y, y_strides, st, name);
+        if (op == NTOPS_UNARY_NEG)
+          return launch_unary<T>(NegF{}, ndim, shape, x, x_strides, y, y_strides, st, name);
+        return launch_unary<T>(AbsF{}, ndim, shape, x, x_strides, y, y_strides, st, name);
+      });
+    }
     default:
       return set_error(NTOPS_ERR_UNSUPPORTED, "%s: unknown op %d", what, op);
   }
@@ -507,7 +976,138 @@ extern "C" int ntops_binary(int op, int dtype, int ndim, const int64_t* shape, c
         return launch_binary<T>(BitF<true>{}, ndim, shape, a, a_strides, b, b_strides, b_f, b_i,
                                 out, out_strides, st, "bitwise_or");
       });
+    case NTOPS_BINARY_SUB:
+      // sub.py:10; torch evaluates a - alpha * b as add with -alpha.
+      if (dtype == NTOPS_BOOL)
+        return set_error(NTOPS_ERR_UNSUPPORTED, "sub: subtraction of bool tensors is not supported");
+      return dispatch_all(dtype, "sub", [&](auto tag) {
+        using T = decltype(tag);
+        AddF<T> f;
+        if constexpr (IsFloat<T>::v)
+          f.alpha = -alpha_f;
+        else
+          f.alpha = static_cast<int64_t>(static_cast<uint64_t>(0) - static_cast<uint64_t>(alpha_i));
+        return launch_binary<T>(f, ndim, shape, a, a_strides, b, b_strides, b_f, b_i, out,
+                                out_strides, st, "sub");
+      });
+    case NTOPS_BINARY_DIV:
+      return dispatch_float(dtype, "div", [&](auto tag) {
+        using T = decltype(tag);
+        return launch_binary<T>(DivF<0, T>{}, ndim, shape, a, a_strides, b, b_strides, b_f, b_i,
+                                out, out_strides, st, "div");
+      });
+    case NTOPS_BINARY_DIV_TRUNC:
+    case NTOPS_BINARY_DIV_FLOOR:
+      if (dtype == NTOPS_BOOL)
+        return set_error(NTOPS_ERR_UNSUPPORTED, "div: rounded division of bool tensors is not supported");
+      return dispatch_all(dtype, "div", [&](auto tag) {
+        using T = decltype(tag);
+        if (op == NTOPS_BINARY_DIV_TRUNC)
+          return launch_binary<T>(DivF<1, T>{}, ndim, shape, a, a_strides, b, b_strides, b_f, b_i,
+                                  out, out_strides, st, "div(trunc)");
+        return launch_binary<T>(DivF<2, T>{}, ndim, shape, a, a_strides, b, b_strides, b_f, b_i,
+                                out, out_strides, st, "div(floor)");
+      });
+    case NTOPS_BINARY_POW:
+      if (dtype == NTOPS_BOOL) return set_error(NTOPS_ERR_UNSUPPORTED, "pow: bool tensors are not supported");
+      return dispatch_all(dtype, "pow", [&](auto tag) {
+        using T = decltype(tag);
+        return launch_binary<T>(PowF<T>{}, ndim, shape, a, a_strides, b, b_strides, b_f, b_i, out,
+                                out_strides, st, "pow");
+      });
     default:
       return set_error(NTOPS_ERR_UNSUPPORTED, "%s: unknown op %d", what, op);
   }
+}
+
+extern "C" int ntops_compare(int op, int dtype, int ndim, const int64_t* shape, const void* a,
+                             const int64_t* a_strides, const void* b, const int64_t* b_strides,
+                             double b_f, int64_t b_i, void* out, const int64_t* out_strides,
+                             void* stream) {
+  const char* what = "ntops_compare";
+  if (int e = check_common(what, ndim, shape, a, out)) return e;
+  if (op < NTOPS_CMP_EQ || op > NTOPS_CMP_LE)
+    return set_error(NTOPS_ERR_UNSUPPORTED, "%s: unknown op %d", what, op);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dispatch_all(dtype, what, [&](auto tag) {
+    using T = decltype(tag);
+    switch (op) {
+      case NTOPS_CMP_EQ:
+        return launch_binary<T>(CmpF<NTOPS_CMP_EQ, T>{}, ndim, shape, a, a_strides, b, b_strides, b_f,
+                                b_i, out, out_strides, st, "eq");
+      case NTOPS_CMP_NE:
+        return launch_binary<T>(CmpF<NTOPS_CMP_NE, T>{}, ndim, shape, a, a_strides, b, b_strides, b_f,
+                                b_i, out, out_strides, st, "ne");
+      case NTOPS_CMP_GT:
+        return launch_binary<T>(CmpF<NTOPS_CMP_GT, T>{}, ndim, shape, a, a_strides, b, b_strides, b_f,
+                                b_i, out, out_strides, st, "gt");
+      case NTOPS_CMP_GE:
+        return launch_binary<T>(CmpF<NTOPS_CMP_GE, T>{}, ndim, shape, a, a_strides, b, b_strides, b_f,
+                                b_i, out, out_strides, st, "ge");
+      case NTOPS_CMP_LT:
+        return launch_binary<T>(CmpF<NTOPS_CMP_LT, T>{}, ndim, shape, a, a_strides, b, b_strides, b_f,
+                                b_i, out, out_strides, st, "lt");
+      default:
+        return launch_binary<T>(CmpF<NTOPS_CMP_LE, T>{}, ndim, shape, a, a_strides, b, b_strides, b_f,
+                                b_i, out, out_strides, st, "le");
+    }
+  });
+}
+
+extern "C" int ntops_classify(int op, int dtype, int ndim, const int64_t* shape, const void* x,
+                              const int64_t* x_strides, void* out, const int64_t* out_strides,
+                              void* stream) {
+  const char* what = "ntops_classify";
+  if (int e = check_common(what, ndim, shape, x, out)) return e;
+  if (op != NTOPS_CLASSIFY_ISINF && op != NTOPS_CLASSIFY_ISNAN)
+    return set_error(NTOPS_ERR_UNSUPPORTED, "%s: unknown op %d", what, op);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dispatch_all(dtype, what, [&](auto tag) {
+    using T = decltype(tag);
+    if (op == NTOPS_CLASSIFY_ISNAN)
+      return launch_unary<T>(ClassifyF<true>{}, ndim, shape, x, x_strides, out, out_strides, st, "isnan");
+    return launch_unary<T>(ClassifyF<false>{}, ndim, shape, x, x_strides, out, out_strides, st, "isinf");
+  });
+}
+
+extern "C" int ntops_clamp(int dtype, int ndim, const int64_t* shape, const void* x,
+                           const int64_t* x_strides, const void* lo, const int64_t* lo_strides,
+                           double lo_f, int64_t lo_i, int has_lo, const void* hi,
+                           const int64_t* hi_strides, double hi_f, int64_t hi_i, int has_hi,
+                           void* out, const int64_t* out_strides, void* stream) {
+  const char* what = "ntops_clamp";
+  if (int e = check_common(what, ndim, shape, x, out)) return e;
+  if (dtype == NTOPS_BOOL) return set_error(NTOPS_ERR_UNSUPPORTED, "clamp: bool tensors are not supported");
+  if (!has_lo && !has_hi) return set_error(NTOPS_ERR_INVALID, "clamp: at least one of min / max is required");
+  const bool lo_t = has_lo && lo != nullptr, hi_t = has_hi && hi != nullptr;
+  if ((lo_t && lo_strides == nullptr) || (hi_t && hi_strides == nullptr))
+    return set_error(NTOPS_ERR_INVALID, "clamp: null bound strides");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dispatch_all(dtype, "clamp", [&](auto tag) {
+    using T = decltype(tag);
+    // Scalar bounds rounded to T; an absent bound is the extreme value.
+    T lo_s, hi_s;
+    if constexpr (IsFloat<T>::v) {
+      lo_s = has_lo ? static_cast<T>(lo_f) : static_cast<T>(-__builtin_huge_val());
+      hi_s = has_hi ? static_cast<T>(hi_f) : static_cast<T>(__builtin_huge_val());
+    } else {
+      lo_s = has_lo ? static_cast<T>(lo_i) : std::numeric_limits<T>::lowest();
+      hi_s = has_hi ? static_cast<T>(hi_i) : std::numeric_limits<T>::max();
+    }
+    const T* xp = static_cast<const T*>(x);
+    const T* lp = static_cast<const T*>(lo);
+    const T* hp = static_cast<const T*>(hi);
+    T* yp = static_cast<T*>(out);
+    if (lo_t && hi_t)
+      return launch_clamp_t<T, true, true>(ndim, shape, xp, x_strides, lp, lo_strides, hp, hi_strides,
+                                           lo_s, hi_s, yp, out_strides, st);
+    if (lo_t)
+      return launch_clamp_t<T, true, false>(ndim, shape, xp, x_strides, lp, lo_strides, hp, hi_strides,
+                                            lo_s, hi_s, yp, out_strides, st);
+    if (hi_t)
+      return launch_clamp_t<T, false, true>(ndim, shape, xp, x_strides, lp, lo_strides, hp, hi_strides,
+                                            lo_s, hi_s, yp, out_strides, st);
+    return launch_unary<T>(ClampSF<T>{lo_s, hi_s}, ndim, shape, x, x_strides, out, out_strides, st,
+                           "clamp");
+  });
 }

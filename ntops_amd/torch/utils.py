@@ -166,24 +166,54 @@ def _is_number(x):
     return isinstance(x, (bool, int, float))
 
 
-def _binary(op, input, other, alpha, out, what):
-    """Shared body of add / mul / bitwise_and / bitwise_or with torch's
-    promotion (torch.result_type) and broadcasting rules."""
+def _split_other(input, other, what):
+    """(other, other_is_tensor, result_dtype) with torch's promotion rules; a
+    0-d CPU tensor `other` is treated as a Python number, as torch does."""
     if not isinstance(input, torch.Tensor):
         raise TypeError(f"{what}: input must be a tensor")
     if isinstance(other, torch.Tensor) and other.dim() == 0 and not other.is_cuda:
-        other_is_tensor = False
-        result_dtype = torch.result_type(input, other)
-        other = other.item()
-    elif isinstance(other, torch.Tensor):
-        other_is_tensor = True
-        result_dtype = torch.result_type(input, other)
-    elif _is_number(other):
-        other_is_tensor = False
-        result_dtype = torch.result_type(input, other)
-    else:
-        raise TypeError(f"{what}: unsupported operand {type(other)}")
+        return other.item(), False, torch.result_type(input, other)
+    if isinstance(other, torch.Tensor):
+        return other, True, torch.result_type(input, other)
+    if _is_number(other):
+        return other, False, torch.result_type(input, other)
+    raise TypeError(f"{what}: unsupported operand {type(other)}")
 
+
+def _scalar_parts(value):
+    """A Python number as the (double, int64) pair the C ABI takes."""
+    return float(value), (int(value) if not isinstance(value, float) else 0)
+
+
+def _launch2(entry, op, dtype, shape, a, other, other_is_tensor, res, what, alpha=(1.0, 1)):
+    """Calls ntops_binary (entry "binary") or ntops_compare ("compare") on
+    `a` (already of `dtype`, broadcast to `shape`) and `other` (a tensor of
+    `dtype` broadcast to `shape`, or a Python number)."""
+    lib = _lib.load()
+    if other_is_tensor:
+        b = other.expand(shape)
+        b_ptr, b_strides, b_f, b_i = b.data_ptr(), _strides(b), 0.0, 0
+    else:
+        b_ptr, b_strides = None, None
+        b_f, b_i = _scalar_parts(other)
+    head = (op, _lib.dtype_code(dtype), len(shape), _lib.i64_array(shape), a.data_ptr(), _strides(a),
+            b_ptr, b_strides, b_f, b_i)
+    tail = (res.data_ptr(), _strides(res), _lib.stream_of(res))
+    if entry == "binary":
+        rc = lib.ntops_binary(*head, alpha[0], alpha[1], *tail)
+    else:
+        rc = lib.ntops_compare(*head, *tail)
+    _lib.check(rc, what)
+
+
+def _binary(op, input, other, alpha, out, what, compute_dtype=None):
+    """Shared body of the binary arithmetic ops (add, sub, mul, div, pow,
+    bitwise_and / or) with torch's promotion (torch.result_type) and
+    broadcasting rules.  `compute_dtype` maps the promoted dtype to the one
+    the kernel runs in (true division promotes integers to float)."""
+    other, other_is_tensor, result_dtype = _split_other(input, other, what)
+    if compute_dtype is not None:
+        result_dtype = compute_dtype(result_dtype)
     dev = _lib.require_cuda(input, other if other_is_tensor else None)
     shape = torch.broadcast_shapes(input.shape, other.shape) if other_is_tensor else input.shape
     target, res = _prepare_out(out, shape, result_dtype, dev, like=input)
@@ -199,35 +229,41 @@ def _binary(op, input, other, alpha, out, what):
             )
         if result_dtype == torch.bool and not isinstance(alpha, bool):
             raise RuntimeError("Boolean alpha only supported for Boolean results.")
-        alpha_f, alpha_i = float(alpha), int(alpha) if not isinstance(alpha, float) else 0
+        alpha_f, alpha_i = _scalar_parts(alpha)
 
-    lib = _lib.load()
     with _DeviceGuard(dev):
-        if other_is_tensor:
-            b = _to_dtype(other, result_dtype).expand(shape)
-            b_ptr, b_strides, b_f, b_i = b.data_ptr(), _strides(b), 0.0, 0
-        else:
-            b_ptr, b_strides = None, None
-            b_f = float(other)
-            b_i = int(other) if not isinstance(other, float) else 0
-        rc = lib.ntops_binary(
-            op,
-            _lib.dtype_code(result_dtype),
-            len(shape),
-            _lib.i64_array(shape),
-            a.data_ptr(),
-            _strides(a),
-            b_ptr,
-            b_strides,
-            b_f,
-            b_i,
-            alpha_f,
-            alpha_i,
-            res.data_ptr(),
-            _strides(res),
-            _lib.stream_of(res),
-        )
-        _lib.check(rc, what)
+        b = _to_dtype(other, result_dtype) if other_is_tensor else other
+        _launch2("binary", op, result_dtype, shape, a, b, other_is_tensor, res, what, (alpha_f, alpha_i))
         if res is not target:
             _cast_into(res, target)
+    return target
+
+
+def _compare(op, input, other, out, what):
+    """eq / ne / gt / ge / lt / le: compares in the promoted dtype and returns
+    bool, like torch (the reference writes into a tensor of input's dtype)."""
+    other, other_is_tensor, common = _split_other(input, other, what)
+    dev = _lib.require_cuda(input, other if other_is_tensor else None)
+    shape = torch.broadcast_shapes(input.shape, other.shape) if other_is_tensor else input.shape
+    target, res = _prepare_out(out, shape, torch.bool, dev)
+    a = _to_dtype(input, common).expand(shape)
+    with _DeviceGuard(dev):
+        b = _to_dtype(other, common) if other_is_tensor else other
+        _launch2("compare", op, common, shape, a, b, other_is_tensor, res, what)
+        if res is not target:
+            _cast_into(res, target)
+    return target
+
+
+def _float_unary(op, input, out, what):
+    """Unary floating op (sigmoid, tanh, rsqrt, sin, cos, exp): integer and
+    bool inputs are promoted to the default floating dtype first, as torch
+    does."""
+    dev = _lib.require_cuda(input)
+    dtype = input.dtype if input.dtype.is_floating_point else torch.get_default_dtype()
+    x = _to_dtype(input, dtype)
+    target, res = _prepare_out(out, input.shape, dtype, dev, like=x)
+    _unary(op, x, res, what)
+    if res is not target:
+        _cast_into(res, target)
     return target

@@ -219,6 +219,307 @@ def bitwise_or(a, b, dt):
     return np.bitwise_or(np.asarray(a), np.asarray(b)).astype(np_dtype(dt))
 
 
+# ------------------------------------------- rest of the elementwise family
+
+
+def _is_number(b):
+    return isinstance(b, (bool, int, float, np.integer, np.floating))
+
+
+def _sign_bits(x, dt):
+    """Unsigned view of a float array's storage and its sign-bit mask."""
+    if dt == "bf16":
+        return np.asarray(x, dtype=np.uint16), np.uint16(0x8000)
+    if dt == "f16":
+        return np.asarray(x, dtype=np.float16).view(np.uint16), np.uint16(0x8000)
+    if dt == "f32":
+        return np.asarray(x, dtype=np.float32).view(np.uint32), np.uint32(0x80000000)
+    return np.asarray(x, dtype=np.float64).view(np.uint64), np.uint64(0x8000000000000000)
+
+
+def _from_bits(u, dt):
+    if dt == "bf16":
+        return u.astype(np.uint16)
+    return u.view({"f16": np.float16, "f32": np.float32, "f64": np.float64}[dt])
+
+
+@_with_errstate
+def relu(x, dt):
+    """kernels/relu.py:9 -- max(0, x) as torch's clamp_min: x where x is not
+    below 0 (so NaN and -0 pass through), else +0."""
+    if dt in FLOAT_DTYPES:
+        c = to_compute(x, dt)
+        zero = round_to(np.zeros_like(c), dt)
+        return np.where(c < 0, zero, np.asarray(x))
+    if dt == "bool":
+        raise ValueError("relu: bool")
+    x = np.asarray(x)
+    return np.where(x < 0, np.zeros_like(x), x)
+
+
+@_with_errstate
+def sigmoid(x, dt):
+    """kernels/sigmoid.py:10 -- 1 / (1 + exp(-x)) in opmath, one rounding."""
+    c = to_compute(x, dt)
+    one = compute_type(dt)(1)
+    return round_to(one / (one + np.exp(-c)), dt)
+
+
+@_with_errstate
+def tanh(x, dt):
+    """kernels/tanh.py:10-13 -- tanh(x) in opmath, one rounding.  The reference
+    writes (e^x - e^-x) / (e^x + e^-x), which is NaN once e^x overflows
+    (|x| > 88 in fp32); the library tanh is the function torch evaluates."""
+    return round_to(np.tanh(to_compute(x, dt)), dt)
+
+
+def neg(x, dt):
+    """kernels/neg.py:9 -- -x (sign bit flipped for floats, NaN included;
+    two's-complement wrap for integers)."""
+    if dt in FLOAT_DTYPES:
+        u, m = _sign_bits(x, dt)
+        return _from_bits(u ^ m, dt)
+    if dt == "bool":
+        raise ValueError("neg: bool")
+    with np.errstate(over="ignore"):
+        return _int_wrap(-np.asarray(x).astype(np.int64), dt)
+
+
+def abs(x, dt):  # noqa: A001 (mirrors the operator's name)
+    """kernels/abs.py:10 -- |x| (sign bit cleared for floats; the integer
+    minimum wraps to itself)."""
+    if dt in FLOAT_DTYPES:
+        u, m = _sign_bits(x, dt)
+        return _from_bits(u & ~m, dt)
+    if dt == "bool":
+        raise ValueError("abs: bool")
+    with np.errstate(over="ignore"):
+        return _int_wrap(np.abs(np.asarray(x).astype(np.int64)), dt)
+
+
+@_with_errstate
+def rsqrt(x, dt):
+    """kernels/rsqrt.py:10 -- 1 / sqrt(x): an IEEE square root, then an IEEE
+    division, in opmath (the form torch's CPU kernel evaluates)."""
+    c = to_compute(x, dt)
+    return round_to(compute_type(dt)(1) / np.sqrt(c), dt)
+
+
+@_with_errstate
+def sin(x, dt):
+    """kernels/sin.py:10 -- sin(x) in opmath, one rounding."""
+    return round_to(np.sin(to_compute(x, dt)), dt)
+
+
+@_with_errstate
+def cos(x, dt):
+    """kernels/cos.py:10 -- cos(x) in opmath, one rounding."""
+    return round_to(np.cos(to_compute(x, dt)), dt)
+
+
+def sub(a, b, dt, alpha=1):
+    """kernels/sub.py:10 -- input - alpha * other, evaluated as torch does:
+    add(input, other, -alpha) (same roundings as add)."""
+    if dt == "bool":
+        raise ValueError("sub: bool")
+    return add(a, b, dt, -alpha)
+
+
+def _opmath_operand(b, dt):
+    """A tensor operand in opmath, or a Python number kept in opmath."""
+    if _is_number(b):
+        return compute_type(dt)(b)
+    return to_compute(b, dt)
+
+
+@_with_errstate
+def floor_divide_float(a, b):
+    """Python's float floor division (CPython's float divmod), elementwise on
+    arrays of one float type: q = (a - fmod(a, b)) / b, minus one when the
+    remainder's sign differs from b's, then rounded to the nearest integer;
+    a zero quotient takes the sign of a / b; b == 0 gives a / b."""
+    a, b = np.broadcast_arrays(a, b)
+    T = a.dtype.type
+    mod = np.fmod(a, b)
+    div = (a - mod) / b
+    adj = (mod != 0) & ((b < 0) != (mod < 0))
+    div = np.where(adj, div - T(1), div)
+    fl = np.floor(div)
+    fl = np.where(div - fl > T(0.5), fl + T(1), fl)
+    res = np.where(div == 0, np.copysign(T(0), a / b), fl)
+    return np.where(b == 0, a / b, res).astype(a.dtype)
+
+
+def _int_divide(a, b, floor):
+    """Integer trunc / floor division in int64: 0 where b == 0 (torch's CPU
+    kernel raises instead), wrap-around negation where b == -1."""
+    a = np.asarray(a).astype(np.int64)
+    b = np.asarray(b).astype(np.int64)
+    a, b = np.broadcast_arrays(a, b)
+    safe = np.where(b == 0, 1, b)
+    q = np.abs(a) // np.abs(safe)  # magnitude of the truncated quotient
+    with np.errstate(over="ignore"):
+        q = np.where((a < 0) != (safe < 0), -q, q)
+        if floor:
+            q = np.where((q * safe != a) & ((a < 0) != (safe < 0)), q - 1, q)
+        q = np.where(b == -1, -a, q)
+    return np.where(b == 0, 0, q)
+
+
+@_with_errstate
+def div(a, b, dt, rounding_mode=None):
+    """kernels/div.py:9-18.  Floating, in opmath with one rounding: a / b,
+    trunc(a / b) (for two 16-bit tensors, of the quotient already rounded to
+    dt, as torch's CPU kernel evaluates it), or Python's floor division (the reference's floor(a / b)
+    differs when the rounded quotient lands on an integer; torch uses the
+    floor-division form).  A Python-number divisor stays in opmath.  Integer
+    dtypes: trunc / floor only (true division promotes to float first)."""
+    if dt in FLOAT_DTYPES:
+        ac, bc = to_compute(a, dt), _opmath_operand(b, dt)
+        if rounding_mode is None:
+            q = ac / bc
+        elif rounding_mode == "trunc":
+            # torch rounds a 16-bit tensor / tensor quotient to dt first; a
+            # Python-number divisor truncates the opmath quotient
+            q = np.trunc(ac / bc if _is_number(b) else rnd(ac / bc, dt))
+        else:
+            q = floor_divide_float(ac, np.asarray(bc, dtype=ac.dtype))
+        return round_to(q, dt)
+    if dt == "bool" or rounding_mode is None:
+        raise ValueError("div: integer true division promotes to float first")
+    return _int_wrap(_int_divide(a, b, rounding_mode == "floor"), dt)
+
+
+def _int_pow(a, e):
+    """Integer power with wrap-around; negative exponents follow torch: base 1
+    -> 1, base -1 -> +-1 by parity, anything else -> 0."""
+    a = np.asarray(a).astype(np.int64)
+    e = np.asarray(e).astype(np.int64)
+    a, e = np.broadcast_arrays(a, e)
+    r = np.ones(a.shape, dtype=np.uint64)
+    base = a.astype(np.uint64)
+    ee = np.where(e < 0, 0, e)
+    with np.errstate(over="ignore"):
+        while np.any(ee):
+            r = np.where(ee & 1, r * base, r)
+            base = base * base
+            ee = ee >> 1
+    r = r.astype(np.int64)
+    neg = np.where(a == 1, 1, np.where(a == -1, np.where(e & 1, -1, 1), 0))
+    return np.where(e < 0, neg, r)
+
+
+@_with_errstate
+def pow(a, b, dt):  # noqa: A001
+    """kernels/pow.py:10 -- a ** b.  Floating tensor ** tensor: the library
+    pow in opmath, one rounding.  A Python-number exponent follows torch's CPU
+    dispatch per dtype: f32 / f64 keep the exponent in double and evaluate
+    0.5 -> sqrt, -0.5 -> 1/sqrt, -1 -> 1/x, 2 -> x*x, 3 -> x*x*x,
+    -2 -> 1/(x*x), anything else -> pow in double, rounded once; bf16 rounds
+    the exponent to bf16, has the same special cases with every product
+    rounded to bf16, else powf; f16 rounds the exponent to f16 and always uses
+    powf.  Integers: see _int_pow."""
+    if dt not in FLOAT_DTYPES:
+        if dt == "bool":
+            raise ValueError("pow: bool")
+        return _int_wrap(_int_pow(a, b), dt)
+    ac = to_compute(a, dt)
+    T = compute_type(dt)
+    if not _is_number(b):
+        return round_to(np.power(ac, to_compute(b, dt)), dt)
+    if dt in ("f32", "f64"):
+        e = float(b)
+    else:
+        e = float(to_compute(round_to(np.asarray([float(b)], dtype=np.float32), dt), dt)[0])
+    one = T(1)
+    if dt != "f16":
+        r = lambda v: rnd(v, dt) if dt == "bf16" else v  # noqa: E731 (bf16: round each product)
+        special = {0.5: np.sqrt, -0.5: lambda x: one / np.sqrt(x), -1.0: lambda x: one / x,
+                   2.0: lambda x: x * x, 3.0: lambda x: r(x * x) * x, -2.0: lambda x: one / r(x * x)}
+        if e in special:
+            return round_to(special[e](ac), dt)
+    if dt == "f32":
+        return round_to(np.power(ac.astype(np.float64), e), dt)
+    return round_to(np.power(ac, T(e)), dt)
+
+
+_CMP = {"eq": np.equal, "ne": np.not_equal, "gt": np.greater, "ge": np.greater_equal,
+        "lt": np.less, "le": np.less_equal}
+
+
+@_with_errstate
+def compare(op, a, b, dt):
+    """kernels/{eq,ne,gt,ge,lt,le}.py:9 -> bool, compared in dt's opmath (exact
+    for the 16-bit floats); a Python-number b is first rounded to dt (the
+    common dtype, as in torch); integers compare as int64."""
+    f = _CMP[op]
+    if dt in FLOAT_DTYPES:
+        ac = to_compute(a, dt)
+        if _is_number(b):
+            bc = to_compute(round_to(np.asarray(float(b), dtype=compute_type(dt)), dt), dt)
+        else:
+            bc = to_compute(b, dt)
+        return f(ac, bc)
+    return f(np.asarray(a).astype(np.int64), np.asarray(b).astype(np.int64))
+
+
+def isinf(x, dt):
+    """kernels/isinf.py:9-11 -> bool (false for integer inputs)."""
+    if dt in FLOAT_DTYPES:
+        return np.isinf(to_compute(x, dt))
+    return np.zeros(np.shape(x), dtype=bool)
+
+
+def isnan(x, dt):
+    """kernels/isnan.py:9 -- x != x -> bool (false for integer inputs)."""
+    if dt in FLOAT_DTYPES:
+        c = to_compute(x, dt)
+        return c != c
+    return np.zeros(np.shape(x), dtype=bool)
+
+
+@_with_errstate
+def clamp(x, lo, hi, dt):
+    """kernels/clamp.py:9 -- min(max(x, lo), hi) with torch's NaN rule: a NaN
+    in x, then in lo, then in hi, is the result (so lo > hi gives hi).  lo /
+    hi are arrays of dt, Python numbers (rounded to dt) or None (absent)."""
+    x = np.asarray(x)
+
+    def bound(v):
+        if v is None:
+            return None
+        if _is_number(v):
+            if dt in FLOAT_DTYPES:
+                return np.broadcast_to(round_to(np.asarray(float(v), dtype=compute_type(dt)), dt), x.shape)
+            return np.broadcast_to(np.asarray(v).astype(np_dtype(dt)), x.shape)
+        return np.broadcast_to(np.asarray(v), x.shape)
+
+    lo, hi = bound(lo), bound(hi)
+    if dt in FLOAT_DTYPES:
+        val = lambda v: to_compute(v, dt)  # noqa: E731
+        xv = val(x)
+        r = x.copy()
+        rv = xv
+        if lo is not None:
+            lv = val(lo)
+            r = np.where(rv < lv, lo, r)
+            rv = val(r)
+        if hi is not None:
+            hv = val(hi)
+            r = np.where(hv < rv, hi, r)
+        if hi is not None:
+            r = np.where(hv != hv, hi, r)
+        if lo is not None:
+            r = np.where(lv != lv, lo, r)
+        return np.where(xv != xv, x, r).astype(x.dtype)
+    r = x.copy()
+    if lo is not None:
+        r = np.where(r < lo, lo, r)
+    if hi is not None:
+        r = np.where(hi < r, hi, r)
+    return r.astype(x.dtype)
+
+
 # --------------------------------------------------------- row reductions -
 
 
