@@ -151,6 +151,7 @@ KERNEL_OF = {
     "mm": "k_gemm_mfma",
     "addmm": "k_gemm_mfma",
     "bmm": "k_gemm_panel",
+    "sdpa": "k_flash_fwd",
 }
 
 
@@ -451,6 +452,32 @@ def make_workloads():
     W.append(Workload("bmm", "bmm bf16 32 x (2048 x 128).(128 x 2048), fp32 accumulate", "GB/s", "hbm",
                       (BB * BM * BK + BB * BK * BN + BB * BM * BN) * 2, 1, bmm_build, bmm_step, bmm_cpu, "bf16"))
     W[-1].flops = 2 * BB * BM * BN * BK
+
+    # scaled_dot_product_attention bf16 causal, (4, 32, 2048, 128): the
+    # algorithmic flops are those of the unmasked (q, kv) pairs, S (S + 1) / 2
+    # per head, each costing 2 D for Q K^T and 2 D for P V
+    AB, AH, AS, AD = 4, 32, 2048, 128
+    sdpa = ntops_amd.torch.scaled_dot_product_attention
+
+    def sdpa_build(i):
+        g = _gen(600 + i)
+        q, k, v = (torch.randn(AB, AH, AS, AD, device="cuda", generator=g).bfloat16() for _ in range(3))
+        return {"q": q, "k": k, "v": v}
+
+    def sdpa_step(s):
+        sdpa(s["q"], s["k"], s["v"], is_causal=True)
+
+    def sdpa_cpu():
+        g = _cpu_gen()
+        q, k, v = (torch.randn(AB, AH, AS, AD, generator=g).bfloat16() for _ in range(3))
+        return (lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True)), \
+            4 * AB * AH * AD * AS * (AS + 1) // 2, \
+            "torch scaled_dot_product_attention bf16 causal (4, 32, 2048, 128) = the whole workload"
+
+    W.append(Workload("sdpa", "scaled_dot_product_attention bf16 causal (4, 32, 2048, 128), fp32 softmax",
+                      "TFLOP/s", "mfma", 4 * AB * AH * AD * AS * (AS + 1) // 2, 1, sdpa_build, sdpa_step,
+                      sdpa_cpu, "bf16"))
+    W[-1].bytes = 4 * AB * AH * AS * AD * 2
     return {w.name: w for w in W}
 
 

@@ -30,6 +30,8 @@
  *   ntops_softmax     <- src/ntops/torch/softmax.py:7-16, kernels/softmax.py:9-29
  *   ntops_rope        <- src/ntops/torch/rotary_position_embedding.py:7-29,
  *                        kernels/rotary_position_embedding.py:6-47
+ *   ntops_sdpa        <- src/ntops/torch/scaled_dot_product_attention.py:10-108,
+ *                        kernels/scaled_dot_product_attention.py:154-201
  *   ntops_gemm        <- src/ntops/torch/{mm,bmm,addmm}.py:7-18,
  *                        kernels/mm.py:54-65, kernels/bmm.py:8-43,
  *                        kernels/addmm.py:64-67
@@ -236,6 +238,26 @@ NTOPS_API int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_t
                const void* B, const int64_t* b_strides,
                const void* C, const int64_t* c_strides,
                double alpha, double beta,
+               void* out, const int64_t* out_strides, void* stream);
+
+/* ---- attention ---------------------------------------------------------- */
+/* out = softmax(q k^T * scale + mask) v for q (B, Hq, Sq, D), k and v
+ * (B, Hkv, Skv, D), out (B, Hq, Sq, D); each tensor is described by its 4
+ * element strides.  Query head h attends key / value head h / (Hq / Hkv)
+ * (GQA; Hq % Hkv == 0).  mask (may be NULL) is broadcast by its 4 strides
+ * (0 = broadcast) over (B, Hq, Sq, Skv): mask_dtype BOOL (true = attend) or
+ * F32 / F16 / BF16 (added to the scaled scores).  causal: 0 none, 1
+ * upper-left (key j visible to query i when j <= i), 2 lower-right
+ * (j <= i + Skv - Sq); mask and causal are exclusive.  dtype in {F32, F16,
+ * BF16}; fp32 accumulation, the probabilities rounded to dtype for the
+ * product with v (16-bit dtypes).  A row with every key masked yields 0.
+ * D <= 256. */
+NTOPS_API int ntops_sdpa(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv,
+               int64_t D, const void* q, const int64_t* q_strides,
+               const void* k, const int64_t* k_strides,
+               const void* v, const int64_t* v_strides,
+               const void* mask, int mask_dtype, const int64_t* mask_strides,
+               int causal, double scale,
                void* out, const int64_t* out_strides, void* stream);
 
 #ifdef __cplusplus

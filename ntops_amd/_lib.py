@@ -71,6 +71,11 @@ _SIGNATURES = {
         _i,
         [_i, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _vp, _i64, _i64, _i, _vp, _c_i64p, _vp],
     ),
+    "ntops_sdpa": (
+        _i,
+        [_i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _i, _c_i64p,
+         _i, _d, _vp, _c_i64p, _vp],
+    ),
     "ntops_gemm": (
         _i,
         [_i, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _d, _vp, _c_i64p, _vp],

@@ -1,0 +1,440 @@
+// scaled_dot_product_attention forward:  O = softmax(Q K^T * scale + M) V.
+//
+// Reference: kernels/scaled_dot_product_attention.py:154-201 (an online
+// softmax over key blocks in base 2: running max, exp2 of the shifted
+// scores, rescaled accumulator; P cast to the value dtype for P @ V; the
+// final O / l), torch/scaled_dot_product_attention.py:10-108 (GQA head
+// mapping, bool masks as 0 / -inf, default scale 1 / sqrt(D), the two causal
+// variants).  Rows whose every score is masked produce 0, as torch's CPU
+// kernel does (the reference would produce NaN).
+//
+// MFMA path (bf16 / f16, head dim 64 or 128, unit stride along D):
+//  * one 4-wave workgroup per (batch, head, 128 query rows); wave w owns 32
+//    rows and keeps their Q fragments in VGPRs for the whole kernel;
+//  * key / value tiles of 64 rows are double-buffered in LDS (the next
+//    tile's global loads are in flight while the current one is used; one
+//    barrier per tile).  K is stored [kv][d] and read as the B operand of
+//    S = Q K^T with ds_read_b128; V is stored [kv][d] and read as the B
+//    operand of O += P V with ds_read_b64_tr_b16 (transposing reads); both
+//    layouts are XOR-swizzled so every fragment read is bank-conflict free;
+//  * S (32 x 64 per wave, fp32) is scaled into the base-2 domain
+//    (scale * log2 e), masked, and folded into the running (max, sum) of each
+//    row: lane l holds row (l & 31) and half of its columns, the other half is
+//    in lane l ^ 32, so a row reduction is an in-lane reduction plus one
+//    exchange.  exp2 is the hardware v_exp_f32;
+//  * P goes from the S accumulators straight into MFMA A operands (rounded to
+//    T): the accumulator layout gives lane l the key columns {0-3, 8-11} of
+//    each 16-key slice (lane l ^ 32 the others), and V's fragments are read in
+//    that same key order, so no cross-lane shuffle is needed;
+//  * blocks are mapped XCD-aware (each XCD walks whole heads, so a head's K
+//    and V stay in one L2) and, under a causal mask, the longest query blocks
+//    of a head start first.
+// Generic path (fp32, other head dims up to 256, any strides): one wave per
+// query row, lanes split D, fp32 throughout.
+#include "mfma.h"
+
+namespace ntops {
+namespace {
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* mask;
+  void* o;
+  int64_t qs[4], ks[4], vs[4], ms[4], os[4];
+  int B, Hq, Hkv, Sq, Skv, D;
+  int mask_dtype;    // -1: none; NTOPS_BOOL (true = attend), NTOPS_F32 / F16 / BF16 (additive)
+  int causal;        // 0: none, 1: upper-left (kv <= q), 2: lower-right (kv <= q + Skv - Sq)
+  float scale_log2;  // scale * log2(e)
+};
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_huge_valf(); }
+
+// Additive mask value at element offset `off`, in the base-2 domain.
+__device__ __forceinline__ float mask_log2(const AttnArgs& a, int64_t off) {
+  switch (a.mask_dtype) {
+    case NTOPS_BOOL:
+      return static_cast<const bool*>(a.mask)[off] ? 0.f : neg_inf();
+    case NTOPS_F32:
+      return static_cast<const float*>(a.mask)[off] * kLog2e;
+    case NTOPS_F16:
+      return static_cast<float>(static_cast<const _Float16*>(a.mask)[off]) * kLog2e;
+    default:
+      return static_cast<float>(static_cast<const __bf16*>(a.mask)[off]) * kLog2e;
+  }
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Chunk slot of 16-byte chunk c of key row r in the V tile ([kv][d] with
+// D / 8 chunks per row), conflict-free for the transposing fragment reads.
+template <int D>
+__device__ __forceinline__ int vslot(int r, int c) {
+  if constexpr (D == 128)
+    return mnslot(r, c);
+  else
+    return c ^ (((r >> 1) & 1) << 2);
+}
+
+// B fragment of S = Q K^T: key rows n0 .. n0 + 31 (lane l: row n0 + (l & 31)),
+// d = 16 ks + 8 (l >> 5) .. + 7.
+template <int D>
+__device__ __forceinline__ u32x4 k_frag(const char* tile, int n0, int ks, int lane) {
+  const int r = n0 + (lane & 31);
+  const int c = ks * 2 + (lane >> 5);
+  return *reinterpret_cast<const u32x4*>(tile + r * (D * 2) + kslot<D>(r, c) * 16);
+}
+
+// B fragment of O += P V for the 16-key slice sl and output columns
+// n0 .. n0 + 31: lane l receives column n0 + (l & 31) at keys
+// 16 sl + 4 (l >> 5) + 0..3 (elements 0..3) and 16 sl + 8 + 4 (l >> 5) + 0..3
+// (elements 4..7) -- the key order in which the S accumulator holds P.
+template <int D>
+__device__ __forceinline__ u32x4 v_frag(const char* tile, int n0, int sl, int lane) {
+  const int i = lane & 15;
+  const int n = n0 + ((lane >> 4) & 1) * 16 + (i & 3) * 4;
+  const int c = n >> 3, half = (n >> 2) & 1;
+  s16x4 v[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int k = sl * 16 + h * 8 + (lane >> 5) * 4 + (i >> 2);
+    const char* p = tile + k * (D * 2) + vslot<D>(k, c) * 16 + half * 8;
+    v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p));
+  }
+  u32x4 r;
+  r.x = static_cast<uint16_t>(v[0][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][1])) << 16);
+  r.y = static_cast<uint16_t>(v[0][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][3])) << 16);
+  r.z = static_cast<uint16_t>(v[1][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][1])) << 16);
+  r.w = static_cast<uint16_t>(v[1][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][3])) << 16);
+  return r;
+}
+
+// Maps a workgroup id to (batch * heads index, query block): XCD-aware
+// (workgroups are dispatched round-robin over the 8 XCDs; each XCD gets a
+// contiguous range of (batch, head, query block)), longest causal query
+// blocks first within a head.
+__device__ __forceinline__ void attn_block(int pid, int total, int nqb, int& bh, int& qb) {
+  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+  bh = pid / nqb;
+  qb = nqb - 1 - (pid - bh * nqb);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int total) {
+  constexpr int BM = 128, BN = 64;
+  constexpr int KS = D / 16;   // k-steps of S = Q K^T
+  constexpr int DT = D / 32;   // 32-column tiles of O
+  constexpr int CPR = D / 8;   // 16-byte chunks per K / V row
+  constexpr int CH = BN * CPR / 256;  // chunks per thread per tile
+  constexpr int kTile = BN * D * 2;   // bytes of one K or V tile
+  static_assert(CH * 256 == BN * CPR, "tile must split evenly over the threads");
+  __shared__ __attribute__((aligned(16))) char smem[2 * 2 * kTile];  // [stage][K, V]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int bh, qb;
+  attn_block(blockIdx.x, total, nqb, bh, qb);
+  const int b = bh / a.Hq, h = bh - b * a.Hq;
+  const int hk = h / (a.Hq / a.Hkv);
+  const int q0 = qb * BM;
+  const int qw = q0 + wave * 32;
+  const int my_q = qw + (lane & 31);
+  const int off = a.causal == 2 ? a.Skv - a.Sq : 0;
+  const T* Q = static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const T* K = static_cast<const T*>(a.k) + b * a.ks[0] + hk * a.ks[1];
+  const T* V = static_cast<const T*>(a.v) + b * a.vs[0] + hk * a.vs[1];
+
+  // Q fragments (A operand of S): row my_q, d = 16 ks + 8 (lane >> 5) .. + 7.
+  u32x4 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (my_q < a.Sq)
+      qf[ks] = *reinterpret_cast<const u32x4*>(Q + my_q * a.qs[2] + ks * 16 + 8 * (lane >> 5));
+    else
+      qf[ks] = u32x4{0, 0, 0, 0};
+  }
+
+  int kv_end = a.Skv;
+  if (a.causal) kv_end = max(0, min(a.Skv, q0 + BM + off));
+  const int nkv = (kv_end + BN - 1) / BN;
+
+  u32x4 kr[CH], vr[CH];
+  auto gload = [&](int j) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int ci = threadIdx.x + 256 * u;
+      const int row = ci / CPR, c = ci - row * CPR;
+      const int kv = j * BN + row;
+      if (kv < a.Skv) {
+        kr[u] = *reinterpret_cast<const u32x4*>(K + kv * a.ks[2] + c * 8);
+        vr[u] = *reinterpret_cast<const u32x4*>(V + kv * a.vs[2] + c * 8);
+      } else {
+        // keys past the end are masked; zero values keep 0 * V finite
+        kr[u] = u32x4{0, 0, 0, 0};
+        vr[u] = u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto swrite = [&](int stage) {
+    char* sk = smem + stage * 2 * kTile;
+    char* sv = sk + kTile;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int ci = threadIdx.x + 256 * u;
+      const int row = ci / CPR, c = ci - row * CPR;
+      *reinterpret_cast<u32x4*>(sk + row * (D * 2) + kslot<D>(row, c) * 16) = kr[u];
+      *reinterpret_cast<u32x4*>(sv + row * (D * 2) + vslot<D>(row, c) * 16) = vr[u];
+    }
+  };
+
+  f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
+  float m_i = neg_inf(), l_i = 0.f;  // running max (base 2) and sum of row my_q
+
+  if (nkv > 0) {
+    gload(0);
+    swrite(0);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < nkv; ++j) {
+    const int cur = j & 1;
+    if (j + 1 < nkv) gload(j + 1);
+    const char* sk = smem + cur * 2 * kTile;
+    const char* sv = sk + kTile;
+
+    // S = Q K^T for this wave's 32 rows x 64 keys (two 32x32 tiles)
+    f32x16 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[t][e] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) s[t] = mfma32<T>(k_frag<D>(sk, t * 32, ks, lane), qf[ks], s[t]);
+
+    // base-2 scores with masking; element 4q + e of tile t is key
+    // kv0 + 32 t + 8 q + 4 (lane >> 5) + e
+    const int kv0 = j * BN;
+    const bool full = kv0 + BN <= a.Skv && a.mask_dtype < 0 &&
+                      (a.causal == 0 || kv0 + BN - 1 <= qw + off);
+    float x[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[t][e] = s[t][e] * a.scale_log2;
+    if (!full) {
+      const int64_t mrow = b * a.ms[0] + h * a.ms[1] + static_cast<int64_t>(my_q) * a.ms[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kv = kv0 + 32 * t + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          bool ok = kv < a.Skv && my_q < a.Sq;
+          if (a.causal) ok = ok && kv <= my_q + off;
+          float val = ok ? x[t][e] : neg_inf();
+          if (ok && a.mask_dtype >= 0) val += mask_log2(a, mrow + kv * a.ms[3]);
+          x[t][e] = val;
+        }
+    }
+
+    // online softmax of row my_q (lanes l and l ^ 32 hold its two halves)
+    float mx = neg_inf();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, x[t][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_i, mx);
+    const float m_use = m_new == neg_inf() ? 0.f : m_new;  // fully masked so far: keep P = 0
+    const float alpha = fast_exp2(m_i - m_use);
+    float rs = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        x[t][e] = fast_exp2(x[t][e] - m_use);
+        rs += x[t][e];
+      }
+    rs += __shfl_xor(rs, 32, 64);
+    l_i = l_i * alpha + rs;
+    m_i = m_new;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
+
+    // O += P V over the four 16-key slices
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) {
+      const u32x4 pf = pack8<T>(&x[sl >> 1][8 * (sl & 1)]);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) o[t] = mfma32<T>(v_frag<D>(sv, t * 32, sl, lane), pf, o[t]);
+    }
+
+    // the other stage was last read in the previous iteration, before the
+    // barrier that ended it
+    if (j + 1 < nkv) swrite(cur ^ 1);
+    __syncthreads();
+  }
+
+  if (my_q >= a.Sq) return;
+  const float inv = l_i > 0.f ? 1.f / l_i : 0.f;
+  T* O = static_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(my_q) * a.os[2];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      T v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
+      *reinterpret_cast<u32x2*>(O + t * 32 + 8 * qq + 4 * (lane >> 5)) = __builtin_bit_cast(u32x2, v4);
+    }
+}
+
+// Generic path: one wave per (batch, head, query row); lane owns d = lane +
+// 64 u.  fp32 arithmetic throughout (accurate exp2).
+template <typename T>
+__global__ __launch_bounds__(64) void k_attn_generic(AttnArgs a) {
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;  // (b, h, q) linear
+  const int q = static_cast<int>(row % a.Sq);
+  const int64_t bh = row / a.Sq;
+  const int h = static_cast<int>(bh % a.Hq);
+  const int b = static_cast<int>(bh / a.Hq);
+  const int hk = h / (a.Hq / a.Hkv);
+  const T* Q = static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1] + q * a.qs[2];
+  const T* K = static_cast<const T*>(a.k) + b * a.ks[0] + hk * a.ks[1];
+  const T* V = static_cast<const T*>(a.v) + b * a.vs[0] + hk * a.vs[1];
+  float qv[4], acc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int d = lane + 64 * u;
+    qv[u] = d < a.D ? static_cast<float>(Q[d * a.qs[3]]) * a.scale_log2 : 0.f;
+    acc[u] = 0.f;
+  }
+  const int off = a.causal == 2 ? a.Skv - a.Sq : 0;
+  int kv_end = a.Skv;
+  if (a.causal) kv_end = max(0, min(a.Skv, q + off + 1));
+  const int64_t mrow = b * a.ms[0] + h * a.ms[1] + static_cast<int64_t>(q) * a.ms[2];
+  float m = neg_inf(), l = 0.f;
+  for (int kv = 0; kv < kv_end; ++kv) {
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int d = lane + 64 * u;
+      if (d < a.D) s += qv[u] * static_cast<float>(K[kv * a.ks[2] + d * a.ks[3]]);
+    }
+    s = wave_sum(s);
+    if (a.mask_dtype >= 0) s += mask_log2(a, mrow + kv * a.ms[3]);
+    if (s == neg_inf()) continue;  // wave-uniform
+    const float m_new = fmaxf(m, s);
+    const float alpha = exp2f(m - m_new);
+    const float p = exp2f(s - m_new);
+    l = l * alpha + p;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int d = lane + 64 * u;
+      const float vv = d < a.D ? static_cast<float>(V[kv * a.vs[2] + d * a.vs[3]]) : 0.f;
+      acc[u] = acc[u] * alpha + p * vv;
+    }
+    m = m_new;
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* O = static_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + q * a.os[2];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int d = lane + 64 * u;
+    if (d < a.D) O[d * a.os[3]] = static_cast<T>(acc[u] * inv);
+  }
+}
+
+template <typename T>
+int run_attention(const AttnArgs& a, hipStream_t st) {
+  const auto unit_d = [&](const int64_t* s) { return s[3] == 1 && s[2] % 8 == 0 && s[1] % 8 == 0 && s[0] % 8 == 0; };
+  const bool mfma = !std::is_same<T, float>::value && (a.D == 64 || a.D == 128) && unit_d(a.qs) &&
+                    unit_d(a.ks) && unit_d(a.vs) && a.os[3] == 1 && a.os[2] % 4 == 0 &&
+                    a.os[1] % 4 == 0 && a.os[0] % 4 == 0 && aligned16(a.q) && aligned16(a.k) &&
+                    aligned16(a.v) && (reinterpret_cast<uintptr_t>(a.o) & 7u) == 0;
+  if constexpr (!std::is_same<T, float>::value) {
+    if (mfma) {
+      const int nqb = (a.Sq + 127) / 128;
+      const int64_t total = static_cast<int64_t>(nqb) * a.Hq * a.B;
+      if (total > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many blocks");
+      if (a.D == 128)
+        hipLaunchKernelGGL((k_flash_fwd<T, 128>), dim3(static_cast<unsigned>(total)), dim3(256), 0, st, a,
+                           nqb, static_cast<int>(total));
+      else
+        hipLaunchKernelGGL((k_flash_fwd<T, 64>), dim3(static_cast<unsigned>(total)), dim3(256), 0, st, a,
+                           nqb, static_cast<int>(total));
+      return check_launch("sdpa");
+    }
+  }
+  const int64_t rows = static_cast<int64_t>(a.B) * a.Hq * a.Sq;
+  if (rows > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many rows");
+  hipLaunchKernelGGL((k_attn_generic<T>), dim3(static_cast<unsigned>(rows)), dim3(64), 0, st, a);
+  return check_launch("sdpa");
+}
+
+}  // namespace
+}  // namespace ntops
+
+using namespace ntops;
+
+extern "C" int ntops_sdpa(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv,
+                          int64_t D, const void* q, const int64_t* q_strides, const void* k,
+                          const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                          const void* mask, int mask_dtype, const int64_t* mask_strides, int causal,
+                          double scale, void* out, const int64_t* out_strides, void* stream) {
+  if (B < 0 || Hq < 0 || Hkv < 0 || Sq < 0 || Skv < 0 || D < 0)
+    return set_error(NTOPS_ERR_INVALID, "sdpa: negative size");
+  if (B > 0x7fffffffLL || Hq > 0x7fffffffLL || Sq > 0x7fffffffLL || Skv > 0x7fffffffLL)
+    return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: size exceeds int32");
+  if (D > 256) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: head dim %lld > 256", (long long)D);
+  if (causal < 0 || causal > 2) return set_error(NTOPS_ERR_INVALID, "sdpa: bad causal mode %d", causal);
+  if (causal && mask) return set_error(NTOPS_ERR_INVALID, "sdpa: a mask and a causal mode together");
+  if (mask && mask_dtype != NTOPS_BOOL && mask_dtype != NTOPS_F32 && mask_dtype != NTOPS_F16 &&
+      mask_dtype != NTOPS_BF16)
+    return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: mask dtype %d", mask_dtype);
+  if (B == 0 || Hq == 0 || Sq == 0 || D == 0) return NTOPS_OK;
+  if (Hkv == 0 || Hq % Hkv != 0)
+    return set_error(NTOPS_ERR_INVALID, "sdpa: query heads %lld not a multiple of key heads %lld",
+                     (long long)Hq, (long long)Hkv);
+  if (!q || !out || !q_strides || !k_strides || !v_strides || !out_strides || (Skv > 0 && (!k || !v)) ||
+      (mask && !mask_strides))
+    return set_error(NTOPS_ERR_INVALID, "sdpa: null pointer");
+  AttnArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.mask = mask;
+  a.o = out;
+  for (int i = 0; i < 4; ++i) {
+    a.qs[i] = q_strides[i];
+    a.ks[i] = k_strides[i];
+    a.vs[i] = v_strides[i];
+    a.ms[i] = mask ? mask_strides[i] : 0;
+    a.os[i] = out_strides[i];
+  }
+  a.B = static_cast<int>(B);
+  a.Hq = static_cast<int>(Hq);
+  a.Hkv = static_cast<int>(Hkv);
+  a.Sq = static_cast<int>(Sq);
+  a.Skv = static_cast<int>(Skv);
+  a.D = static_cast<int>(D);
+  a.mask_dtype = mask ? mask_dtype : -1;
+  a.causal = causal;
+  a.scale_log2 = static_cast<float>(scale * 1.4426950408889634);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dispatch_float16_32(dtype, "sdpa", [&](auto tag) {
+    using T = decltype(tag);
+    return run_attention<T>(a, st);
+  });
+}

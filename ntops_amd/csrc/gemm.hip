@@ -39,28 +39,10 @@
 //    offset past the resource's extent and read as zero.
 // Generic path (fp32, or any other strides): 64x64 LDS-tiled FMA kernel with
 // fp32 accumulation (IEEE; gfx950 has no reduced-precision fp32 MFMA input).
-#include "dispatch.h"
+#include "mfma.h"
 
 namespace ntops {
 namespace {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
-
-template <typename T>
-__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
-  if constexpr (std::is_same<T, __bf16>::value)
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
 
 struct GemmArgs {
   const void* A;
@@ -79,33 +61,6 @@ struct GemmArgs {
 
 constexpr uint32_t kOOB = 0x80000000u;  // past every resource extent (< 2 GiB)
 
-// Chunk slot of 16-byte chunk `c` of row `r` in a K-major tile whose rows
-// hold BK k values (BK / 8 chunks); conflict-free for the fragment reads
-// (16 lanes per pass, rows r .. r + 15).
-template <int BK>
-__device__ __forceinline__ int kslot(int r, int c) {
-  if constexpr (BK == 128)
-    return c ^ (r & 15);
-  else if constexpr (BK == 64)
-    return c ^ (((r >> 1) + (r >> 4)) & 7);
-  else
-    return c ^ ((r >> 2) & 3);
-}
-// Chunk slot of chunk `c` of k-row `k` in an M/N-major tile.
-__device__ __forceinline__ int mnslot(int k, int c) { return c ^ ((k & 3) << 2); }
-
-// s_waitcnt with only the vector-memory counter constrained (<= n).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
-}
-
-// s_waitcnt lgkmcnt(0) (LDS reads returned), other counters unconstrained.
-__device__ __forceinline__ void wait_lgkmcnt0() {
-  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
-}
-
 // Waits until at most `younger` tiles' worth of this wave's DMA loads
 // (loads_per_tile each) are still in flight.
 __device__ __forceinline__ void wait_tile(int younger, int loads_per_tile) {
@@ -122,14 +77,6 @@ __device__ __forceinline__ void wait_tile(int younger, int loads_per_tile) {
     wait_vmcnt<2>();
   else
     wait_vmcnt<0>();
-}
-
-// Workgroup barrier without a memory fence (the kernel orders its LDS DMA
-// with explicit vmcnt waits); also a scheduling fence for the compiler.
-__device__ __forceinline__ void block_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_barrier" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
 }
 
 // Maps a linear workgroup id to (batch, tile_m, tile_n).

@@ -2,8 +2,9 @@
 
 The reference's kernels/ package holds NineToothed kernel descriptions; here
 the kernels are the HIP sources under ntops_amd/csrc, so this package only
-keeps the one public symbol callers use (`mm.InputPrecisionVariant`)."""
+keeps the public symbols callers use (`mm.InputPrecisionVariant`,
+`scaled_dot_product_attention.CausalVariant`)."""
 
-from ntops_amd.kernels import mm
+from ntops_amd.kernels import mm, scaled_dot_product_attention
 
-__all__ = ["mm"]
+__all__ = ["mm", "scaled_dot_product_attention"]

@@ -32,6 +32,7 @@ from ntops_amd.torch.relu import relu
 from ntops_amd.torch.rms_norm import rms_norm
 from ntops_amd.torch.rotary_position_embedding import rotary_position_embedding
 from ntops_amd.torch.rsqrt import rsqrt
+from ntops_amd.torch.scaled_dot_product_attention import scaled_dot_product_attention
 from ntops_amd.torch.sigmoid import sigmoid
 from ntops_amd.torch.silu import silu
 from ntops_amd.torch.sin import sin
@@ -70,6 +71,7 @@ __all__ = [
     "rms_norm",
     "rotary_position_embedding",
     "rsqrt",
+    "scaled_dot_product_attention",
     "sigmoid",
     "silu",
     "sin",

@@ -658,3 +658,51 @@ def gemm(a, b, dt, c=None, alpha=1.0, beta=0.0):
     if c is not None and beta != 0:
         out = out + np.float64(beta) * to_compute(c, dt).astype(np.float64)
     return round_to(out.astype(np.float32) if dt != "f64" else out, dt)
+
+
+# ---------------------------------------------------------------- attention
+
+
+@_with_errstate
+def scaled_dot_product_attention(q, k, v, dt, mask=None, mask_dt=None, causal=0, scale=None):
+    """kernels/scaled_dot_product_attention.py:154-201 (an online, base-2
+    softmax over key blocks) restated as its closed form, in float64:
+    out = softmax(q k^T * scale + mask) v per (batch, query head), with query
+    head h reading key / value head h // (Hq // Hkv) (GQA,
+    torch/scaled_dot_product_attention.py:33-45).  mask: None, bool (True =
+    attend) or additive float of mask_dt, broadcast to (B, Hq, Sq, Skv).
+    causal: 0 none, 1 upper-left (j <= i), 2 lower-right (j <= i + Skv - Sq).
+    scale defaults to 1 / sqrt(D).  A row with every key masked gives 0, as
+    torch's CPU kernel does (the reference's loop would give NaN).  Inputs are
+    (B, H, S, D) arrays of dt; the result is rounded to dt once."""
+    qf = to_compute(q, dt).astype(np.float64)
+    kf = to_compute(k, dt).astype(np.float64)
+    vf = to_compute(v, dt).astype(np.float64)
+    B, Hq, Sq, D = qf.shape
+    Hkv, Skv = kf.shape[1], kf.shape[2]
+    rep = Hq // Hkv
+    kf = np.repeat(kf, rep, axis=1)
+    vf = np.repeat(vf, rep, axis=1)
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    sc = np.matmul(qf, kf.swapaxes(-1, -2)) * scale
+    allowed = np.ones(sc.shape, dtype=bool)
+    if mask is not None:
+        m = np.broadcast_to(np.asarray(mask), sc.shape)
+        if m.dtype == np.bool_:
+            allowed &= m
+        else:
+            sc = sc + to_compute(m, mask_dt).astype(np.float64)
+    if causal:
+        off = Skv - Sq if causal == 2 else 0
+        i = np.arange(Sq)[:, None]
+        j = np.arange(Skv)[None, :]
+        allowed &= (j <= i + off)[None, None]
+    sc = np.where(allowed, sc, -np.inf)
+    mx = np.max(sc, axis=-1, keepdims=True)
+    mx = np.where(np.isfinite(mx), mx, 0.0)
+    p = np.exp(sc - mx)
+    den = np.sum(p, axis=-1, keepdims=True)
+    out = np.matmul(p, vf) / np.where(den > 0, den, 1.0)
+    out = np.where(den > 0, out, 0.0)
+    return round_to(out.astype(np.float32) if dt != "f64" else out, dt)

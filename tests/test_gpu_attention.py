@@ -1,0 +1,148 @@
+"""GPU parity: scaled_dot_product_attention through the C ABI against the
+oracle.
+
+Mirrors the reference's tests/test_scaled_dot_product_attention.py: batch
+1-4, 2-32 query heads over a power-of-two divisor of key / value heads (GQA),
+sequence lengths 1-512, head dim 32 / 64 (plus 128), no mask / bool / float
+masks, both causal variants, random scales, the KV-cache slot write, fp32
+and fp16 -- with bf16 added, edge shapes (one query, one key, fully masked
+rows, Sq > Skv), strided inputs, and the config shape at full size.
+Tolerances: 16-bit (the MFMA path rounds P to the input dtype before P @ V,
+as the reference does) 2.5e-2 -- the reference test's fp16 bound; fp32
+(fp32 throughout) 1e-4."""
+
+import itertools
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+import ntops_amd
+from ntops_amd.kernels.scaled_dot_product_attention import CausalVariant
+from oracle import ops as O
+from tests.helpers import DT_NAME, assert_close, from_np, to_np
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+
+TOL = {torch.float32: (1e-4, 1e-4), torch.float16: (2.5e-2, 2.5e-2), torch.bfloat16: (2.5e-2, 2.5e-2)}
+sdpa = ntops_amd.torch.scaled_dot_product_attention
+
+
+def oracle(q, k, v, mask=None, causal=0, scale=None):
+    dt = DT_NAME[q.dtype]
+    m, mdt = None, None
+    if mask is not None:
+        m = to_np(mask)
+        mdt = DT_NAME[mask.dtype]
+    return from_np(O.scaled_dot_product_attention(to_np(q), to_np(k), to_np(v), dt, m, mdt, causal, scale), dt)
+
+
+def cases():
+    random.seed(0)
+    out = []
+    for mask_type, is_causal, scale, dtype, kv_cache, variant in itertools.product(
+        (None, torch.bool, torch.float32), (False, True), (None, random.uniform(0.05, 0.5)),
+        (torch.float32, torch.float16, torch.bfloat16), (False, True),
+        (None, CausalVariant.LOWER_RIGHT, CausalVariant.UPPER_LEFT),
+    ):
+        if mask_type is not None and is_causal:
+            continue
+        hq = 2 ** random.randint(1, 5)
+        hkv = 2 ** random.randint(1, int(math.log2(hq)))
+        sq, skv = random.randint(1, 512), random.randint(1, 512)
+        if variant == CausalVariant.LOWER_RIGHT and sq > skv:
+            continue
+        d = random.choice([32, 64, 128])
+        out.append((random.randint(1, 4), hq, sq, d, hkv, skv, mask_type, is_causal, scale, variant, kv_cache, dtype))
+    return out
+
+
+@pytest.mark.parametrize("b, hq, sq, d, hkv, skv, mask_type, is_causal, scale, variant, kv_cache, dtype", cases())
+def test_sdpa(b, hq, sq, d, hkv, skv, mask_type, is_causal, scale, variant, kv_cache, dtype):
+    torch.manual_seed(b * 1000 + sq * 7 + skv)
+    q = torch.randn(b, hq, sq, d).to(dtype)
+    k = torch.randn(b, hkv, skv, d).to(dtype)
+    v = torch.randn(b, hkv, skv, d).to(dtype)
+    mask = None
+    if mask_type is not None:
+        r = torch.rand(sq, skv)
+        mask = r > 0.5 if mask_type is torch.bool else torch.where(r > 0.5, 0.0, float("-inf")).to(dtype)
+    kg, vg = k.clone().cuda(), v.clone().cuda()
+    pk = pv = sk = sv = None
+    if kv_cache:
+        pk, pv = kg[:, :, -1:, :].clone(), vg[:, :, -1:, :].clone()
+        sk, sv = kg[:, :, -1:, :], vg[:, :, -1:, :]
+        sk[...] = 0
+        sv[...] = 0
+    got = sdpa(q.cuda(), kg, vg, attn_mask=None if mask is None else mask.cuda(), is_causal=is_causal, scale=scale,
+               enable_gqa=True, causal_variant=variant, present_key=pk, present_value=pv,
+               present_key_slot=sk, present_value_slot=sv)
+    causal = 0
+    if is_causal:
+        causal = 2 if variant == CausalVariant.LOWER_RIGHT else 1
+    exp = oracle(q, k, v, mask, causal, scale)
+    assert got.dtype == dtype and got.shape == q.shape
+    assert_close(got, exp, *TOL[dtype], "sdpa")
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("d", (64, 128))
+def test_sdpa_edges(dtype, d):
+    g = torch.Generator().manual_seed(d)
+    rt = lambda *s: torch.randn(*s, generator=g).to(dtype)  # noqa: E731
+    for (sq, skv, causal) in ((1, 300, 0), (1, 300, 2), (300, 1, 1), (200, 70, 1), (70, 200, 2), (129, 129, 1), (128, 64, 0)):
+        q, k, v = rt(2, 4, sq, d), rt(2, 2, skv, d), rt(2, 2, skv, d)
+        variant = CausalVariant.LOWER_RIGHT if causal == 2 else None
+        got = sdpa(q.cuda(), k.cuda(), v.cuda(), is_causal=causal > 0, enable_gqa=True, causal_variant=variant)
+        assert_close(got, oracle(q, k, v, None, causal), *TOL[dtype], f"sq {sq} skv {skv} causal {causal}")
+    # fully masked rows give zeros
+    q, k, v = rt(1, 2, 40, d), rt(1, 2, 50, d), rt(1, 2, 50, d)
+    m = torch.rand(40, 50, generator=g) > 0.3
+    m[7] = False
+    got = sdpa(q.cuda(), k.cuda(), v.cuda(), attn_mask=m.cuda())
+    assert (got[:, :, 7].cpu() == 0).all()
+    assert_close(got, oracle(q, k, v, m), *TOL[dtype], "bool mask with a masked row")
+    # (B, S, H, D) storage viewed as (B, H, S, D): strided inputs and a 3-D call
+    qs, ks, vs = rt(2, 96, 4, d), rt(2, 80, 4, d), rt(2, 80, 4, d)
+    qt, kt, vt = (t.cuda().transpose(1, 2) for t in (qs, ks, vs))
+    got = sdpa(qt, kt, vt, is_causal=True)
+    assert_close(got, oracle(qs.transpose(1, 2), ks.transpose(1, 2), vs.transpose(1, 2), None, 1), *TOL[dtype], "strided")
+    got3 = sdpa(qs[0].cuda().transpose(0, 1), ks[0].cuda().transpose(0, 1), vs[0].cuda().transpose(0, 1))
+    exp3 = oracle(qs[:1].transpose(1, 2), ks[:1].transpose(1, 2), vs[:1].transpose(1, 2))[0]
+    assert_close(got3, exp3, *TOL[dtype], "3-D")
+
+
+def test_sdpa_argument_checks():
+    q = torch.randn(1, 4, 8, 64, device="cuda")
+    k = torch.randn(1, 2, 8, 64, device="cuda")
+    with pytest.raises(AssertionError):
+        sdpa(q, k, k)  # GQA not enabled
+    with pytest.raises(AssertionError):
+        sdpa(q, q, q, attn_mask=torch.ones(8, 8, dtype=torch.bool, device="cuda"), is_causal=True)
+    with pytest.raises(AssertionError):
+        sdpa(q, q, q, dropout_p=0.1)
+    with pytest.raises(RuntimeError):
+        sdpa(q, q.half(), q)
+
+
+def test_sdpa_config_full_size():
+    """bf16 (4, 32, 2048, 128) causal, the softmax / bmm config shape: three
+    (batch, head) pairs against the oracle on every row, and on every head
+    the size-independent facts that causal query 0 returns exactly V[0] and
+    every output is finite."""
+    B, H, S, D = 4, 32, 2048, 128
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, H, S, D, generator=g).bfloat16()
+    k = torch.randn(B, H, S, D, generator=g).bfloat16()
+    v = torch.randn(B, H, S, D, generator=g).bfloat16()
+    got = sdpa(q.cuda(), k.cuda(), v.cuda(), is_causal=True)
+    for b, h in ((0, 0), (1, 17), (3, 31)):
+        exp = oracle(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], None, 1)
+        assert_close(got[b:b + 1, h:h + 1], exp, 2.5e-2, 2.5e-2, f"config head ({b}, {h})")
+    assert torch.equal(got[:, :, 0].cpu(), v[:, :, 0])
+    assert torch.isfinite(got).all()
