@@ -151,7 +151,7 @@ KERNEL_OF = {
     "mm": "k_gemm_mfma",
     "addmm": "k_gemm_mfma",
     "bmm": "k_gemm_panel",
-    "sdpa": "k_flash_fwd",
+    "sdpa": "k_flash_attn",
 }
 
 

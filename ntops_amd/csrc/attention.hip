@@ -69,6 +69,15 @@ __device__ __forceinline__ float mask_log2(const AttnArgs& a, int64_t off) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max(a, b, c) in one instruction, without the NaN-quieting moves the
+// compiler puts in front of fmaxf in IEEE mode (a NaN operand may be
+// dropped; a NaN score still reaches the output through its exponential).
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Chunk slot of 16-byte chunk c of key row r in the V tile ([kv][d] with
 // D / 8 chunks per row), conflict-free for the transposing fragment reads.
 template <int D>
@@ -299,6 +308,314 @@ __global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int t
     }
 }
 
+// ---- flash forward without an explicit mask (none or causal) ---------------
+//
+// One 8-wave workgroup per (batch, head, 256 query rows), one per CU; wave w
+// owns rows 32w .. 32w + 31 of the block with their Q fragments in VGPRs.
+// K and V tiles of 64 keys go global -> LDS by direct DMA (no VGPR staging)
+// into a ring of kFaStages stages; tile t lives in stage t % kFaStages, with
+// the swizzles of k_frag / v_frag applied on the global side (a lane's LDS
+// destination is fixed, so it fetches the chunk that belongs there).
+// Iteration j of a wave:
+//   barrier (K_{j+1} and V_j landed for every wave; stage (j - 1) % NS free)
+//   DMA tile j + NS - 1 into that stage
+//   S_{j+1} = Q K_{j+1}^T on the matrix cores while P_j = exp2(S_j c - m)
+//   runs on the VALU (independent instructions of one wave overlap);
+//   O += P_j V_j while S_{j+1} is masked and reduced to its row max.
+// Lazy rescaling: exponentials use a running reference max m that is raised
+// only when a row's max exceeds it by more than 2^8 (then O and l are scaled
+// by exp2(m_old - m_new) once); P <= 256 keeps fp32 sums and the T-rounded P
+// exact in relative terms, and O / l is unchanged by the choice of m.
+// Causal: the block walks keys up to its last row's limit; a wave skips the
+// tiles beyond its own rows' limit (it still issues its share of the DMA and
+// joins the barriers).
+constexpr int kFaRows = 256;
+constexpr int kFaWaves = 8;
+constexpr int kFaStages = 4;
+constexpr int kPrefetch = 4;  // LDS fragment reads in flight ahead of the MFMA that uses them
+
+// Instruction classes of the scheduler's group barriers.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
+// Asks the scheduler for a group of N instructions of class MASK here (in
+// order with the other groups of the region).
+template <int MASK, int N>
+__device__ __forceinline__ void sched_group() {
+  __builtin_amdgcn_sched_group_barrier(MASK, N, 0);
+}
+
+// DMA of one 64 x D K or V tile: D * 2 bytes per key row, 1 KiB per
+// instruction, instructions spread evenly over the NW waves.
+template <int D, bool IS_V, int NW>
+struct KvDma {
+  static constexpr int kRowsPerInst = 1024 / (D * 2);
+  static constexpr int kInst = 64 / kRowsPerInst / NW;
+  static_assert(kInst >= 1 && kInst * NW * kRowsPerInst == 64, "tile must split evenly over the waves");
+  u32x4 rsrc;
+  uint32_t voff[kInst];
+  uint32_t tile_bytes;  // byte distance between consecutive 64-key tiles
+  int lds_off;
+
+  // base: element pointer of key row 0; ld: row stride in elements;
+  // extent: readable bytes (rows at or past the end read as zero).
+  __device__ __forceinline__ void init(const void* base, int64_t ld, uint32_t extent, int wave, int lane) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    rsrc.x = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
+    rsrc.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32) & 0xffffu);
+    rsrc.z = __builtin_amdgcn_readfirstlane(extent);
+    rsrc.w = 0x00020000u;
+    lds_off = wave * kInst * 1024;
+    constexpr int cpr = D / 8;
+#pragma unroll
+    for (int i = 0; i < kInst; ++i) {
+      const int row = (wave * kInst + i) * kRowsPerInst + lane / cpr;
+      const int slot = lane % cpr;
+      const int c = IS_V ? vslot<D>(row, slot) : kslot<D>(row, slot);  // swizzles are involutions
+      voff[i] = static_cast<uint32_t>(row * ld * 2 + c * 16);
+    }
+    tile_bytes = static_cast<uint32_t>(64 * ld * 2);
+  }
+
+  // Loads tile t into `tile` (its LDS home); a tile past the end loads
+  // nothing but still counts once per instruction in vmcnt.
+  __device__ __forceinline__ void issue(char* tile, int t, bool valid) const {
+#pragma unroll
+    for (int i = 0; i < kInst; ++i) {
+      const uint32_t off = valid ? voff[i] + static_cast<uint32_t>(t) * tile_bytes : kOOB;
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(
+          static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(tile + lds_off + i * 1024))));
+      dma16(rsrc, dst, off);
+    }
+  }
+};
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int total) {
+  constexpr int BN = 64;
+  constexpr int NS = kFaStages;
+  constexpr int NW = kFaWaves;
+  constexpr int KS = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int kTile = BN * D * 2;
+  constexpr int kStage = 2 * kTile;                  // K tile, then V tile
+  constexpr int L = 2 * KvDma<D, false, NW>::kInst;  // DMA instructions per lane per tile
+  static_assert(NS == 4, "the phase schedule refills the stage of tile k - 2 with tile k + 2");
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;  // 0: leads, 1: one phase behind (one wave of each per SIMD)
+  int bh, qb;
+  attn_block(blockIdx.x, total, nqb, bh, qb);
+  const int b = bh / a.Hq, h = bh - b * a.Hq;
+  const int hk = h / (a.Hq / a.Hkv);
+  const int q0 = qb * kFaRows;
+  const int qw = q0 + wave * 32;
+  const int my_q = qw + (lane & 31);
+  const int off = (CAUSAL && a.causal == 2) ? a.Skv - a.Sq : 0;
+  const float c = a.scale_log2;  // > 0 on this path
+  const T* Q = static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1];
+
+  int kv_end = a.Skv;
+  if (CAUSAL) kv_end = max(0, min(a.Skv, q0 + kFaRows + off));
+  const int nkv = (kv_end + BN - 1) / BN;
+  // last tile this wave needs (-1: none)
+  int jl = nkv - 1;
+  if (CAUSAL) {
+    const int last = qw + 31 + off;
+    jl = min(jl, last >= 0 ? last / BN : -1);
+  }
+  if (qw >= a.Sq) jl = -1;
+  // last key of row my_q, relative to a tile's first key and this lane's
+  // column group: element (u, e) of a tile is key 32 u + 8 (e >> 2) + (e & 3)
+  // past that origin
+  int lim = a.Skv - 1;
+  if (CAUSAL) lim = min(lim, my_q + off);
+  lim -= 4 * (lane >> 5);
+
+  // Q fragments (A operand of S): row my_q, d = 16 ks + 8 (lane >> 5) .. + 7
+  u32x4 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (my_q < a.Sq)
+      qf[ks] = *reinterpret_cast<const u32x4*>(Q + my_q * a.qs[2] + ks * 16 + 8 * (lane >> 5));
+    else
+      qf[ks] = u32x4{0, 0, 0, 0};
+  }
+
+  KvDma<D, false, NW> kd;
+  KvDma<D, true, NW> vd;
+  kd.init(static_cast<const T*>(a.k) + b * a.ks[0] + hk * a.ks[1], a.ks[2],
+          static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane);
+  vd.init(static_cast<const T*>(a.v) + b * a.vs[0] + hk * a.vs[1], a.vs[2],
+          static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane);
+  auto dma = [&](int t) {
+    char* st = smem + (t % NS) * kStage;
+    kd.issue(st, t, t < nkv);
+    vd.issue(st + kTile, t, t < nkv);
+  };
+  dma(0);
+  dma(1);
+
+  f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
+  float m_run = neg_inf();  // reference max (base 2) of row my_q
+  float l_half = 0.f;       // this lane's half of the row's sum of exponentials
+  f32x16 s[2];              // S of the tile being softmaxed
+  u32x4 pf[4];              // P of that tile, as MFMA A operands per 16-key slice
+
+  // matrix phase of tile j: O += P_j V_j (if j >= 0) and S = Q K_{j+1}^T
+  // (if j + 1 <= jl)
+  auto matrix_phase = [&](int j) {
+    if (j >= 0) {
+      const char* sv = smem + (j % NS) * kStage + kTile;
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl)
+#pragma unroll
+        for (int t2 = 0; t2 < DT; ++t2) o[t2] = mfma32<T>(v_frag<D>(sv, t2 * 32, sl, lane), pf[sl], o[t2]);
+      // fragment reads run kPrefetch MFMAs ahead of their use
+      constexpr int nm = 4 * DT;
+      sched_group<kSchedDsRead, 2 * kPrefetch>();
+#pragma unroll
+      for (int i = 0; i < nm - kPrefetch; ++i) {
+        sched_group<kSchedMfma, 1>();
+        sched_group<kSchedDsRead, 2>();
+      }
+      sched_group<kSchedMfma, kPrefetch>();
+    }
+    if (j + 1 <= jl) {
+      const char* sk = smem + ((j + 1) % NS) * kStage;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[u][e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) s[u] = mfma32<T>(k_frag<D>(sk, u * 32, ks, lane), qf[ks], s[u]);
+      constexpr int nm = 2 * KS;
+      sched_group<kSchedDsRead, kPrefetch>();
+#pragma unroll
+      for (int i = 0; i < nm - kPrefetch; ++i) {
+        sched_group<kSchedMfma, 1>();
+        sched_group<kSchedDsRead, 1>();
+      }
+      sched_group<kSchedMfma, kPrefetch>();
+    }
+  };
+  // vector phase of tile t: mask (on tiles that reach the end of the keys or
+  // cross the wave's diagonal); a raise of the reference max of the rows
+  // whose tile max exceeds it by more than 2^8 (rescaling O and l) -- each
+  // lane tests its own half of the row, so the exchange with the other half
+  // (lane l ^ 32) happens only when some row needs the raise; then
+  // P = exp2(S c - m) rounded to T (masked: 0; nothing unmasked yet: m = 0).
+  // Reductions are trees so the phase is not one long dependency chain.
+  auto vector_phase = [&](int t) {
+    const int kv0 = t * BN;
+    bool edge = kv0 + BN > a.Skv;
+    if (CAUSAL) edge = edge || kv0 + BN - 1 > qw + off;
+    if (edge) {
+      const int rel = lim - kv0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[u][e] = 32 * u + 8 * (e >> 2) + (e & 3) <= rel ? s[u][e] : neg_inf();
+    }
+    // max of this lane's half of the row: 16 three-way maxima in a tree
+    float mh;
+    {
+      float v[32];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[16 * u + e] = s[u][e];
+      float m1[11];
+#pragma unroll
+      for (int i = 0; i < 10; ++i) m1[i] = max3(v[3 * i], v[3 * i + 1], v[3 * i + 2]);
+      m1[10] = max3(v[30], v[31], v[31]);
+      const float m2a = max3(m1[0], m1[1], m1[2]), m2b = max3(m1[3], m1[4], m1[5]);
+      const float m2c = max3(m1[6], m1[7], m1[8]), m2d = max3(m1[9], m1[10], m1[10]);
+      mh = max3(m2a, m2b, max3(m2c, m2d, m2d));
+    }
+    const float th = mh * c;  // max of this lane's half of the row (base 2)
+    if (__any(th > m_run + 8.f)) {
+      const float tmax = fmaxf(th, __shfl_xor(th, 32, 64));
+      const bool up = tmax > m_run + 8.f;
+      const float alpha = up ? fast_exp2(m_run - tmax) : 1.f;
+      m_run = up ? tmax : m_run;
+      l_half *= alpha;
+#pragma unroll
+      for (int t2 = 0; t2 < DT; ++t2)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[t2][e] *= alpha;
+    }
+    const float mb = m_run == neg_inf() ? 0.f : m_run;
+    float x[2][16];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[u][e] = fast_exp2(fmaf(s[u][e], c, -mb));
+    float r[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) r[e] = x[0][e] + x[1][e];
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int e = 0; e < w; ++e) r[e] += r[e + w];
+    l_half += r[0];
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) pf[sl] = pack8<T>(&x[sl >> 1][8 * (sl & 1)]);
+  };
+
+  // Each tile period k has two phases separated by barriers.  Group 0 runs
+  // the matrix phase of tile k - 1 then the vector phase of tile k; group 1
+  // runs the vector phase of tile k - 1 then the matrix phase of tile k - 1,
+  // so the two waves sharing a SIMD are always in opposite kinds of phase.
+  // Tile k is read from the first phase of period k to the second phase of
+  // period k + 1; at the start of period k it must have landed, and the
+  // stage of tile k - 2 is free for tile k + 2.  Each group has a loop of its
+  // own so that S and P are never both live across an iteration.
+  auto period_start = [&](int k) {
+    wait_vmcnt<L>();  // this wave's DMA of tile k landed (tile k + 1 may be in flight)
+    block_barrier();
+    dma(k + 2);
+  };
+  if (grp == 0) {
+    for (int k = 0; k <= nkv; ++k) {
+      period_start(k);
+      if (k - 1 <= jl) matrix_phase(k - 1);
+      block_barrier();
+      if (k <= jl) vector_phase(k);
+    }
+  } else {
+    for (int k = 0; k <= nkv; ++k) {
+      period_start(k);
+      if (k >= 1 && k - 1 <= jl) vector_phase(k - 1);
+      block_barrier();
+      if (k - 1 <= jl) matrix_phase(k - 1);
+    }
+  }
+  wait_vmcnt<0>();  // no DMA may land after the workgroup ends
+
+  const float l = l_half + __shfl_xor(l_half, 32, 64);
+  if (my_q >= a.Sq) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* O = static_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(my_q) * a.os[2];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      T v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
+      *reinterpret_cast<u32x2*>(O + t * 32 + 8 * qq + 4 * (lane >> 5)) = __builtin_bit_cast(u32x2, v4);
+    }
+}
+
 // Generic path: one wave per (batch, head, query row); lane owns d = lane +
 // 64 u.  fp32 arithmetic throughout (accurate exp2).
 template <typename T>
@@ -356,6 +673,30 @@ __global__ __launch_bounds__(64) void k_attn_generic(AttnArgs a) {
   }
 }
 
+template <typename T, int D, bool CAUSAL>
+int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
+  constexpr int kLds = kFaStages * 2 * 64 * D * 2;
+  auto kern = k_flash_attn<T, D, CAUSAL>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kLds) != hipSuccess)
+      return set_error(NTOPS_ERR_HIP, "sdpa: cannot reserve %d bytes of LDS", kLds);
+    attr_set = true;
+  }
+  const int nqb = (a.Sq + kFaRows - 1) / kFaRows;
+  const int64_t total = static_cast<int64_t>(nqb) * a.Hq * a.B;
+  if (total > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many blocks");
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(total)), dim3(kFaWaves * 64), kLds, st, a, nqb,
+                     static_cast<int>(total));
+  return check_launch("sdpa");
+}
+
+template <typename T, int D>
+int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
+  return a.causal ? launch_flash_attn<T, D, true>(a, st) : launch_flash_attn<T, D, false>(a, st);
+}
+
 template <typename T>
 int run_attention(const AttnArgs& a, hipStream_t st) {
   const auto unit_d = [&](const int64_t* s) { return s[3] == 1 && s[2] % 8 == 0 && s[1] % 8 == 0 && s[0] % 8 == 0; };
@@ -364,6 +705,13 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
                     a.os[1] % 4 == 0 && a.os[0] % 4 == 0 && aligned16(a.q) && aligned16(a.k) &&
                     aligned16(a.v) && (reinterpret_cast<uintptr_t>(a.o) & 7u) == 0;
   if constexpr (!std::is_same<T, float>::value) {
+    // DMA path: no explicit mask, a positive scale (the max of the scaled
+    // scores is the scaled max), rows that do not overlap, and every key
+    // row's byte offset within 2^31
+    const int64_t ld = std::max(a.ks[2], a.vs[2]);
+    const bool dma = mfma && a.mask_dtype < 0 && a.scale_log2 > 0.f && a.Sq > 128 && a.Skv > 0 &&
+                     a.ks[2] >= a.D && a.vs[2] >= a.D && (static_cast<int64_t>(a.Skv) + 256) * ld * 2 < 0x7fffffffLL;
+    if (dma) return a.D == 128 ? launch_flash_attn<T, 128>(a, st) : launch_flash_attn<T, 64>(a, st);
     if (mfma) {
       const int nqb = (a.Sq + 127) / 128;
       const int64_t total = static_cast<int64_t>(nqb) * a.Hq * a.B;

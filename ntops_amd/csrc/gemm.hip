@@ -59,7 +59,6 @@ struct GemmArgs {
   int staged;  // out is 16-byte aligned with unit column stride and N % 8 == 0
 };
 
-constexpr uint32_t kOOB = 0x80000000u;  // past every resource extent (< 2 GiB)
 
 // Waits until at most `younger` tiles' worth of this wave's DMA loads
 // (loads_per_tile each) are still in flight.
@@ -96,18 +95,6 @@ __device__ __forceinline__ void tile_of(int pid, int nblocks, int tm_count, int 
   tn = r / gm;
 }
 
-// 16-byte global -> LDS copy per lane: lane l's 16 bytes land at LDS byte
-// address lds_dst + 16 * l.  Written as inline assembly so the compiler does
-// not see an LDS store it would have to order against every later LDS read
-// (it would wait for all outstanding loads before each K tile's first
-// fragment read); the kernel orders it explicitly with vmcnt waits and the
-// per-tile barrier.
-__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_dst, uint32_t voffset) {
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voffset), "s"(rsrc), "{m0}"(lds_dst)
-               : "memory");
-}
 
 // One operand's global -> LDS stream for a tile of R rows/columns x BK k.
 // The tile is R * BK * 2 bytes: R * BK / 512 one-KiB load instructions,

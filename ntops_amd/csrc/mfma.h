@@ -1,6 +1,7 @@
 // Matrix-core building blocks shared by the GEMM and attention kernels
 // (gfx950, wave64): operand vector types, the 32x32x16 bf16 / f16 MFMA,
-// conflict-free LDS chunk swizzles, explicit waitcnt and barrier helpers.
+// conflict-free LDS chunk swizzles, direct global -> LDS loads, explicit
+// waitcnt and barrier helpers.
 #pragma once
 
 #include "dispatch.h"
@@ -62,6 +63,21 @@ __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_barrier" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
+}
+
+constexpr uint32_t kOOB = 0x80000000u;  // buffer offset past every resource extent (< 2 GiB)
+
+// 16-byte global -> LDS copy per lane: lane l's 16 bytes land at LDS byte
+// address lds_dst + 16 * l.  Written as inline assembly so the compiler does
+// not see an LDS store it would have to order against every later LDS read
+// (it would wait for all outstanding loads before each K tile's first
+// fragment read); the kernel orders it explicitly with vmcnt waits and the
+// per-tile barrier.
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_dst, uint32_t voffset) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "{m0}"(lds_dst)
+               : "memory");
 }
 
 // Packs 8 fp32 values into an MFMA operand of 8 T elements (one rounding).
