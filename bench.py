@@ -152,6 +152,7 @@ KERNEL_OF = {
     "addmm": "k_gemm_mfma",
     "bmm": "k_gemm_panel",
     "sdpa": "k_flash_attn",
+    "conv2d": "k_gemm_mfma",
 }
 
 
@@ -478,6 +479,34 @@ def make_workloads():
                       "TFLOP/s", "mfma", 4 * AB * AH * AD * AS * (AS + 1) // 2, 1, sdpa_build, sdpa_step,
                       sdpa_cpu, "bf16"))
     W[-1].bytes = 4 * AB * AH * AS * AD * 2
+
+    # conv2d bf16 (32, 256, 56, 56) * (256, 256, 3, 3), padding 1: one call
+    # is the unfold of the input into the workspace plus the matrix-core GEMM
+    CN, CC, CH, CK = 32, 256, 56, 256
+    conv = ntops_amd.torch.conv2d
+
+    def conv_build(i):
+        g = _gen(700 + i)
+        x = torch.randn(CN, CC, CH, CH, device="cuda", generator=g).bfloat16()
+        w = (torch.randn(CK, CC, 3, 3, device="cuda", generator=g) / 48).bfloat16()
+        b = torch.randn(CK, device="cuda", generator=g).bfloat16()
+        return {"x": x, "w": w, "b": b}
+
+    def conv_step(s):
+        conv(s["x"], s["w"], s["b"], padding=1)
+
+    def conv_cpu():
+        g = _cpu_gen()
+        x = torch.randn(2, CC, CH, CH, generator=g).bfloat16()
+        w = (torch.randn(CK, CC, 3, 3, generator=g) / 48).bfloat16()
+        b = torch.randn(CK, generator=g).bfloat16()
+        return (lambda: F.conv2d(x, w, b, padding=1)), 2 * 2 * CK * CC * 9 * CH * CH, \
+            "torch conv2d bf16 (2, 256, 56, 56) * (256, 256, 3, 3) = 1/16 of the workload"
+
+    W.append(Workload("conv2d", "conv2d bf16 (32, 256, 56, 56) * (256, 256, 3, 3) + bias, padding 1 "
+                      "(unfold + MFMA GEMM)", "TFLOP/s", "mfma", 2 * CN * CK * CC * 9 * CH * CH, 1, conv_build,
+                      conv_step, conv_cpu, "bf16"))
+    W[-1].bytes = (2 * CN * CC * CH * CH + CK * CC * 9 + CK) * 2
     return {w.name: w for w in W}
 
 

@@ -35,6 +35,10 @@
  *   ntops_gemm        <- src/ntops/torch/{mm,bmm,addmm}.py:7-18,
  *                        kernels/mm.py:54-65, kernels/bmm.py:8-43,
  *                        kernels/addmm.py:64-67
+ *   ntops_conv2d      <- src/ntops/torch/conv2d.py:8-53, kernels/conv2d.py:12-104
+ *   ntops_conv2d_workspace <- no ntops counterpart (Triton tiles the unfolded
+ *                        input on the fly); sizes the caller-owned buffer that
+ *                        the GEMM path of ntops_conv2d unfolds into
  */
 #ifndef NTOPS_AMD_H
 #define NTOPS_AMD_H
@@ -259,6 +263,34 @@ NTOPS_API int ntops_sdpa(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t 
                const void* mask, int mask_dtype, const int64_t* mask_strides,
                int causal, double scale,
                void* out, const int64_t* out_strides, void* stream);
+
+/* ---- convolution -------------------------------------------------------- */
+/* out (N, K, P, Q) = conv2d(x (N, C, H, W), w (K, C, R, S)) + bias (K),
+ * groups == 1: out[n,k,p,q] = bias[k] + sum_{c,r,s} x[n, c, p*stride_h -
+ * pad_h + r*dil_h, q*stride_w - pad_w + s*dil_w] * w[k,c,r,s], zero outside
+ * the image (pad_h / pad_w are the top / left padding; P and Q are given, so
+ * asymmetric padding is expressed by the output size).  Each tensor is
+ * described by its 4 element strides; bias may be NULL (bias_stride is its
+ * element stride).  fp32 accumulation, one rounding to dtype (BF16, F16,
+ * F32).  workspace (device memory of workspace_bytes, 16-byte aligned, may
+ * be NULL) lets large problems run as an unfold + matrix-core GEMM over
+ * chunks of images; ntops_conv2d_workspace returns the bytes that cover the
+ * whole batch in one chunk (0 when the problem runs without a workspace).
+ * Without enough workspace for one image the direct kernel runs. */
+NTOPS_API int64_t ntops_conv2d_workspace(int dtype, int64_t N, int64_t C, int64_t H, int64_t W,
+               int64_t K, int64_t R, int64_t S, int64_t P, int64_t Q,
+               int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+               int64_t dil_h, int64_t dil_w,
+               const int64_t* w_strides, const int64_t* out_strides);
+NTOPS_API int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t W,
+               int64_t K, int64_t R, int64_t S, int64_t P, int64_t Q,
+               int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+               int64_t dil_h, int64_t dil_w,
+               const void* x, const int64_t* x_strides,
+               const void* w, const int64_t* w_strides,
+               const void* bias, int64_t bias_stride,
+               void* out, const int64_t* out_strides,
+               void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

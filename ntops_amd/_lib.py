@@ -76,6 +76,14 @@ _SIGNATURES = {
         [_i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _i, _c_i64p,
          _i, _d, _vp, _c_i64p, _vp],
     ),
+    "ntops_conv2d_workspace": (
+        _i64,
+        [_i] + [_i64] * 15 + [_c_i64p, _c_i64p],
+    ),
+    "ntops_conv2d": (
+        _i,
+        [_i] + [_i64] * 15 + [_vp, _c_i64p, _vp, _c_i64p, _vp, _i64, _vp, _c_i64p, _vp, _i64, _vp],
+    ),
     "ntops_gemm": (
         _i,
         [_i, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _d, _vp, _c_i64p, _vp],

@@ -1,0 +1,317 @@
+// conv2d: out[n, k, p, q] = bias[k] + sum_{c, r, s} x[n, c, ih, iw] * w[k, c, r, s]
+// with ih = p * sh - ph + r * dh, iw = q * sw - pw + s * dw (zero outside the
+// image), fp32 accumulation and one rounding of the biased sum.
+//
+// Reference: kernels/conv2d.py:12-104 (im2col arrangement of the padded,
+// strided, dilated input over the mm tiling; bias added to the fp32 product,
+// lines 102-104), torch/conv2d.py:8-53 (argument forms, output size from
+// torch/pooling.py:4-19, groups == 1).
+//
+// Two paths:
+//  * GEMM path (when C * R * S and K are large enough to feed the matrix
+//    cores): the input of a chunk of images is unfolded into a caller-owned
+//    workspace col[n][c * R * S + r * S + s][p * Q + q] (k-rows padded to a
+//    multiple of 8 pixels), then ntops_gemm computes, per image,
+//    out_n = W (K x CRS) . col_n (CRS x PQ) + bias, with W shared across the
+//    batch (batch stride 0) and the bias as a C operand broadcast along the
+//    pixels (strides 0, 1, 0).  bf16 / fp16 run on MFMA, fp32 on the IEEE
+//    FMA GEMM.
+//  * direct path (small channel counts, any strides): one thread per output
+//    element, fp32 accumulation.
+#include "dispatch.h"
+
+namespace ntops {
+namespace {
+
+struct ConvArgs {
+  const void* x;
+  const void* w;
+  const void* bias;
+  void* out;
+  int64_t xs[4], ws[4], os[4], bs;
+  int N, C, H, W, K, R, S, P, Q;
+  int sh, sw, ph, pw, dh, dw;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_direct(ConvArgs a, int64_t total) {
+  using O = typename OpMath<T>::T_;
+  const T* x = static_cast<const T*>(a.x);
+  const T* w = static_cast<const T*>(a.w);
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    // i -> (n, k, p, q) with q fastest, so neighbouring threads read
+    // neighbouring input pixels and share one weight
+    const int q = static_cast<int>(i % a.Q);
+    int64_t t = i / a.Q;
+    const int p = static_cast<int>(t % a.P);
+    t /= a.P;
+    const int k = static_cast<int>(t % a.K);
+    const int n = static_cast<int>(t / a.K);
+    float acc = 0.f;
+    const T* xn = x + n * a.xs[0];
+    const T* wk = w + k * a.ws[0];
+    for (int c = 0; c < a.C; ++c) {
+      for (int r = 0; r < a.R; ++r) {
+        const int ih = p * a.sh - a.ph + r * a.dh;
+        if (ih < 0 || ih >= a.H) continue;
+        for (int s = 0; s < a.S; ++s) {
+          const int iw = q * a.sw - a.pw + s * a.dw;
+          if (iw < 0 || iw >= a.W) continue;
+          acc += static_cast<float>(xn[c * a.xs[1] + ih * a.xs[2] + iw * a.xs[3]]) *
+                 static_cast<float>(wk[c * a.ws[1] + r * a.ws[2] + s * a.ws[3]]);
+        }
+      }
+    }
+    if (a.bias) acc += static_cast<float>(static_cast<const T*>(a.bias)[k * a.bs]);
+    static_cast<T*>(a.out)[n * a.os[0] + k * a.os[1] + p * a.os[2] + q * a.os[3]] = static_cast<T>(acc);
+  }
+}
+
+// col[b][kg][pix] for images n0 .. n0 + nb - 1 (b = n - n0), pixel rows of
+// ld elements (pixels PQ .. ld - 1 are zero).  One thread per 8 pixels of one
+// (b, kg) row: a 16-byte (or 32-byte for fp32) run of the output row.
+template <typename T>
+__global__ __launch_bounds__(256) void k_im2col(ConvArgs a, T* col, int n0, int nb, int64_t ld) {
+  const int crs = a.C * a.R * a.S;
+  const int64_t chunks = ld / 8;
+  const int64_t total = static_cast<int64_t>(nb) * crs * chunks;
+  const T* x = static_cast<const T*>(a.x);
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t ch = i % chunks;
+    const int64_t row = i / chunks;  // b * crs + kg
+    const int kg = static_cast<int>(row % crs);
+    const int b = static_cast<int>(row / crs);
+    const int s = kg % a.S;
+    const int r = (kg / a.S) % a.R;
+    const int c = kg / (a.R * a.S);
+    const T* xc = x + (n0 + b) * a.xs[0] + c * a.xs[1];
+    T v[8];
+    const int pq0 = static_cast<int>(ch * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int pq = pq0 + e;
+      T val = static_cast<T>(0.f);
+      if (pq < a.P * a.Q) {
+        const int p = pq / a.Q, q = pq - (pq / a.Q) * a.Q;
+        const int ih = p * a.sh - a.ph + r * a.dh;
+        const int iw = q * a.sw - a.pw + s * a.dw;
+        if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W) val = xc[ih * a.xs[2] + iw * a.xs[3]];
+      }
+      v[e] = val;
+    }
+    T* dst = col + row * ld + pq0;
+    if constexpr (sizeof(T) == 2) {
+      *reinterpret_cast<u32x4*>(dst) = __builtin_bit_cast(u32x4, v);
+    } else {
+      reinterpret_cast<u32x4*>(dst)[0] = u32x4{__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                                               __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
+      reinterpret_cast<u32x4*>(dst)[1] = u32x4{__builtin_bit_cast(uint32_t, v[4]), __builtin_bit_cast(uint32_t, v[5]),
+                                               __builtin_bit_cast(uint32_t, v[6]), __builtin_bit_cast(uint32_t, v[7])};
+    }
+  }
+}
+
+// Same output as k_im2col, one workgroup per (image, channel): the input
+// plane is staged in LDS once (read from HBM once, any strides), then every
+// tap's unfolded row is written from LDS with 16-byte stores, neighbouring
+// threads writing neighbouring pixel runs.  Used when the plane fits in
+// kPlaneLds bytes (the launch reserves exactly the plane, so small planes
+// leave room for many workgroups per CU).
+constexpr int kPlaneLds = 64 * 1024;
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_im2col_plane(ConvArgs a, T* col, int n0, int64_t ld) {
+  extern __shared__ __attribute__((aligned(16))) char sm[];  // H * W elements
+  T* plane = reinterpret_cast<T*>(sm);
+  const int b = blockIdx.x / a.C;
+  const int c = blockIdx.x - b * a.C;
+  const T* xc = static_cast<const T*>(a.x) + (n0 + b) * a.xs[0] + c * a.xs[1];
+  const int hw = a.H * a.W;
+  for (int i = threadIdx.x; i < hw; i += blockDim.x) {
+    const int ih = i / a.W, iw = i - (i / a.W) * a.W;
+    plane[i] = xc[ih * a.xs[2] + iw * a.xs[3]];
+  }
+  __syncthreads();
+  const int rs = a.R * a.S;
+  const int pq = a.P * a.Q;
+  const int nch = static_cast<int>(ld / 8);
+  T* dst0 = col + (static_cast<int64_t>(b) * a.C * rs + static_cast<int64_t>(c) * rs) * ld;
+  for (int j = threadIdx.x; j < nch; j += blockDim.x) {
+    // the 8 pixels of run j: output (p, q) computed once, then reused for
+    // every tap
+    int p = (8 * j) / a.Q;
+    int q = 8 * j - p * a.Q;
+    int hbase[8], wbase[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool in = 8 * j + e < pq;
+      hbase[e] = in ? p * a.sh - a.ph : -0x40000000;  // out-of-range pixels never land in the plane
+      wbase[e] = q * a.sw - a.pw;
+      if (++q == a.Q) {
+        q = 0;
+        ++p;
+      }
+    }
+    for (int r = 0; r < a.R; ++r) {
+      for (int s = 0; s < a.S; ++s) {
+        T v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int ih = hbase[e] + r * a.dh;
+          const int iw = wbase[e] + s * a.dw;
+          const bool ok = static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
+                          static_cast<unsigned>(iw) < static_cast<unsigned>(a.W);
+          v[e] = ok ? plane[ih * a.W + iw] : static_cast<T>(0.f);
+        }
+        T* dst = dst0 + static_cast<int64_t>(r * a.S + s) * ld + 8 * j;
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<u32x4*>(dst) = __builtin_bit_cast(u32x4, v);
+        } else {
+          reinterpret_cast<u32x4*>(dst)[0] = u32x4{__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                                                   __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
+          reinterpret_cast<u32x4*>(dst)[1] = u32x4{__builtin_bit_cast(uint32_t, v[4]), __builtin_bit_cast(uint32_t, v[5]),
+                                                   __builtin_bit_cast(uint32_t, v[6]), __builtin_bit_cast(uint32_t, v[7])};
+        }
+      }
+    }
+  }
+}
+
+unsigned grid_for(int64_t work, int per_block) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g > 65536) g = 65536;  // grid-stride loops cover the rest
+  return static_cast<unsigned>(g < 1 ? 1 : g);
+}
+
+// Pixels per unfolded row (a multiple of 8, so rows stay 16-byte aligned).
+int64_t col_ld(const ConvArgs& a) { return (static_cast<int64_t>(a.P) * a.Q + 7) / 8 * 8; }
+
+// Whether the GEMM path applies: enough reduction depth and output channels
+// to feed the matrix cores, unit-stride weight rows of a multiple of 8
+// elements, and pixel planes of the output that are contiguous.
+bool use_gemm(const ConvArgs& a, int dt) {
+  const int64_t crs = static_cast<int64_t>(a.C) * a.R * a.S;
+  const int64_t pq = static_cast<int64_t>(a.P) * a.Q;
+  const bool w_rows = a.ws[3] == 1 && a.ws[2] == a.S && a.ws[1] == static_cast<int64_t>(a.R) * a.S &&
+                      a.ws[0] % 8 == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15u) == 0;
+  const bool out_plane = a.os[3] == 1 && a.os[2] == a.Q;
+  return dt != NTOPS_F64 && crs >= 64 && crs % 8 == 0 && a.K >= 32 && pq >= 64 && w_rows && out_plane &&
+         crs * col_ld(a) <= 0x7fffffffLL;
+}
+
+int64_t col_bytes_per_image(const ConvArgs& a, int dt) {
+  return static_cast<int64_t>(a.C) * a.R * a.S * col_ld(a) * dtype_size(dt);
+}
+
+int fill_args(ConvArgs& a, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
+              int64_t P, int64_t Q, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw) {
+  const int64_t v[] = {N, C, H, W, K, R, S, P, Q, sh, sw, ph, pw, dh, dw};
+  for (int64_t x : v)
+    if (x < 0 || x > 0x7fffffffLL) return set_error(NTOPS_ERR_INVALID, "conv2d: size or parameter out of range");
+  if (sh < 1 || sw < 1 || dh < 1 || dw < 1) return set_error(NTOPS_ERR_INVALID, "conv2d: stride and dilation must be >= 1");
+  a.N = static_cast<int>(N);
+  a.C = static_cast<int>(C);
+  a.H = static_cast<int>(H);
+  a.W = static_cast<int>(W);
+  a.K = static_cast<int>(K);
+  a.R = static_cast<int>(R);
+  a.S = static_cast<int>(S);
+  a.P = static_cast<int>(P);
+  a.Q = static_cast<int>(Q);
+  a.sh = static_cast<int>(sh);
+  a.sw = static_cast<int>(sw);
+  a.ph = static_cast<int>(ph);
+  a.pw = static_cast<int>(pw);
+  a.dh = static_cast<int>(dh);
+  a.dw = static_cast<int>(dw);
+  return NTOPS_OK;
+}
+
+}  // namespace
+}  // namespace ntops
+
+using namespace ntops;
+
+extern "C" int64_t ntops_conv2d_workspace(int dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K,
+                                          int64_t R, int64_t S, int64_t P, int64_t Q, int64_t stride_h,
+                                          int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dil_h,
+                                          int64_t dil_w, const int64_t* w_strides, const int64_t* out_strides) {
+  ConvArgs a{};
+  if (fill_args(a, N, C, H, W, K, R, S, P, Q, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w) != NTOPS_OK) return 0;
+  if (!w_strides || !out_strides || dtype_size(dtype) == 0) return 0;
+  for (int i = 0; i < 4; ++i) {
+    a.ws[i] = w_strides[i];
+    a.os[i] = out_strides[i];
+  }
+  a.w = nullptr;  // alignment is checked again on the call
+  if (!use_gemm(a, dtype)) return 0;
+  return col_bytes_per_image(a, dtype) * N;
+}
+
+extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R,
+                            int64_t S, int64_t P, int64_t Q, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                            int64_t pad_w, int64_t dil_h, int64_t dil_w, const void* x, const int64_t* x_strides,
+                            const void* w, const int64_t* w_strides, const void* bias, int64_t bias_stride,
+                            void* out, const int64_t* out_strides, void* workspace, int64_t workspace_bytes,
+                            void* stream) {
+  ConvArgs a{};
+  int rc = fill_args(a, N, C, H, W, K, R, S, P, Q, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w);
+  if (rc != NTOPS_OK) return rc;
+  if (N == 0 || K == 0 || P == 0 || Q == 0) return NTOPS_OK;
+  if (!x || !w || !out || !x_strides || !w_strides || !out_strides)
+    return set_error(NTOPS_ERR_INVALID, "conv2d: null pointer");
+  if (workspace_bytes < 0) return set_error(NTOPS_ERR_INVALID, "conv2d: negative workspace size");
+  a.x = x;
+  a.w = w;
+  a.bias = bias;
+  a.out = out;
+  a.bs = bias_stride;
+  for (int i = 0; i < 4; ++i) {
+    a.xs[i] = x_strides[i];
+    a.ws[i] = w_strides[i];
+    a.os[i] = out_strides[i];
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t per_image = dtype_size(dtype) ? col_bytes_per_image(a, dtype) : 0;
+  const bool gemm = dtype_size(dtype) && use_gemm(a, dtype) && workspace && per_image > 0 &&
+                    workspace_bytes >= per_image && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0;
+  if (!gemm) {
+    return dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
+      using T = decltype(tag);
+      const int64_t total = N * K * P * Q;
+      hipLaunchKernelGGL(k_conv_direct<T>, dim3(grid_for(total, 256)), dim3(256), 0, st, a, total);
+      return check_launch("conv2d");
+    });
+  }
+  // GEMM path, in chunks of images that fit the workspace
+  const int64_t crs = C * R * S;
+  const int64_t ld = col_ld(a);
+  const int64_t nb_max = std::min<int64_t>(N, workspace_bytes / per_image);
+  const int64_t a_str[3] = {0, w_strides[0], 1};
+  const int64_t b_str[3] = {crs * ld, ld, 1};
+  const int64_t c_str[3] = {0, bias_stride, 0};
+  const int64_t d_str[3] = {out_strides[0], out_strides[1], 1};
+  const int es = dtype_size(dtype);
+  for (int64_t n0 = 0; n0 < N; n0 += nb_max) {
+    const int64_t nb = std::min(nb_max, N - n0);
+    rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
+      using T = decltype(tag);
+      if (static_cast<int64_t>(H) * W * static_cast<int64_t>(sizeof(T)) <= kPlaneLds && nb * C <= 0x7fffffffLL)
+        hipLaunchKernelGGL(k_im2col_plane<T>, dim3(static_cast<unsigned>(nb * C)), dim3(256),
+                           static_cast<unsigned>(H * W * sizeof(T)), st, a, static_cast<T*>(workspace),
+                           static_cast<int>(n0), ld);
+      else
+        hipLaunchKernelGGL(k_im2col<T>, dim3(grid_for(nb * crs * (ld / 8), 256)), dim3(256), 0, st, a,
+                           static_cast<T*>(workspace), static_cast<int>(n0), static_cast<int>(nb), ld);
+      return check_launch("conv2d");
+    });
+    if (rc != NTOPS_OK) return rc;
+    void* dst = static_cast<char*>(out) + n0 * out_strides[0] * es;
+    rc = ntops_gemm(dtype, nb, K, P * Q, crs, w, a_str, workspace, b_str, bias, bias ? c_str : nullptr, 1.0,
+                    bias ? 1.0 : 0.0, dst, d_str, stream);
+    if (rc != NTOPS_OK) return rc;
+  }
+  return NTOPS_OK;
+}

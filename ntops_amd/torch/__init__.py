@@ -10,6 +10,7 @@ from ntops_amd.torch.bitwise_not import bitwise_not
 from ntops_amd.torch.bitwise_or import bitwise_or
 from ntops_amd.torch.bmm import bmm
 from ntops_amd.torch.clamp import clamp
+from ntops_amd.torch.conv2d import conv2d
 from ntops_amd.torch.cos import cos
 from ntops_amd.torch.div import div
 from ntops_amd.torch.eq import eq
@@ -49,6 +50,7 @@ __all__ = [
     "bitwise_or",
     "bmm",
     "clamp",
+    "conv2d",
     "cos",
     "div",
     "eq",

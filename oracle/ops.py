@@ -706,3 +706,39 @@ def scaled_dot_product_attention(q, k, v, dt, mask=None, mask_dt=None, causal=0,
     out = np.matmul(p, vf) / np.where(den > 0, den, 1.0)
     out = np.where(den > 0, out, 0.0)
     return round_to(out.astype(np.float32) if dt != "f64" else out, dt)
+
+
+def conv2d(x, w, dt, bias=None, stride=(1, 1), pad=(0, 0), dilation=(1, 1), out_hw=None):
+    """kernels/conv2d.py:12-104 (the padded input unfolded with the given
+    stride and dilation, times the flattened weight, fp32 product plus bias,
+    lines 102-104) with the output size of torch/pooling.py:4-19, restated
+    directly in float64: out[n, k, p, q] = bias[k] + sum_{c, r, s}
+    x[n, c, p*sh - ph + r*dh, q*sw - pw + s*dw] * w[k, c, r, s], zero outside
+    the image, rounded to dt once.  x (N, C, H, W), w (K, C, R, S), bias (K,)
+    or None, all of dt.  pad is the top / left padding; out_hw overrides the
+    symmetric-padding output size (asymmetric 'same' padding)."""
+    xf = to_compute(x, dt).astype(np.float64)
+    wf = to_compute(w, dt).astype(np.float64)
+    N, C, H, W = xf.shape
+    K, _, R, S = wf.shape
+    sh, sw = stride
+    ph, pw = pad
+    dh, dw = dilation
+    if out_hw is None:
+        P = (H + 2 * ph - dh * (R - 1) - 1) // sh + 1
+        Q = (W + 2 * pw - dw * (S - 1) - 1) // sw + 1
+    else:
+        P, Q = out_hw
+    # zero-pad far enough on every side for every tap of every output
+    hb = max(0, (P - 1) * sh - ph + (R - 1) * dh + 1 - H)
+    wb = max(0, (Q - 1) * sw - pw + (S - 1) * dw + 1 - W)
+    xp = np.zeros((N, C, ph + H + hb, pw + W + wb))
+    xp[:, :, ph:ph + H, pw:pw + W] = xf
+    out = np.zeros((N, K, P, Q))
+    for r in range(R):
+        for s in range(S):
+            tap = xp[:, :, r * dh: r * dh + sh * (P - 1) + 1: sh, s * dw: s * dw + sw * (Q - 1) + 1: sw]
+            out += np.einsum("ncpq,kc->nkpq", tap, wf[:, :, r, s], optimize=True)
+    if bias is not None:
+        out += to_compute(bias, dt).astype(np.float64)[None, :, None, None]
+    return round_to(out.astype(np.float32) if dt != "f64" else out, dt)

@@ -1,0 +1,169 @@
+"""GPU parity: conv2d through the C ABI against the oracle.
+
+Mirrors the reference's tests/test_conv2d.py grid -- (n, c, h, w, k) =
+(2, 3, 112, 112, 4), 1x1 and 3x3 kernels, stride / padding / dilation in
+{1, 2 or 0, 1, (2, 3)}, fp32 (1e-5) and fp16 (1e-3) -- plus bf16
+(1.6e-2), shapes that take the unfold + matrix-core GEMM path (fp32, fp16,
+bf16), several image chunks through a small workspace, strided and
+channels-last inputs, unbatched input, 'same' / 'valid' padding, no bias,
+the argument checks, and the (32, 256, 56, 56) x (256, 256, 3, 3) workload
+on sampled images and channels."""
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+import ntops_amd
+from ntops_amd import _lib
+from oracle import ops as O
+from tests.helpers import DT_NAME, assert_close, from_np, to_np
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+
+conv2d = ntops_amd.torch.conv2d
+TOL = {torch.float32: (1e-5, 1e-5), torch.float16: (1e-3, 1e-3), torch.bfloat16: (1.6e-2, 1.6e-2)}
+
+
+def pair(v):
+    return (v, v) if isinstance(v, int) else tuple(v)
+
+
+def oracle(x, w, b, stride, padding, dilation, out_hw=None):
+    dt = DT_NAME[x.dtype]
+    return from_np(O.conv2d(to_np(x), to_np(w), dt, None if b is None else to_np(b), pair(stride), pair(padding),
+                            pair(dilation), out_hw), dt)
+
+
+REF_GRID = list(itertools.product(((1, 1), (3, 3)), (1, 2, (2, 3)), (0, 1, (2, 3)), (1, 2, (2, 3))))
+
+
+@pytest.mark.parametrize("dtype", (torch.float32, torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("rs, stride, padding, dilation", REF_GRID)
+def test_conv2d_reference_grid(rs, stride, padding, dilation, dtype):
+    g = torch.Generator().manual_seed(hash((rs, stride, padding, dilation)) & 0xffff)
+    n, c, h, w, k = 2, 3, 112, 112, 4
+    x = torch.randn(n, c, h, w, generator=g).to(dtype)
+    wt = torch.randn(k, c, *rs, generator=g).to(dtype)
+    b = torch.randn(k, generator=g).to(dtype)
+    got = conv2d(x.cuda(), wt.cuda(), bias=b.cuda(), stride=stride, padding=padding, dilation=dilation)
+    assert_close(got, oracle(x, wt, b, stride, padding, dilation), *TOL[dtype], "conv2d")
+
+
+GEMM_CASES = [
+    # (n, c, h, w, k, r, s, stride, padding, dilation, bias)
+    (2, 64, 28, 28, 64, 3, 3, 1, 1, 1, True),
+    (3, 32, 17, 19, 48, 3, 3, 2, 1, 1, True),
+    (2, 64, 20, 21, 40, 3, 3, (2, 3), (2, 3), (2, 3), False),
+    (1, 128, 14, 14, 256, 1, 1, 1, 0, 1, True),
+    (2, 16, 31, 29, 64, 5, 5, 1, 2, 1, True),
+]
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("case", GEMM_CASES)
+def test_conv2d_gemm_path(case, dtype):
+    n, c, h, w, k, r, s, stride, padding, dilation, has_bias = case
+    g = torch.Generator().manual_seed(n * 1000 + c + k)
+    x = torch.randn(n, c, h, w, generator=g).to(dtype)
+    wt = (torch.randn(k, c, r, s, generator=g) / (c * r * s) ** 0.5).to(dtype)
+    b = torch.randn(k, generator=g).to(dtype) if has_bias else None
+    (sh, sw), (ph, pw), (dh, dw) = pair(stride), pair(padding), pair(dilation)
+    P = (h + 2 * ph - dh * (r - 1) - 1) // sh + 1
+    Q = (w + 2 * pw - dw * (s - 1) - 1) // sw + 1
+    ws = _lib.load().ntops_conv2d_workspace(_lib.dtype_code(dtype), n, c, h, w, k, r, s, P, Q, sh, sw, ph, pw, dh, dw,
+                                            _lib.i64_array(wt.stride()), _lib.i64_array((k * P * Q, P * Q, Q, 1)))
+    assert ws > 0, "expected the GEMM path"
+    got = conv2d(x.cuda(), wt.cuda(), bias=None if b is None else b.cuda(), stride=stride, padding=padding,
+                 dilation=dilation)
+    exp = oracle(x, wt, b, stride, padding, dilation)
+    tol = (2e-5, 2e-5) if dtype == torch.float32 else TOL[dtype]
+    assert_close(got, exp, *tol, "conv2d gemm path")
+
+
+def test_conv2d_workspace_chunks():
+    """One image per chunk (workspace of exactly one image), and a workspace
+    too small for one image (direct kernel): both equal the one-chunk run."""
+    dtype = torch.bfloat16
+    n, c, h, w, k = 5, 64, 18, 18, 64
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(n, c, h, w, generator=g).to(dtype).cuda()
+    wt = (torch.randn(k, c, 3, 3, generator=g) / 24).to(dtype).cuda()
+    b = torch.randn(k, generator=g).to(dtype).cuda()
+    full = conv2d(x, wt, bias=b, padding=1)
+    lib = _lib.load()
+    geo = (n, c, h, w, k, 3, 3, h, w, 1, 1, 1, 1, 1, 1)
+    st = lambda t: _lib.i64_array(t.stride())  # noqa: E731
+    total = lib.ntops_conv2d_workspace(_lib.dtype_code(dtype), *geo, st(wt), st(full))
+    assert total > 0 and total % n == 0
+    for ws_bytes in (total // n, total // n - 16):
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
+        out = torch.empty_like(full)
+        rc = lib.ntops_conv2d(_lib.dtype_code(dtype), *geo, x.data_ptr(), st(x), wt.data_ptr(), st(wt), b.data_ptr(), 1,
+                              out.data_ptr(), st(out), ws.data_ptr(), ws_bytes, _lib.stream_of(out))
+        _lib.check(rc, "conv2d")
+        assert_close(out, full, 1.6e-2, 1.6e-2, f"workspace {ws_bytes}")
+    assert_close(full, oracle(x.cpu(), wt.cpu(), b.cpu(), 1, 1, 1), 1.6e-2, 1.6e-2, "one chunk")
+
+
+@pytest.mark.parametrize("dtype", (torch.float32, torch.bfloat16))
+def test_conv2d_layouts_and_forms(dtype):
+    g = torch.Generator().manual_seed(3)
+    tol = TOL[dtype] if dtype != torch.float32 else (2e-5, 2e-5)
+    # channels-last input (strided NCHW view) on both paths
+    for c, k in ((3, 4), (64, 64)):
+        x = torch.randn(2, c, 15, 16, generator=g).to(dtype)
+        wt = (torch.randn(k, c, 3, 3, generator=g) / (9 * c) ** 0.5).to(dtype)
+        xc = x.cuda().to(memory_format=torch.channels_last)
+        assert not xc.is_contiguous()
+        assert_close(conv2d(xc, wt.cuda(), padding=1), oracle(x, wt, None, 1, 1, 1), *tol, "channels-last")
+        # a sliced (non-contiguous) weight runs the direct kernel
+        wbig = torch.randn(k, c, 3, 5, generator=g).to(dtype)
+        ws = wbig[:, :, :, 1:4]
+        assert_close(conv2d(x.cuda(), wbig.cuda()[:, :, :, 1:4], stride=2), oracle(x, ws.contiguous(), None, 2, 0, 1),
+                     *tol, "strided weight")
+    # unbatched input, 'valid' and 'same' (asymmetric: even kernel)
+    x = torch.randn(3, 12, 13, generator=g).to(dtype)
+    wt = torch.randn(5, 3, 2, 4, generator=g).to(dtype)
+    b = torch.randn(5, generator=g).to(dtype)
+    got = conv2d(x.cuda(), wt.cuda(), b.cuda(), padding="valid")
+    assert got.shape == (5, 11, 10)
+    assert_close(got, oracle(x[None], wt, b, 1, 0, 1)[0], *tol, "valid")
+    got = conv2d(x.cuda(), wt.cuda(), b.cuda(), padding="same")
+    assert got.shape == (5, 12, 13)
+    assert_close(got, oracle(x[None], wt, b, 1, (0, 1), 1, (12, 13))[0], *tol, "same")
+
+
+def test_conv2d_argument_checks():
+    x = torch.randn(1, 4, 8, 8, device="cuda")
+    w = torch.randn(4, 4, 3, 3, device="cuda")
+    with pytest.raises(AssertionError):
+        conv2d(x, w, groups=2)
+    with pytest.raises(RuntimeError):
+        conv2d(x, w.half())
+    with pytest.raises(RuntimeError):
+        conv2d(x, w, padding="same", stride=2)
+    with pytest.raises(RuntimeError):
+        conv2d(x, torch.randn(4, 4, 9, 9, device="cuda"))
+    with pytest.raises(RuntimeError):
+        conv2d(x, torch.randn(4, 3, 3, 3, device="cuda"))
+
+
+def test_conv2d_workload_full_size():
+    """bf16 (32, 256, 56, 56) * (256, 256, 3, 3), padding 1: images 0 and 31
+    on 16 output channels against the oracle, and every output finite."""
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(32, 256, 56, 56, generator=g).to(dtype)
+    wt = (torch.randn(256, 256, 3, 3, generator=g) / 48).to(dtype)
+    b = torch.randn(256, generator=g).to(dtype)
+    got = conv2d(x.cuda(), wt.cuda(), b.cuda(), padding=1)
+    ch = torch.arange(0, 256, 16)
+    for img in (0, 31):
+        exp = oracle(x[img:img + 1], wt[ch], b[ch], 1, 1, 1)
+        assert_close(got[img:img + 1, ch], exp, 1.6e-2, 1.6e-2, f"image {img}")
+    assert torch.isfinite(got).all()
