@@ -148,6 +148,8 @@ KERNEL_OF = {
     "layer_norm": "k_ln_vec",
     "softmax": "k_softmax_vec",
     "rope": "k_rope_half_vec",
+    "rope_qk": "k_rope_half_vec",
+    "add_rms_norm": "k_add_rms_vec",
     "mm": "k_gemm_mfma",
     "addmm": "k_gemm_mfma",
     "bmm": "k_gemm_panel",
@@ -391,6 +393,48 @@ def make_workloads():
     W.append(Workload("rope", "rotary_position_embedding bf16 q and k (4, 4096, 32, 128), (4096, 128) tables, "
                       "non-interleaved", "GB/s", "hbm", 2 * (2 * RB * RS * RH * RD * 2 + 2 * RS * RD * 2), 2,
                       rope_build, rope_step, rope_cpu, "bf16"))
+
+    # the same q and k rotated in one launch (tables read once)
+    def rope_qk_step(s):
+        check(lib.ntops_rope_qk(_lib.BF16, RB, RS, RH, RH, RD, s["q"].data_ptr(), s["st"], s["k"].data_ptr(),
+                                s["st"], sin_t.data_ptr(), cos_t.data_ptr(), RD, RD, 0, s["qo"].data_ptr(), s["st"],
+                                s["ko"].data_ptr(), s["st"], stream()), "rope_qk")
+
+    def rope_qk_cpu():
+        run, work, sample = rope_cpu()
+        return run, work, sample + " (q and k cost the same)"
+
+    W.append(Workload("rope_qk", "rotary_position_embedding_qk bf16 q and k (4, 4096, 32, 128) in one launch, "
+                      "(4096, 128) tables, non-interleaved", "GB/s", "hbm",
+                      2 * 2 * RB * RS * RH * RD * 2 + 2 * RS * RD * 2, 1, rope_build, rope_qk_step, rope_qk_cpu,
+                      "bf16"))
+
+    # residual add + rms_norm bf16 (16384, 4096): reads x and the residual,
+    # writes the new residual and the output
+    def arn_build(i):
+        s = norm_build(i)
+        s["r"] = torch.randn(R, C, device="cuda", generator=_gen(150 + i)).bfloat16()
+        s["ro"] = torch.empty_like(s["x"])
+        return s
+
+    def arn_step(s):
+        check(lib.ntops_add_rms_norm(_lib.BF16, R, C, s["x"].data_ptr(), C, s["r"].data_ptr(), C, s["w"].data_ptr(),
+                                     _lib.BF16, 1e-6, s["y"].data_ptr(), C, s["ro"].data_ptr(), C, stream()),
+              "add_rms_norm")
+
+    def arn_cpu():
+        x, w, _ = norm_cpu_inputs()
+        r = torch.randn(x.shape, generator=_cpu_gen(1)).bfloat16()
+
+        def run():
+            h = x + r
+            return F.rms_norm(h, (C,), w, 1e-6), h
+
+        return run, 4 * x.numel() * 2 + C * 2, "torch x + residual then F.rms_norm, bf16 (4096, 4096) = 1/4 of the workload"
+
+    W.append(Workload("add_rms_norm", "add_rms_norm bf16 (16384, 4096): new residual = x + residual, "
+                      "rms_norm(new residual) * weight, eps 1e-6", "GB/s", "hbm", 4 * R * C * 2 + C * 2, 1,
+                      arn_build, arn_step, arn_cpu, "bf16"))
 
     # GEMMs
     M, N, K = 8192, 14336, 4096

@@ -36,6 +36,13 @@
  *                        kernels/mm.py:54-65, kernels/bmm.py:8-43,
  *                        kernels/addmm.py:64-67
  *   ntops_conv2d      <- src/ntops/torch/conv2d.py:8-53, kernels/conv2d.py:12-104
+ *   ntops_add_rms_norm <- no ntops counterpart: the composition
+ *                        rms_norm(x + residual) (torch/add.py:7-15 then
+ *                        torch/rms_norm.py:9-31) fused into one pass that also
+ *                        returns the new residual
+ *   ntops_rope_qk     <- no ntops counterpart: two calls of
+ *                        torch/rotary_position_embedding.py:7-29 (q and k with
+ *                        the same tables) in one launch
  *   ntops_conv2d_workspace <- no ntops counterpart (Triton tiles the unfolded
  *                        input on the fly); sizes the caller-owned buffer that
  *                        the GEMM path of ntops_conv2d unfolds into
@@ -263,6 +270,31 @@ NTOPS_API int ntops_sdpa(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t 
                const void* mask, int mask_dtype, const int64_t* mask_strides,
                int causal, double scale,
                void* out, const int64_t* out_strides, void* stream);
+
+/* ---- fused variants ------------------------------------------------------- */
+/* residual_out = x + residual (rounded to dtype) and y = rms_norm(residual_out)
+ * over rows x cols with the conventions of ntops_rms_norm (weight of dtype or
+ * F32, may be NULL; fp32 accumulation; one rounding).  Element for element
+ * equal to ntops_binary(ADD) followed by ntops_rms_norm, in one pass (reads
+ * x and residual once, writes residual_out and y once).  y may alias x and
+ * residual_out may alias residual; y and residual_out must differ. */
+NTOPS_API int ntops_add_rms_norm(int dtype, int64_t rows, int64_t cols,
+               const void* x, int64_t x_row_stride,
+               const void* residual, int64_t residual_row_stride,
+               const void* w, int w_dtype, double eps,
+               void* y, int64_t y_row_stride,
+               void* residual_out, int64_t residual_out_row_stride, void* stream);
+
+/* ntops_rope on q (B, S, Hq, D) and k (B, S, Hk, D) with the same sin / cos
+ * tables in one launch (either head count may be 0); results equal two
+ * ntops_rope calls.  In-place per tensor is allowed with equal strides. */
+NTOPS_API int ntops_rope_qk(int dtype, int64_t B, int64_t S, int64_t Hq, int64_t Hk, int64_t D,
+               const void* q, const int64_t* q_strides,
+               const void* k, const int64_t* k_strides,
+               const void* sin_table, const void* cos_table,
+               int64_t table_row_stride, int64_t table_cols, int interleaved,
+               void* q_out, const int64_t* q_out_strides,
+               void* k_out, const int64_t* k_out_strides, void* stream);
 
 /* ---- convolution -------------------------------------------------------- */
 /* out (N, K, P, Q) = conv2d(x (N, C, H, W), w (K, C, R, S)) + bias (K),

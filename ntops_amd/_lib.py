@@ -76,6 +76,15 @@ _SIGNATURES = {
         [_i, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _i, _c_i64p,
          _i, _d, _vp, _c_i64p, _vp],
     ),
+    "ntops_add_rms_norm": (
+        _i,
+        [_i, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i, _d, _vp, _i64, _vp, _i64, _vp],
+    ),
+    "ntops_rope_qk": (
+        _i,
+        [_i, _i64, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _vp, _i64, _i64, _i, _vp, _c_i64p,
+         _vp, _c_i64p, _vp],
+    ),
     "ntops_conv2d_workspace": (
         _i64,
         [_i] + [_i64] * 15 + [_c_i64p, _c_i64p],

@@ -9,6 +9,12 @@
 //              rstd = 1 / sqrt(var + eps); written as torch's CPU kernel
 //              evaluates it: y = (x * rstd + (-mean * rstd)) * w + b.
 //
+//   add_rms_norm  (no ntops counterpart; the residual step of an LLM block)
+//              h = x + residual rounded to the element type (what torch's
+//              `x + residual` produces), written out as the new residual,
+//              then y = rms_norm(h) as above -- identical, element for
+//              element, to the two separate kernels, in one pass.
+//
 // Vector path: one HBM read + one HBM write per element, row held in VGPRs
 // (see rowcommon.h).  Looped path (unaligned rows, or rows wider than 64K
 // 16-bit elements): one 256-thread block per row, scalar strided accesses,
@@ -96,6 +102,91 @@ __global__ __launch_bounds__(256) void k_rms_loop(const T* x, int64_t xs, const 
   for (int64_t j = threadIdx.x; j < cols; j += 256) {
     const float wv = w != nullptr ? static_cast<float>(w[j]) : 1.0f;
     yr[j] = static_cast<T>(mul_nc(mul_nc(to_f(xr[j]), rstd), wv));
+  }
+}
+
+// ---------------------------------------------------- residual + rms_norm --
+// Reads x and residual once, writes the rounded sum h (the new residual) and
+// y = rms_norm(h); h stays in VGPRs between the two.  out / res_out may
+// alias x / residual (each element is read and written by one thread).
+template <typename T, typename W, int CHUNKS, int WPR>
+__global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
+    const T* x, int64_t xs, const T* res, int64_t rs, const W* __restrict__ w, T* y, int64_t ys, T* ro,
+    int64_t ros, int64_t rows, int cols, float eps) {
+  constexpr int V = Pack16<T>::N;
+  constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
+  __shared__ float red[RPB * WPR];
+  const RowPos p = row_pos<WPR>();
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + p.row_in_block;
+  const bool row_ok = row < rows;
+  const int npk = cols / V;
+
+  Pack16<T> h[CHUNKS];
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int pk = pack_of<WPR>(p, c);
+    if (row_ok && pk < npk) {
+      const Pack16<T> a = load16_nt(x + row * xs + pk * V);
+      const Pack16<T> b = load16_nt(res + row * rs + pk * V);
+#pragma unroll
+      for (int i = 0; i < V; ++i) h[c].v[i] = static_cast<T>(add_nc(to_f(a.v[i]), to_f(b.v[i])));
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) h[c].v[i] = T(0);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float f = to_f(h[c].v[i]);
+      ss += f * f;
+    }
+  ss = row_sum<WPR>(ss, red, p);
+  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+
+  if (!row_ok) return;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int pk = pack_of<WPR>(p, c);
+    if (pk < npk) {
+      store16_nt(ro + row * ros + pk * V, h[c]);
+      float wv[V];
+      if (w != nullptr)
+        load_as_float<W, V>(w + pk * V, wv);
+      else
+#pragma unroll
+        for (int i = 0; i < V; ++i) wv[i] = 1.0f;
+      Pack16<T> o;
+#pragma unroll
+      for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(h[c].v[i]), rstd), wv[i]));
+      store16_nt(y + row * ys + pk * V, o);
+    }
+  }
+}
+
+// Looped form: one block per row; pass 1 forms and stores h and its sum of
+// squares, pass 2 re-reads h from the stored new residual (each element is
+// re-read by the thread that wrote it).
+template <typename T, typename W>
+__global__ __launch_bounds__(256) void k_add_rms_loop(const T* x, int64_t xs, const T* res, int64_t rs,
+                                                       const W* w, T* y, int64_t ys, T* ro, int64_t ros,
+                                                       int64_t cols, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  float ss = 0.f;
+  for (int64_t j = threadIdx.x; j < cols; j += 256) {
+    const T hv = static_cast<T>(add_nc(to_f(x[row * xs + j]), to_f(res[row * rs + j])));
+    ro[row * ros + j] = hv;
+    const float f = to_f(hv);
+    ss += f * f;
+  }
+  ss = block_sum256(ss, red);
+  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+  for (int64_t j = threadIdx.x; j < cols; j += 256) {
+    const float wv = w != nullptr ? static_cast<float>(w[j]) : 1.0f;
+    y[row * ys + j] = static_cast<T>(mul_nc(mul_nc(to_f(ro[row * ros + j]), rstd), wv));
   }
 }
 
@@ -261,6 +352,37 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
   return check_launch("layer_norm");
 }
 
+template <typename T, typename W>
+int run_add_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* rv, int64_t rs,
+                const void* wv, double eps, void* yv, int64_t ys, void* rov, int64_t ros, hipStream_t st) {
+  const T* x = static_cast<const T*>(xv);
+  const T* r = static_cast<const T*>(rv);
+  const W* w = static_cast<const W*>(wv);
+  T* y = static_cast<T*>(yv);
+  T* ro = static_cast<T*>(rov);
+  constexpr int V = Pack16<T>::N;
+  VecCfg cfg;
+  const bool vec = (cols % V == 0) && (xs % V == 0) && (rs % V == 0) && (ys % V == 0) && (ros % V == 0) &&
+                   aligned16(x) && aligned16(r) && aligned16(y) && aligned16(ro) && (w == nullptr || aligned16(w)) &&
+                   pick_row_cfg(cols / V, &cfg);
+  const float feps = static_cast<float>(eps);
+  if (vec) {
+#define NTOPS_ADD_RMS_CASE(CH, WP)                                                            \
+  if (cfg.chunks == CH && cfg.wpr == WP) {                                                    \
+    constexpr int RPB = RowShape<WP>::kRowsPerBlock;                                          \
+    hipLaunchKernelGGL((k_add_rms_vec<T, W, CH, WP>), dim3(ceil_div(rows, RPB)),              \
+                       dim3(RowShape<WP>::kThreads), 0, st, x, xs, r, rs, w, y, ys, ro, ros,  \
+                       rows, static_cast<int>(cols), feps);                                   \
+    return check_launch("add_rms_norm");                                                      \
+  }
+    NTOPS_ROW_CASES(NTOPS_ADD_RMS_CASE)
+#undef NTOPS_ADD_RMS_CASE
+  }
+  hipLaunchKernelGGL((k_add_rms_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, r, rs, w, y, ys, ro, ros, cols,
+                     feps);
+  return check_launch("add_rms_norm");
+}
+
 int check_rows(const char* what, int64_t rows, int64_t cols, const void* x, const void* y) {
   if (rows < 0 || cols < 0) return set_error(NTOPS_ERR_INVALID, "%s: negative size", what);
   if (rows > 0 && cols > 0 && (x == nullptr || y == nullptr))
@@ -304,5 +426,26 @@ extern "C" int ntops_layer_norm(int dtype, int64_t rows, int64_t cols, const voi
     if ((w != nullptr || b != nullptr) && wb_dtype == NTOPS_F32 && dtype != NTOPS_F32)
       return run_ln<T, float>(rows, cols, x, x_row_stride, w, b, eps, y, y_row_stride, st);
     return run_ln<T, T>(rows, cols, x, x_row_stride, w, b, eps, y, y_row_stride, st);
+  });
+}
+
+extern "C" int ntops_add_rms_norm(int dtype, int64_t rows, int64_t cols, const void* x, int64_t x_row_stride,
+                                  const void* residual, int64_t residual_row_stride, const void* w, int w_dtype,
+                                  double eps, void* y, int64_t y_row_stride, void* residual_out,
+                                  int64_t residual_out_row_stride, void* stream) {
+  if (int e = check_rows("add_rms_norm", rows, cols, x, y)) return e;
+  if (rows == 0 || cols == 0) return NTOPS_OK;
+  if (residual == nullptr || residual_out == nullptr) return set_error(NTOPS_ERR_INVALID, "add_rms_norm: null pointer");
+  if (y == residual_out) return set_error(NTOPS_ERR_INVALID, "add_rms_norm: out and residual_out must differ");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (w != nullptr && w_dtype != dtype && w_dtype != NTOPS_F32)
+    return set_error(NTOPS_ERR_UNSUPPORTED, "add_rms_norm: weight dtype must equal input dtype or be F32");
+  return dispatch_float16_32(dtype, "add_rms_norm", [&](auto tag) {
+    using T = decltype(tag);
+    if (w != nullptr && w_dtype == NTOPS_F32 && dtype != NTOPS_F32)
+      return run_add_rms<T, float>(rows, cols, x, x_row_stride, residual, residual_row_stride, w, eps, y,
+                                   y_row_stride, residual_out, residual_out_row_stride, st);
+    return run_add_rms<T, T>(rows, cols, x, x_row_stride, residual, residual_row_stride, w, eps, y, y_row_stride,
+                             residual_out, residual_out_row_stride, st);
   });
 }

@@ -4,6 +4,7 @@ family."""
 
 from ntops_amd.torch.abs import abs
 from ntops_amd.torch.add import add
+from ntops_amd.torch.add_rms_norm import add_rms_norm
 from ntops_amd.torch.addmm import addmm
 from ntops_amd.torch.bitwise_and import bitwise_and
 from ntops_amd.torch.bitwise_not import bitwise_not
@@ -32,6 +33,7 @@ from ntops_amd.torch.pow import pow
 from ntops_amd.torch.relu import relu
 from ntops_amd.torch.rms_norm import rms_norm
 from ntops_amd.torch.rotary_position_embedding import rotary_position_embedding
+from ntops_amd.torch.rotary_position_embedding_qk import rotary_position_embedding_qk
 from ntops_amd.torch.rsqrt import rsqrt
 from ntops_amd.torch.scaled_dot_product_attention import scaled_dot_product_attention
 from ntops_amd.torch.sigmoid import sigmoid
@@ -44,6 +46,7 @@ from ntops_amd.torch.tanh import tanh
 __all__ = [
     "abs",
     "add",
+    "add_rms_norm",
     "addmm",
     "bitwise_and",
     "bitwise_not",
@@ -72,6 +75,7 @@ __all__ = [
     "relu",
     "rms_norm",
     "rotary_position_embedding",
+    "rotary_position_embedding_qk",
     "rsqrt",
     "scaled_dot_product_attention",
     "sigmoid",

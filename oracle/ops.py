@@ -742,3 +742,19 @@ def conv2d(x, w, dt, bias=None, stride=(1, 1), pad=(0, 0), dilation=(1, 1), out_
     if bias is not None:
         out += to_compute(bias, dt).astype(np.float64)[None, :, None, None]
     return round_to(out.astype(np.float32) if dt != "f64" else out, dt)
+
+
+def add_rms_norm(x, residual, dt, cols, weight=None, eps=None, w_dt=None):
+    """No ntops counterpart: the composition add (kernels/add.py:10, alpha 1)
+    then rms_norm (kernels/rms_norm.py:10-20) that the fused kernel computes in
+    one pass.  Returns (rms_norm(h), h) with h = x + residual rounded to dt."""
+    h = add(x, residual, dt)
+    return rms_norm(h, dt, cols, weight, eps, w_dt), h
+
+
+def rotary_position_embedding_qk(q, k, sin_table, cos_table, dt, interleaved=True):
+    """No ntops counterpart: kernels/rotary_position_embedding.py:6-47 applied
+    to q and to k with the same tables (two calls of
+    rotary_position_embedding).  Returns (q_out, k_out)."""
+    return (rotary_position_embedding(q, sin_table, cos_table, dt, interleaved),
+            rotary_position_embedding(k, sin_table, cos_table, dt, interleaved))
