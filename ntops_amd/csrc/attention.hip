@@ -310,8 +310,10 @@ __global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int t
 
 // ---- flash forward without an explicit mask (none or causal) ---------------
 //
-// One 8-wave workgroup per (batch, head, 256 query rows), one per CU; wave w
-// owns rows 32w .. 32w + 31 of the block with their Q fragments in VGPRs.
+// 8-wave workgroups over work items of (batch, head, 256 query rows) -- one
+// per item, or (causal) persistent, one per CU walking items longest first;
+// wave w owns rows 32w .. 32w + 31 of the item with their Q fragments in
+// VGPRs.
 // K and V tiles of 64 keys go global -> LDS by direct DMA (no VGPR staging)
 // into a ring of kFaStages stages; tile t lives in stage t % kFaStages, with
 // the swizzles of k_frag / v_frag applied on the global side (a lane's LDS
@@ -390,7 +392,35 @@ struct KvDma {
   }
 };
 
-template <typename T, int D, bool CAUSAL>
+// Work item of this workgroup in round r (false: no more items).
+// Workgroups are dispatched round-robin over the 8 XCDs, so workgroup g runs
+// on XCD g % 8; with a grid that is a multiple of 8, XCD x owns the heads
+// bh = x, x + 8, ...  Its workgroups process those heads in groups of HG
+// heads whose HG * nqb query blocks roughly fill them (so a head's K / V is
+// read into the XCD's L2 once per group); within a group, items go longest
+// query block first (more keys under a causal mask), and the slot order is
+// reversed every other round so that long and short items pair up.
+__device__ __forceinline__ bool fa_item(int r, int nbh, int nqb, int& bh, int& qb) {
+  const int grid = static_cast<int>(gridDim.x);
+  const int nx = (grid % 8 == 0) ? 8 : 1;
+  const int x = static_cast<int>(blockIdx.x) % nx;
+  const int gl = grid / nx;                      // workgroups on this XCD
+  const int lb = static_cast<int>(blockIdx.x) / nx;
+  const int hx = nbh > x ? (nbh - x + nx - 1) / nx : 0;  // heads of this XCD
+  const int li = r * gl + ((r & 1) ? gl - 1 - lb : lb);
+  if (li >= hx * nqb) return false;
+  const int hg = max(1, gl / nqb);              // heads per group
+  const int g = li / (hg * nqb);
+  const int hg_g = min(hg, hx - g * hg);         // the last group may be smaller
+  const int pos = li - g * hg * nqb;
+  const int rank = pos / hg_g;
+  const int hl = g * hg + (pos - rank * hg_g);
+  bh = hl * nx + x;
+  qb = nqb - 1 - rank;
+  return true;
+}
+
+template <typename T, int D, bool CAUSAL, bool PERSIST>
 __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int total) {
   constexpr int BN = 64;
   constexpr int NS = kFaStages;
@@ -406,8 +436,13 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2;  // 0: leads, 1: one phase behind (one wave of each per SIMD)
-  int bh, qb;
-  attn_block(blockIdx.x, total, nqb, bh, qb);
+  // One work item (batch * head, query block) per workgroup, or, in the
+  // persistent form (causal: items of unequal length), one workgroup per CU
+  // walking the items that fa_item picks so that a head's query blocks run
+  // together on one XCD (its K and V stay in that L2) and per-workgroup work
+  // evens out.  (Equal items are left to the hardware dispatcher, which also
+  // lets a finished workgroup's stores drain off the next one's path.)
+  auto item = [&](int bh, int qb) {
   const int b = bh / a.Hq, h = bh - b * a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
   const int q0 = qb * kFaRows;
@@ -599,21 +634,35 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
       if (k - 1 <= jl) matrix_phase(k - 1);
     }
   }
-  wait_vmcnt<0>();  // no DMA may land after the workgroup ends
+  wait_vmcnt<0>();  // this item's DMA has landed (the next item reuses the stages)
 
   const float l = l_half + __shfl_xor(l_half, 32, 64);
-  if (my_q >= a.Sq) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  T* O = static_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(my_q) * a.os[2];
+  if (my_q < a.Sq) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    T* O = static_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(my_q) * a.os[2];
 #pragma unroll
-  for (int t = 0; t < DT; ++t)
+    for (int t = 0; t < DT; ++t)
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      T v4[4];
+      for (int qq = 0; qq < 4; ++qq) {
+        T v4[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
-      *reinterpret_cast<u32x2*>(O + t * 32 + 8 * qq + 4 * (lane >> 5)) = __builtin_bit_cast(u32x2, v4);
+        for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
+        *reinterpret_cast<u32x2*>(O + t * 32 + 8 * qq + 4 * (lane >> 5)) = __builtin_bit_cast(u32x2, v4);
+      }
+  }
+  };  // item
+  if constexpr (PERSIST) {
+    for (int round = 0;; ++round) {
+      int bh, qb;
+      if (!fa_item(round, a.B * a.Hq, nqb, bh, qb)) break;
+      if (round > 0) block_barrier();  // every wave is done with the previous item's LDS stages
+      item(bh, qb);
     }
+  } else {
+    int bh, qb;
+    attn_block(static_cast<int>(blockIdx.x), total, nqb, bh, qb);
+    item(bh, qb);
+  }
 }
 
 // Generic path: one wave per (batch, head, query row); lane owns d = lane +
@@ -673,10 +722,25 @@ __global__ __launch_bounds__(64) void k_attn_generic(AttnArgs a) {
   }
 }
 
+// Number of CUs of the current device (queried once per device; 256 if the
+// query fails).
+int cu_count_cached() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 template <typename T, int D, bool CAUSAL>
 int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
   constexpr int kLds = kFaStages * 2 * 64 * D * 2;
-  auto kern = k_flash_attn<T, D, CAUSAL>;
+  constexpr bool kPersist = CAUSAL;
+  auto kern = k_flash_attn<T, D, CAUSAL, kPersist>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -686,8 +750,10 @@ int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
   }
   const int nqb = (a.Sq + kFaRows - 1) / kFaRows;
   const int64_t total = static_cast<int64_t>(nqb) * a.Hq * a.B;
-  if (total > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many blocks");
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(total)), dim3(kFaWaves * 64), kLds, st, a, nqb,
+  if (total > 0x3fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many work items");
+  // persistent: one workgroup per CU (each takes 128 KiB of LDS)
+  const int64_t grid = kPersist ? std::min<int64_t>(total, cu_count_cached()) : total;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kFaWaves * 64), kLds, st, a, nqb,
                      static_cast<int>(total));
   return check_launch("sdpa");
 }
