@@ -7,7 +7,15 @@
 // lines 102-104), torch/conv2d.py:8-53 (argument forms, output size from
 // torch/pooling.py:4-19, groups == 1).
 //
-// Two paths:
+// Three paths:
+//  * implicit GEMM (stride 1, bf16 / fp16, output rows of a multiple of 8
+//    pixels): each image is copied once into a caller-owned workspace as S
+//    column-shifted, zero-padded planes xs[s][c][row][q] =
+//    x[c][row - ph][q + s * dw - pw] with Hp = P + (R - 1) * dh rows of Q
+//    pixels, so that the unfolded row (c, r, s) is the contiguous run
+//    xs[s][c][r * dh ..][0 ..) of P * Q pixels -- the GEMM's operand loader
+//    computes each k-row's base from (c, r, s) instead of reading a
+//    materialised unfold (3x the input instead of R * S x);
 //  * GEMM path (when C * R * S and K are large enough to feed the matrix
 //    cores): the input of a chunk of images is unfolded into a caller-owned
 //    workspace col[n][c * R * S + r * S + s][p * Q + q] (k-rows padded to a
@@ -18,7 +26,7 @@
 //    FMA GEMM.
 //  * direct path (small channel counts, any strides): one thread per output
 //    element, fp32 accumulation.
-#include "dispatch.h"
+#include "gemm.h"
 
 namespace ntops {
 namespace {
@@ -127,12 +135,7 @@ __global__ __launch_bounds__(256) void k_im2col_plane(ConvArgs a, T* col, int n0
   T* plane = reinterpret_cast<T*>(sm);
   const int b = blockIdx.x / a.C;
   const int c = blockIdx.x - b * a.C;
-  const T* xc = static_cast<const T*>(a.x) + (n0 + b) * a.xs[0] + c * a.xs[1];
-  const int hw = a.H * a.W;
-  for (int i = threadIdx.x; i < hw; i += blockDim.x) {
-    const int ih = i / a.W, iw = i - (i / a.W) * a.W;
-    plane[i] = xc[ih * a.xs[2] + iw * a.xs[3]];
-  }
+  stage_plane<T>(a, static_cast<const T*>(a.x) + (n0 + b) * a.xs[0] + c * a.xs[1], plane);
   __syncthreads();
   const int rs = a.R * a.S;
   const int pq = a.P * a.Q;
@@ -179,6 +182,99 @@ __global__ __launch_bounds__(256) void k_im2col_plane(ConvArgs a, T* col, int n0
   }
 }
 
+// xs[b][s][c][row][q] for images n0 .. n0 + nb - 1 (stride-1 convolutions):
+// one thread per 8 consecutive q of one (b, s, c, row).
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_shift(ConvArgs a, T* xs, int n0, int nb, int hp) {
+  const int q8 = a.Q / 8;
+  const int64_t total = static_cast<int64_t>(nb) * a.S * a.C * hp * q8;
+  const T* x = static_cast<const T*>(a.x);
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int qc = static_cast<int>(i % q8);
+    int64_t t = i / q8;
+    const int row = static_cast<int>(t % hp);
+    t /= hp;
+    const int c = static_cast<int>(t % a.C);
+    t /= a.C;
+    const int s = static_cast<int>(t % a.S);
+    const int b = static_cast<int>(t / a.S);
+    const int ih = row - a.ph;
+    const int iw0 = qc * 8 + s * a.dw - a.pw;
+    const T* xr = x + (n0 + b) * a.xs[0] + c * a.xs[1] + static_cast<int64_t>(ih) * a.xs[2];
+    const bool row_ok = ih >= 0 && ih < a.H;
+    T v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int iw = iw0 + e;
+      v[e] = (row_ok && iw >= 0 && iw < a.W) ? xr[iw * a.xs[3]] : static_cast<T>(0.f);
+    }
+    *reinterpret_cast<u32x4*>(xs + i * 8) = __builtin_bit_cast(u32x4, v);
+  }
+}
+
+// Same output as k_conv_shift, one workgroup per (image, channel) with the
+// input plane staged in LDS (read from HBM once); every thread then writes
+// 16-byte runs of the S shifted planes.
+// Same output as k_conv_shift, one workgroup per (image, channel) with the
+// input plane staged in LDS (read from HBM once); every thread then writes
+// 16-byte runs of the S shifted planes.
+// Stages x[n][c] (H x W elements) into LDS: 16-byte loads when the rows are
+// contiguous, 16-byte aligned runs of a multiple of 8 elements, else one
+// element per load.
+template <typename T>
+__device__ __forceinline__ void stage_plane(const ConvArgs& a, const T* xc, T* plane) {
+  constexpr int V = 16 / sizeof(T);
+  const int hw = a.H * a.W;
+  if (a.xs[3] == 1 && a.W % V == 0 && a.xs[2] % V == 0 && (reinterpret_cast<uintptr_t>(xc) & 15u) == 0) {
+    const int wv = a.W / V;
+    for (int i = threadIdx.x; i < a.H * wv; i += blockDim.x) {
+      const int ih = i / wv, c8 = i - (i / wv) * wv;
+      *reinterpret_cast<u32x4*>(plane + ih * a.W + c8 * V) = *reinterpret_cast<const u32x4*>(xc + ih * a.xs[2] + c8 * V);
+    }
+  } else {
+    for (int i = threadIdx.x; i < hw; i += blockDim.x) {
+      const int ih = i / a.W, iw = i - (i / a.W) * a.W;
+      plane[i] = xc[ih * a.xs[2] + iw * a.xs[3]];
+    }
+  }
+}
+
+// Same output as k_conv_shift, one workgroup per (image, channel) with the
+// input plane staged in LDS (read from HBM once); a thread then writes the
+// same 8-pixel run of every shifted plane.
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_shift_plane(ConvArgs a, T* xs, int n0, int hp) {
+  extern __shared__ __attribute__((aligned(16))) char sm[];  // H * W elements
+  T* plane = reinterpret_cast<T*>(sm);
+  const int b = blockIdx.x / a.C;
+  const int c = blockIdx.x - b * a.C;
+  stage_plane<T>(a, static_cast<const T*>(a.x) + (n0 + b) * a.xs[0] + c * a.xs[1], plane);
+  __syncthreads();
+  const int q8 = a.Q / 8;
+  const int64_t plane_elems = static_cast<int64_t>(hp) * a.Q;
+  const int64_t s_stride = static_cast<int64_t>(a.C) * plane_elems;  // between shifted planes
+  T* dst0 = xs + (static_cast<int64_t>(b) * a.S * a.C + c) * plane_elems;
+  for (int j = threadIdx.x; j < hp * q8; j += blockDim.x) {
+    const int row = j / q8;
+    const int q0 = (j - row * q8) * 8;
+    const int ih = row - a.ph;
+    const bool row_ok = static_cast<unsigned>(ih) < static_cast<unsigned>(a.H);
+    T* dst = dst0 + static_cast<int64_t>(row) * a.Q + q0;
+    for (int s = 0; s < a.S; ++s) {
+      const int iw0 = q0 + s * a.dw - a.pw;
+      T v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int iw = iw0 + e;
+        v[e] = (row_ok && static_cast<unsigned>(iw) < static_cast<unsigned>(a.W)) ? plane[ih * a.W + iw]
+                                                                                  : static_cast<T>(0.f);
+      }
+      *reinterpret_cast<u32x4*>(dst + s * s_stride) = __builtin_bit_cast(u32x4, v);
+    }
+  }
+}
+
 unsigned grid_for(int64_t work, int per_block) {
   int64_t g = (work + per_block - 1) / per_block;
   if (g > 65536) g = 65536;  // grid-stride loops cover the rest
@@ -203,6 +299,21 @@ bool use_gemm(const ConvArgs& a, int dt) {
 
 int64_t col_bytes_per_image(const ConvArgs& a, int dt) {
   return static_cast<int64_t>(a.C) * a.R * a.S * col_ld(a) * dtype_size(dt);
+}
+
+// Rows of each shifted plane of the implicit path.
+int64_t shift_rows(const ConvArgs& a) { return static_cast<int64_t>(a.P) + static_cast<int64_t>(a.R - 1) * a.dh; }
+
+// Whether the implicit GEMM applies (on top of use_gemm).
+bool use_implicit(const ConvArgs& a, int dt) {
+  const int64_t elems = static_cast<int64_t>(a.S) * a.C * shift_rows(a) * a.Q;
+  return (dt == NTOPS_BF16 || dt == NTOPS_F16) && a.sh == 1 && a.sw == 1 && a.Q % 8 == 0 && elems * 2 < (int64_t(1) << 31);
+}
+
+// Workspace bytes per image of the chosen GEMM path.
+int64_t ws_bytes_per_image(const ConvArgs& a, int dt) {
+  if (use_implicit(a, dt)) return static_cast<int64_t>(a.S) * a.C * shift_rows(a) * a.Q * dtype_size(dt);
+  return col_bytes_per_image(a, dt);
 }
 
 int fill_args(ConvArgs& a, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
@@ -247,7 +358,7 @@ extern "C" int64_t ntops_conv2d_workspace(int dtype, int64_t N, int64_t C, int64
   }
   a.w = nullptr;  // alignment is checked again on the call
   if (!use_gemm(a, dtype)) return 0;
-  return col_bytes_per_image(a, dtype) * N;
+  return ws_bytes_per_image(a, dtype) * N;
 }
 
 extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R,
@@ -274,7 +385,7 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
     a.os[i] = out_strides[i];
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t per_image = dtype_size(dtype) ? col_bytes_per_image(a, dtype) : 0;
+  const int64_t per_image = dtype_size(dtype) ? ws_bytes_per_image(a, dtype) : 0;
   const bool gemm = dtype_size(dtype) && use_gemm(a, dtype) && workspace && per_image > 0 &&
                     workspace_bytes >= per_image && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0;
   if (!gemm) {
@@ -285,8 +396,41 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
       return check_launch("conv2d");
     });
   }
-  // GEMM path, in chunks of images that fit the workspace
   const int64_t crs = C * R * S;
+  if (use_implicit(a, dtype)) {
+    // implicit GEMM, in chunks of images that fit the workspace
+    const int64_t hp = shift_rows(a);
+    const int64_t plane = hp * Q;  // elements of one shifted plane of one channel
+    const int64_t nb_max = std::min<int64_t>(N, workspace_bytes / per_image);
+    for (int64_t n0 = 0; n0 < N; n0 += nb_max) {
+      const int64_t nb = std::min(nb_max, N - n0);
+      rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
+        using T = decltype(tag);
+        if constexpr (sizeof(T) != 2) {
+          return set_error(NTOPS_ERR_INVALID, "conv2d: the implicit path needs 16-bit data");
+        } else {
+          if (H * W * static_cast<int64_t>(sizeof(T)) <= kPlaneLds && nb * C <= 0x7fffffffLL)
+            hipLaunchKernelGGL(k_conv_shift_plane<T>, dim3(static_cast<unsigned>(nb * C)), dim3(256),
+                               static_cast<unsigned>(H * W * sizeof(T)), st, a, static_cast<T*>(workspace),
+                               static_cast<int>(n0), static_cast<int>(hp));
+          else
+            hipLaunchKernelGGL(k_conv_shift<T>, dim3(grid_for(nb * S * C * hp * (Q / 8), 256)), dim3(256), 0, st, a,
+                               static_cast<T*>(workspace), static_cast<int>(n0), static_cast<int>(nb),
+                               static_cast<int>(hp));
+          return check_launch("conv2d");
+        }
+      });
+      if (rc != NTOPS_OK) return rc;
+      void* dst = static_cast<char*>(out) + n0 * out_strides[0] * dtype_size(dtype);
+      rc = gemm_implicit_conv(dtype, static_cast<int>(nb), static_cast<int>(K), static_cast<int>(P * Q),
+                              static_cast<int>(crs), w, w_strides[0], workspace, S * C * plane, static_cast<int>(R),
+                              static_cast<int>(S), C * plane, plane, dil_h * Q, bias, bias_stride, dst,
+                              out_strides[0], out_strides[1], st);
+      if (rc != NTOPS_OK) return rc;
+    }
+    return NTOPS_OK;
+  }
+  // GEMM path, in chunks of images that fit the workspace
   const int64_t ld = col_ld(a);
   const int64_t nb_max = std::min<int64_t>(N, workspace_bytes / per_image);
   const int64_t a_str[3] = {0, w_strides[0], 1};

@@ -39,6 +39,7 @@
 //    offset past the resource's extent and read as zero.
 // Generic path (fp32, or any other strides): 64x64 LDS-tiled FMA kernel with
 // fp32 accumulation (IEEE; gfx950 has no reduced-precision fp32 MFMA input).
+#include "gemm.h"
 #include "mfma.h"
 
 namespace ntops {
@@ -57,6 +58,13 @@ struct GemmArgs {
   float alpha, beta;
   int use_c;
   int staged;  // out is 16-byte aligned with unit column stride and N % 8 == 0
+  // Implicit convolution operand (used only by the CONV instantiation): B's
+  // k-row kg = (c * R + r) * S + s starts at element
+  // s * cv_per_s + c * cv_per_c + r * cv_per_r of the batch's B buffer, and
+  // its N elements are contiguous from there.
+  int cv_rs, cv_r, cv_s;
+  int cv_ds, cv_dr, cv_dc;  // BK k-rows expressed as (s, r, c) steps: BK = (dc * R + dr) * S + ds
+  int64_t cv_per_s, cv_per_c, cv_per_r;
 };
 
 
@@ -99,8 +107,9 @@ __device__ __forceinline__ void tile_of(int pid, int nblocks, int tm_count, int 
 // One operand's global -> LDS stream for a tile of R rows/columns x BK k.
 // The tile is R * BK * 2 bytes: R * BK / 512 one-KiB load instructions,
 // spread evenly over the NW waves of the block.
-template <int R, bool KMAJ, int NW, bool EVEN, int BK>
+template <int R, bool KMAJ, int NW, bool EVEN, int BK, bool CONV = false>
 struct TileLoader {
+  static_assert(!CONV || !KMAJ, "the implicit convolution operand is N-major");
   static constexpr int kInst = R * BK / 512 / NW;
   static_assert(kInst * NW * 512 == R * BK, "tile must split evenly over the waves");
   static constexpr int kCprK = BK / 8;  // chunks per row (K-major)
@@ -111,6 +120,9 @@ struct TileLoader {
   int lim_col[kInst];     // K-major: k of the chunk; M/N-major: column of the chunk
   uint32_t k_stride_bytes;
   int lds_base;           // first instruction's LDS offset inside the operand tile
+  // implicit convolution (CONV): this lane's k-row of each instruction for
+  // the next tile to issue, as (c, r, s) -- advanced by BK per tile
+  int cv_c[CONV ? kInst : 1], cv_r[CONV ? kInst : 1], cv_s[CONV ? kInst : 1];
 
   // base: element pointer at the tile origin; ld: row stride (K-major) or
   // k-row stride (M/N-major), in elements; extent_bytes: readable bytes.
@@ -145,9 +157,24 @@ struct TileLoader {
         const int q = wave * kInst + i;
         const int krow = q * rows_per_inst + lane / kCprMN;
         const int c = mnslot(krow, lane % kCprMN);
-        voff[i] = static_cast<uint32_t>(krow * ld * 2 + c * 16);
+        voff[i] = static_cast<uint32_t>((CONV ? 0 : krow * ld * 2) + c * 16);
         lim_row[i] = krow;
         lim_col[i] = c * 8;
+      }
+    }
+  }
+
+  // Implicit convolution: the (c, r, s) of each instruction's k-row at
+  // k0 = 0 (k-row kg = (c * R + r) * S + s).
+  __device__ __forceinline__ void conv_init(const GemmArgs& g) {
+    if constexpr (CONV) {
+#pragma unroll
+      for (int i = 0; i < kInst; ++i) {
+        const int kg = lim_row[i];
+        cv_c[i] = kg / g.cv_rs;
+        const int rs = kg - cv_c[i] * g.cv_rs;
+        cv_r[i] = rs / g.cv_s;
+        cv_s[i] = rs - cv_r[i] * g.cv_s;
       }
     }
   }
@@ -163,10 +190,26 @@ struct TileLoader {
   // Issues the loads of the K tile starting at k0 into `lds` (this operand's
   // tile in one LDS stage).  `valid` is the number of valid tile rows
   // (K-major) or tile columns (M/N-major); K bounds the k axis.
-  __device__ __forceinline__ void issue(char* lds, int k0, int valid, int K) const {
+  // CONV: tiles must be issued in order k0 = 0, BK, 2 BK, ... (each call
+  // advances the (c, r, s) state by BK k-rows).
+  __device__ __forceinline__ void issue(char* lds, int k0, int valid, int K, const GemmArgs* cv = nullptr) {
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
-      uint32_t off = voff[i] + static_cast<uint32_t>(k0) * k_stride_bytes;
+      uint32_t off;
+      if constexpr (CONV) {
+        // row base of k-row (c, r, s), then advance it by BK k-rows
+        const int64_t base = cv_s[i] * cv->cv_per_s + cv_c[i] * cv->cv_per_c + cv_r[i] * cv->cv_per_r;
+        off = voff[i] + static_cast<uint32_t>(base * 2);
+        cv_s[i] += cv->cv_ds;
+        const int cs = cv_s[i] >= cv->cv_s ? 1 : 0;
+        cv_s[i] -= cs * cv->cv_s;
+        cv_r[i] += cv->cv_dr + cs;
+        const int cr = cv_r[i] >= cv->cv_r ? 1 : 0;
+        cv_r[i] -= cr * cv->cv_r;
+        cv_c[i] += cv->cv_dc + cr;
+      } else {
+        off = voff[i] + static_cast<uint32_t>(k0) * k_stride_bytes;
+      }
       if constexpr (!EVEN) {
         bool ok;
         if constexpr (KMAJ)
@@ -337,7 +380,8 @@ constexpr bool kStreamOutPanel = true;
 // STAGES LDS stages, prefetch distance STAGES - 1: the loads of tile
 // kt + STAGES - 1 are issued right after the barrier that opens tile kt, so
 // an operand fetch that misses L2 has STAGES - 1 tiles of MFMA work to land.
-template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN>
+template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN,
+          bool CONV = false>
 __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
@@ -345,7 +389,7 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
   constexpr int kATile = BM * BK * 2, kBTile = BN * BK * 2;
   constexpr int kStage = kATile + kBTile;
   using LA = TileLoader<BM, AK, NW, EVEN, BK>;
-  using LB = TileLoader<BN, BKM, NW, EVEN, BK>;
+  using LB = TileLoader<BN, BKM, NW, EVEN, BK, CONV>;
   constexpr int kLoadsPerTile = LA::kInst + LB::kInst;  // per wave
   static_assert(STAGES >= 2 && STAGES <= 5, "stages");
   extern __shared__ __attribute__((aligned(1024))) char smem[];
@@ -370,7 +414,11 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
             (static_cast<int64_t>(m_valid - 1) * g.sa_m + g.K) * 2, wave, lane);
   else
     la.init(A + m0, g.sa_k, (static_cast<int64_t>(g.K - 1) * g.sa_k + m_valid) * 2, wave, lane);
-  if constexpr (BKM)
+  if constexpr (CONV) {
+    lb.init(B + n0, 0, (g.sb_b - n0) * 2, wave, lane);  // the batch's whole buffer
+    lb.conv_init(g);
+  }
+  else if constexpr (BKM)
     lb.init(B + static_cast<int64_t>(n0) * g.sb_n, g.sb_n,
             (static_cast<int64_t>(n_valid - 1) * g.sb_n + g.K) * 2, wave, lane);
   else
@@ -379,7 +427,7 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
   auto issue = [&](int stage, int k0) {
     char* base = smem + stage * kStage;
     la.issue(base, k0, m_valid, g.K);
-    lb.issue(base + kATile, k0, n_valid, g.K);
+    lb.issue(base + kATile, k0, n_valid, g.K, &g);
   };
 
   f32x16 acc[TM][TN];
@@ -679,11 +727,12 @@ __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
 }
 
 // ---- host dispatch ---------------------------------------------------------
-template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN>
+template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN,
+          bool CONV = false>
 int launch_mfma(const GemmArgs& g, hipStream_t st) {
   constexpr int NT = WM * WN * 64;
   constexpr int kLds = STAGES * (BM + BN) * BK * 2;
-  auto kern = k_gemm_mfma<T, BM, BN, WM, WN, BK, STAGES, AK, BKM, EVEN>;
+  auto kern = k_gemm_mfma<T, BM, BN, WM, WN, BK, STAGES, AK, BKM, EVEN, CONV>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -799,6 +848,78 @@ int run_gemm(GemmArgs g, hipStream_t st) {
   return check_launch("gemm");
 }
 
+template <typename T>
+int run_implicit_conv(const GemmArgs& g, hipStream_t st) {
+  constexpr int kBK = 32, kStages = 4;
+  const int64_t big_tiles = static_cast<int64_t>((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
+  if (big_tiles >= 240 && g.K > 256) {
+    if (g.M % 256 == 0 && g.N % 256 == 0 && g.K % kBK == 0)
+      return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, true, false, true, true>(g, st);
+    return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, true, false, false, true>(g, st);
+  }
+  if (g.M % 128 == 0 && g.N % 128 == 0 && g.K % kBK == 0)
+    return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, true, false, true, true>(g, st);
+  return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, true, false, false, true>(g, st);
+}
+
+}  // namespace
+
+int gemm_implicit_conv(int dtype, int batch, int M, int N, int K, const void* w, int64_t w_ld,
+                       const void* b_base, int64_t b_batch, int R, int S, int64_t per_s, int64_t per_c,
+                       int64_t per_r, const void* bias, int64_t bias_stride, void* out, int64_t out_batch,
+                       int64_t out_ld, hipStream_t st) {
+  if (batch <= 0 || M <= 0 || N <= 0 || K <= 0) return NTOPS_OK;
+  if (!aligned16(w) || !aligned16(b_base) || w_ld % 8 || N % 8 || per_s % 8 || per_c % 8 || per_r % 8 ||
+      b_batch % 8 || K % 8 || out_ld % 4 || out_batch % 4 || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return set_error(NTOPS_ERR_UNSUPPORTED, "conv2d: operand layout unsuited to the implicit GEMM");
+  if (b_batch * 2 >= (int64_t(1) << 31) || (256 * w_ld + K) * 2 >= (int64_t(1) << 31))
+    return set_error(NTOPS_ERR_UNSUPPORTED, "conv2d: operand exceeds the 2 GiB buffer range");
+  GemmArgs g{};
+  g.A = w;
+  g.B = b_base;
+  g.D = out;
+  g.sa_b = 0;
+  g.sa_m = w_ld;
+  g.sa_k = 1;
+  g.sb_b = b_batch;
+  g.sb_k = 0;  // rows come from the convolution descriptor
+  g.sb_n = 1;
+  g.sd_b = out_batch;
+  g.sd_m = out_ld;
+  g.sd_n = 1;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.batch = batch;
+  g.alpha = 1.f;
+  g.beta = bias ? 1.f : 0.f;
+  g.use_c = bias ? 1 : 0;
+  g.C = bias;
+  g.sc_b = 0;
+  g.sc_m = bias ? bias_stride : 0;
+  g.sc_n = 0;
+  g.staged = (out_ld % 8 == 0 && (batch == 1 || out_batch % 8 == 0) && N % 8 == 0 &&
+              (reinterpret_cast<uintptr_t>(out) & 15u) == 0)
+                 ? 1
+                 : 0;
+  constexpr int kBK = 32;  // k-rows per tile of the kernels run_implicit_conv launches
+  g.cv_rs = R * S;
+  g.cv_r = R;
+  g.cv_s = S;
+  g.cv_ds = kBK % S;
+  g.cv_dr = (kBK / S) % R;
+  g.cv_dc = kBK / (R * S);
+  g.cv_per_s = per_s;
+  g.cv_per_c = per_c;
+  g.cv_per_r = per_r;
+  switch (dtype) {
+    case NTOPS_BF16: return run_implicit_conv<__bf16>(g, st);
+    case NTOPS_F16: return run_implicit_conv<_Float16>(g, st);
+    default: return set_error(NTOPS_ERR_UNSUPPORTED, "conv2d: the implicit GEMM needs BF16 or F16");
+  }
+}
+
+namespace {
 }  // namespace
 }  // namespace ntops
 
