@@ -722,20 +722,6 @@ __global__ __launch_bounds__(64) void k_attn_generic(AttnArgs a) {
   }
 }
 
-// Number of CUs of the current device (queried once per device; 256 if the
-// query fails).
-int cu_count_cached() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
-
 template <typename T, int D, bool CAUSAL>
 int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
   constexpr int kLds = kFaStages * 2 * 64 * D * 2;

@@ -2,6 +2,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+
 #include "common.h"
 
 namespace ntops {
@@ -21,6 +23,18 @@ int check_launch(const char* what) {
   if (e != hipSuccess)
     return set_error(NTOPS_ERR_HIP, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
   return NTOPS_OK;
+}
+
+int cu_count_cached() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 }  // namespace ntops

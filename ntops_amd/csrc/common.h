@@ -20,6 +20,9 @@ namespace ntops {
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Converts the HIP runtime's sticky launch error (if any) into a status.
 int check_launch(const char* what);
+// Number of CUs of the current device (queried once per device; 256 if the
+// query fails).
+int cu_count_cached();
 
 // ------------------------------------------------------------ wave size --
 constexpr int kWave = 64;
@@ -142,12 +145,77 @@ __device__ __forceinline__ void store16_nt(T* p, const Pack16<T>& v) {
   __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
 }
 
+// Buffer resource (V#) over `bytes` bytes at the wave-uniform address
+// `base` (raw, stride 0).  Buffer loads at byte offsets at or past `bytes`
+// return zeros and buffer stores there are dropped, so a ragged tail or a
+// row past the end needs no branch around its accesses -- and without such
+// branches the compiler can count outstanding memory operations exactly
+// (a load issued on a maybe-skipped path forces a full vmcnt(0) wait).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+constexpr int kBufNT = 2;  // cache-policy bit: nontemporal (streamed once)
+template <typename T>
+__device__ __forceinline__ Pack16<T> buffer_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(Pack16<T>, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufNT));
+}
+template <typename T>
+__device__ __forceinline__ void buffer_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, const Pack16<T>& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kBufNT);
+}
+
 // ------------------------------------------------------- wave reductions --
-// Butterfly over the 64 lanes of a wavefront; every lane gets the result.
+// All-reduce over the 64 lanes of a wavefront; every lane gets the result.
+// float: within each 16-lane row the partners arrive through DPP operand
+// swizzles (quad_perm xor 1, quad_perm xor 2, half-row mirror, row mirror:
+// no LDS round trip, a few cycles each); the four row results are then read
+// with v_readlane and combined as op(op(r0, r16), op(r32, r48)).  After the
+// two quad steps every lane of a quad holds the same value, so the mirrors
+// pair exactly the lanes a xor-4 / xor-8 butterfly pairs: for a commutative
+// op the result is bit-identical to the 64-lane xor butterfly.  All 64 lanes
+// must be active (every caller reduces in wave-uniform control flow).
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- lane 7-i within 8
+constexpr int kDppMirror = 0x140;      // lane i <- lane 15-i within 16
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_read(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// op(a, b) -> combined value; commutative.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+  v = op(v, dpp_mov<kDppXor1>(v));
+  v = op(v, dpp_mov<kDppXor2>(v));
+  v = op(v, dpp_mov<kDppHalfMirror>(v));
+  v = op(v, dpp_mov<kDppMirror>(v));
+  return op(op(lane_read(v, 0), lane_read(v, 16)), op(lane_read(v, 32), lane_read(v, 48)));
+}
+
+// Two-value form: merge(a, b, a2, b2) folds (a2, b2) into (a, b); commutative.
+template <typename Merge>
+__device__ __forceinline__ void wave_reduce2(float& a, float& b, Merge merge) {
+  merge(a, b, dpp_mov<kDppXor1>(a), dpp_mov<kDppXor1>(b));
+  merge(a, b, dpp_mov<kDppXor2>(a), dpp_mov<kDppXor2>(b));
+  merge(a, b, dpp_mov<kDppHalfMirror>(a), dpp_mov<kDppHalfMirror>(b));
+  merge(a, b, dpp_mov<kDppMirror>(a), dpp_mov<kDppMirror>(b));
+  float a0 = lane_read(a, 0), b0 = lane_read(b, 0);
+  float a2 = lane_read(a, 32), b2 = lane_read(b, 32);
+  merge(a0, b0, lane_read(a, 16), lane_read(b, 16));
+  merge(a2, b2, lane_read(a, 48), lane_read(b, 48));
+  merge(a0, b0, a2, b2);
+  a = a0;
+  b = b0;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+  return wave_reduce(v, [](float x, float y) { return x + y; });
 }
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
@@ -155,9 +223,7 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
+  return wave_reduce(v, [](float x, float y) { return fmaxf(x, y); });
 }
 __device__ __forceinline__ double wave_max(double v) {
 #pragma unroll

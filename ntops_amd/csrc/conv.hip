@@ -121,6 +121,27 @@ __global__ __launch_bounds__(256) void k_im2col(ConvArgs a, T* col, int n0, int 
   }
 }
 
+// Stages x[n][c] (H x W elements) into LDS: 16-byte loads when the rows are
+// contiguous, 16-byte aligned runs of a multiple of 8 elements, else one
+// element per load.
+template <typename T>
+__device__ __forceinline__ void stage_plane(const ConvArgs& a, const T* xc, T* plane) {
+  constexpr int V = 16 / sizeof(T);
+  const int hw = a.H * a.W;
+  if (a.xs[3] == 1 && a.W % V == 0 && a.xs[2] % V == 0 && (reinterpret_cast<uintptr_t>(xc) & 15u) == 0) {
+    const int wv = a.W / V;
+    for (int i = threadIdx.x; i < a.H * wv; i += blockDim.x) {
+      const int ih = i / wv, c8 = i - (i / wv) * wv;
+      *reinterpret_cast<u32x4*>(plane + ih * a.W + c8 * V) = *reinterpret_cast<const u32x4*>(xc + ih * a.xs[2] + c8 * V);
+    }
+  } else {
+    for (int i = threadIdx.x; i < hw; i += blockDim.x) {
+      const int ih = i / a.W, iw = i - (i / a.W) * a.W;
+      plane[i] = xc[ih * a.xs[2] + iw * a.xs[3]];
+    }
+  }
+}
+
 // Same output as k_im2col, one workgroup per (image, channel): the input
 // plane is staged in LDS once (read from HBM once, any strides), then every
 // tap's unfolded row is written from LDS with 16-byte stores, neighbouring
@@ -210,33 +231,6 @@ __global__ __launch_bounds__(256) void k_conv_shift(ConvArgs a, T* xs, int n0, i
       v[e] = (row_ok && iw >= 0 && iw < a.W) ? xr[iw * a.xs[3]] : static_cast<T>(0.f);
     }
     *reinterpret_cast<u32x4*>(xs + i * 8) = __builtin_bit_cast(u32x4, v);
-  }
-}
-
-// Same output as k_conv_shift, one workgroup per (image, channel) with the
-// input plane staged in LDS (read from HBM once); every thread then writes
-// 16-byte runs of the S shifted planes.
-// Same output as k_conv_shift, one workgroup per (image, channel) with the
-// input plane staged in LDS (read from HBM once); every thread then writes
-// 16-byte runs of the S shifted planes.
-// Stages x[n][c] (H x W elements) into LDS: 16-byte loads when the rows are
-// contiguous, 16-byte aligned runs of a multiple of 8 elements, else one
-// element per load.
-template <typename T>
-__device__ __forceinline__ void stage_plane(const ConvArgs& a, const T* xc, T* plane) {
-  constexpr int V = 16 / sizeof(T);
-  const int hw = a.H * a.W;
-  if (a.xs[3] == 1 && a.W % V == 0 && a.xs[2] % V == 0 && (reinterpret_cast<uintptr_t>(xc) & 15u) == 0) {
-    const int wv = a.W / V;
-    for (int i = threadIdx.x; i < a.H * wv; i += blockDim.x) {
-      const int ih = i / wv, c8 = i - (i / wv) * wv;
-      *reinterpret_cast<u32x4*>(plane + ih * a.W + c8 * V) = *reinterpret_cast<const u32x4*>(xc + ih * a.xs[2] + c8 * V);
-    }
-  } else {
-    for (int i = threadIdx.x; i < hw; i += blockDim.x) {
-      const int ih = i / a.W, iw = i - (i / a.W) * a.W;
-      plane[i] = xc[ih * a.xs[2] + iw * a.xs[3]];
-    }
   }
 }
 

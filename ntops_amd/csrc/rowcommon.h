@@ -26,11 +26,14 @@ struct RowPos {
   int lane, wave_in_row, row_in_block;
 };
 
-template <int WPR>
+// SCALAR: read the wave index through lane 0 so that row indices and row
+// base addresses live in SGPRs (scalar address math; required by the buffer
+// resources of RowLoader and the branch-free stores).
+template <int WPR, bool SCALAR = true>
 __device__ __forceinline__ RowPos row_pos() {
   RowPos p;
   p.lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = SCALAR ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : (threadIdx.x >> 6);
   p.wave_in_row = wave % WPR;
   p.row_in_block = wave / WPR;
   return p;
@@ -103,16 +106,110 @@ inline bool pick_row_cfg(int64_t npk, VecCfg* cfg) {
   MACRO(4, 16)                 \
   MACRO(8, 16)
 
-// Loads V consecutive elements of type W (16-byte aligned) as float.
+// The V per-column parameters (weight or bias, type W) that go with one
+// 16-byte pack of the row, kept in their own type from load to use
+// (V * sizeof(W) bytes: one 16-byte load for W == T, two for float with a
+// 16-bit T).
+// Row-group loop.  A block handles row groups (the RPB rows it holds at
+// once) g0, g0 + G, g0 + 2G, ...  Kernels with a long reduction phase
+// (layer_norm: two dependent reductions) run it streaming (STREAM): the grid
+// is the number of blocks resident at once and the block carries one group
+// of register prefetch, so while group g is reduced and written, group
+// g + G's loads are in flight and each CU keeps HBM reads outstanding
+// through the reduction and store phases; per-column parameters (weight,
+// bias) are then loaded once per block, since every row a lane touches uses
+// the same packs.  Measured on MI355X this lifts layer_norm bf16
+// (16384, 4096) from 63% to 69% of HBM peak, while rms_norm, whose
+// reduction is short, loses ~2% to it: those kernels run one group per block
+// (grid = groups) and load parameters at the point of use.  The 1024-thread
+// shapes (16 waves per row) never stream: a second group or resident
+// parameters would cost occupancy or spill.
+template <int CHUNKS, int WPR>
+constexpr bool kCanStream = CHUNKS * WPR <= 16;
+
+// Group stride of the loop.  Without streaming the grid is `groups`, and a
+// stride of `groups` lets the compiler see the single trip and keep the
+// register allocation of a straight-line kernel.
+template <bool STREAM>
+__device__ __forceinline__ int64_t row_step(int64_t groups) {
+  return STREAM ? static_cast<int64_t>(gridDim.x) : groups;
+}
+
+template <typename T, int CHUNKS, int WPR, bool STREAM>
+struct RowLoader {
+  static constexpr int V = Pack16<T>::N;
+  static constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
+  const T* base;
+  int64_t stride, rows;
+  RowPos p;
+  int npk;
+  Pack16<T> buf[CHUNKS];
+
+  __device__ __forceinline__ RowLoader(const T* b, int64_t s, int64_t nrows, const RowPos& pos, int n)
+      : base(b), stride(s), rows(nrows), p(pos), npk(n) {}
+
+  // Group g's packs of this lane; zeros past the row end or past `rows`
+  // (buffer loads against the row's extent: no branches).
+  __device__ __forceinline__ void load(Pack16<T> (&r)[CHUNKS], int64_t g) const {
+    const int64_t row = g * RPB + p.row_in_block;
+    const bool ok = row < rows;
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(base + (ok ? row : 0) * stride, ok ? npk * 16u : 0u);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) r[c] = buffer_load16_nt<T>(rs, pack_of<WPR>(p, c) * 16u);
+  }
+  __device__ __forceinline__ void start(int64_t g) {
+    if constexpr (STREAM) load(buf, g);
+  }
+  // Hands back group g and (streaming) issues group gn's loads.
+  __device__ __forceinline__ void next(Pack16<T> (&r)[CHUNKS], int64_t g, int64_t gn) {
+    if constexpr (STREAM) {
+#pragma unroll
+      for (int c = 0; c < CHUNKS; ++c) r[c] = buf[c];
+      load(buf, gn);
+    } else {
+      load(r, g);
+    }
+  }
+};
+
 template <typename W, int V>
-__device__ __forceinline__ void load_as_float(const W* p, float (&out)[V]) {
-  constexpr int PER = 16 / sizeof(W);
-  static_assert(V % PER == 0, "V must be a multiple of the pack width");
+struct ParamPack {
+  static constexpr int kPer = Pack16<W>::N;
+  static constexpr int kLoads = V / kPer;
+  static_assert(kLoads >= 1 && V % kPer == 0, "parameter type narrower than the row type");
+  Pack16<W> q[kLoads];
+  __device__ __forceinline__ void load(const W* p) {
 #pragma unroll
-  for (int j = 0; j < V / PER; ++j) {
-    Pack16<W> pk = load16(p + j * PER);
+    for (int j = 0; j < kLoads; ++j) q[j] = load16(p + j * kPer);
+  }
+  __device__ __forceinline__ float get(int i) const { return static_cast<float>(q[i / kPer].v[i % kPer]); }
+};
+
+template <int WPR, typename W, int V, int CHUNKS>
+__device__ __forceinline__ void load_params(ParamPack<W, V> (&q)[CHUNKS], const W* w, const RowPos& p,
+                                            int npk) {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) out[j * PER + i] = static_cast<float>(pk.v[i]);
+  for (int c = 0; c < CHUNKS; ++c)
+    if (pack_of<WPR>(p, c) < npk) q[c].load(w + pack_of<WPR>(p, c) * V);
+}
+
+// Grid of a vec row kernel K of WPR waves per row over `rows` rows: with
+// STREAM the number of blocks resident at once (K's occupancy, queried once
+// per kernel, times the CU count) capped by the group count, else one block
+// per group.
+template <auto K, bool STREAM, int WPR>
+int64_t row_grid(int64_t rows) {
+  constexpr int kThreads = RowShape<WPR>::kThreads;
+  const int64_t groups = ceil_div(rows, RowShape<WPR>::kRowsPerBlock);
+  if constexpr (!STREAM) {
+    return groups;
+  } else {
+    static const int per_cu = [] {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K, kThreads, 0) != hipSuccess || n <= 0) n = 1;
+      return n;
+    }();
+    return std::min<int64_t>(groups, static_cast<int64_t>(per_cu) * cu_count_cached());
   }
 }
 

@@ -16,7 +16,8 @@
 //              element, to the two separate kernels, in one pass.
 //
 // Vector path: one HBM read + one HBM write per element, row held in VGPRs
-// (see rowcommon.h).  Looped path (unaligned rows, or rows wider than 64K
+// (see rowcommon.h); layer_norm runs it streaming (persistent blocks with
+// one row group of register prefetch), rms_norm one row group per block.  Looped path (unaligned rows, or rows wider than 64K
 // 16-bit elements): one 256-thread block per row, scalar strided accesses,
 // re-reading the row from L2 for the second / third pass.
 #include "dispatch.h"
@@ -37,50 +38,40 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_vec(
     int64_t rows, int cols, float eps) {
   constexpr int V = Pack16<T>::N;
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
-  __shared__ float red[RPB * WPR];
+  __shared__ float red[2][RPB * WPR];
   const RowPos p = row_pos<WPR>();
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + p.row_in_block;
-  const bool row_ok = row < rows;
   const int npk = cols / V;
-  const T* xr = x + row * xs;
-
-  Pack16<T> r[CHUNKS];
+  const int64_t groups = (rows + RPB - 1) / RPB;
+  const int64_t step = row_step<false>(groups);
+  RowLoader<T, CHUNKS, WPR, false> in(x, xs, rows, p, npk);
+  for (int64_t g = blockIdx.x, it = 0; g < groups; g += step, ++it) {
+    Pack16<T> r[CHUNKS];
+    in.next(r, g, g + step);
+    float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int pk = pack_of<WPR>(p, c);
-    if (row_ok && pk < npk)
-      r[c] = load16_nt(xr + pk * V);
-    else
+    for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
-      for (int i = 0; i < V; ++i) r[c].v[i] = T(0);
-  }
-  float ss = 0.f;
+      for (int i = 0; i < V; ++i) {
+        const float f = to_f(r[c].v[i]);
+        ss += f * f;
+      }
+    ss = row_sum<WPR>(ss, red[it & 1], p);
+    const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+    const int64_t row = g * RPB + p.row_in_block;
+    const bool row_ok = row < rows;
+    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c)
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float f = to_f(r[c].v[i]);
-      ss += f * f;
-    }
-  ss = row_sum<WPR>(ss, red, p);
-  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
-
-  if (!row_ok) return;
-  T* yr = y + row * ys;
-#pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int pk = pack_of<WPR>(p, c);
-    if (pk < npk) {
-      float wv[V];
-      if (w != nullptr)
-        load_as_float<W, V>(w + pk * V, wv);
-      else
-#pragma unroll
-        for (int i = 0; i < V; ++i) wv[i] = 1.0f;
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int pk = pack_of<WPR>(p, c);
+      ParamPack<W, V> wq;
+      if (w != nullptr && pk < npk) wq.load(w + pk * V);
       Pack16<T> o;
 #pragma unroll
-      for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(r[c].v[i]), rstd), wv[i]));
-      store16_nt(yr + pk * V, o);
+      for (int i = 0; i < V; ++i) {
+        const float wv = w != nullptr ? wq.get(i) : 1.0f;
+        o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(r[c].v[i]), rstd), wv));
+      }
+      buffer_store16_nt(out, pk * 16u, o);
     }
   }
 }
@@ -120,20 +111,22 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + p.row_in_block;
   const bool row_ok = row < rows;
   const int npk = cols / V;
+  const uint32_t extent = row_ok ? npk * 16u : 0u;  // past the row end: loads give 0, stores dropped
+  const int64_t row_c = row_ok ? row : 0;
 
+  const __amdgpu_buffer_rsrc_t in_x = buffer_rsrc(x + row_c * xs, extent);
+  const __amdgpu_buffer_rsrc_t in_r = buffer_rsrc(res + row_c * rs, extent);
   Pack16<T> h[CHUNKS];
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
-    const int pk = pack_of<WPR>(p, c);
-    if (row_ok && pk < npk) {
-      const Pack16<T> a = load16_nt(x + row * xs + pk * V);
-      const Pack16<T> b = load16_nt(res + row * rs + pk * V);
+    const Pack16<T> a = buffer_load16_nt<T>(in_x, pack_of<WPR>(p, c) * 16u);
+    const Pack16<T> b = buffer_load16_nt<T>(in_r, pack_of<WPR>(p, c) * 16u);
 #pragma unroll
-      for (int i = 0; i < V; ++i) h[c].v[i] = static_cast<T>(add_nc(to_f(a.v[i]), to_f(b.v[i])));
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i) h[c].v[i] = T(0);
-    }
+    for (int i = 0; i < V; ++i) h[c].v[i] = static_cast<T>(add_nc(to_f(a.v[i]), to_f(b.v[i])));
+    // Wide shapes: at most four chunks of both inputs in flight, or the
+    // two inputs plus the sums overflow the 128 VGPRs of a 1024-thread block.
+    if constexpr (CHUNKS > 4)
+      if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
   }
   float ss = 0.f;
 #pragma unroll
@@ -143,32 +136,36 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
       const float f = to_f(h[c].v[i]);
       ss += f * f;
     }
+  // Wide shapes: keep h packed across the reduction (the fp32 copies the
+  // compiler would otherwise carry do not fit beside it).
+  if constexpr (CHUNKS > 4)
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      u32x4 bits = __builtin_bit_cast(u32x4, h[c]);
+      asm volatile("" : "+v"(bits));
+      h[c] = __builtin_bit_cast(Pack16<T>, bits);
+    }
   ss = row_sum<WPR>(ss, red, p);
   const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
 
-  if (!row_ok) return;
+  const __amdgpu_buffer_rsrc_t out_r = buffer_rsrc(ro + row_c * ros, extent);
+  const __amdgpu_buffer_rsrc_t out_y = buffer_rsrc(y + row_c * ys, extent);
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const int pk = pack_of<WPR>(p, c);
-    if (pk < npk) {
-      store16_nt(ro + row * ros + pk * V, h[c]);
-      float wv[V];
-      if (w != nullptr)
-        load_as_float<W, V>(w + pk * V, wv);
-      else
+    buffer_store16_nt(out_r, pk * 16u, h[c]);
+    ParamPack<W, V> wq;
+    if (w != nullptr && pk < npk) wq.load(w + pk * V);
+    Pack16<T> o;
 #pragma unroll
-        for (int i = 0; i < V; ++i) wv[i] = 1.0f;
-      Pack16<T> o;
-#pragma unroll
-      for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(h[c].v[i]), rstd), wv[i]));
-      store16_nt(y + row * ys + pk * V, o);
+    for (int i = 0; i < V; ++i) {
+      const float wv = w != nullptr ? wq.get(i) : 1.0f;
+      o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(h[c].v[i]), rstd), wv));
     }
+    buffer_store16_nt(out_y, pk * 16u, o);
   }
 }
 
-// Looped form: one block per row; pass 1 forms and stores h and its sum of
-// squares, pass 2 re-reads h from the stored new residual (each element is
-// re-read by the thread that wrote it).
 template <typename T, typename W>
 __global__ __launch_bounds__(256) void k_add_rms_loop(const T* x, int64_t xs, const T* res, int64_t rs,
                                                        const W* w, T* y, int64_t ys, T* ro, int64_t ros,
@@ -197,68 +194,62 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_ln_vec(
     T* __restrict__ y, int64_t ys, int64_t rows, int cols, float eps) {
   constexpr int V = Pack16<T>::N;
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
-  __shared__ float red0[RPB * WPR];
-  __shared__ float red1[RPB * WPR];
+  __shared__ float red0[2][RPB * WPR];
+  __shared__ float red1[2][RPB * WPR];
   const RowPos p = row_pos<WPR>();
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + p.row_in_block;
-  const bool row_ok = row < rows;
   const int npk = cols / V;
-  const T* xr = x + row * xs;
-
-  Pack16<T> r[CHUNKS];
-#pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int pk = pack_of<WPR>(p, c);
-    if (row_ok && pk < npk)
-      r[c] = load16_nt(xr + pk * V);
-    else
-#pragma unroll
-      for (int i = 0; i < V; ++i) r[c].v[i] = T(0);
+  const int64_t groups = (rows + RPB - 1) / RPB;
+  constexpr bool kStream = kCanStream<CHUNKS, WPR>;
+  const int64_t step = row_step<kStream>(groups);
+  ParamPack<W, V> wq[CHUNKS], bq[CHUNKS];
+  if constexpr (kStream) {
+    if (w != nullptr) load_params<WPR>(wq, w, p, npk);
+    if (b != nullptr) load_params<WPR>(bq, b, p, npk);
   }
-  float s = 0.f;
+  RowLoader<T, CHUNKS, WPR, kStream> in(x, xs, rows, p, npk);
+  in.start(blockIdx.x);
+  for (int64_t g = blockIdx.x, it = 0; g < groups; g += step, ++it) {
+    Pack16<T> r[CHUNKS];
+    in.next(r, g, g + step);
+    float s = 0.f;
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c)
+    for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
-    for (int i = 0; i < V; ++i) s += to_f(r[c].v[i]);
-  const float mean = row_sum<WPR>(s, red0, p) / static_cast<float>(cols);
-  float q = 0.f;
+      for (int i = 0; i < V; ++i) s += to_f(r[c].v[i]);
+    const float mean = row_sum<WPR>(s, red0[it & 1], p) / static_cast<float>(cols);
+    float q = 0.f;
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const bool ok = pack_of<WPR>(p, c) < npk;
+    for (int c = 0; c < CHUNKS; ++c) {
+      const bool ok = pack_of<WPR>(p, c) < npk;
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float d = ok ? to_f(r[c].v[i]) - mean : 0.f;
-      q += d * d;
+      for (int i = 0; i < V; ++i) {
+        const float d = ok ? to_f(r[c].v[i]) - mean : 0.f;
+        q += d * d;
+      }
     }
-  }
-  const float var = row_sum<WPR>(q, red1, p) / static_cast<float>(cols);
-  const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
-  const float shift = -rstd * mean;
-
-  if (!row_ok) return;
-  T* yr = y + row * ys;
+    const float var = row_sum<WPR>(q, red1[it & 1], p) / static_cast<float>(cols);
+    const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
+    const float shift = -rstd * mean;
+    const int64_t row = g * RPB + p.row_in_block;
+    const bool row_ok = row < rows;
+    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int pk = pack_of<WPR>(p, c);
-    if (pk < npk) {
-      float wv[V], bv[V];
-      if (w != nullptr)
-        load_as_float<W, V>(w + pk * V, wv);
-      else
-#pragma unroll
-        for (int i = 0; i < V; ++i) wv[i] = 1.0f;
-      if (b != nullptr)
-        load_as_float<W, V>(b + pk * V, bv);
-      else
-#pragma unroll
-        for (int i = 0; i < V; ++i) bv[i] = 0.0f;
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int pk = pack_of<WPR>(p, c);
+      if constexpr (!kStream)
+        if (pk < npk) {
+          if (w != nullptr) wq[c].load(w + pk * V);
+          if (b != nullptr) bq[c].load(b + pk * V);
+        }
       Pack16<T> o;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
+        const float wv = w != nullptr ? wq[c].get(i) : 1.0f;
+        const float bv = b != nullptr ? bq[c].get(i) : 0.0f;
         const float n = add_nc(mul_nc(to_f(r[c].v[i]), rstd), shift);
-        o.v[i] = static_cast<T>(add_nc(mul_nc(n, wv[i]), bv[i]));
+        o.v[i] = static_cast<T>(add_nc(mul_nc(n, wv), bv));
       }
-      store16_nt(yr + pk * V, o);
+      buffer_store16_nt(out, pk * 16u, o);
     }
   }
 }
@@ -302,13 +293,12 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
                    aligned16(y) && (w == nullptr || aligned16(w)) && pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
   if (vec) {
-#define NTOPS_RMS_CASE(CH, WP)                                                                \
-  if (cfg.chunks == CH && cfg.wpr == WP) {                                                    \
-    constexpr int RPB = RowShape<WP>::kRowsPerBlock;                                          \
-    hipLaunchKernelGGL((k_rms_vec<T, W, CH, WP>), dim3(ceil_div(rows, RPB)),                  \
-                       dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, y, ys, rows,            \
-                       static_cast<int>(cols), feps);                                         \
-    return check_launch("rms_norm");                                                          \
+#define NTOPS_RMS_CASE(CH, WP)                                                                    \
+  if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
+    hipLaunchKernelGGL((k_rms_vec<T, W, CH, WP>), dim3(row_grid<k_rms_vec<T, W, CH, WP>, false, WP>(rows)), \
+                       dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, y, ys, rows,                \
+                       static_cast<int>(cols), feps);                                             \
+    return check_launch("rms_norm");                                                              \
   }
     NTOPS_ROW_CASES(NTOPS_RMS_CASE)
 #undef NTOPS_RMS_CASE
@@ -330,21 +320,15 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
                    aligned16(y) && (w == nullptr || aligned16(w)) &&
                    (b == nullptr || aligned16(b)) && pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
-  // layer_norm carries two dependent reductions and twice the per-element
-  // VALU work of rms_norm; for rows of 257..512 packs (e.g. 4096 bf16) four
-  // packs per lane over two waves measured ~4% faster than two over four.
-  if (vec && cfg.chunks == 2 && cfg.wpr == 4) cfg = VecCfg{4, 2};
   if (vec) {
-#define NTOPS_LN_CASE(CH, WP)                                                                 \
-  if (cfg.chunks == CH && cfg.wpr == WP) {                                                    \
-    constexpr int RPB = RowShape<WP>::kRowsPerBlock;                                          \
-    hipLaunchKernelGGL((k_ln_vec<T, W, CH, WP>), dim3(ceil_div(rows, RPB)),                   \
-                       dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, b, y, ys, rows,         \
-                       static_cast<int>(cols), feps);                                         \
-    return check_launch("layer_norm");                                                        \
+#define NTOPS_LN_CASE(CH, WP)                                                                     \
+  if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
+    hipLaunchKernelGGL((k_ln_vec<T, W, CH, WP>), dim3(row_grid<k_ln_vec<T, W, CH, WP>, kCanStream<CH, WP>, WP>(rows)), \
+                       dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, b, y, ys, rows,             \
+                       static_cast<int>(cols), feps);                                             \
+    return check_launch("layer_norm");                                                            \
   }
     NTOPS_ROW_CASES(NTOPS_LN_CASE)
-    NTOPS_LN_CASE(4, 2)
 #undef NTOPS_LN_CASE
   }
   hipLaunchKernelGGL((k_ln_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, b, y, ys, cols,
@@ -367,13 +351,12 @@ int run_add_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const vo
                    pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
   if (vec) {
-#define NTOPS_ADD_RMS_CASE(CH, WP)                                                            \
-  if (cfg.chunks == CH && cfg.wpr == WP) {                                                    \
-    constexpr int RPB = RowShape<WP>::kRowsPerBlock;                                          \
-    hipLaunchKernelGGL((k_add_rms_vec<T, W, CH, WP>), dim3(ceil_div(rows, RPB)),              \
-                       dim3(RowShape<WP>::kThreads), 0, st, x, xs, r, rs, w, y, ys, ro, ros,  \
-                       rows, static_cast<int>(cols), feps);                                   \
-    return check_launch("add_rms_norm");                                                      \
+#define NTOPS_ADD_RMS_CASE(CH, WP)                                                                \
+  if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
+    hipLaunchKernelGGL((k_add_rms_vec<T, W, CH, WP>), dim3(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
+                       dim3(RowShape<WP>::kThreads), 0, st, x, xs, r, rs, w, y, ys, ro, ros,      \
+                       rows, static_cast<int>(cols), feps);                                       \
+    return check_launch("add_rms_norm");                                                          \
   }
     NTOPS_ROW_CASES(NTOPS_ADD_RMS_CASE)
 #undef NTOPS_ADD_RMS_CASE

@@ -62,7 +62,10 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_softmax_vec(
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
   __shared__ C red_m[RPB * WPR];
   __shared__ C red_s[RPB * WPR];
-  const RowPos p = row_pos<WPR>();
+  // Vector-register row position and per-lane branches around the loads:
+  // on MI355X this measured ~3% faster for bf16 rows of 2048 than the
+  // scalar position with branch-free buffer loads used by the norms.
+  const RowPos p = row_pos<WPR, false>();
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + p.row_in_block;
   const bool row_ok = row < rows;
   const int npk = cols / V;
@@ -99,8 +102,12 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_softmax_vec(
     }
   // row summary
   C m = ml, s = sl;
+  if constexpr (sizeof(C) == 4) {
+    wave_reduce2(m, s, [](C& a, C& b, C a2, C b2) { merge_max_sum(a, b, a2, b2); });
+  } else {
 #pragma unroll
-  for (int k = 1; k < 64; k <<= 1) merge_max_sum(m, s, __shfl_xor(m, k, 64), __shfl_xor(s, k, 64));
+    for (int k = 1; k < 64; k <<= 1) merge_max_sum(m, s, __shfl_xor(m, k, 64), __shfl_xor(s, k, 64));
+  }
   if constexpr (WPR > 1) {
     if (p.lane == 0) {
       red_m[p.row_in_block * WPR + p.wave_in_row] = m;
