@@ -51,7 +51,23 @@ __device__ __forceinline__ float sq(float v) { return __builtin_sqrtf(v); }  // 
 __device__ __forceinline__ double sq(double v) { return __builtin_sqrt(v); }
 __device__ __forceinline__ float pw(float a, float b) { return powf(a, b); }
 __device__ __forceinline__ double pw(double a, double b) { return pow(a, b); }
-__device__ __forceinline__ float fmd(float a, float b) { return fmodf(a, b); }
+// Exact fmod.  When a and b are finite and the rounded quotient q = a / b
+// has |trunc(q)| < 2^23, r = fma(-trunc(q), b, a) is exact: trunc(q) is the
+// true truncated quotient n or, when a / b lies within half an ulp below an
+// integer, n + 1 in magnitude; in the second case a - (n+1) b is a multiple
+// of ulp(b) smaller than |b| (representable, so the fma is exact), has the
+// opposite sign to a, and adding back |b| with a's sign is exact too.  A zero
+// remainder takes a's sign, as fmod's does.  Everything else (huge
+// quotients, infinities, NaN) goes to the library's bit-by-bit fmodf.
+__device__ __forceinline__ float fmd(float a, float b) {
+  const float n = __builtin_truncf(a / b);
+  if (__builtin_fabsf(n) < 8388608.0f && __builtin_isfinite(b)) {
+    float r = __builtin_fmaf(-n, b, a);
+    if (r != 0.0f && __builtin_signbit(r) != __builtin_signbit(a)) r += __builtin_copysignf(__builtin_fabsf(b), a);
+    return r == 0.0f ? __builtin_copysignf(0.0f, a) : r;
+  }
+  return fmodf(a, b);
+}
 __device__ __forceinline__ double fmd(double a, double b) { return fmod(a, b); }
 __device__ __forceinline__ float flr(float v) { return floorf(v); }
 __device__ __forceinline__ double flr(double v) { return floor(v); }
@@ -342,6 +358,31 @@ __device__ __forceinline__ C floor_divide(C a, C b) {
   if (div - fl > C(0.5)) fl += C(1);
   return fl;
 }
+// fp32: the same result without the second division.  When b is finite and
+// the rounded quotient q = a / b has |trunc(q)| < 2^21, the exact remainder
+// and truncated quotient n come from one fma (as in fmd), and the sequence
+// above provably returns n - corr (corr = 1 when the remainder is nonzero
+// with the opposite sign to b): its (a - mod) / b is n times two roundings
+// of relative size 2^-24, i.e. within 2^21 * 2^-23 = 0.25 of n, the "- 1"
+// adds at most 0.125 more, and floor plus round-half-down then lands on the
+// integer.  A zero result takes the sign of a / b, as above.  Larger
+// quotients and non-finite operands run the sequence above.
+__device__ __forceinline__ float floor_divide(float a, float b) {
+  if (b == 0.0f) return a / b;
+  const float q = a / b;
+  float n = __builtin_truncf(q);
+  if (__builtin_fabsf(n) < 2097152.0f && __builtin_isfinite(b)) {
+    float r = __builtin_fmaf(-n, b, a);
+    if (r != 0.0f && __builtin_signbit(r) != __builtin_signbit(a)) {
+      r += __builtin_copysignf(__builtin_fabsf(b), a);
+      n -= __builtin_copysignf(1.0f, n);
+    }
+    const float res = n - ((r != 0.0f && ((b < 0.0f) != (r < 0.0f))) ? 1.0f : 0.0f);
+    return res == 0.0f ? __builtin_copysignf(0.0f, q) : res;
+  }
+  return floor_divide<float>(a, b);
+}
+
 template <int MODE, typename T, bool F = IsFloat<T>::v>
 struct DivF;
 template <int MODE, typename T>

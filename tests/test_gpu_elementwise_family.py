@@ -311,3 +311,48 @@ def test_div_floor_full_size_fp32():
     got = T.div(a.cuda(), b.cuda(), rounding_mode="floor")
     same(got, ora(lambda x, y, d: O.div(x, y, d, "floor"), a.numpy(), b.numpy(), dt="f32"), "floor full size")
     del got
+
+
+def _floor_div_hard_cases(seed=3):
+    """fp32 (a, b) pairs aimed at the exact-remainder fast path of floor
+    division: quotients within a few ulps of an integer (the rounded quotient
+    can round up across it), |a| just below |b|, subnormal operands, huge
+    quotients (|a / b| >= 2^23, the fallback), signed zeros, infinities and
+    NaN."""
+    rng = np.random.default_rng(seed)
+    a_parts, b_parts = [], []
+    b = (rng.standard_normal(20000) * 10.0 ** rng.uniform(-2, 2, 20000)).astype(np.float32)
+    k = rng.integers(-5_000_000, 5_000_000, 20000).astype(np.float32)
+    a = (k * b).astype(np.float32)
+    for steps in (-2, -1, 0, 1, 2):
+        s = a.copy()
+        for _ in range(abs(steps)):
+            s = np.nextafter(s, np.float32(np.inf if steps > 0 else -np.inf)).astype(np.float32)
+        a_parts.append(s)
+        b_parts.append(b)
+    bb = rng.standard_normal(20000).astype(np.float32)
+    near = np.nextafter(bb, np.float32(0)).astype(np.float32)
+    a_parts.append(np.where(rng.random(20000) < 0.5, near, -near).astype(np.float32))
+    b_parts.append(bb)
+    tiny = np.float32(1e-45)
+    a_parts.append((rng.integers(-10**6, 10**6, 20000).astype(np.float32) * tiny).astype(np.float32))
+    b_parts.append((rng.integers(1, 1000, 20000) * rng.choice([-1, 1], 20000)).astype(np.float32) * tiny)
+    a_parts.append((rng.standard_normal(20000) * 1e30).astype(np.float32))
+    b_parts.append((rng.standard_normal(20000) * 1e-3).astype(np.float32))
+    sp_a = np.array([0.0, -0.0, -0.0, 5.0, -5.0, np.inf, np.nan, 2.0, 3e38, -7.5, 7.5, 1.0], np.float32)
+    sp_b = np.array([3.0, 3.0, -3.0, np.inf, -np.inf, 2.0, 2.0, np.nan, 1e-3, 2.5, -2.5, 0.0], np.float32)
+    a_parts.append(sp_a)
+    b_parts.append(sp_b)
+    return np.concatenate(a_parts), np.concatenate(b_parts)
+
+
+def test_div_floor_exact_remainder_cases():
+    """Floor division's remainder is computed exactly (fast fma path for
+    |a / b| < 2^23, library fmod beyond): bit-exact against the oracle's
+    numpy fmod on the hard cases, fp32 and bf16 (bf16 computes in fp32)."""
+    a, b = _floor_div_hard_cases()
+    got = T.div(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), rounding_mode="floor")
+    same(got, ora(lambda x, y, d: O.div(x, y, d, "floor"), a, b, dt="f32"), "floor hard cases f32")
+    ab, bb = torch.from_numpy(a).bfloat16(), torch.from_numpy(b).bfloat16()
+    got = T.div(ab.cuda(), bb.cuda(), rounding_mode="floor")
+    same(got, ora(lambda x, y, d: O.div(x, y, d, "floor"), to_np(ab), to_np(bb), dt="bf16"), "floor hard cases bf16")
