@@ -504,23 +504,25 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
   u32x4 pf[4];              // P of that tile, as MFMA A operands per 16-key slice
 
   // matrix phase of tile j: O += P_j V_j (if j >= 0) and S = Q K_{j+1}^T
-  // (if j + 1 <= jl)
+  // (if j + 1 <= jl).  Software-pipelined by hand: fragment i + kPrefetch is
+  // read while MFMA i runs, and a scheduling fence per step pins that order
+  // (left to the scheduler, the phase was compiled with one fragment register
+  // set and an LDS round trip before every MFMA).
   auto matrix_phase = [&](int j) {
     if (j >= 0) {
       const char* sv = smem + (j % NS) * kStage + kTile;
+      constexpr int nm = 4 * DT;  // MFMA i: key slice i / DT, d tile i % DT
+      u32x4 f[kPrefetch];
 #pragma unroll
-      for (int sl = 0; sl < 4; ++sl)
+      for (int i = 0; i < kPrefetch; ++i) f[i] = v_frag<D>(sv, (i % DT) * 32, i / DT, lane);
 #pragma unroll
-        for (int t2 = 0; t2 < DT; ++t2) o[t2] = mfma32<T>(v_frag<D>(sv, t2 * 32, sl, lane), pf[sl], o[t2]);
-      // fragment reads run kPrefetch MFMAs ahead of their use
-      constexpr int nm = 4 * DT;
-      sched_group<kSchedDsRead, 2 * kPrefetch>();
-#pragma unroll
-      for (int i = 0; i < nm - kPrefetch; ++i) {
-        sched_group<kSchedMfma, 1>();
-        sched_group<kSchedDsRead, 2>();
+      for (int i = 0; i < nm; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        o[i % DT] = mfma32<T>(f[i % kPrefetch], pf[i / DT], o[i % DT]);
+        if (i + kPrefetch < nm)
+          f[i % kPrefetch] = v_frag<D>(sv, ((i + kPrefetch) % DT) * 32, (i + kPrefetch) / DT, lane);
       }
-      sched_group<kSchedMfma, kPrefetch>();
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (j + 1 <= jl) {
       const char* sk = smem + ((j + 1) % NS) * kStage;
@@ -528,18 +530,17 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int e = 0; e < 16; ++e) s[u][e] = 0.f;
+      constexpr int nm = 2 * KS;  // MFMA i: d slice i / 2, key half i % 2
+      u32x4 f[kPrefetch];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int i = 0; i < kPrefetch; ++i) f[i] = k_frag<D>(sk, (i % 2) * 32, i / 2, lane);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) s[u] = mfma32<T>(k_frag<D>(sk, u * 32, ks, lane), qf[ks], s[u]);
-      constexpr int nm = 2 * KS;
-      sched_group<kSchedDsRead, kPrefetch>();
-#pragma unroll
-      for (int i = 0; i < nm - kPrefetch; ++i) {
-        sched_group<kSchedMfma, 1>();
-        sched_group<kSchedDsRead, 1>();
+      for (int i = 0; i < nm; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        s[i % 2] = mfma32<T>(f[i % kPrefetch], qf[i / 2], s[i % 2]);
+        if (i + kPrefetch < nm) f[i % kPrefetch] = k_frag<D>(sk, ((i + kPrefetch) % 2) * 32, (i + kPrefetch) / 2, lane);
       }
-      sched_group<kSchedMfma, kPrefetch>();
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   // vector phase of tile t: mask (on tiles that reach the end of the keys or
