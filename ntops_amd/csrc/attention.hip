@@ -379,15 +379,31 @@ struct KvDma {
     tile_bytes = static_cast<uint32_t>(64 * ld * 2);
   }
 
-  // Loads tile t into `tile` (its LDS home); a tile past the end loads
-  // nothing but still counts once per instruction in vmcnt.
-  __device__ __forceinline__ void issue(char* tile, int t, bool valid) const {
+  // Resource of the same operand for another (batch, head): same strides
+  // and extent, so the per-lane offsets carry over.
+  __device__ __forceinline__ u32x4 rsrc_at(const void* base) const {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    u32x4 r = rsrc;
+    r.x = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
+    r.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32) & 0xffffu);
+    return r;
+  }
+
+  // Loads tile t into `tile` (its LDS home) through resource r (this
+  // operand's own by default); a tile past the end loads nothing but still
+  // counts once per instruction in vmcnt.
+  __device__ __forceinline__ void issue(char* tile, int t, bool valid) const { issue(rsrc, tile, t, valid); }
+  __device__ __forceinline__ void issue(u32x4 r, char* tile, int t, bool valid) const {
+    // t passes through an empty asm so that the offsets of tiles issued at
+    // fixed points (an item's first and last tiles) are computed here, not
+    // hoisted out of the item loop to sit in registers for the whole kernel
+    asm volatile("" : "+s"(t));
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
       const uint32_t off = valid ? voff[i] + static_cast<uint32_t>(t) * tile_bytes : kOOB;
       const uint32_t dst = __builtin_amdgcn_readfirstlane(
           static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(tile + lds_off + i * 1024))));
-      dma16(rsrc, dst, off);
+      dma16(r, dst, off);
     }
   }
 };
@@ -442,19 +458,70 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
   // together on one XCD (its K and V stay in that L2) and per-workgroup work
   // evens out.  (Equal items are left to the hardware dispatcher, which also
   // lets a finished workgroup's stores drain off the next one's path.)
-  auto item = [&](int bh, int qb) {
+  //
+  // Consecutive items of a workgroup are chained: the LDS ring keeps
+  // rotating (item i's tile t lives in stage (base_i + t) mod 4, base_{i+1} =
+  // base_i + nkv_i), the K / V loads of the next item's first two tiles take
+  // the slots of item i's last two periods (the slots a lone item fills with
+  // empty loads), and its Q fragments are loaded at the start of item i's
+  // last period, when every wave has computed its last S.  So an item
+  // starts with its first tiles and Q on chip instead of paying two memory
+  // round trips.  Between those tiles and the item's first period the
+  // wave's vector-memory queue then also holds the Q loads and the previous
+  // item's O stores (kHandoff of them), which the first two waits allow for.
+  constexpr int kHandoff = KS + 4 * DT;
+  u32x4 qf[KS];             // Q fragments (A operand of S): row my_q, d = 16 ks + 8 (lane >> 5) .. + 7
+  int base = 0;             // stage of the current item's tile 0
+  const int off = (CAUSAL && a.causal == 2) ? a.Skv - a.Sq : 0;
+  // key tiles of query block qb
+  auto tiles_of = [&](int qb) {
+    int kv_end = a.Skv;
+    if (CAUSAL) kv_end = max(0, min(a.Skv, qb * kFaRows + kFaRows + off));
+    return (kv_end + BN - 1) / BN;
+  };
+  // Q rows of item (bh, qb) into qf (buffer loads: rows past Sq read as zero)
+  auto load_q = [&](int bh, int qb) {
+    const int b = bh / a.Hq, h = bh - b * a.Hq;
+    const T* Q = static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1];
+    const __amdgpu_buffer_rsrc_t rq =
+        buffer_rsrc(Q, static_cast<uint32_t>(static_cast<int64_t>(a.Sq) * a.qs[2] * 2));
+    const uint32_t row = static_cast<uint32_t>((qb * kFaRows + wave * 32 + (lane & 31)) * a.qs[2] * 2);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rq, row + ks * 32 + 16 * (lane >> 5), 0, 0));
+  };
+  // K / V of (batch * head) bh
+  auto k_base = [&](int bh) {
+    const int b = bh / a.Hq, h = bh - b * a.Hq;
+    return static_cast<const T*>(a.k) + b * a.ks[0] + (h / (a.Hq / a.Hkv)) * a.ks[1];
+  };
+  auto v_base = [&](int bh) {
+    const int b = bh / a.Hq, h = bh - b * a.Hq;
+    return static_cast<const T*>(a.v) + b * a.vs[0] + (h / (a.Hq / a.Hkv)) * a.vs[1];
+  };
+  KvDma<D, false, NW> kd;
+  KvDma<D, true, NW> vd;
+  kd.init(k_base(0), a.ks[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane);
+  vd.init(v_base(0), a.vs[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane);
+  // One work item (batch * head, query block) per workgroup, or, in the
+  // persistent form (causal: items of unequal length), one workgroup per CU
+  // walking the items that fa_item picks so that a head's query blocks run
+  // together on one XCD (its K and V stay in that L2) and per-workgroup work
+  // evens out.  (Equal items are left to the hardware dispatcher, which also
+  // lets a finished workgroup's stores drain off the next one's path.)
+  // nbh < 0: no next item.  CHAINED (a std::bool_constant): the item's
+  // first tiles and Q were issued by the previous item.
+  auto item = [&](auto chained_tag, int bh, int qb, int nbh, int nqbi) {
+  constexpr bool chained = decltype(chained_tag)::value;
   const int b = bh / a.Hq, h = bh - b * a.Hq;
-  const int hk = h / (a.Hq / a.Hkv);
   const int q0 = qb * kFaRows;
   const int qw = q0 + wave * 32;
   const int my_q = qw + (lane & 31);
-  const int off = (CAUSAL && a.causal == 2) ? a.Skv - a.Sq : 0;
   const float c = a.scale_log2;  // > 0 on this path
-  const T* Q = static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1];
-
-  int kv_end = a.Skv;
-  if (CAUSAL) kv_end = max(0, min(a.Skv, q0 + kFaRows + off));
-  const int nkv = (kv_end + BN - 1) / BN;
+  const int nkv = tiles_of(qb);
+  const bool has_next = nbh >= 0;
+  const int nkv_next = has_next ? tiles_of(nqbi) : 0;
   // last tile this wave needs (-1: none)
   int jl = nkv - 1;
   if (CAUSAL) {
@@ -469,29 +536,37 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
   if (CAUSAL) lim = min(lim, my_q + off);
   lim -= 4 * (lane >> 5);
 
-  // Q fragments (A operand of S): row my_q, d = 16 ks + 8 (lane >> 5) .. + 7
-  u32x4 qf[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    if (my_q < a.Sq)
-      qf[ks] = *reinterpret_cast<const u32x4*>(Q + my_q * a.qs[2] + ks * 16 + 8 * (lane >> 5));
-    else
-      qf[ks] = u32x4{0, 0, 0, 0};
-  }
-
-  KvDma<D, false, NW> kd;
-  KvDma<D, true, NW> vd;
-  kd.init(static_cast<const T*>(a.k) + b * a.ks[0] + hk * a.ks[1], a.ks[2],
-          static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane);
-  vd.init(static_cast<const T*>(a.v) + b * a.vs[0] + hk * a.vs[1], a.vs[2],
-          static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane);
-  auto dma = [&](int t) {
-    char* st = smem + (t % NS) * kStage;
-    kd.issue(st, t, t < nkv);
-    vd.issue(st + kTile, t, t < nkv);
+  const u32x4 rk = kd.rsrc_at(k_base(bh)), rv = vd.rsrc_at(v_base(bh));
+  const u32x4 rkn = kd.rsrc_at(k_base(has_next ? nbh : bh)), rvn = vd.rsrc_at(v_base(has_next ? nbh : bh));
+  // Slot g of the load stream: this item's tile g, then the next item's
+  // tiles 0 and 1 (empty loads when there is no next item, so that every
+  // period issues L instructions until the last one), then nothing.
+  auto dma = [&](int g) {
+    char* st = smem + ((base + g) & 3) * kStage;
+    if (g < nkv) {
+      kd.issue(rk, st, g, true);
+      vd.issue(rv, st + kTile, g, true);
+    } else if (!has_next) {
+      kd.issue(rk, st, 0, false);
+      vd.issue(rv, st + kTile, 0, false);
+    } else if (g - nkv < 2) {
+      kd.issue(rkn, st, g - nkv, g - nkv < nkv_next);
+      vd.issue(rvn, st + kTile, g - nkv, g - nkv < nkv_next);
+    }
   };
-  dma(0);
-  dma(1);
+  if constexpr (!chained) {
+    load_q(bh, qb);
+    dma(0);
+    dma(1);
+  }
+  // The S products read qf: settle its loads here, once per item, rather
+  // than let the compiler wait for them (and so for every memory operation
+  // in flight) inside the tile loop.  First items are compiled apart from
+  // chained ones so that for the latter the compiler sees what the wave's
+  // queue holds -- Q loads older than the previous item's O stores only --
+  // and waits for Q alone.
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qf[ks]));
 
   f32x16 o[DT];
 #pragma unroll
@@ -508,9 +583,9 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
   // read while MFMA i runs, and a scheduling fence per step pins that order
   // (left to the scheduler, the phase was compiled with one fragment register
   // set and an LDS round trip before every MFMA).
-  auto matrix_phase = [&](int j) {
-    if (j >= 0) {
-      const char* sv = smem + (j % NS) * kStage + kTile;
+  auto pv_part = [&](int j) {
+    {
+      const char* sv = smem + ((base + j) & 3) * kStage + kTile;
       constexpr int nm = 4 * DT;  // MFMA i: key slice i / DT, d tile i % DT
       u32x4 f[kPrefetch];
 #pragma unroll
@@ -524,8 +599,10 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (j + 1 <= jl) {
-      const char* sk = smem + ((j + 1) % NS) * kStage;
+  };
+  auto qk_part = [&](int j) {
+    {
+      const char* sk = smem + ((base + j + 1) & 3) * kStage;
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -542,6 +619,10 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  auto matrix_phase = [&](int j) {
+    if (j >= 0) pv_part(j);
+    if (j + 1 <= jl) qk_part(j);
   };
   // vector phase of tile t: mask (on tiles that reach the end of the keys or
   // cross the wave's diagonal); a raise of the reference max of the rows
@@ -616,54 +697,81 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
   // stage of tile k - 2 is free for tile k + 2.  Each group has a loop of its
   // own so that S and P are never both live across an iteration.
   auto period_start = [&](int k) {
-    wait_vmcnt<L>();  // this wave's DMA of tile k landed (tile k + 1 may be in flight)
+    // this wave's DMA of tile k landed (tile k + 1 may be in flight, and in a
+    // chained item's first two periods the Q loads and previous O stores)
+    if (chained && k < 2)
+      wait_vmcnt<L + kHandoff>();
+    else
+      wait_vmcnt<L>();
     block_barrier();
     dma(k + 2);
   };
   if (grp == 0) {
-    for (int k = 0; k <= nkv; ++k) {
+    for (int k = 0; k < nkv; ++k) {
       period_start(k);
       if (k - 1 <= jl) matrix_phase(k - 1);
       block_barrier();
       if (k <= jl) vector_phase(k);
     }
   } else {
-    for (int k = 0; k <= nkv; ++k) {
+    for (int k = 0; k < nkv; ++k) {
       period_start(k);
       if (k >= 1 && k - 1 <= jl) vector_phase(k - 1);
       block_barrier();
       if (k - 1 <= jl) matrix_phase(k - 1);
     }
   }
-  wait_vmcnt<0>();  // this item's DMA has landed (the next item reuses the stages)
-
-  const float l = l_half + __shfl_xor(l_half, 32, 64);
-  if (my_q < a.Sq) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    T* O = static_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(my_q) * a.os[2];
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        T v4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
-        *reinterpret_cast<u32x2*>(O + t * 32 + 8 * qq + 4 * (lane >> 5)) = __builtin_bit_cast(u32x2, v4);
-      }
+  // last period (k = nkv): only P V of the last tile is left, so Q is dead
+  // and the next item's Q loads go out first (peeled out of the loops so the
+  // compiler never sees them pending at an S product inside a loop)
+  period_start(nkv);
+  if (has_next) load_q(nbh, nqbi);
+  const bool last_pv = nkv - 1 <= jl && nkv >= 1;
+  if (grp == 0) {
+    if (last_pv) pv_part(nkv - 1);
+    block_barrier();
+  } else {
+    if (last_pv) vector_phase(nkv - 1);
+    block_barrier();
+    if (last_pv) pv_part(nkv - 1);
   }
+  const float l = l_half + __shfl_xor(l_half, 32, 64);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  // O rows via buffer stores: rows past Sq are dropped, and every lane
+  // issues exactly 4 DT stores (the count the next item's waits rely on)
+  T* O = static_cast<T*>(a.o) + b * a.os[0] + h * a.os[1];
+  const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(O, static_cast<uint32_t>(static_cast<int64_t>(a.Sq) * a.os[2] * 2));
+  const uint32_t orow = static_cast<uint32_t>(my_q * a.os[2] * 2);
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      T v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v4), ro,
+                                            orow + (t * 32 + 8 * qq + 4 * (lane >> 5)) * 2, 0, 0);
+    }
+  base = (base + nkv) & 3;
   };  // item
   if constexpr (PERSIST) {
-    for (int round = 0;; ++round) {
-      int bh, qb;
-      if (!fa_item(round, a.B * a.Hq, nqb, bh, qb)) break;
-      if (round > 0) block_barrier();  // every wave is done with the previous item's LDS stages
-      item(bh, qb);
+    int bh, qb, nbh, nqbi;
+    if (fa_item(0, a.B * a.Hq, nqb, bh, qb)) {
+      bool more = fa_item(1, a.B * a.Hq, nqb, nbh, nqbi);
+      item(std::false_type{}, bh, qb, more ? nbh : -1, more ? nqbi : 0);
+      for (int round = 1; more; ++round) {
+        bh = nbh;
+        qb = nqbi;
+        more = fa_item(round + 1, a.B * a.Hq, nqb, nbh, nqbi);
+        item(std::true_type{}, bh, qb, more ? nbh : -1, more ? nqbi : 0);
+      }
     }
   } else {
     int bh, qb;
     attn_block(static_cast<int>(blockIdx.x), total, nqb, bh, qb);
-    item(bh, qb);
+    item(std::false_type{}, bh, qb, -1, 0);
   }
+  wait_vmcnt<0>();  // no DMA may land after the workgroup ends
 }
 
 // Generic path: one wave per (batch, head, query row); lane owns d = lane +
@@ -759,11 +867,14 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
                     aligned16(a.v) && (reinterpret_cast<uintptr_t>(a.o) & 7u) == 0;
   if constexpr (!std::is_same<T, float>::value) {
     // DMA path: no explicit mask, a positive scale (the max of the scaled
-    // scores is the scaled max), rows that do not overlap, and every key
-    // row's byte offset within 2^31
+    // scores is the scaled max), rows that do not overlap, and every key,
+    // query and output row's byte offset (up to one block past the end)
+    // within 2^31
     const int64_t ld = std::max(a.ks[2], a.vs[2]);
+    const int64_t qo = std::max(a.qs[2], a.os[2]);
     const bool dma = mfma && a.mask_dtype < 0 && a.scale_log2 > 0.f && a.Sq > 128 && a.Skv > 0 &&
-                     a.ks[2] >= a.D && a.vs[2] >= a.D && (static_cast<int64_t>(a.Skv) + 256) * ld * 2 < 0x7fffffffLL;
+                     a.ks[2] >= a.D && a.vs[2] >= a.D && (static_cast<int64_t>(a.Skv) + 256) * ld * 2 < 0x7fffffffLL &&
+                     (static_cast<int64_t>(a.Sq) + kFaRows) * qo * 2 < 0x7fffffffLL;
     if (dma) return a.D == 128 ? launch_flash_attn<T, 128>(a, st) : launch_flash_attn<T, 64>(a, st);
     if (mfma) {
       const int nqb = (a.Sq + 127) / 128;

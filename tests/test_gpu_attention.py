@@ -146,3 +146,25 @@ def test_sdpa_config_full_size():
         assert_close(got[b:b + 1, h:h + 1], exp, 2.5e-2, 2.5e-2, f"config head ({b}, {h})")
     assert torch.equal(got[:, :, 0].cpu(), v[:, :, 0])
     assert torch.isfinite(got).all()
+
+
+@pytest.mark.parametrize("b, hq, hkv, sq, skv, d, variant, dtype", [
+    (4, 64, 16, 384, 384, 128, CausalVariant.UPPER_LEFT, torch.bfloat16),
+    (2, 128, 32, 320, 700, 64, CausalVariant.LOWER_RIGHT, torch.float16),
+    (3, 96, 96, 520, 520, 128, CausalVariant.UPPER_LEFT, torch.float16),
+])
+def test_sdpa_causal_many_items_per_workgroup(b, hq, hkv, sq, skv, d, variant, dtype):
+    """Causal attention runs one workgroup per CU over several (batch, head,
+    query block) items, each item starting on K / V tiles and Q rows its
+    predecessor loaded: more items than CUs (ragged last query blocks,
+    unequal key counts, GQA, both causal corners), every head against the
+    oracle."""
+    torch.manual_seed(sq * 31 + skv)
+    q = torch.randn(b, hq, sq, d).to(dtype)
+    k = torch.randn(b, hkv, skv, d).to(dtype)
+    v = torch.randn(b, hkv, skv, d).to(dtype)
+    assert b * hq * ((sq + 255) // 256) > 256
+    got = sdpa(q.cuda(), k.cuda(), v.cuda(), is_causal=True, enable_gqa=True, causal_variant=variant)
+    causal = 2 if variant == CausalVariant.LOWER_RIGHT else 1
+    exp = oracle(q, k, v, None, causal)
+    assert_close(got, exp, *TOL[dtype], "sdpa causal, many items per workgroup")
