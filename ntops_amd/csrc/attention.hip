@@ -436,8 +436,8 @@ __device__ __forceinline__ bool fa_item(int r, int nbh, int nqb, int& bh, int& q
   return true;
 }
 
-template <typename T, int D, bool CAUSAL, bool PERSIST>
-__global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int total) {
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb) {
   constexpr int BN = 64;
   constexpr int NS = kFaStages;
   constexpr int NW = kFaWaves;
@@ -452,13 +452,6 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2;  // 0: leads, 1: one phase behind (one wave of each per SIMD)
-  // One work item (batch * head, query block) per workgroup, or, in the
-  // persistent form (causal: items of unequal length), one workgroup per CU
-  // walking the items that fa_item picks so that a head's query blocks run
-  // together on one XCD (its K and V stay in that L2) and per-workgroup work
-  // evens out.  (Equal items are left to the hardware dispatcher, which also
-  // lets a finished workgroup's stores drain off the next one's path.)
-  //
   // Consecutive items of a workgroup are chained: the LDS ring keeps
   // rotating (item i's tile t lives in stage (base_i + t) mod 4, base_{i+1} =
   // base_i + nkv_i), the K / V loads of the next item's first two tiles take
@@ -504,13 +497,10 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
   KvDma<D, true, NW> vd;
   kd.init(k_base(0), a.ks[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane);
   vd.init(v_base(0), a.vs[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane);
-  // One work item (batch * head, query block) per workgroup, or, in the
-  // persistent form (causal: items of unequal length), one workgroup per CU
-  // walking the items that fa_item picks so that a head's query blocks run
-  // together on one XCD (its K and V stay in that L2) and per-workgroup work
-  // evens out.  (Equal items are left to the hardware dispatcher, which also
-  // lets a finished workgroup's stores drain off the next one's path.)
-  // nbh < 0: no next item.  CHAINED (a std::bool_constant): the item's
+  // Work item (batch * head, query block) of a persistent workgroup (one
+  // per CU) walking the items fa_item picks, so that a head's query blocks
+  // run together on one XCD (its K and V stay in that L2) and per-workgroup
+  // work evens out under a causal mask.  nbh < 0: no next item.  CHAINED (a std::bool_constant): the item's
   // first tiles and Q were issued by the previous item.
   auto item = [&](auto chained_tag, int bh, int qb, int nbh, int nqbi) {
   constexpr bool chained = decltype(chained_tag)::value;
@@ -754,22 +744,16 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb, int 
     }
   base = (base + nkv) & 3;
   };  // item
-  if constexpr (PERSIST) {
-    int bh, qb, nbh, nqbi;
-    if (fa_item(0, a.B * a.Hq, nqb, bh, qb)) {
-      bool more = fa_item(1, a.B * a.Hq, nqb, nbh, nqbi);
-      item(std::false_type{}, bh, qb, more ? nbh : -1, more ? nqbi : 0);
-      for (int round = 1; more; ++round) {
-        bh = nbh;
-        qb = nqbi;
-        more = fa_item(round + 1, a.B * a.Hq, nqb, nbh, nqbi);
-        item(std::true_type{}, bh, qb, more ? nbh : -1, more ? nqbi : 0);
-      }
+  int bh, qb, nbh, nqbi;
+  if (fa_item(0, a.B * a.Hq, nqb, bh, qb)) {
+    bool more = fa_item(1, a.B * a.Hq, nqb, nbh, nqbi);
+    item(std::false_type{}, bh, qb, more ? nbh : -1, more ? nqbi : 0);
+    for (int round = 1; more; ++round) {
+      bh = nbh;
+      qb = nqbi;
+      more = fa_item(round + 1, a.B * a.Hq, nqb, nbh, nqbi);
+      item(std::true_type{}, bh, qb, more ? nbh : -1, more ? nqbi : 0);
     }
-  } else {
-    int bh, qb;
-    attn_block(static_cast<int>(blockIdx.x), total, nqb, bh, qb);
-    item(std::false_type{}, bh, qb, -1, 0);
   }
   wait_vmcnt<0>();  // no DMA may land after the workgroup ends
 }
@@ -834,8 +818,7 @@ __global__ __launch_bounds__(64) void k_attn_generic(AttnArgs a) {
 template <typename T, int D, bool CAUSAL>
 int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
   constexpr int kLds = kFaStages * 2 * 64 * D * 2;
-  constexpr bool kPersist = CAUSAL;
-  auto kern = k_flash_attn<T, D, CAUSAL, kPersist>;
+  auto kern = k_flash_attn<T, D, CAUSAL>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -846,10 +829,11 @@ int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
   const int nqb = (a.Sq + kFaRows - 1) / kFaRows;
   const int64_t total = static_cast<int64_t>(nqb) * a.Hq * a.B;
   if (total > 0x3fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many work items");
-  // persistent: one workgroup per CU (each takes 128 KiB of LDS)
-  const int64_t grid = kPersist ? std::min<int64_t>(total, cu_count_cached()) : total;
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kFaWaves * 64), kLds, st, a, nqb,
-                     static_cast<int>(total));
+  // persistent: one workgroup per CU (each takes 128 KiB of LDS), chained
+  // items of equal or unequal length (same-box A/B, non-causal
+  // (4, 32, 2048, 128): 903 against 865 TFLOP/s for one workgroup per item)
+  const int64_t grid = std::min<int64_t>(total, cu_count_cached());
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kFaWaves * 64), kLds, st, a, nqb);
   return check_launch("sdpa");
 }
 

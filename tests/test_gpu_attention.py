@@ -168,3 +168,20 @@ def test_sdpa_causal_many_items_per_workgroup(b, hq, hkv, sq, skv, d, variant, d
     causal = 2 if variant == CausalVariant.LOWER_RIGHT else 1
     exp = oracle(q, k, v, None, causal)
     assert_close(got, exp, *TOL[dtype], "sdpa causal, many items per workgroup")
+
+
+@pytest.mark.parametrize("b, hq, hkv, sq, skv, d, dtype", [
+    (4, 64, 64, 300, 448, 128, torch.bfloat16),
+    (3, 96, 24, 260, 260, 64, torch.float16),
+])
+def test_sdpa_many_items_per_workgroup(b, hq, hkv, sq, skv, d, dtype):
+    """Non-causal attention over more items than CUs (one persistent
+    workgroup per CU, chained items, ragged last query blocks, GQA): every
+    head against the oracle."""
+    torch.manual_seed(sq * 13 + skv)
+    q = torch.randn(b, hq, sq, d).to(dtype)
+    k = torch.randn(b, hkv, skv, d).to(dtype)
+    v = torch.randn(b, hkv, skv, d).to(dtype)
+    assert b * hq * ((sq + 255) // 256) > 256
+    got = sdpa(q.cuda(), k.cuda(), v.cuda(), enable_gqa=True)
+    assert_close(got, oracle(q, k, v), *TOL[dtype], "sdpa, many items per workgroup")
