@@ -131,222 +131,6 @@ __device__ __forceinline__ void attn_block(int pid, int total, int nqb, int& bh,
   qb = nqb - 1 - (pid - bh * nqb);
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int total) {
-  constexpr int BM = 128, BN = 64;
-  constexpr int KS = D / 16;   // k-steps of S = Q K^T
-  constexpr int DT = D / 32;   // 32-column tiles of O
-  constexpr int CPR = D / 8;   // 16-byte chunks per K / V row
-  constexpr int CH = BN * CPR / 256;  // chunks per thread per tile
-  constexpr int kTile = BN * D * 2;   // bytes of one K or V tile
-  static_assert(CH * 256 == BN * CPR, "tile must split evenly over the threads");
-  __shared__ __attribute__((aligned(16))) char smem[2 * 2 * kTile];  // [stage][K, V]
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  int bh, qb;
-  attn_block(blockIdx.x, total, nqb, bh, qb);
-  const int b = bh / a.Hq, h = bh - b * a.Hq;
-  const int hk = h / (a.Hq / a.Hkv);
-  const int q0 = qb * BM;
-  const int qw = q0 + wave * 32;
-  const int my_q = qw + (lane & 31);
-  const int off = a.causal == 2 ? a.Skv - a.Sq : 0;
-  const T* Q = static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1];
-  const T* K = static_cast<const T*>(a.k) + b * a.ks[0] + hk * a.ks[1];
-  const T* V = static_cast<const T*>(a.v) + b * a.vs[0] + hk * a.vs[1];
-
-  // Q fragments (A operand of S): row my_q, d = 16 ks + 8 (lane >> 5) .. + 7.
-  u32x4 qf[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    if (my_q < a.Sq)
-      qf[ks] = *reinterpret_cast<const u32x4*>(Q + my_q * a.qs[2] + ks * 16 + 8 * (lane >> 5));
-    else
-      qf[ks] = u32x4{0, 0, 0, 0};
-  }
-
-  int kv_end = a.Skv;
-  if (a.causal) kv_end = max(0, min(a.Skv, q0 + BM + off));
-  const int nkv = (kv_end + BN - 1) / BN;
-
-  u32x4 kr[CH], vr[CH];
-  auto gload = [&](int j) {
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int ci = threadIdx.x + 256 * u;
-      const int row = ci / CPR, c = ci - row * CPR;
-      const int kv = j * BN + row;
-      if (kv < a.Skv) {
-        kr[u] = *reinterpret_cast<const u32x4*>(K + kv * a.ks[2] + c * 8);
-        vr[u] = *reinterpret_cast<const u32x4*>(V + kv * a.vs[2] + c * 8);
-      } else {
-        // keys past the end are masked; zero values keep 0 * V finite
-        kr[u] = u32x4{0, 0, 0, 0};
-        vr[u] = u32x4{0, 0, 0, 0};
-      }
-    }
-  };
-  auto swrite = [&](int stage) {
-    char* sk = smem + stage * 2 * kTile;
-    char* sv = sk + kTile;
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int ci = threadIdx.x + 256 * u;
-      const int row = ci / CPR, c = ci - row * CPR;
-      *reinterpret_cast<u32x4*>(sk + row * (D * 2) + kslot<D>(row, c) * 16) = kr[u];
-      *reinterpret_cast<u32x4*>(sv + row * (D * 2) + vslot<D>(row, c) * 16) = vr[u];
-    }
-  };
-
-  f32x16 o[DT];
-#pragma unroll
-  for (int t = 0; t < DT; ++t)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
-  float m_i = neg_inf(), l_i = 0.f;  // running max (base 2) and sum of row my_q
-
-  if (nkv > 0) {
-    gload(0);
-    swrite(0);
-  }
-  __syncthreads();
-
-  for (int j = 0; j < nkv; ++j) {
-    const int cur = j & 1;
-    if (j + 1 < nkv) gload(j + 1);
-    const char* sk = smem + cur * 2 * kTile;
-    const char* sv = sk + kTile;
-
-    // S = Q K^T for this wave's 32 rows x 64 keys (two 32x32 tiles)
-    f32x16 s[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s[t][e] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) s[t] = mfma32<T>(k_frag<D>(sk, t * 32, ks, lane), qf[ks], s[t]);
-
-    // base-2 scores with masking; element 4q + e of tile t is key
-    // kv0 + 32 t + 8 q + 4 (lane >> 5) + e
-    const int kv0 = j * BN;
-    const bool full = kv0 + BN <= a.Skv && a.mask_dtype < 0 &&
-                      (a.causal == 0 || kv0 + BN - 1 <= qw + off);
-    float x[2][16];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) x[t][e] = s[t][e] * a.scale_log2;
-    if (!full) {
-      const int64_t mrow = b * a.ms[0] + h * a.ms[1] + static_cast<int64_t>(my_q) * a.ms[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int kv = kv0 + 32 * t + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-          bool ok = kv < a.Skv && my_q < a.Sq;
-          if (a.causal) ok = ok && kv <= my_q + off;
-          float val = ok ? x[t][e] : neg_inf();
-          if (ok && a.mask_dtype >= 0) val += mask_log2(a, mrow + kv * a.ms[3]);
-          x[t][e] = val;
-        }
-    }
-
-    // online softmax of row my_q (lanes l and l ^ 32 hold its two halves)
-    float mx = neg_inf();
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, x[t][e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_i, mx);
-    const float m_use = m_new == neg_inf() ? 0.f : m_new;  // fully masked so far: keep P = 0
-    const float alpha = fast_exp2(m_i - m_use);
-    float rs = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        x[t][e] = fast_exp2(x[t][e] - m_use);
-        rs += x[t][e];
-      }
-    rs += __shfl_xor(rs, 32, 64);
-    l_i = l_i * alpha + rs;
-    m_i = m_new;
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
-
-    // O += P V over the four 16-key slices
-#pragma unroll
-    for (int sl = 0; sl < 4; ++sl) {
-      const u32x4 pf = pack8<T>(&x[sl >> 1][8 * (sl & 1)]);
-#pragma unroll
-      for (int t = 0; t < DT; ++t) o[t] = mfma32<T>(v_frag<D>(sv, t * 32, sl, lane), pf, o[t]);
-    }
-
-    // the other stage was last read in the previous iteration, before the
-    // barrier that ended it
-    if (j + 1 < nkv) swrite(cur ^ 1);
-    __syncthreads();
-  }
-
-  if (my_q >= a.Sq) return;
-  const float inv = l_i > 0.f ? 1.f / l_i : 0.f;
-  T* O = static_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(my_q) * a.os[2];
-#pragma unroll
-  for (int t = 0; t < DT; ++t)
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      T v4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
-      *reinterpret_cast<u32x2*>(O + t * 32 + 8 * qq + 4 * (lane >> 5)) = __builtin_bit_cast(u32x2, v4);
-    }
-}
-
-// ---- flash forward without an explicit mask (none or causal) ---------------
-//
-// 8-wave workgroups over work items of (batch, head, 256 query rows) -- one
-// per item, or (causal) persistent, one per CU walking items longest first;
-// wave w owns rows 32w .. 32w + 31 of the item with their Q fragments in
-// VGPRs.
-// K and V tiles of 64 keys go global -> LDS by direct DMA (no VGPR staging)
-// into a ring of kFaStages stages; tile t lives in stage t % kFaStages, with
-// the swizzles of k_frag / v_frag applied on the global side (a lane's LDS
-// destination is fixed, so it fetches the chunk that belongs there).
-// Iteration j of a wave:
-//   barrier (K_{j+1} and V_j landed for every wave; stage (j - 1) % NS free)
-//   DMA tile j + NS - 1 into that stage
-//   S_{j+1} = Q K_{j+1}^T on the matrix cores while P_j = exp2(S_j c - m)
-//   runs on the VALU (independent instructions of one wave overlap);
-//   O += P_j V_j while S_{j+1} is masked and reduced to its row max.
-// Lazy rescaling: exponentials use a running reference max m that is raised
-// only when a row's max exceeds it by more than 2^8 (then O and l are scaled
-// by exp2(m_old - m_new) once); P <= 256 keeps fp32 sums and the T-rounded P
-// exact in relative terms, and O / l is unchanged by the choice of m.
-// Causal: the block walks keys up to its last row's limit; a wave skips the
-// tiles beyond its own rows' limit (it still issues its share of the DMA and
-// joins the barriers).
-constexpr int kFaRows = 256;
-constexpr int kFaWaves = 8;
-constexpr int kFaStages = 4;
-constexpr int kPrefetch = 4;  // LDS fragment reads in flight ahead of the MFMA that uses them
-
-// Instruction classes of the scheduler's group barriers.
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedDsRead = 0x100;
-
-// Asks the scheduler for a group of N instructions of class MASK here (in
-// order with the other groups of the region).
-template <int MASK, int N>
-__device__ __forceinline__ void sched_group() {
-  __builtin_amdgcn_sched_group_barrier(MASK, N, 0);
-}
-
 // DMA of one 64 x D K or V tile: D * 2 bytes per key row, 1 KiB per
 // instruction, instructions spread evenly over the NW waves.
 template <int D, bool IS_V, int NW>
@@ -407,6 +191,306 @@ struct KvDma {
     }
   }
 };
+
+// MM: explicit-mask mode -- 0 none, 1 runs of 4 keys per access (rows
+// 4-element aligned), 2 element loads; ESZ: mask element bytes (1 bool, 2
+// fp16 / bf16, 4 fp32).  Both are template parameters so that every mask
+// load writes fixed registers.
+template <typename T, int D, int MM, int ESZ>
+__global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int total) {
+  constexpr int BM = 128, BN = 64;
+  constexpr int kFwdAhead = 4;  // fragments read ahead of the MFMA that uses them
+  constexpr int KS = D / 16;   // k-steps of S = Q K^T
+  constexpr int DT = D / 32;   // 32-column tiles of O
+  constexpr int kTile = BN * D * 2;   // bytes of one K or V tile
+  constexpr int L = 2 * KvDma<D, false, 4>::kInst;  // DMA instructions per lane per tile
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * kTile];  // [stage][K, V]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int bh, qb;
+  attn_block(blockIdx.x, total, nqb, bh, qb);
+  const int b = bh / a.Hq, h = bh - b * a.Hq;
+  const int hk = h / (a.Hq / a.Hkv);
+  const int q0 = qb * BM;
+  const int qw = q0 + wave * 32;
+  const int my_q = qw + (lane & 31);
+  const int off = a.causal == 2 ? a.Skv - a.Sq : 0;
+  const T* Q = static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const T* K = static_cast<const T*>(a.k) + b * a.ks[0] + hk * a.ks[1];
+  const T* V = static_cast<const T*>(a.v) + b * a.vs[0] + hk * a.vs[1];
+
+  // Q fragments (A operand of S): row my_q, d = 16 ks + 8 (lane >> 5) .. + 7.
+  u32x4 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (my_q < a.Sq)
+      qf[ks] = *reinterpret_cast<const u32x4*>(Q + my_q * a.qs[2] + ks * 16 + 8 * (lane >> 5));
+    else
+      qf[ks] = u32x4{0, 0, 0, 0};
+  }
+
+  int kv_end = a.Skv;
+  if (a.causal) kv_end = max(0, min(a.Skv, q0 + BM + off));
+  const int nkv = (kv_end + BN - 1) / BN;
+
+  // Explicit mask (keys contiguous; other layouts take the generic kernel).
+  // It enters S as the MFMA accumulator's initial value, mask / scale, so
+  // S * scale carries it; its raw data for tile j + 1 is loaded while tile j
+  // is softmaxed and multiplied by V (S's registers are free then), through
+  // a buffer resource over this (batch, head)'s plane (a row past Sq or a key
+  // past the plane reads 0; such keys are masked anyway).  mmode 1: every run
+  // of 4 keys of a lane is one access (rows 4-element aligned); 2: element
+  // loads.
+  constexpr int esz = ESZ;
+  constexpr int mmode = MM;
+  const char* mp = mmode != 0 ? static_cast<const char*>(a.mask) + (b * a.ms[0] + h * a.ms[1]) * esz
+                              : static_cast<const char*>(a.q);
+  const int64_t mext =
+      mmode != 0 ? (static_cast<int64_t>(a.Sq - 1) * a.ms[2] + static_cast<int64_t>(a.Skv - 1) + 1) * esz : 0;
+  const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(mp, static_cast<uint32_t>(mext));
+  const int64_t mrow = static_cast<int64_t>(my_q) * a.ms[2];
+  const float inv_scale = kLog2e / a.scale_log2;
+  // raw mask data, run r (keys kv .. kv + 3 of mask_issue) in mraw[4 r ..]:
+  // one word (bool runs), two (16-bit runs), four (fp32 runs or elementwise
+  // loads) -- the same slots in every mode, so that the compiler, which
+  // merges the branches' stores, never sees a variable index
+  uint32_t mraw[32];
+  auto mask_issue = [&](int j) {
+    const bool row_ok = my_q < a.Sq;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {  // run r: keys kv .. kv + 3
+      const int kv = j * BN + 32 * (r >> 2) + 8 * (r & 3) + 4 * (lane >> 5);
+      const uint32_t o = row_ok && kv < a.Skv ? static_cast<uint32_t>((mrow + kv) * esz) : kOOB;
+      if constexpr (mmode == 1) {
+        if constexpr (esz == 1) {
+          mraw[4 * r] = __builtin_amdgcn_raw_buffer_load_b32(rm, o, 0, 0);
+        } else if constexpr (esz == 2) {
+          const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rm, o, 0, 0));
+          mraw[4 * r] = w.x;
+          mraw[4 * r + 1] = w.y;
+        } else {
+          const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rm, o, 0, 0));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mraw[4 * r + e] = w[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (esz == 1)
+            mraw[4 * r + e] = __builtin_amdgcn_raw_buffer_load_b8(rm, o, e, 0);
+          else if constexpr (esz == 2)
+            mraw[4 * r + e] = __builtin_amdgcn_raw_buffer_load_b16(rm, o, 2 * e, 0);
+          else
+            mraw[4 * r + e] = __builtin_amdgcn_raw_buffer_load_b32(rm, o, 4 * e, 0);
+        }
+      }
+    }
+  };
+  // S's initial value: mask / scale (bool: 0 or -inf) for element 4 q + e of half t
+  auto mask_init = [&](f32x16 (&sv)[2]) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t w;
+        if constexpr (mmode == 1)
+          w = esz == 1 ? (mraw[4 * r] >> (8 * e)) : esz == 2 ? (mraw[4 * r + (e >> 1)] >> (16 * (e & 1))) : mraw[4 * r + e];
+        else
+          w = mraw[4 * r + e];
+        float m;
+        if constexpr (esz == 1)
+          m = (w & 0xffu) ? 0.f : neg_inf();
+        else if constexpr (esz == 4)
+          m = __builtin_bit_cast(float, w) * inv_scale;
+        else if (a.mask_dtype == NTOPS_F16)
+          m = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w))) * inv_scale;
+        else
+          m = static_cast<float>(__builtin_bit_cast(__bf16, static_cast<uint16_t>(w))) * inv_scale;
+        sv[r >> 2][4 * (r & 3) + e] = m;
+      }
+  };
+
+  // K and V tiles go global -> LDS by direct DMA into two stages (keys past
+  // the end read as zero, keeping 0 * V finite)
+  KvDma<D, false, 4> kd;
+  KvDma<D, true, 4> vd;
+  kd.init(K, a.ks[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane);
+  vd.init(V, a.vs[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane);
+  auto dma = [&](int t) {
+    char* st = smem + (t & 1) * 2 * kTile;
+    kd.issue(st, t, true);
+    vd.issue(st + kTile, t, true);
+  };
+
+  f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
+  float m_i = neg_inf(), l_i = 0.f;  // running max (base 2) and sum of row my_q
+
+  if (nkv > 0) {
+    dma(0);
+    if constexpr (mmode != 0) mask_issue(0);
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  for (int j = 0; j < nkv; ++j) {
+    const int cur = j & 1;
+    const char* sk = smem + cur * 2 * kTile;
+    const char* sv = sk + kTile;
+
+    // S = Q K^T (+ mask / scale) for this wave's 32 rows x 64 keys (two
+    // 32x32 tiles)
+    f32x16 s[2];
+    if constexpr (mmode != 0) {
+      mask_init(s);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[t][e] = 0.f;
+    }
+    // the other stage was last read in the previous iteration, before the
+    // barrier that ended it
+    if (j + 1 < nkv) dma(j + 1);
+    {
+      // fragment i + kFwdAhead is read while MFMA i runs (hand-pipelined, one
+      // scheduling fence per step)
+      constexpr int nm = 2 * KS;  // MFMA i: d slice i / 2, key half i % 2
+      u32x4 f[kFwdAhead];
+#pragma unroll
+      for (int i = 0; i < kFwdAhead; ++i) f[i] = k_frag<D>(sk, (i % 2) * 32, i / 2, lane);
+#pragma unroll
+      for (int i = 0; i < nm; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        s[i % 2] = mfma32<T>(f[i % kFwdAhead], qf[i / 2], s[i % 2]);
+        if (i + kFwdAhead < nm) f[i % kFwdAhead] = k_frag<D>(sk, ((i + kFwdAhead) % 2) * 32, (i + kFwdAhead) / 2, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // base-2 scores with masking; element 4q + e of tile t is key
+    // kv0 + 32 t + 8 q + 4 (lane >> 5) + e
+    const int kv0 = j * BN;
+    const bool full = kv0 + BN <= a.Skv && a.mask_dtype < 0 &&
+                      (a.causal == 0 || kv0 + BN - 1 <= qw + off);
+    float x[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[t][e] = s[t][e] * a.scale_log2;
+    if constexpr (mmode != 0)
+      if (j + 1 < nkv) mask_issue(j + 1);
+    if (!full) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kv = kv0 + 32 * t + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          bool ok = kv < a.Skv && my_q < a.Sq;
+          if (a.causal) ok = ok && kv <= my_q + off;
+          x[t][e] = ok ? x[t][e] : neg_inf();
+        }
+    }
+
+    // online softmax of row my_q (lanes l and l ^ 32 hold its two halves)
+    float mx = neg_inf();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, x[t][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_i, mx);
+    const float m_use = m_new == neg_inf() ? 0.f : m_new;  // fully masked so far: keep P = 0
+    const float alpha = fast_exp2(m_i - m_use);
+    float rs = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        x[t][e] = fast_exp2(x[t][e] - m_use);
+        rs += x[t][e];
+      }
+    rs += __shfl_xor(rs, 32, 64);
+    l_i = l_i * alpha + rs;
+    m_i = m_new;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
+
+    // O += P V over the four 16-key slices, hand-pipelined as S above
+    {
+      u32x4 pf[4];
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) pf[sl] = pack8<T>(&x[sl >> 1][8 * (sl & 1)]);
+      constexpr int nm = 4 * DT;  // MFMA i: key slice i / DT, d tile i % DT
+      u32x4 f[kFwdAhead];
+#pragma unroll
+      for (int i = 0; i < kFwdAhead; ++i) f[i] = v_frag<D>(sv, (i % DT) * 32, i / DT, lane);
+#pragma unroll
+      for (int i = 0; i < nm; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        o[i % DT] = mfma32<T>(f[i % kFwdAhead], pf[i / DT], o[i % DT]);
+        if (i + kFwdAhead < nm)
+          f[i % kFwdAhead] = v_frag<D>(sv, ((i + kFwdAhead) % DT) * 32, (i + kFwdAhead) / DT, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // tile j + 1 landed (the next tile's mask loads, issued after it, may
+    // still be in flight)
+    if (j + 1 < nkv) {
+      if constexpr (mmode == 1)
+        wait_vmcnt<8>();
+      else if constexpr (mmode == 2)
+        wait_vmcnt<32>();
+      else
+        wait_vmcnt<0>();
+    }
+    __syncthreads();
+  }
+
+  if (my_q >= a.Sq) return;
+  const float inv = l_i > 0.f ? 1.f / l_i : 0.f;
+  T* O = static_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(my_q) * a.os[2];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      T v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
+      *reinterpret_cast<u32x2*>(O + t * 32 + 8 * qq + 4 * (lane >> 5)) = __builtin_bit_cast(u32x2, v4);
+    }
+}
+
+// ---- flash forward without an explicit mask (none or causal) ---------------
+//
+// Persistent 8-wave workgroups (one per CU) over work items of (batch, head,
+// 256 query rows); wave w owns rows 32w .. 32w + 31 of the item with their
+// Q fragments in VGPRs.
+// K and V tiles of 64 keys go global -> LDS by direct DMA (no VGPR staging)
+// into a ring of kFaStages stages, with the swizzles of k_frag / v_frag
+// applied on the global side (a lane's LDS destination is fixed, so it
+// fetches the chunk that belongs there).  The two waves sharing a SIMD run
+// half a tile apart: while one runs a matrix phase (O += P_j V_j, then
+// S_{j+1} = Q K_{j+1}^T) the other runs a vector phase (mask, max, exp2,
+// sum, pack P), two barriers per tile (see the loops in k_flash_attn).
+// Lazy rescaling: exponentials use a running reference max m that is raised
+// only when a row's max exceeds it by more than 2^8 (then O and l are scaled
+// by exp2(m_old - m_new) once); P <= 256 keeps fp32 sums and the T-rounded P
+// exact in relative terms, and O / l is unchanged by the choice of m.
+// Causal: the block walks keys up to its last row's limit; a wave skips the
+// tiles beyond its own rows' limit (it still issues its share of the DMA and
+// joins the barriers).
+constexpr int kFaRows = 256;
+constexpr int kFaWaves = 8;
+constexpr int kFaStages = 4;
+constexpr int kPrefetch = 4;  // fragments read ahead of the MFMA that uses them
 
 // Work item of this workgroup in round r (false: no more items).
 // Workgroups are dispatched round-robin over the 8 XCDs, so workgroup g runs
@@ -860,16 +944,37 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
                      a.ks[2] >= a.D && a.vs[2] >= a.D && (static_cast<int64_t>(a.Skv) + 256) * ld * 2 < 0x7fffffffLL &&
                      (static_cast<int64_t>(a.Sq) + kFaRows) * qo * 2 < 0x7fffffffLL;
     if (dma) return a.D == 128 ? launch_flash_attn<T, 128>(a, st) : launch_flash_attn<T, 64>(a, st);
-    if (mfma) {
+    // the masked MFMA kernel takes the mask with contiguous keys through a
+    // per-(batch, head) buffer resource (its plane spanning less than 2^31
+    // bytes) and folds it into S as mask / scale (scale != 0)
+    const int esz = a.mask_dtype == NTOPS_BOOL ? 1 : a.mask_dtype == NTOPS_F32 ? 4 : 2;
+    const bool mask_fits = a.mask_dtype < 0 ||
+                           (a.ms[3] == 1 && a.scale_log2 != 0.f &&
+                            (static_cast<int64_t>(a.Sq) * a.ms[2] + a.Skv + 68) * esz < 0x7fffffffLL);
+    if (mfma && mask_fits) {
       const int nqb = (a.Sq + 127) / 128;
       const int64_t total = static_cast<int64_t>(nqb) * a.Hq * a.B;
       if (total > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many blocks");
-      if (a.D == 128)
-        hipLaunchKernelGGL((k_flash_fwd<T, 128>), dim3(static_cast<unsigned>(total)), dim3(256), 0, st, a,
-                           nqb, static_cast<int>(total));
-      else
-        hipLaunchKernelGGL((k_flash_fwd<T, 64>), dim3(static_cast<unsigned>(total)), dim3(256), 0, st, a,
-                           nqb, static_cast<int>(total));
+      const uintptr_t mp = reinterpret_cast<uintptr_t>(a.mask);
+      const int mm = a.mask_dtype < 0 ? 0
+                     : (a.ms[2] % 4 == 0 && a.ms[1] % 4 == 0 && a.ms[0] % 4 == 0 && mp % (4 * esz) == 0) ? 1 : 2;
+      const dim3 grid(static_cast<unsigned>(total)), block(256);
+#define NTOPS_FWD(DD, MM, ES) hipLaunchKernelGGL((k_flash_fwd<T, DD, MM, ES>), grid, block, 0, st, a, nqb, static_cast<int>(total))
+#define NTOPS_FWD_D(DD)                         \
+  if (mm == 0) NTOPS_FWD(DD, 0, 1);             \
+  else if (mm == 1 && esz == 1) NTOPS_FWD(DD, 1, 1); \
+  else if (mm == 1 && esz == 2) NTOPS_FWD(DD, 1, 2); \
+  else if (mm == 1) NTOPS_FWD(DD, 1, 4);        \
+  else if (esz == 1) NTOPS_FWD(DD, 2, 1);       \
+  else if (esz == 2) NTOPS_FWD(DD, 2, 2);       \
+  else NTOPS_FWD(DD, 2, 4);
+      if (a.D == 128) {
+        NTOPS_FWD_D(128)
+      } else {
+        NTOPS_FWD_D(64)
+      }
+#undef NTOPS_FWD_D
+#undef NTOPS_FWD
       return check_launch("sdpa");
     }
   }

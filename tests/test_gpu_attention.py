@@ -185,3 +185,25 @@ def test_sdpa_many_items_per_workgroup(b, hq, hkv, sq, skv, d, dtype):
     assert b * hq * ((sq + 255) // 256) > 256
     got = sdpa(q.cuda(), k.cuda(), v.cuda(), enable_gqa=True)
     assert_close(got, oracle(q, k, v), *TOL[dtype], "sdpa, many items per workgroup")
+
+
+@pytest.mark.parametrize("skv", (384, 383))
+@pytest.mark.parametrize("mask_dtype", (torch.bool, torch.float32, torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("d", (64, 128))
+def test_sdpa_mask_load_paths(skv, mask_dtype, d):
+    """Explicit masks enter S through the MFMA accumulator, loaded four keys
+    per access when mask rows are 4-element aligned (skv 384) and key by key
+    otherwise (skv 383), for every mask element type; broadcast over batch
+    and heads, and per (batch, head)."""
+    dtype = torch.bfloat16 if mask_dtype is torch.bfloat16 else torch.float16
+    torch.manual_seed(skv + d)
+    b, h, sq = 2, 4, 200
+    q, k, v = torch.randn(b, h, sq, d).to(dtype), torch.randn(b, h, skv, d).to(dtype), torch.randn(b, h, skv, d).to(dtype)
+    for shape in ((sq, skv), (b, h, sq, skv)):
+        r = torch.rand(shape)
+        if mask_dtype is torch.bool:
+            mask = r > 0.3
+        else:
+            mask = torch.where(r > 0.3, torch.randn(shape) * 0.5, torch.tensor(float("-inf"))).to(mask_dtype)
+        got = sdpa(q.cuda(), k.cuda(), v.cuda(), attn_mask=mask.cuda())
+        assert_close(got, oracle(q, k, v, mask), *TOL[dtype], f"mask {mask_dtype} {tuple(shape)}")
