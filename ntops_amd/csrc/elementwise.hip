@@ -101,6 +101,61 @@ __device__ __forceinline__ T clamp_value(T x, T lo, T hi) {
   }
 }
 
+// ------------------------------------------------- 16-bit fast routines --
+// A 16-bit result keeps 8 (bf16) or 11 (fp16) significant bits, so for
+// 16-bit T the transcendental ops below use the hardware exp2 / rcp / sin /
+// cos (a few fp32 ulps) instead of the library's fp32-accurate routines,
+// which made the bf16 forms VALU-bound (~58 % of HBM against ~77 % for
+// fp32).  The error stays far below half a 16-bit ulp, so results differ
+// from the fp32-accurate ones only where the fp32 value sits at a 16-bit
+// rounding boundary (then by one ulp).
+constexpr float kLog2eF = 1.44269504088896341f;
+constexpr float kInv2PiF = 0.159154943091895336f;
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2eF); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+// 1 / (1 + exp(-x)): exp overflows to inf for x -> -inf, giving 0.
+__device__ __forceinline__ float fast_sigmoid(float x) { return fast_rcp(1.0f + fast_exp(-x)); }
+// tanh x = 1 - 2 / (exp(2x) + 1), odd-extended; below |x| = 2^-4 the odd
+// Taylor polynomial x (1 - x^2/3 + 2x^4/15) (truncation < 2^-26 relative)
+// avoids the cancellation.
+__device__ __forceinline__ float fast_tanh(float x) {
+  const float ax = __builtin_fabsf(x);
+  const float big = 1.0f - 2.0f * fast_rcp(fast_exp(2.0f * ax) + 1.0f);
+  const float x2 = x * x;
+  const float small = ax * __builtin_fmaf(x2, __builtin_fmaf(x2, 0.133333333f, -0.333333333f), 1.0f);
+  return __builtin_copysignf(ax < 0.0625f ? small : big, x);
+}
+// erf by Abramowitz & Stegun 7.1.26 (absolute error < 1.5e-7), odd-extended.
+__device__ __forceinline__ float fast_erf(float x) {
+  const float ax = __builtin_fabsf(x);
+  const float t = fast_rcp(__builtin_fmaf(0.3275911f, ax, 1.0f));
+  float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.254829592f);
+  const float r = 1.0f - p * t * fast_exp(-ax * ax);
+  return __builtin_copysignf(r, x);
+}
+// sin / cos from the hardware's v_sin / v_cos, which take the phase in
+// revolutions (valid within +-256): x / (2 pi) carries an absolute error
+// below |x| 2^-24 revolutions, so beyond |x| = 1024 (163 revolutions) the
+// library routine (exact argument reduction) is used.
+__device__ __forceinline__ float fast_sin(float x) {
+  return __builtin_fabsf(x) < 1024.0f ? __builtin_amdgcn_sinf(x * kInv2PiF) : sinf(x);
+}
+__device__ __forceinline__ float fast_cos(float x) {
+  return __builtin_fabsf(x) < 1024.0f ? __builtin_amdgcn_cosf(x * kInv2PiF) : cosf(x);
+}
+// a^b for a > 0, both finite: exp2(b log2 a) with the hardware log2 / exp2
+// (relative error about |b log2 a| 2^-23 -- below 2^-12 while the result is
+// within fp32 range of 2^+-126, far below a 16-bit ulp); every other case
+// (negative or zero base, infinities, NaN, the integer-exponent rules) goes
+// to the library pow.
+__device__ __forceinline__ float fast_pow(float a, float b) {
+  const bool plain = a > 0.0f && a < __builtin_huge_valf() && __builtin_fabsf(b) < __builtin_huge_valf();
+  return plain ? __builtin_amdgcn_exp2f(b * __builtin_amdgcn_logf(a)) : powf(a, b);
+}
+
 // ------------------------------------------------------------ unary ops --
 // silu.py:10   output = input / (1 + exp(-fp32(input)))
 struct SiluF {
@@ -108,7 +163,10 @@ struct SiluF {
   __device__ __forceinline__ T operator()(T v) const {
     using C = opmath_t<T>;
     const C x = convert<C>(v);
-    return convert<T>(x / (C(1) + ex(-x)));
+    if constexpr (sizeof(T) == 2)
+      return convert<T>(x * fast_sigmoid(x));
+    else
+      return convert<T>(x / (C(1) + ex(-x)));
   }
 };
 // gelu.py:11   input * 0.5 * (1 + erf(input / sqrt(2))); the 1/sqrt(2) factor
@@ -118,7 +176,10 @@ struct GeluF {
   __device__ __forceinline__ T operator()(T v) const {
     using C = opmath_t<T>;
     const C x = convert<C>(v);
-    return convert<T>(x * C(0.5) * (C(1) + er(x * C(M_SQRT1_2))));
+    if constexpr (sizeof(T) == 2)
+      return convert<T>(x * C(0.5) * (C(1) + fast_erf(x * C(M_SQRT1_2))));
+    else
+      return convert<T>(x * C(0.5) * (C(1) + er(x * C(M_SQRT1_2))));
   }
 };
 // gelu.py:14-26  0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 x^3)))
@@ -131,7 +192,10 @@ struct GeluTanhF {
     const C kappa = C(0.044715);
     const C cube = x * x * x;
     const C inner = beta * (x + kappa * cube);
-    return convert<T>(C(0.5) * x * (C(1) + th(inner)));
+    if constexpr (sizeof(T) == 2)
+      return convert<T>(C(0.5) * x * (C(1) + fast_tanh(inner)));
+    else
+      return convert<T>(C(0.5) * x * (C(1) + th(inner)));
   }
 };
 // exp.py:10
@@ -139,7 +203,10 @@ struct ExpF {
   template <typename T>
   __device__ __forceinline__ T operator()(T v) const {
     using C = opmath_t<T>;
-    return convert<T>(ex(convert<C>(v)));
+    if constexpr (sizeof(T) == 2)
+      return convert<T>(fast_exp(convert<C>(v)));
+    else
+      return convert<T>(ex(convert<C>(v)));
   }
 };
 // bitwise_not.py:10 (~x) and :14 (logical not for bool)
@@ -172,7 +239,10 @@ struct SigmoidF {
   template <typename T>
   __device__ __forceinline__ T operator()(T v) const {
     using C = opmath_t<T>;
-    return convert<T>(C(1) / (C(1) + ex(-convert<C>(v))));
+    if constexpr (sizeof(T) == 2)
+      return convert<T>(fast_sigmoid(convert<C>(v)));
+    else
+      return convert<T>(C(1) / (C(1) + ex(-convert<C>(v))));
   }
 };
 // tanh.py:10-13 (the reference spells tanh out through exp, which overflows
@@ -181,7 +251,10 @@ struct TanhF {
   template <typename T>
   __device__ __forceinline__ T operator()(T v) const {
     using C = opmath_t<T>;
-    return convert<T>(th(convert<C>(v)));
+    if constexpr (sizeof(T) == 2)
+      return convert<T>(fast_tanh(convert<C>(v)));
+    else
+      return convert<T>(th(convert<C>(v)));
   }
 };
 // neg.py:9
@@ -223,14 +296,20 @@ struct SinF {
   template <typename T>
   __device__ __forceinline__ T operator()(T v) const {
     using C = opmath_t<T>;
-    return convert<T>(sn(convert<C>(v)));
+    if constexpr (sizeof(T) == 2)
+      return convert<T>(fast_sin(convert<C>(v)));
+    else
+      return convert<T>(sn(convert<C>(v)));
   }
 };
 struct CosF {
   template <typename T>
   __device__ __forceinline__ T operator()(T v) const {
     using C = opmath_t<T>;
-    return convert<T>(cs(convert<C>(v)));
+    if constexpr (sizeof(T) == 2)
+      return convert<T>(fast_cos(convert<C>(v)));
+    else
+      return convert<T>(cs(convert<C>(v)));
   }
 };
 // clamp with scalar (or absent) bounds, already rounded to T.
@@ -446,7 +525,10 @@ struct PowF<T, true> {
   static constexpr bool kF16 = std::is_same<T, _Float16>::value;
   static constexpr bool kBF16 = std::is_same<T, __bf16>::value;
   __device__ __forceinline__ T operator()(T a, T b) const {
-    return convert<T>(pw(convert<C>(a), convert<C>(b)));
+    if constexpr (kF16 || kBF16)
+      return convert<T>(fast_pow(convert<C>(a), convert<C>(b)));
+    else
+      return convert<T>(pw(convert<C>(a), convert<C>(b)));
   }
   __device__ __forceinline__ double scalar_b(double b) const {
     if constexpr (kF16 || kBF16)
@@ -475,7 +557,7 @@ struct PowF<T, true> {
     else if constexpr (std::is_same<T, double>::value)
       return pow(x, e);
     else
-      return convert<T>(pw(x, static_cast<float>(e)));
+      return convert<T>(fast_pow(x, static_cast<float>(e)));
   }
 };
 // Integer powers by squaring with wraparound; negative exponents follow
