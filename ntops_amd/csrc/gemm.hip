@@ -512,69 +512,70 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
 // one DMA per operand (32 KiB each), and the kernel is bound by writing the
 // output, not by the MFMAs.
 //
-// Work is walked in units of `seg` consecutive tiles along one tile row
-// (same batch and 128-row block of A): the unit's A panel is loaded once
-// into one of two A buffers (alternating per unit) and only the B panel is
-// loaded per tile, which halves the operand traffic through the CU's memory
-// queue, where loads otherwise wait behind the output stores.
+// Blocks of 4 waves (2 x 2 wave tiles of 64 x 64) hold one A panel and one
+// B panel (64 KiB of LDS), two blocks per CU, persistent, with no
+// synchronisation between blocks: the output stores of one block drain
+// while the other computes, instead of every store burst being gated by
+// block barriers shared with MFMA work.  A block runs tile after tile: the
+// tile's MFMAs; the epilogue staged through the A panel it has just finished
+// with; then the next tile's DMA, queued ahead of this tile's stores.
 //
-// One 8-wave block per CU runs two groups of four waves (one wave per SIMD
-// in each group) that take alternate tiles in opposite phases: in phase p
-// the group owning tile p runs its MFMAs while the other group issues the
-// DMA of its next tile, rounds and stages its previous tile through a
-// shared 32 KiB area and stores it as full 128-byte lines; one block barrier
-// ends each phase.  Each SIMD thus has one wave feeding the matrix core and
-// one driving LDS and the store path.  LDS: 2 x 32 KiB A + 2 x 32 KiB B
-// (one per group) + 32 KiB staging = 160 KiB.
+// Work is walked in units of `seg` consecutive tiles down one tile column
+// (same batch and 128-column block of B): the unit's B panel is loaded once
+// and only the A panel per tile.  Units are dealt so that each XCD takes a
+// contiguous range, i.e. the blocks working at the same time on one batch
+// hold neighbouring tile columns and write whole output rows together.
+// Measured on MI355X for bmm (32, 2048 x 128)(128 x 2048) this column order
+// writes ~7 % faster than walking tile rows (each output row then written in
+// 256-byte pieces at far-apart times), and the pair of barrier-free blocks
+// ~2 % faster than one 8-wave block whose two 4-wave halves alternate MFMA
+// and epilogue phases between block barriers.  Temporal (L2-allocating)
+// output stores are ~25 % slower than streaming ones here.
 //
-// Requires M % 128 == 0, N % 128 == 0, K % 8 == 0, seg | N / 128 and the
+// Requires M % 128 == 0, N % 128 == 0, K % 8 == 0, seg | M / 128 and the
 // staged (16-byte aligned, unit column stride) output; k >= K reads as zero.
 constexpr int kPanelK = 128;
-constexpr int kPanelTile = 128 * kPanelK * 2;                     // one operand panel
-constexpr int kPanelLds = 4 * kPanelTile + 4 * 64 * 64 * 2;       // 160 KiB
+constexpr int kPanelTile = 128 * kPanelK * 2;  // one operand panel
+constexpr int kPanelLds = 2 * kPanelTile;      // 64 KiB
+constexpr int kPanelBlocksPerCu = 2;
 
 template <typename T, bool AK, bool BKM>
-__global__ __launch_bounds__(512) void k_gemm_panel(GemmArgs g, int seg) {
-  constexpr int BM = 128, BN = 128, NWG = 4;  // waves per group
+__global__ __launch_bounds__(256, 2) void k_gemm_panel(GemmArgs g, int seg) {
+  constexpr int BM = 128, BN = 128, NW = 4;
   constexpr int WTM = 64, WTN = 64, TM = 2, TN = 2, KS = kPanelK / 16;
-  using LA = TileLoader<BM, AK, NWG, false, kPanelK>;
-  using LB = TileLoader<BN, BKM, NWG, false, kPanelK>;
+  using LA = TileLoader<BM, AK, NW, false, kPanelK>;
+  using LB = TileLoader<BN, BKM, NW, false, kPanelK>;
   constexpr int kStores = WTM / 8;  // store instructions per wave per tile
-  // LDS map: A buffers 0/1, B stages 0/1 (group), staging.
-  constexpr int kOffA = 0, kOffB = 2 * kPanelTile, kOffStage = 4 * kPanelTile;
+  constexpr int kOffA = 0, kOffB = kPanelTile;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = wave >> 2, gw = wave & 3;
-  const int wm = gw >> 1, wn = gw & 1;
+  const int wm = wave >> 1, wn = wave & 1;
   const int tm_count = g.M / BM, tn_count = g.N / BN;
-  const int ups = tn_count / seg;                    // units per tile row
-  const int units = g.batch * tm_count * ups;
+  const int upc = tm_count / seg;  // units per tile column
+  const int units = g.batch * tn_count * upc;
   const int G = gridDim.x;
   const int u0 = blockIdx.x;
   if (u0 >= units) return;
-  const int n = ((units - 1 - u0) / G + 1) * seg;   // tiles of this block
+  const int n = ((units - 1 - u0) / G + 1) * seg;  // tiles of this block
 
   const uint16_t* A0 = static_cast<const uint16_t*>(g.A);
   const uint16_t* B0 = static_cast<const uint16_t*>(g.B);
-  // Every panel has the same leading dimension and extent: set the per-lane
-  // offsets once, move only the scalar base address per panel.
   LA la;
   LB lb;
   if constexpr (AK)
-    la.init(A0, g.sa_m, (static_cast<int64_t>(BM - 1) * g.sa_m + g.K) * 2, gw, lane);
+    la.init(A0, g.sa_m, (static_cast<int64_t>(BM - 1) * g.sa_m + g.K) * 2, wave, lane);
   else
-    la.init(A0, g.sa_k, (static_cast<int64_t>(g.K - 1) * g.sa_k + BM) * 2, gw, lane);
+    la.init(A0, g.sa_k, (static_cast<int64_t>(g.K - 1) * g.sa_k + BM) * 2, wave, lane);
   if constexpr (BKM)
-    lb.init(B0, g.sb_n, (static_cast<int64_t>(BN - 1) * g.sb_n + g.K) * 2, gw, lane);
+    lb.init(B0, g.sb_n, (static_cast<int64_t>(BN - 1) * g.sb_n + g.K) * 2, wave, lane);
   else
-    lb.init(B0, g.sb_k, (static_cast<int64_t>(g.K - 1) * g.sb_k + BN) * 2, gw, lane);
+    lb.init(B0, g.sb_k, (static_cast<int64_t>(g.K - 1) * g.sb_k + BN) * 2, wave, lane);
 
   struct Coord {
     int bat, m0, n0;
-    int abuf;    // A buffer of the tile's unit
-    bool first;  // first tile of its unit: loads the unit's A panel
+    bool first;  // first tile of its unit: loads the unit's B panel
   };
   // Tile i of this block: unit k = i / seg (global unit u0 + k * G, remapped
   // so each XCD walks a contiguous range of units), tile j = i % seg of it.
@@ -583,91 +584,73 @@ __global__ __launch_bounds__(512) void k_gemm_panel(GemmArgs g, int seg) {
     const int k = i / seg, j = i - k * seg;
     int u = u0 + k * G;
     if ((units & 7) == 0 && (G & 7) == 0) u = (u & 7) * (units >> 3) + (u >> 3);
-    const int row = u / ups, s = u - row * ups;
-    c.bat = row / tm_count;
-    c.m0 = (row - c.bat * tm_count) * BM;
-    c.n0 = (s * seg + j) * BN;
-    c.abuf = k & 1;
+    const int col = u / upc, s = u - col * upc;
+    c.bat = col / tn_count;
+    c.n0 = (col - c.bat * tn_count) * BN;
+    c.m0 = (s * seg + j) * BM;
     c.first = j == 0;
     return c;
   };
-  // Issues tile c's B panel into `stage` (and its unit's A panel first).
-  auto issue = [&](const Coord& c, int stage) {
+  auto issue = [&](const Coord& c) {
+    la.rebase(A0 + c.bat * g.sa_b + (AK ? static_cast<int64_t>(c.m0) * g.sa_m : c.m0));
+    la.issue(smem + kOffA, 0, BM, g.K);
     if (c.first) {
-      la.rebase(A0 + c.bat * g.sa_b + (AK ? static_cast<int64_t>(c.m0) * g.sa_m : c.m0));
-      la.issue(smem + kOffA + c.abuf * kPanelTile, 0, BM, g.K);
+      lb.rebase(B0 + c.bat * g.sb_b + (BKM ? static_cast<int64_t>(c.n0) * g.sb_n : c.n0));
+      lb.issue(smem + kOffB, 0, BN, g.K);
     }
-    lb.rebase(B0 + c.bat * g.sb_b + (BKM ? static_cast<int64_t>(c.n0) * g.sb_n : c.n0));
-    lb.issue(smem + kOffB + stage * kPanelTile, 0, BN, g.K);
   };
 
-  // Prologue: group 0's first tile lands before phase 0.
-  if (grp == 0) {
-    issue(coord(0), 0);
-    wait_vmcnt<0>();
-  }
-  block_barrier();
-
+  issue(coord(0));
   f32x16 acc[TM][TN];
-  Coord done_c = {0, 0, 0, 0, false};  // this group's tile whose MFMAs are done
-  for (int p = 0; p <= n; ++p) {
-    if ((p & 1) == grp) {
-      // MFMA phase of tile p (this group's; B in stage grp).
-      if (p < n) {
-        done_c = coord(p);
-        const char* sa = smem + kOffA + done_c.abuf * kPanelTile;
-        const char* sb = smem + kOffB + grp * kPanelTile;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          u32x4 af[TM], bf[TN];
-#pragma unroll
-          for (int i = 0; i < TM; ++i) af[i] = load_frag<BM, AK, kPanelK>(sa, wm * WTM + i * 32, ks, lane);
-#pragma unroll
-          for (int j = 0; j < TN; ++j) bf[j] = load_frag<BN, BKM, kPanelK>(sb, wn * WTN + j * 32, ks, lane);
-#pragma unroll
-          for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[j], af[i], acc[i][j]);
-        }
-        // Buffers are refilled only after the barrier ending this phase.
-        wait_lgkmcnt0();
-      }
-    } else {
-      // Epilogue phase of tile p - 1 (this group's previous tile), after
-      // issuing the DMA of this group's next tile p + 1 so those loads are
-      // queued ahead of the stores.  B stage grp was last read by tile
-      // p - 1 (previous phase); an A buffer is refilled two units after its
-      // last use.
-      const bool load_next = p + 1 < n;
-      if (load_next) issue(coord(p + 1), grp);
-      if (p >= 1) {
-        T* D = static_cast<T*>(g.D) + done_c.bat * g.sd_b;
-        char* ep = smem + kOffStage + gw * (WTM * WTN * 2);
-        const int mw = done_c.m0 + wm * WTM, nw = done_c.n0 + wn * WTN;
-        if (g.use_c)
-          store_tile_staged<T, true, TM, TN, WTM, WTN, true, kStreamOutPanel>(
-              g, acc, ep, D, static_cast<const T*>(g.C) + done_c.bat * g.sc_b, mw, nw, lane);
-        else
-          store_tile_staged<T, false, TM, TN, WTM, WTN, true, kStreamOutPanel>(g, acc, ep, D, nullptr,
-                                                                              mw, nw, lane);
-      }
-      // The next tile's operands have landed (only the stores just issued
-      // may still be in flight) before the barrier that opens its MFMA phase.
-      if (load_next) {
-        if (p >= 1)
-          wait_vmcnt<kStores>();
-        else
-          wait_vmcnt<0>();
-      }
-    }
+  for (int t = 0; t < n; ++t) {
+    const Coord c = coord(t);
+    // Tile t's operands have landed (only tile t - 1's stores may still be
+    // in flight), in every wave's share.
+    if (t == 0)
+      wait_vmcnt<0>();
+    else
+      wait_vmcnt<kStores>();
     block_barrier();
+    const char* sa = smem + kOffA;
+    const char* sb = smem + kOffB;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = load_frag<BM, AK, kPanelK>(sa, wm * WTM + i * 32, ks, lane);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = load_frag<BN, BKM, kPanelK>(sb, wn * WTN + j * 32, ks, lane);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[j], af[i], acc[i][j]);
+    }
+    wait_lgkmcnt0();
+    // Every wave is done reading the A panel: it becomes the staging area.
+    block_barrier();
+    T* D = static_cast<T*>(g.D) + c.bat * g.sd_b;
+    char* ep = smem + kOffA + wave * (WTM * WTN * 2);
+    const int mw = c.m0 + wm * WTM, nw = c.n0 + wn * WTN;
+    u32x4 rows[WTM / 8];
+    if (g.use_c)
+      stage_tile<T, true, TM, TN, WTM, WTN, true>(g, acc, ep, static_cast<const T*>(g.C) + c.bat * g.sc_b,
+                                                   mw, nw, lane, rows);
+    else
+      stage_tile<T, false, TM, TN, WTM, WTN, true>(g, acc, ep, nullptr, mw, nw, lane, rows);
+    wait_lgkmcnt0();
+    // Every wave holds its rows: the panels may be refilled.  The next
+    // tile's DMA is queued ahead of this tile's stores.
+    block_barrier();
+    if (t + 1 < n) issue(coord(t + 1));
+    store_rows<T, WTM, true, kStreamOutPanel>(g, rows, D, mw, nw, lane);
   }
+  wait_vmcnt<0>();
 }
 
 // ---- generic kernel (any dtype among F32/F16/BF16, any strides) -------------
@@ -770,25 +753,25 @@ int launch_panel(const GemmArgs& g, hipStream_t st) {
       return set_error(NTOPS_ERR_HIP, "gemm: cannot reserve %d bytes of LDS", kLds);
     attr_set = true;
   }
-  // Units of `seg` tiles along a tile row: the longest divisor of the row's
-  // tile count that still leaves a unit for every CU.
+  // Units of `seg` tiles down a tile column: the longest divisor of the
+  // column's tile count that still leaves a unit for every block.
   const int cus = cu_count() > 0 ? cu_count() : 256;
-  const int tn = g.N / 128;
-  const int64_t rows = static_cast<int64_t>(g.M / 128) * g.batch;
+  const int tm = g.M / 128;
+  const int64_t cols = static_cast<int64_t>(g.N / 128) * g.batch;
   int seg = 1;
-  for (int d = tn; d >= 1; --d) {
-    if (tn % d == 0 && rows * (tn / d) >= cus) {
+  for (int d = tm; d >= 1; --d) {
+    if (tm % d == 0 && cols * (tm / d) >= cus * kPanelBlocksPerCu) {
       seg = d;
       break;
     }
   }
-  const int64_t units = rows * (tn / seg);
-  // One 8-wave block per CU (it takes all of the CU's LDS); a multiple of 8
-  // keeps each block on one XCD for the whole walk.
-  int64_t grid = (cus / 8) * 8;
+  const int64_t units = cols * (tm / seg);
+  // Two blocks per CU; a multiple of 8 keeps each block on one XCD for the
+  // whole walk.
+  int64_t grid = (cus * kPanelBlocksPerCu / 8) * 8;
   if (grid <= 0) grid = 256;
   if (grid > units) grid = units;
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(512), kLds, st, g, seg);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(256), kLds, st, g, seg);
   return check_launch("gemm");
 }
 

@@ -111,7 +111,8 @@ def test_addmm_bias_and_beta_zero(dtype):
 # Short-K shapes (K <= 128, M and N multiples of 128): the persistent panel
 # kernel.  Tile counts below, at and above one block per CU, divisible by 8
 # or not (XCD remap on / off), K below the 128-wide panel (zero-filled tail),
-# all four operand layouts, and an addmm bias read in its epilogue.
+# all four operand layouts, units of several tiles (one operand panel reused
+# across them), and an addmm bias read in its epilogue.
 SHORT_K = [
     (1, 128, 128, 8),
     (3, 384, 256, 64),
@@ -119,6 +120,7 @@ SHORT_K = [
     (11, 640, 640, 128),
     (5, 1024, 896, 96),
     (2, 2048, 2048, 128),
+    (4, 2048, 2048, 64),
 ]
 
 

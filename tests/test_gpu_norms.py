@@ -91,6 +91,31 @@ def test_norm_widths(cols, dtype):
     assert_close(got, from_np(O.layer_norm(to_np(x), dt, cols, to_np(w), to_np(b), 1e-5), dt), rtol, atol, f"ln {cols}")
 
 
+@pytest.mark.parametrize("cols", [64, 1000, 4096, 8192, 16384])
+@pytest.mark.parametrize("dtype", FLOATS)
+def test_layer_norm_offset_rows(cols, dtype):
+    """Rows offset by 30 standard deviations, a row whose first element is
+    an outlier (3000 standard deviations for fp32, 300 for 16-bit types) and
+    a constant row: the variance must not lose precision to cancellation
+    (the fp32 tolerance is 1e-5; larger offsets amplify the rounding of the
+    mean through torch's output formula x * rstd - rstd * mean beyond it,
+    for torch's CPU kernel as much as for any other summation order)."""
+    g = torch.Generator().manual_seed(cols)
+    x = torch.randn(5, cols, generator=g)
+    x[1] += 30.0
+    x[2] -= 30.0
+    x[3, 0] = 3000.0 if dtype == torch.float32 else 300.0
+    x[4] = 7.0
+    x = x.to(dtype)
+    w = (1 + 0.02 * torch.randn(cols, generator=g)).to(dtype)
+    b = (0.02 * torch.randn(cols, generator=g)).to(dtype)
+    dt = DT_NAME[dtype]
+    rtol, atol = TOL_REDUCTION[dt]
+    got = ntops_amd.torch.layer_norm(x.cuda(), (cols,), w.cuda(), b.cuda(), 1e-5)
+    exp = from_np(O.layer_norm(to_np(x), dt, cols, to_np(w), to_np(b), 1e-5), dt)
+    assert_close(got, exp, rtol, atol, f"ln offset rows {cols}")
+
+
 def test_norm_noncontiguous_input_and_fp32_weight():
     x = torch.randn(64, 96).bfloat16()
     xg = x.cuda().t()  # (96, 64) non-contiguous
