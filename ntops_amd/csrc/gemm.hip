@@ -37,6 +37,10 @@
 //    M-grouped range of tiles that share A and B panels in its L2;
 //  * edges: buffer loads with a per-tile resource; out-of-range chunks get an
 //    offset past the resource's extent and read as zero.
+// Skinny path (M <= 64, K-major A): 16-column blocks whose waves split K,
+// operands straight to registers in the v_mfma_f32_16x16x32 layout.
+// Short-K path (K <= 128, M and N multiples of 128): a persistent kernel
+// built around the output stream.
 // Generic path (fp32, or any other strides): 64x64 LDS-tiled FMA kernel with
 // fp32 accumulation (IEEE; gfx950 has no reduced-precision fp32 MFMA input).
 #include "gemm.h"
@@ -653,6 +657,152 @@ __global__ __launch_bounds__(256, 2) void k_gemm_panel(GemmArgs g, int seg) {
   wait_vmcnt<0>();
 }
 
+// ---- skinny kernel (M <= 64) -------------------------------------------------
+// Decode-shaped products (a few rows of A against a large B) are bound by
+// streaming B once.  A block owns 16 output columns of one batch and all of
+// M (MB blocks of 16 rows); its 4 waves split K in 32-wide steps (wave w
+// takes steps w, w + 4, ...), so each column's B is read front to back by
+// the block, and merge their fp32 partial sums through LDS at the end.
+// Operands go straight from global memory to registers in the layout of
+// v_mfma_f32_16x16x32 (lane l: row / column l & 15, k = 8 (l >> 4) .. + 7):
+// A and K-major B with one 16-byte buffer load per lane; M/N-major B
+// loaded as 16-byte row pieces and transposed through a 1 KiB per-wave LDS
+// area with ds_read_b64_tr_b16.  U steps are loaded before their MFMAs so
+// each wave keeps U * (MB + 1) 16-byte loads in flight (refilling each step's
+// registers as soon as they are consumed measured no faster).  Blocks are
+// mapped so that consecutive n-slices share an XCD: for an M/N-major B each
+// block reads 32 bytes of every k-row, and its neighbours' pieces of the same
+// 128-byte lines then come from the same L2 (16 x 14336 x 4096 NN: 75 -> 40
+// us).  Out-of-range rows, columns and k read as zero (buffer offsets past
+// the extent).
+// Requires A K-major, K % 8 == 0; M/N-major B also N % 8 == 0.
+constexpr int kSkinnyMaxM = 64;
+
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (std::is_same<T, __bf16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+template <typename T, bool BKM, int MB>
+__global__ __launch_bounds__(256) void k_gemm_skinny(GemmArgs g) {
+  constexpr int NW = 4, U = MB <= 2 ? 8 : 4;
+  __shared__ float red[NW][MB][4][64];
+  __shared__ __attribute__((aligned(16))) uint16_t trs[NW][32 * 16];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Consecutive n-slices on one XCD (workgroups are dealt round-robin over
+  // the 8 XCDs), so neighbouring pieces of an M/N-major B row share an L2.
+  int bx = blockIdx.x;
+  if ((gridDim.x & 7) == 0) bx = (bx & 7) * (gridDim.x >> 3) + (bx >> 3);
+  const int n0 = bx * 16;
+  const int bat = blockIdx.y;
+  const int nv = min(16, g.N - n0);
+  const int r16 = lane & 15, kq = (lane >> 4) * 8;
+
+  const uint16_t* A = static_cast<const uint16_t*>(g.A) + bat * g.sa_b;
+  const uint16_t* B = static_cast<const uint16_t*>(g.B) + bat * g.sb_b;
+  const __amdgpu_buffer_rsrc_t ra =
+      buffer_rsrc(A, static_cast<uint32_t>((static_cast<int64_t>(g.M - 1) * g.sa_m + g.K) * 2));
+  const __amdgpu_buffer_rsrc_t rb =
+      BKM ? buffer_rsrc(B + static_cast<int64_t>(n0) * g.sb_n,
+                        static_cast<uint32_t>((static_cast<int64_t>(nv - 1) * g.sb_n + g.K) * 2))
+          : buffer_rsrc(B + n0, static_cast<uint32_t>((static_cast<int64_t>(g.K - 1) * g.sb_k + nv) * 2));
+  // Per-lane byte offsets at k0 = 0.
+  uint32_t a_off[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) a_off[mb] = static_cast<uint32_t>(((mb * 16 + r16) * g.sa_m + kq) * 2);
+  const bool b_row_ok = BKM ? r16 < nv : 8 * (lane & 1) < nv;
+  const uint32_t b_off = BKM ? static_cast<uint32_t>((r16 * g.sb_n + kq) * 2)
+                             : static_cast<uint32_t>(((lane >> 1) * g.sb_k + 8 * (lane & 1)) * 2);
+  const uint32_t b_kstep = BKM ? 2u : static_cast<uint32_t>(g.sb_k * 2);  // bytes per k
+
+  f32x4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int s0 = wave; s0 * 32 < g.K; s0 += NW * U) {
+    u32x4 bq[U], aq[U][MB];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k0 = (s0 + NW * u) * 32;
+      const bool b_ok = b_row_ok && (BKM ? k0 + kq < g.K : k0 + (lane >> 1) < g.K);
+      bq[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rb, b_ok ? b_off + static_cast<uint32_t>(k0) * b_kstep : kOOB, 0, 0));
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const bool a_ok = mb * 16 + r16 < g.M && k0 + kq < g.K;
+        aq[u][mb] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, a_ok ? a_off[mb] + k0 * 2u : kOOB, 0, 0));
+      }
+    }
+    // All U steps' loads are issued before the first MFMA needs one.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      u32x4 bf = bq[u];
+      if constexpr (!BKM) {
+        // Lane l holds k-row l >> 1, columns 8 (l & 1) .. + 7: store the
+        // 32 x 16 tile row-major, read it back transposed.
+        *reinterpret_cast<u32x4*>(&trs[wave][lane * 8]) = bf;
+        s16x4 v[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int k = kq + 4 * h + (r16 >> 2);
+          v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(&trs[wave][k * 16 + 4 * (r16 & 3)]));
+        }
+        bf.x = static_cast<uint16_t>(v[0][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][1])) << 16);
+        bf.y = static_cast<uint16_t>(v[0][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][3])) << 16);
+        bf.z = static_cast<uint16_t>(v[1][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][1])) << 16);
+        bf.w = static_cast<uint16_t>(v[1][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][3])) << 16);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16<T>(aq[u][mb], bf, acc[mb]);
+    }
+  }
+  // Lane l holds rows 4 (l >> 4) + r of each 16-row block, column l & 15.
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][mb][r][lane] = acc[mb][r];
+  __syncthreads();
+  T* D = static_cast<T*>(g.D) + bat * g.sd_b;
+  const T* Cp = g.use_c ? static_cast<const T*>(g.C) + bat * g.sc_b : nullptr;
+  for (int mb = wave; mb < MB; mb += NW) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = mb * 16 + (lane >> 4) * 4 + r, n = n0 + r16;
+      if (m < g.M && n < g.N) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[w][mb][r][lane];
+        v *= g.alpha;
+        if (Cp != nullptr) v += g.beta * static_cast<float>(Cp[m * g.sc_m + n * g.sc_n]);
+        D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = static_cast<T>(v);
+      }
+    }
+  }
+}
+
+template <typename T, bool BKM>
+int launch_skinny(const GemmArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((g.N + 15) / 16), static_cast<unsigned>(g.batch));
+  const int mb = (g.M + 15) / 16;
+  if (mb == 1)
+    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 1>), grid, dim3(256), 0, st, g);
+  else if (mb == 2)
+    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 2>), grid, dim3(256), 0, st, g);
+  else if (mb == 3)
+    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 3>), grid, dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 4>), grid, dim3(256), 0, st, g);
+  return check_launch("gemm");
+}
+
 // ---- generic kernel (any dtype among F32/F16/BF16, any strides) -------------
 template <typename T>
 __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
@@ -819,6 +969,8 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     // K == 0 goes to the generic kernel, which never touches A or B (they may
     // be null, and an empty M/N-major operand has no valid buffer extent).
     if (g.K > 0 && (a_k || a_m) && (b_k || b_n) && d_ok && batch_ok && fits && al(g.A) && al(g.B)) {
+      if (a_k && g.M <= kSkinnyMaxM && g.batch <= 65535)
+        return b_k ? launch_skinny<T, true>(g, st) : launch_skinny<T, false>(g, st);
       if (a_k && b_n) return pick_tile<T, true, false>(g, st);
       if (a_k && b_k) return pick_tile<T, true, true>(g, st);
       if (a_m && b_n) return pick_tile<T, false, false>(g, st);

@@ -58,6 +58,47 @@ def test_mm_layouts(m, n, k, dtype, layout):
     assert_close(got, from_np(O.gemm(to_np(a), to_np(b), dt), dt), 1.6e-2, 1.6e-2, f"mm {layout}")
 
 
+# Small M (decode shapes): the skinny kernel for a K-major A with either B
+# layout -- M across 16-row blocks (1..4), ragged N (multiples of 8 for an
+# N-major B) and K (not a multiple of the 32-wide step, shorter than one
+# step per wave, longer than one load group), a bias, and small-M bmm.
+SKINNY = [
+    (1, 4096, 4096),
+    (5, 1000, 40),
+    (16, 24, 8),
+    (17, 520, 1000),
+    (33, 2048, 3000),
+    (64, 136, 4104),
+]
+
+
+@pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+@pytest.mark.parametrize("m, n, k", SKINNY)
+def test_mm_small_m(m, n, k, dtype, layout):
+    a = (0.1 * torch.randn(m, k)).to(dtype)
+    b = (0.1 * torch.randn(k, n)).to(dtype)
+    ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
+    bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
+    got = ntops_amd.torch.mm(ag, bg)
+    dt = DT_NAME[dtype]
+    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), dt), dt), 1.6e-2, 1.6e-2 * max(1.0, (k / 100) ** 0.5),
+                 f"mm small m {layout}")
+
+
+def test_addmm_and_bmm_small_m():
+    bias = torch.randn(1000).bfloat16()
+    x = (0.1 * torch.randn(7, 512)).bfloat16()
+    w = (0.1 * torch.randn(1000, 512)).bfloat16()  # F.linear-style weight: B = w.t() is K-major
+    got = ntops_amd.torch.addmm(bias.cuda(), x.cuda(), w.cuda().t(), beta=0.5, alpha=2.0)
+    exp = from_np(O.gemm(to_np(x), to_np(w.t().contiguous()), "bf16", to_np(bias), 2.0, 0.5), "bf16")
+    assert_close(got, exp, 1.6e-2, 1.6e-2, "addmm small m")
+    q = (0.1 * torch.randn(12, 1, 128)).bfloat16()
+    kt = (0.1 * torch.randn(12, 128, 777 + 7)).bfloat16()
+    got = ntops_amd.torch.bmm(q.cuda(), kt.cuda())
+    assert_close(got, from_np(O.gemm(to_np(q), to_np(kt), "bf16"), "bf16"), 1.6e-2, 1.6e-2, "bmm small m")
+
+
 def test_mm_small_integers_exact():
     """Small-integer bf16 operands: fp32 accumulation is exact and the result
     is representable, so the kernel must match integer matmul exactly."""
