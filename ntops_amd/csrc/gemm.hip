@@ -659,10 +659,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_panel(GemmArgs g, int seg) {
 
 // ---- skinny kernel (M <= 64) -------------------------------------------------
 // Decode-shaped products (a few rows of A against a large B) are bound by
-// streaming B once.  A block owns 16 output columns of one batch and all of
-// M (MB blocks of 16 rows); its 4 waves split K in 32-wide steps (wave w
-// takes steps w, w + 4, ...), so each column's B is read front to back by
+// streaming B once.  A block owns 16 J output columns of one batch and all
+// of M (MB blocks of 16 rows); its NW waves split K in 32-wide steps (wave w
+// takes steps w, w + NW, ...), so each column's B is read front to back by
 // the block, and merge their fp32 partial sums through LDS at the end.
+// Each A fragment serves J B fragments.
 // Operands go straight from global memory to registers in the layout of
 // v_mfma_f32_16x16x32 (lane l: row / column l & 15, k = 8 (l >> 4) .. + 7):
 // A and K-major B with one 16-byte buffer load per lane; M/N-major B
@@ -677,6 +678,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_panel(GemmArgs g, int seg) {
 // the extent).
 // Requires A K-major, K % 8 == 0; M/N-major B also N % 8 == 0.
 constexpr int kSkinnyMaxM = 64;
+// Widest column slice (in 16-column groups) for MB 16-row blocks of A: the
+// partial-sum exchange (4 * J * MB KiB of LDS) stays within 32 KiB.
+constexpr int kSkinnyMaxJ(int mb) { return mb == 2 ? 4 : 2; }
 
 template <typename T>
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
@@ -688,20 +692,20 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-template <typename T, bool BKM, int MB>
-__global__ __launch_bounds__(256) void k_gemm_skinny(GemmArgs g) {
-  constexpr int NW = 4, U = MB <= 2 ? 8 : 4;
-  __shared__ float red[NW][MB][4][64];
-  __shared__ __attribute__((aligned(16))) uint16_t trs[NW][32 * 16];
+template <typename T, bool BKM, int MB, int J, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmArgs g) {
+  constexpr int U = MB + J <= 3 ? 8 : 4, NB = 16 * J;
+  __shared__ float red[NW][J][MB][4][64];
+  __shared__ __attribute__((aligned(16))) uint16_t trs[BKM ? 1 : NW][32 * NB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // Consecutive n-slices on one XCD (workgroups are dealt round-robin over
   // the 8 XCDs), so neighbouring pieces of an M/N-major B row share an L2.
   int bx = blockIdx.x;
   if ((gridDim.x & 7) == 0) bx = (bx & 7) * (gridDim.x >> 3) + (bx >> 3);
-  const int n0 = bx * 16;
+  const int n0 = bx * NB;
   const int bat = blockIdx.y;
-  const int nv = min(16, g.N - n0);
+  const int nv = min(NB, g.N - n0);
   const int r16 = lane & 15, kq = (lane >> 4) * 8;
 
   const uint16_t* A = static_cast<const uint16_t*>(g.A) + bat * g.sa_b;
@@ -712,27 +716,47 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(GemmArgs g) {
       BKM ? buffer_rsrc(B + static_cast<int64_t>(n0) * g.sb_n,
                         static_cast<uint32_t>((static_cast<int64_t>(nv - 1) * g.sb_n + g.K) * 2))
           : buffer_rsrc(B + n0, static_cast<uint32_t>((static_cast<int64_t>(g.K - 1) * g.sb_k + nv) * 2));
-  // Per-lane byte offsets at k0 = 0.
+  // Per-lane byte offsets at k0 = 0.  K-major B: load j covers columns
+  // 16 j + (l & 15).  M/N-major B: load j covers k-rows j * 32 / J +
+  // l / (2 J), 16-byte chunk l % (2 J) of the slice's row piece.
   uint32_t a_off[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) a_off[mb] = static_cast<uint32_t>(((mb * 16 + r16) * g.sa_m + kq) * 2);
-  const bool b_row_ok = BKM ? r16 < nv : 8 * (lane & 1) < nv;
-  const uint32_t b_off = BKM ? static_cast<uint32_t>((r16 * g.sb_n + kq) * 2)
-                             : static_cast<uint32_t>(((lane >> 1) * g.sb_k + 8 * (lane & 1)) * 2);
+  uint32_t b_off[J];
+  bool b_col_ok[J];
+  int b_krow[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if constexpr (BKM) {
+      b_off[j] = static_cast<uint32_t>(((16 * j + r16) * g.sb_n + kq) * 2);
+      b_col_ok[j] = 16 * j + r16 < nv;
+      b_krow[j] = kq;
+    } else {
+      b_krow[j] = j * (32 / J) + lane / (2 * J);
+      b_off[j] = static_cast<uint32_t>((b_krow[j] * g.sb_k + 8 * (lane % (2 * J))) * 2);
+      b_col_ok[j] = 8 * (lane % (2 * J)) < nv;
+    }
+  }
   const uint32_t b_kstep = BKM ? 2u : static_cast<uint32_t>(g.sb_k * 2);  // bytes per k
 
-  f32x4 acc[MB];
+  f32x4 acc[J][MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[j][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int s0 = wave; s0 * 32 < g.K; s0 += NW * U) {
-    u32x4 bq[U], aq[U][MB];
+    u32x4 bq[U][J], aq[U][MB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k0 = (s0 + NW * u) * 32;
-      const bool b_ok = b_row_ok && (BKM ? k0 + kq < g.K : k0 + (lane >> 1) < g.K);
-      bq[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rb, b_ok ? b_off + static_cast<uint32_t>(k0) * b_kstep : kOOB, 0, 0));
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const bool b_ok = b_col_ok[j] && k0 + b_krow[j] < g.K;
+        bq[u][j] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rb, b_ok ? b_off[j] + static_cast<uint32_t>(k0) * b_kstep : kOOB, 0, 0));
+      }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const bool a_ok = mb * 16 + r16 < g.M && k0 + kq < g.K;
@@ -744,42 +768,56 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      u32x4 bf = bq[u];
-      if constexpr (!BKM) {
-        // Lane l holds k-row l >> 1, columns 8 (l & 1) .. + 7: store the
-        // 32 x 16 tile row-major, read it back transposed.
-        *reinterpret_cast<u32x4*>(&trs[wave][lane * 8]) = bf;
-        s16x4 v[2];
+      u32x4 bf[J];
+      if constexpr (BKM) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int k = kq + 4 * h + (r16 >> 2);
-          v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(&trs[wave][k * 16 + 4 * (r16 & 3)]));
+        for (int j = 0; j < J; ++j) bf[j] = bq[u][j];
+      } else {
+        // Store the 32 x NB step tile row-major (load j's 64 lanes write
+        // bytes j KiB + 16 l), read each 16-column group back transposed.
+#pragma unroll
+        for (int j = 0; j < J; ++j) *reinterpret_cast<u32x4*>(&trs[wave][j * 512 + lane * 8]) = bq[u][j];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          s16x4 v[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int k = kq + 4 * h + (r16 >> 2);
+            v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4_t*)(&trs[wave][k * NB + 16 * j + 4 * (r16 & 3)]));
+          }
+          bf[j].x = static_cast<uint16_t>(v[0][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][1])) << 16);
+          bf[j].y = static_cast<uint16_t>(v[0][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][3])) << 16);
+          bf[j].z = static_cast<uint16_t>(v[1][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][1])) << 16);
+          bf[j].w = static_cast<uint16_t>(v[1][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][3])) << 16);
         }
-        bf.x = static_cast<uint16_t>(v[0][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][1])) << 16);
-        bf.y = static_cast<uint16_t>(v[0][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[0][3])) << 16);
-        bf.z = static_cast<uint16_t>(v[1][0]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][1])) << 16);
-        bf.w = static_cast<uint16_t>(v[1][2]) | (static_cast<uint32_t>(static_cast<uint16_t>(v[1][3])) << 16);
       }
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16<T>(aq[u][mb], bf, acc[mb]);
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[j][mb] = mfma16<T>(aq[u][mb], bf[j], acc[j][mb]);
     }
   }
-  // Lane l holds rows 4 (l >> 4) + r of each 16-row block, column l & 15.
+  // Lane l holds rows 4 (l >> 4) + r of each 16-row block, column
+  // 16 j + (l & 15) of the slice.
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int j = 0; j < J; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][mb][r][lane] = acc[mb][r];
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][j][mb][r][lane] = acc[j][mb][r];
   __syncthreads();
   T* D = static_cast<T*>(g.D) + bat * g.sd_b;
   const T* Cp = g.use_c ? static_cast<const T*>(g.C) + bat * g.sc_b : nullptr;
-  for (int mb = wave; mb < MB; mb += NW) {
+  for (int q = wave; q < J * MB; q += NW) {
+    const int j = q / MB, mb = q - j * MB;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = mb * 16 + (lane >> 4) * 4 + r, n = n0 + r16;
+      const int m = mb * 16 + (lane >> 4) * 4 + r, n = n0 + 16 * j + r16;
       if (m < g.M && n < g.N) {
         float v = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) v += red[w][mb][r][lane];
+        for (int w = 0; w < NW; ++w) v += red[w][j][mb][r][lane];
         v *= g.alpha;
         if (Cp != nullptr) v += g.beta * static_cast<float>(Cp[m * g.sc_m + n * g.sc_n]);
         D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = static_cast<T>(v);
@@ -788,19 +826,39 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(GemmArgs g) {
   }
 }
 
+template <typename T, bool BKM, int MB>
+int launch_skinny_mb(const GemmArgs& g, hipStream_t st, int j) {
+  const unsigned by = static_cast<unsigned>(g.batch);
+  if constexpr (kSkinnyMaxJ(MB) >= 4)
+    if (j == 4) {
+      hipLaunchKernelGGL((k_gemm_skinny<T, BKM, MB, 4, 4>), dim3((g.N + 63) / 64, by), dim3(256), 0, st, g);
+      return check_launch("gemm");
+    }
+  if (j == 2)
+    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, MB, 2, 4>), dim3((g.N + 31) / 32, by), dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, MB, 1, 4>), dim3((g.N + 15) / 16, by), dim3(256), 0, st, g);
+  return check_launch("gemm");
+}
+
+// Column-slice width 16 j: the widest that still gives every CU a block.
+// (16-wave blocks splitting K finer for the few-block shapes, e.g.
+// 16 x 4096 x 14336, measured no faster than 4-wave ones.)
 template <typename T, bool BKM>
 int launch_skinny(const GemmArgs& g, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((g.N + 15) / 16), static_cast<unsigned>(g.batch));
   const int mb = (g.M + 15) / 16;
-  if (mb == 1)
-    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 1>), grid, dim3(256), 0, st, g);
-  else if (mb == 2)
-    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 2>), grid, dim3(256), 0, st, g);
-  else if (mb == 3)
-    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 3>), grid, dim3(256), 0, st, g);
-  else
-    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 4>), grid, dim3(256), 0, st, g);
-  return check_launch("gemm");
+  const int cus = cu_count_cached() > 0 ? cu_count_cached() : 256;
+  int j = 1;
+  for (int c : {4, 2}) {
+    if (c <= kSkinnyMaxJ(mb) && static_cast<int64_t>((g.N + 16 * c - 1) / (16 * c)) * g.batch >= cus) {
+      j = c;
+      break;
+    }
+  }
+  if (mb == 1) return launch_skinny_mb<T, BKM, 1>(g, st, j);
+  if (mb == 2) return launch_skinny_mb<T, BKM, 2>(g, st, j);
+  if (mb == 3) return launch_skinny_mb<T, BKM, 3>(g, st, j);
+  return launch_skinny_mb<T, BKM, 4>(g, st, j);
 }
 
 // ---- generic kernel (any dtype among F32/F16/BF16, any strides) -------------

@@ -59,16 +59,21 @@ def test_mm_layouts(m, n, k, dtype, layout):
 
 
 # Small M (decode shapes): the skinny kernel for a K-major A with either B
-# layout -- M across 16-row blocks (1..4), ragged N (multiples of 8 for an
-# N-major B) and K (not a multiple of the 32-wide step, shorter than one
-# step per wave, longer than one load group), a bias, and small-M bmm.
+# layout -- M across 16-row blocks (1..4), 16-, 32- and 64-column slices
+# (wide N), ragged N (multiples of 8 for an N-major B; any N for a K-major
+# one) and K (not a multiple of the 32-wide step, shorter than one step per
+# wave, longer than one load group), a bias, and small-M bmm.
 SKINNY = [
     (1, 4096, 4096),
     (5, 1000, 40),
+    (5, 1001, 40),
     (16, 24, 8),
     (17, 520, 1000),
     (33, 2048, 3000),
     (64, 136, 4104),
+    (8, 8200, 100),
+    (24, 16448, 520),
+    (40, 8208, 72),
 ]
 
 
