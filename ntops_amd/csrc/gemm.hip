@@ -483,13 +483,16 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
     wait_lgkmcnt0();
     if (k + 1 < ktiles) wait_tile(min(STAGES - 2, ktiles - 2 - k), kLoadsPerTile);
     block_barrier();
-    // MFMA phase.
+    // MFMA phase, at raised wave priority so the SIMD's arbiter issues the
+    // matrix wave ahead of its memory-phase partner (+0.8 % on mm).
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[ks][j], af[ks][i], acc[i][j]);
+    __builtin_amdgcn_s_setprio(0);
     block_barrier();
   }
   if (grp == 0) block_barrier();
