@@ -694,9 +694,13 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
+  // The matrix phase runs at raised wave priority, so the SIMD's arbiter
+  // issues it ahead of the partner wave's vector phase (+2 % causal).
   auto matrix_phase = [&](int j) {
+    __builtin_amdgcn_s_setprio(1);
     if (j >= 0) pv_part(j);
     if (j + 1 <= jl) qk_part(j);
+    __builtin_amdgcn_s_setprio(0);
   };
   // vector phase of tile t: mask (on tiles that reach the end of the keys or
   // cross the wave's diagonal); a raise of the reference max of the rows
