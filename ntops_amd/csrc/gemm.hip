@@ -37,8 +37,9 @@
 //    M-grouped range of tiles that share A and B panels in its L2;
 //  * edges: buffer loads with a per-tile resource; out-of-range chunks get an
 //    offset past the resource's extent and read as zero.
-// Skinny path (M <= 64, K-major A): 16-column blocks whose waves split K,
-// operands straight to registers in the v_mfma_f32_16x16x32 layout.
+// Skinny path (M <= 64, K-major A): 16/32/64-column blocks whose waves
+// split K, operands straight to registers in the v_mfma_f32_16x16x32 layout
+// (fp32: v_mfma_f32_16x16x4_f32).
 // Short-K path (K <= 128, M and N multiples of 128): a persistent kernel
 // built around the output stream.
 // Generic path (fp32, or any other strides): 64x64 LDS-tiled FMA kernel with
@@ -864,6 +865,163 @@ int launch_skinny(const GemmArgs& g, hipStream_t st) {
   return launch_skinny_mb<T, BKM, 4>(g, st, j);
 }
 
+// fp32 variant of the skinny kernel: v_mfma_f32_16x16x4_f32 (IEEE fp32
+// products, fp32 accumulation) in 16-wide K steps.  A lane's 16-byte load
+// holds 4 consecutive k of one row, k0 + 4 (l >> 4) + e, and element e of
+// every operand feeds MFMA e of the step, so the four MFMAs cover the
+// step's 16 k values in a fixed permutation shared by A and B.  An M/N-major
+// B goes through a per-wave LDS tile [16 k][16 J n] read back per column.
+template <bool BKM, int MB, int J>
+__global__ __launch_bounds__(256) void k_gemm_skinny_f32(GemmArgs g) {
+  constexpr int NW = 4, U = MB + J <= 3 ? 8 : 4, NB = 16 * J;
+  __shared__ float red[NW][J][MB][4][64];
+  __shared__ __attribute__((aligned(16))) float trs[BKM ? 1 : NW][16 * NB];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int bx = blockIdx.x;
+  if ((gridDim.x & 7) == 0) bx = (bx & 7) * (gridDim.x >> 3) + (bx >> 3);
+  const int n0 = bx * NB;
+  const int bat = blockIdx.y;
+  const int nv = min(NB, g.N - n0);
+  const int r16 = lane & 15, kq = (lane >> 4) * 4;
+
+  const float* A = static_cast<const float*>(g.A) + bat * g.sa_b;
+  const float* B = static_cast<const float*>(g.B) + bat * g.sb_b;
+  const __amdgpu_buffer_rsrc_t ra =
+      buffer_rsrc(A, static_cast<uint32_t>((static_cast<int64_t>(g.M - 1) * g.sa_m + g.K) * 4));
+  const __amdgpu_buffer_rsrc_t rb =
+      BKM ? buffer_rsrc(B + static_cast<int64_t>(n0) * g.sb_n,
+                        static_cast<uint32_t>((static_cast<int64_t>(nv - 1) * g.sb_n + g.K) * 4))
+          : buffer_rsrc(B + n0, static_cast<uint32_t>((static_cast<int64_t>(g.K - 1) * g.sb_k + nv) * 4));
+  uint32_t a_off[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) a_off[mb] = static_cast<uint32_t>(((mb * 16 + r16) * g.sa_m + kq) * 4);
+  uint32_t b_off[J];
+  bool b_col_ok[J];
+  int b_krow[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if constexpr (BKM) {
+      b_off[j] = static_cast<uint32_t>(((16 * j + r16) * g.sb_n + kq) * 4);
+      b_col_ok[j] = 16 * j + r16 < nv;
+      b_krow[j] = kq;
+    } else {
+      // load j: k-rows j * 16 / J + l / (4 J), 4-float chunk l % (4 J)
+      b_krow[j] = j * (16 / J) + lane / (4 * J);
+      b_off[j] = static_cast<uint32_t>((b_krow[j] * g.sb_k + 4 * (lane % (4 * J))) * 4);
+      b_col_ok[j] = 4 * (lane % (4 * J)) < nv;
+    }
+  }
+  const uint32_t b_kstep = BKM ? 4u : static_cast<uint32_t>(g.sb_k * 4);  // bytes per k
+
+  f32x4 acc[J][MB];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[j][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int s0 = wave; s0 * 16 < g.K; s0 += NW * U) {
+    f32x4 bq[U][J], aq[U][MB];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k0 = (s0 + NW * u) * 16;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const bool b_ok = b_col_ok[j] && k0 + b_krow[j] < g.K;
+        bq[u][j] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rb, b_ok ? b_off[j] + static_cast<uint32_t>(k0) * b_kstep : kOOB, 0, 0));
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const bool a_ok = mb * 16 + r16 < g.M && k0 + kq < g.K;
+        aq[u][mb] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, a_ok ? a_off[mb] + k0 * 4u : kOOB, 0, 0));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      f32x4 bf[J];
+      if constexpr (BKM) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) bf[j] = bq[u][j];
+      } else {
+        // row-major [16 k][NB] tile: load j's lanes write floats j * 256 + 4 l
+#pragma unroll
+        for (int j = 0; j < J; ++j) *reinterpret_cast<f32x4*>(&trs[wave][j * 256 + lane * 4]) = bq[u][j];
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bf[j][e] = trs[wave][(kq + e) * NB + 16 * j + r16];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            acc[j][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[u][mb][e], bf[j][e], acc[j][mb], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][j][mb][r][lane] = acc[j][mb][r];
+  __syncthreads();
+  float* D = static_cast<float*>(g.D) + bat * g.sd_b;
+  const float* Cp = g.use_c ? static_cast<const float*>(g.C) + bat * g.sc_b : nullptr;
+  for (int q = wave; q < J * MB; q += NW) {
+    const int j = q / MB, mb = q - j * MB;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = mb * 16 + (lane >> 4) * 4 + r, n = n0 + 16 * j + r16;
+      if (m < g.M && n < g.N) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[w][j][mb][r][lane];
+        v *= g.alpha;
+        if (Cp != nullptr) v += g.beta * Cp[m * g.sc_m + n * g.sc_n];
+        D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = v;
+      }
+    }
+  }
+}
+
+template <bool BKM, int MB>
+int launch_skinny_f32_mb(const GemmArgs& g, hipStream_t st, int j) {
+  const unsigned by = static_cast<unsigned>(g.batch);
+  if constexpr (kSkinnyMaxJ(MB) >= 4)
+    if (j == 4) {
+      hipLaunchKernelGGL((k_gemm_skinny_f32<BKM, MB, 4>), dim3((g.N + 63) / 64, by), dim3(256), 0, st, g);
+      return check_launch("gemm");
+    }
+  if (j == 2)
+    hipLaunchKernelGGL((k_gemm_skinny_f32<BKM, MB, 2>), dim3((g.N + 31) / 32, by), dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((k_gemm_skinny_f32<BKM, MB, 1>), dim3((g.N + 15) / 16, by), dim3(256), 0, st, g);
+  return check_launch("gemm");
+}
+
+template <bool BKM>
+int launch_skinny_f32(const GemmArgs& g, hipStream_t st) {
+  const int mb = (g.M + 15) / 16;
+  const int cus = cu_count_cached() > 0 ? cu_count_cached() : 256;
+  int j = 1;
+  for (int c : {4, 2}) {
+    if (c <= kSkinnyMaxJ(mb) && static_cast<int64_t>((g.N + 16 * c - 1) / (16 * c)) * g.batch >= cus) {
+      j = c;
+      break;
+    }
+  }
+  if (mb == 1) return launch_skinny_f32_mb<BKM, 1>(g, st, j);
+  if (mb == 2) return launch_skinny_f32_mb<BKM, 2>(g, st, j);
+  if (mb == 3) return launch_skinny_f32_mb<BKM, 3>(g, st, j);
+  return launch_skinny_f32_mb<BKM, 4>(g, st, j);
+}
+
 // ---- generic kernel (any dtype among F32/F16/BF16, any strides) -------------
 template <typename T>
 __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
@@ -1037,6 +1195,19 @@ int run_gemm(GemmArgs g, hipStream_t st) {
       if (a_m && b_n) return pick_tile<T, false, false>(g, st);
       return pick_tile<T, false, true>(g, st);
     }
+  }
+  if constexpr (std::is_same<T, float>::value) {
+    // fp32 with few rows: the skinny MFMA kernel (K-major A, 16-byte rows).
+    const bool a_k = g.sa_k == 1 && g.sa_m % 4 == 0 && g.K % 4 == 0;
+    const bool b_k = g.sb_k == 1 && g.sb_n % 4 == 0;
+    const bool b_n = g.sb_n == 1 && g.sb_k % 4 == 0 && g.N % 4 == 0 && !b_k;
+    const bool batch_ok = g.batch <= 65535 && (g.batch == 1 || (g.sa_b % 4 == 0 && g.sb_b % 4 == 0));
+    const int64_t lim = int64_t(1) << 31;
+    const bool fits = (static_cast<int64_t>(kSkinnyMaxM) * g.sa_m + g.K) * 4 < lim &&
+                      (b_k ? (16 * 64 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 64)) * 4 < lim;
+    if (g.K > 0 && g.M <= kSkinnyMaxM && a_k && (b_k || b_n) && batch_ok && fits && aligned16(g.A) &&
+        aligned16(g.B))
+      return b_k ? launch_skinny_f32<true>(g, st) : launch_skinny_f32<false>(g, st);
   }
   const int64_t tiles = static_cast<int64_t>((g.M + 63) / 64) * ((g.N + 63) / 64) * g.batch;
   if (tiles > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "gemm: too many tiles");

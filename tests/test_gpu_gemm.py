@@ -91,6 +91,21 @@ def test_mm_small_m(m, n, k, dtype, layout):
                  f"mm small m {layout}")
 
 
+@pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
+@pytest.mark.parametrize("m, n, k", SKINNY)
+def test_mm_small_m_f32(m, n, k, layout):
+    """fp32 with few rows: the fp32 skinny kernel (IEEE fp32 MFMA products,
+    fp32 accumulation) against the oracle at the fp32 GEMM tolerance."""
+    a = torch.randn(m, k)
+    b = torch.randn(k, n)
+    ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
+    bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
+    got = ntops_amd.torch.mm(ag, bg)
+    rtol, atol = tol(torch.float32, k)
+    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), rtol, atol * max(1.0, k**0.5),
+                 f"mm f32 small m {layout}")
+
+
 def test_addmm_and_bmm_small_m():
     bias = torch.randn(1000).bfloat16()
     x = (0.1 * torch.randn(7, 512)).bfloat16()
