@@ -98,7 +98,7 @@ __device__ __forceinline__ void tile_of(int pid, int nblocks, int tm_count, int 
   const int per_batch = tm_count * tn_count;
   bat = pid / per_batch;
   const int t = pid - bat * per_batch;
-  constexpr int kGroupM = 8;
+  constexpr int kGroupM = 4;  // 4 measured ~0.7 % over 8 and 2 on mm, 16 ~2.5 % below
   const int group_size = kGroupM * tn_count;
   const int g = t / group_size;
   const int first_m = g * kGroupM;
