@@ -42,8 +42,9 @@
 // (fp32: v_mfma_f32_16x16x4_f32).
 // Short-K path (K <= 128, M and N multiples of 128): a persistent kernel
 // built around the output stream.
-// Generic path (fp32, or any other strides): 64x64 LDS-tiled FMA kernel with
-// fp32 accumulation (IEEE; gfx950 has no reduced-precision fp32 MFMA input).
+// fp32 tile path (K-major A): LDS-free v_mfma_f32_16x16x4_f32 wave tiles.
+// Generic path (any other strides): 64x64 LDS-tiled FMA kernel with fp32
+// accumulation (IEEE; gfx950 has no reduced-precision fp32 MFMA input).
 #include "gemm.h"
 #include "mfma.h"
 
@@ -1022,6 +1023,113 @@ int launch_skinny_f32(const GemmArgs& g, hipStream_t st) {
   return launch_skinny_f32_mb<BKM, 4>(g, st, j);
 }
 
+// ---- fp32 tile kernel -------------------------------------------------------
+// fp32 products on v_mfma_f32_16x16x4_f32 without LDS: each wave owns a
+// 64 x 64 output tile (4 x 4 MFMA tiles, 64 accumulator registers) and loads
+// its operands straight from global memory (L2) into the MFMA layout, 16 k
+// per step.  A (K-major) comes as one 16-byte load per lane and 16-row block
+// holding k0 + 4 (l >> 4) + e, e = 0..3; element e feeds MFMA e of the
+// step.  B matches that k order: K-major B the same way, M/N-major B as
+// 4-byte loads of k-row k0 + 4 (l >> 4) + e, column l & 15 (16 consecutive
+// columns of 4 k-rows per instruction).  Each loaded fragment serves four
+// MFMAs, so a step moves 8 KiB per 64 MFMAs and the kernel needs no
+// barriers.  Blocks of 2 x 2 waves cover 128 x 128 and are ordered like the
+// bf16 tiles.  Out-of-range rows, columns and k read as zero.
+template <bool BKM>
+__global__ __launch_bounds__(256) void k_gemm_f32_tile(GemmArgs g) {
+  constexpr int TM = 4, TN = 4, U = 2;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tm_count = (g.M + 127) / 128, tn_count = (g.N + 127) / 128;
+  int bat, tmi, tni;
+  tile_of(blockIdx.x, gridDim.x, tm_count, tn_count, bat, tmi, tni);
+  const int m0 = tmi * 128 + (wave >> 1) * 64, n0 = tni * 128 + (wave & 1) * 64;
+  const int mv = max(0, min(64, g.M - m0)), nv = max(0, min(64, g.N - n0));
+  const int r16 = lane & 15, kq = (lane >> 4) * 4;
+  const float* A = static_cast<const float*>(g.A) + bat * g.sa_b;
+  const float* B = static_cast<const float*>(g.B) + bat * g.sb_b;
+  const __amdgpu_buffer_rsrc_t ra =
+      buffer_rsrc(A + static_cast<int64_t>(m0) * g.sa_m,
+                  mv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(mv - 1) * g.sa_m + g.K) * 4) : 0u);
+  const __amdgpu_buffer_rsrc_t rb =
+      BKM ? buffer_rsrc(B + static_cast<int64_t>(n0) * g.sb_n,
+                        nv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(nv - 1) * g.sb_n + g.K) * 4) : 0u)
+          : buffer_rsrc(B + n0, nv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(g.K - 1) * g.sb_k + nv) * 4) : 0u);
+  uint32_t a_off[TM];
+  bool a_ok[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    a_off[i] = static_cast<uint32_t>(((16 * i + r16) * g.sa_m + kq) * 4);
+    a_ok[i] = 16 * i + r16 < mv;
+  }
+  uint32_t b_off[TN];
+  bool b_ok[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    b_off[j] = BKM ? static_cast<uint32_t>(((16 * j + r16) * g.sb_n + kq) * 4)
+                   : static_cast<uint32_t>((kq * g.sb_k + 16 * j + r16) * 4);
+    b_ok[j] = 16 * j + r16 < nv;
+  }
+  const uint32_t b_kstep = BKM ? 4u : static_cast<uint32_t>(g.sb_k * 4);  // bytes per k
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < g.K; k0 += 16 * U) {
+    f32x4 aq[U][TM], bq[U][TN];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = k0 + 16 * u;
+      const bool k_ok = k + kq < g.K;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        aq[u][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 ra, a_ok[i] && k_ok ? a_off[i] + k * 4u : kOOB, 0, 0));
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (BKM) {
+          bq[u][j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rb, b_ok[j] && k_ok ? b_off[j] + k * 4u : kOOB, 0, 0));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            bq[u][j][e] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(
+                           rb, b_ok[j] && k_ok ? b_off[j] + static_cast<uint32_t>(k + e) * b_kstep : kOOB, 0, 0));
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[u][i][e], bq[u][j][e], acc[i][j], 0, 0, 0);
+  }
+  float* D = static_cast<float*>(g.D) + bat * g.sd_b;
+  const float* Cp = g.use_c ? static_cast<const float*>(g.C) + bat * g.sc_b : nullptr;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * i + (lane >> 4) * 4 + r, n = n0 + 16 * j + r16;
+        if (m < g.M && n < g.N) {
+          float v = g.alpha * acc[i][j][r];
+          if (Cp != nullptr) v += g.beta * Cp[m * g.sc_m + n * g.sc_n];
+          D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = v;
+        }
+      }
+}
+
 // ---- generic kernel (any dtype among F32/F16/BF16, any strides) -------------
 template <typename T>
 __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
@@ -1208,6 +1316,19 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     if (g.K > 0 && g.M <= kSkinnyMaxM && a_k && (b_k || b_n) && batch_ok && fits && aligned16(g.A) &&
         aligned16(g.B))
       return b_k ? launch_skinny_f32<true>(g, st) : launch_skinny_f32<false>(g, st);
+    // Larger fp32 products: the LDS-free MFMA tile kernel.
+    const bool b_n4 = g.sb_n == 1 && !b_k;  // 4-byte B loads: any k-row stride
+    const bool fits_t = (128 * g.sa_m + g.K) * 4 < lim &&
+                        (b_k ? (128 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 128)) * 4 < lim;
+    const int64_t tiles = static_cast<int64_t>((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
+    if (g.K > 0 && a_k && (b_k || b_n4) && fits_t && aligned16(g.A) && (!b_k || aligned16(g.B)) &&
+        (g.batch == 1 || g.sa_b % 4 == 0) && tiles <= 0x7fffffffLL) {
+      if (b_k)
+        hipLaunchKernelGGL((k_gemm_f32_tile<true>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, g);
+      else
+        hipLaunchKernelGGL((k_gemm_f32_tile<false>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, g);
+      return check_launch("gemm");
+    }
   }
   const int64_t tiles = static_cast<int64_t>((g.M + 63) / 64) * ((g.N + 63) / 64) * g.batch;
   if (tiles > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "gemm: too many tiles");

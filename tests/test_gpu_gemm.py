@@ -106,6 +106,34 @@ def test_mm_small_m_f32(m, n, k, layout):
                  f"mm f32 small m {layout}")
 
 
+@pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
+@pytest.mark.parametrize("m, n, k", [(256, 512, 128), (300, 200, 72), (1000, 1024, 640), (130, 1000, 4), (65, 129, 1028)])
+def test_mm_f32_tiles(m, n, k, layout):
+    """fp32 beyond the skinny rows: the LDS-free fp32 MFMA tile kernel
+    (K-major A; B either way), partial 64 x 64 wave tiles at every edge."""
+    a = torch.randn(m, k)
+    b = torch.randn(k, n)
+    ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
+    bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
+    got = ntops_amd.torch.mm(ag, bg)
+    rtol, atol = tol(torch.float32, k)
+    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), rtol, atol * max(1.0, k**0.5),
+                 f"mm f32 tiles {layout}")
+
+
+def test_addmm_and_bmm_f32_tiles():
+    bias = torch.randn(300)
+    x = torch.randn(200, 96)
+    y = torch.randn(96, 300)
+    got = ntops_amd.torch.addmm(bias.cuda(), x.cuda(), y.cuda(), beta=0.5, alpha=2.0)
+    exp = from_np(O.gemm(to_np(x), to_np(y), "f32", to_np(bias), 2.0, 0.5), "f32")
+    assert_close(got, exp, 1e-5, 1e-5 * 96**0.5, "addmm f32 tiles")
+    a = torch.randn(3, 130, 64)
+    b = torch.randn(3, 64, 260)
+    got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
+    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), 1e-5, 1e-5 * 8, "bmm f32 tiles")
+
+
 def test_addmm_and_bmm_small_m():
     bias = torch.randn(1000).bfloat16()
     x = (0.1 * torch.randn(7, 512)).bfloat16()
