@@ -42,7 +42,8 @@
 // (fp32: v_mfma_f32_16x16x4_f32).
 // Short-K path (K <= 128, M and N multiples of 128): a persistent kernel
 // built around the output stream.
-// fp32 tile path (K-major A): LDS-free v_mfma_f32_16x16x4_f32 wave tiles.
+// fp32 tile path (K-major A): v_mfma_f32_16x16x4_f32 wave tiles, operands
+// from L2 per wave.
 // Generic path (any other strides): 64x64 LDS-tiled FMA kernel with fp32
 // accumulation (IEEE; gfx950 has no reduced-precision fp32 MFMA input).
 #include "gemm.h"
@@ -1024,20 +1025,22 @@ int launch_skinny_f32(const GemmArgs& g, hipStream_t st) {
 }
 
 // ---- fp32 tile kernel -------------------------------------------------------
-// fp32 products on v_mfma_f32_16x16x4_f32 without LDS: each wave owns a
+// fp32 products on v_mfma_f32_16x16x4_f32 without shared LDS tiles: each wave owns a
 // 64 x 64 output tile (4 x 4 MFMA tiles, 64 accumulator registers) and loads
 // its operands straight from global memory (L2) into the MFMA layout, 16 k
 // per step.  A (K-major) comes as one 16-byte load per lane and 16-row block
 // holding k0 + 4 (l >> 4) + e, e = 0..3; element e feeds MFMA e of the
-// step.  B matches that k order: K-major B the same way, M/N-major B as
-// 4-byte loads of k-row k0 + 4 (l >> 4) + e, column l & 15 (16 consecutive
-// columns of 4 k-rows per instruction).  Each loaded fragment serves four
-// MFMAs, so a step moves 8 KiB per 64 MFMAs and the kernel needs no
-// barriers.  Blocks of 2 x 2 waves cover 128 x 128 and are ordered like the
+// step.  B matches that k order: K-major B the same way; an M/N-major B as
+// 16-byte row pieces (4 k-rows x 64 columns per instruction) staged in a
+// per-wave LDS tile with padded rows and read back per column.  Each loaded
+// fragment serves four MFMAs, so a step moves 8 KiB per 64 MFMAs and the
+// kernel needs no barriers.  Blocks of 2 x 2 waves cover 128 x 128 and are ordered like the
 // bf16 tiles.  Out-of-range rows, columns and k read as zero.
 template <bool BKM>
 __global__ __launch_bounds__(256) void k_gemm_f32_tile(GemmArgs g) {
   constexpr int TM = 4, TN = 4, U = 2;
+  constexpr int kTrRow = 68;  // floats per k-row of the M/N-major B tile (64 + 4: conflict-free reads)
+  __shared__ __attribute__((aligned(16))) float trs[BKM ? 1 : 4][16 * kTrRow];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tm_count = (g.M + 127) / 128, tn_count = (g.N + 127) / 128;
@@ -1066,9 +1069,10 @@ __global__ __launch_bounds__(256) void k_gemm_f32_tile(GemmArgs g) {
   bool b_ok[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
+    // M/N-major: load j covers k-rows 4 j + (l >> 4), columns 4 (l & 15) .. + 3
     b_off[j] = BKM ? static_cast<uint32_t>(((16 * j + r16) * g.sb_n + kq) * 4)
-                   : static_cast<uint32_t>((kq * g.sb_k + 16 * j + r16) * 4);
-    b_ok[j] = 16 * j + r16 < nv;
+                   : static_cast<uint32_t>(((4 * j + (lane >> 4)) * g.sb_k + 4 * r16) * 4);
+    b_ok[j] = BKM ? 16 * j + r16 < nv : 4 * r16 < nv;
   }
   const uint32_t b_kstep = BKM ? 4u : static_cast<uint32_t>(g.sb_k * 4);  // bytes per k
 
@@ -1094,24 +1098,39 @@ __global__ __launch_bounds__(256) void k_gemm_f32_tile(GemmArgs g) {
           bq[u][j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                    rb, b_ok[j] && k_ok ? b_off[j] + k * 4u : kOOB, 0, 0));
         } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            bq[u][j][e] = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(
-                           rb, b_ok[j] && k_ok ? b_off[j] + static_cast<uint32_t>(k + e) * b_kstep : kOOB, 0, 0));
+          const bool ok = b_ok[j] && k + 4 * j + (lane >> 4) < g.K;
+          bq[u][j] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         rb, ok ? b_off[j] + static_cast<uint32_t>(k) * b_kstep : kOOB, 0, 0));
         }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
+      f32x4 bf[TN];
+      if constexpr (BKM) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[j] = bq[u][j];
+      } else {
+        // Stage the step's 16 x 64 tile (row-major, padded rows) and read
+        // column l & 15 of k-rows 4 (l >> 4) + e back for each 16-column group.
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          *reinterpret_cast<f32x4*>(&trs[wave][(4 * j + (lane >> 4)) * kTrRow + 4 * r16]) = bq[u][j];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bf[j][e] = trs[wave][(kq + e) * kTrRow + 16 * j + r16];
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[u][i][e], bq[u][j][e], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[u][i][e], bf[j][e], acc[i][j], 0, 0, 0);
+    }
   }
   float* D = static_cast<float*>(g.D) + bat * g.sd_b;
   const float* Cp = g.use_c ? static_cast<const float*>(g.C) + bat * g.sc_b : nullptr;
@@ -1317,12 +1336,12 @@ int run_gemm(GemmArgs g, hipStream_t st) {
         aligned16(g.B))
       return b_k ? launch_skinny_f32<true>(g, st) : launch_skinny_f32<false>(g, st);
     // Larger fp32 products: the LDS-free MFMA tile kernel.
-    const bool b_n4 = g.sb_n == 1 && !b_k;  // 4-byte B loads: any k-row stride
+    const bool b_n4 = g.sb_n == 1 && g.sb_k % 4 == 0 && g.N % 4 == 0 && !b_k;
     const bool fits_t = (128 * g.sa_m + g.K) * 4 < lim &&
                         (b_k ? (128 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 128)) * 4 < lim;
     const int64_t tiles = static_cast<int64_t>((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
-    if (g.K > 0 && a_k && (b_k || b_n4) && fits_t && aligned16(g.A) && (!b_k || aligned16(g.B)) &&
-        (g.batch == 1 || g.sa_b % 4 == 0) && tiles <= 0x7fffffffLL) {
+    if (g.K > 0 && a_k && (b_k || b_n4) && fits_t && aligned16(g.A) && aligned16(g.B) &&
+        (g.batch == 1 || (g.sa_b % 4 == 0 && g.sb_b % 4 == 0)) && tiles <= 0x7fffffffLL) {
       if (b_k)
         hipLaunchKernelGGL((k_gemm_f32_tile<true>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, g);
       else
