@@ -673,15 +673,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_panel(GemmArgs g, int seg) {
 // Operands go straight from global memory to registers in the layout of
 // v_mfma_f32_16x16x32 (lane l: row / column l & 15, k = 8 (l >> 4) .. + 7):
 // A and K-major B with one 16-byte buffer load per lane; M/N-major B
-// loaded as 16-byte row pieces and transposed through a 1 KiB per-wave LDS
+// loaded as 16-byte row pieces and transposed through a J KiB per-wave LDS
 // area with ds_read_b64_tr_b16.  U steps are loaded before their MFMAs so
-// each wave keeps U * (MB + 1) 16-byte loads in flight (refilling each step's
-// registers as soon as they are consumed measured no faster).  Blocks are
-// mapped so that consecutive n-slices share an XCD: for an M/N-major B each
-// block reads 32 bytes of every k-row, and its neighbours' pieces of the same
-// 128-byte lines then come from the same L2 (16 x 14336 x 4096 NN: 75 -> 40
-// us).  Out-of-range rows, columns and k read as zero (buffer offsets past
-// the extent).
+// each wave keeps U * (MB + J) 16-byte loads in flight (refilling each
+// step's registers as soon as they are consumed measured no faster).  Blocks
+// are mapped so that consecutive n-slices share an XCD: for an M/N-major B
+// each block reads 32 J bytes of every k-row, and its neighbours' pieces of
+// the same 128-byte lines then come from the same L2 (16-column slices,
+// 16 x 14336 x 4096 NN: 75 -> 40 us).  Out-of-range rows, columns and k
+// read as zero (buffer offsets past the extent).
 // Requires A K-major, K % 8 == 0; M/N-major B also N % 8 == 0.
 constexpr int kSkinnyMaxM = 64;
 // Widest column slice (in 16-column groups) for MB 16-row blocks of A: the
