@@ -686,7 +686,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_panel(GemmArgs g, int seg) {
 constexpr int kSkinnyMaxM = 64;
 // Widest column slice (in 16-column groups) for MB 16-row blocks of A: the
 // partial-sum exchange (4 * J * MB KiB of LDS) stays within 32 KiB.
-constexpr int kSkinnyMaxJ(int mb) { return mb == 2 ? 4 : 2; }
+constexpr int kSkinnyMaxJ(int mb) { return mb <= 2 ? 4 : 2; }
 
 template <typename T>
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {

@@ -72,6 +72,7 @@ SKINNY = [
     (33, 2048, 3000),
     (64, 136, 4104),
     (8, 8200, 100),
+    (3, 16448, 40),
     (24, 16448, 520),
     (40, 8208, 72),
 ]
