@@ -48,6 +48,7 @@ _d = ctypes.c_double
 _SIGNATURES = {
     "ntops_abi_version": (_i, []),
     "ntops_last_error": (ctypes.c_char_p, []),
+    "ntops_last_kernel": (ctypes.c_char_p, []),
     "ntops_unary": (_i, [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp]),
     "ntops_binary": (
         _i,
@@ -136,6 +137,11 @@ def dtype_code(dtype):
 
 def stream_of(tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+
+
+def last_kernel():
+    """Name of the kernel this thread's most recent GEMM-family call launched."""
+    return load().ntops_last_kernel().decode()
 
 
 def check(rc, what):

@@ -9,6 +9,7 @@
 namespace ntops {
 
 static thread_local char g_last_error[512] = "";
+static thread_local char g_last_kernel[128] = "";
 
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
@@ -16,6 +17,13 @@ int set_error(int code, const char* fmt, ...) {
   vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
   va_end(ap);
   return code;
+}
+
+void note_kernel(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_kernel, sizeof(g_last_kernel), fmt, ap);
+  va_end(ap);
 }
 
 int check_launch(const char* what) {
@@ -42,3 +50,5 @@ int cu_count_cached() {
 extern "C" int ntops_abi_version(void) { return 1; }
 
 extern "C" const char* ntops_last_error(void) { return ntops::g_last_error; }
+
+extern "C" const char* ntops_last_kernel(void) { return ntops::g_last_kernel; }

@@ -20,6 +20,9 @@ namespace ntops {
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Converts the HIP runtime's sticky launch error (if any) into a status.
 int check_launch(const char* what);
+// Records the name of the kernel this thread is about to launch (returned by
+// ntops_last_kernel(), so tests can assert which path served a call).
+void note_kernel(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 // Number of CUs of the current device (queried once per device; 256 if the
 // query fails).
 int cu_count_cached();

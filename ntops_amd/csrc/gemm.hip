@@ -835,6 +835,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmArgs g) {
 template <typename T, bool BKM, int MB>
 int launch_skinny_mb(const GemmArgs& g, hipStream_t st, int j) {
   const unsigned by = static_cast<unsigned>(g.batch);
+  note_kernel("gemm_skinny m%d n%d %s", 16 * MB, 16 * j, BKM ? "B:K" : "B:N");
   if constexpr (kSkinnyMaxJ(MB) >= 4)
     if (j == 4) {
       hipLaunchKernelGGL((k_gemm_skinny<T, BKM, MB, 4, 4>), dim3((g.N + 63) / 64, by), dim3(256), 0, st, g);
@@ -995,6 +996,7 @@ __global__ __launch_bounds__(256) void k_gemm_skinny_f32(GemmArgs g) {
 template <bool BKM, int MB>
 int launch_skinny_f32_mb(const GemmArgs& g, hipStream_t st, int j) {
   const unsigned by = static_cast<unsigned>(g.batch);
+  note_kernel("gemm_skinny_f32 m%d n%d %s", 16 * MB, 16 * j, BKM ? "B:K" : "B:N");
   if constexpr (kSkinnyMaxJ(MB) >= 4)
     if (j == 4) {
       hipLaunchKernelGGL((k_gemm_skinny_f32<BKM, MB, 4>), dim3((g.N + 63) / 64, by), dim3(256), 0, st, g);
@@ -1221,6 +1223,8 @@ int launch_mfma(const GemmArgs& g, hipStream_t st) {
   }
   const int64_t tiles = static_cast<int64_t>((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN) * g.batch;
   if (tiles > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "gemm: too many tiles");
+  note_kernel("gemm_mfma %dx%d s%d %s %s %s%s", BM, BN, STAGES, AK ? "A:K" : "A:M", BKM ? "B:K" : "B:N",
+              EVEN ? "even" : "ragged", CONV ? " conv" : "");
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles)), dim3(NT), kLds, st, g);
   return check_launch("gemm");
 }
@@ -1267,6 +1271,7 @@ int launch_panel(const GemmArgs& g, hipStream_t st) {
   int64_t grid = (cus * kPanelBlocksPerCu / 8) * 8;
   if (grid <= 0) grid = 256;
   if (grid > units) grid = units;
+  note_kernel("gemm_panel %s %s seg%d", AK ? "A:K" : "A:M", BKM ? "B:K" : "B:N", seg);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(256), kLds, st, g, seg);
   return check_launch("gemm");
 }
@@ -1342,6 +1347,7 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     const int64_t tiles = static_cast<int64_t>((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
     if (g.K > 0 && a_k && (b_k || b_n4) && fits_t && aligned16(g.A) && aligned16(g.B) &&
         (g.batch == 1 || (g.sa_b % 4 == 0 && g.sb_b % 4 == 0)) && tiles <= 0x7fffffffLL) {
+      note_kernel("gemm_f32_tile %s", b_k ? "B:K" : "B:N");
       if (b_k)
         hipLaunchKernelGGL((k_gemm_f32_tile<true>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, g);
       else
@@ -1351,6 +1357,7 @@ int run_gemm(GemmArgs g, hipStream_t st) {
   }
   const int64_t tiles = static_cast<int64_t>((g.M + 63) / 64) * ((g.N + 63) / 64) * g.batch;
   if (tiles > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "gemm: too many tiles");
+  note_kernel("gemm_generic");
   hipLaunchKernelGGL((k_gemm_generic<T>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, g);
   return check_launch("gemm");
 }

@@ -645,18 +645,31 @@ def rope_tables(seq_len, emb_dim, base=10000.0, full=False):
 # ------------------------------------------------------------------ GEMM --
 
 
+def gemm_f64(a, b, dt, c=None, alpha=1.0, beta=0.0, magnitude=False):
+    """The unrounded value of gemm() in float64: alpha * sum_k a[..., m, k] *
+    b[..., k, n] + beta * c (beta == 0 ignores c).  With magnitude=True also
+    returns |alpha| * sum_k |a b| + |beta| |c|, the quantity that bounds any
+    fp32 summation order's error (Higham, Accuracy and Stability of Numerical
+    Algorithms, 2nd ed., eq. 4.4: |error| <= (n - 1) u sum |x_i|)."""
+    af = to_compute(a, dt).astype(np.float64)
+    bf = to_compute(b, dt).astype(np.float64)
+    out = np.float64(alpha) * np.matmul(af, bf)
+    mag = np.abs(np.float64(alpha)) * np.matmul(np.abs(af), np.abs(bf)) if magnitude else None
+    if c is not None and beta != 0:
+        cf = np.float64(beta) * to_compute(c, dt).astype(np.float64)
+        out = out + cf
+        if magnitude:
+            mag = mag + np.abs(cf)
+    return (out, mag) if magnitude else out
+
+
 def gemm(a, b, dt, c=None, alpha=1.0, beta=0.0):
     """kernels/mm.py:54-65, kernels/bmm.py:26-39, kernels/addmm.py:64-67 --
     acc = sum_k a[..., m, k] * b[..., k, n] accumulated at (at least) fp32
     precision (here fp64, exact enough to bound the kernel's fp32 summation
     error), out = alpha * acc + beta * c rounded once to dt.  beta == 0
     ignores c."""
-    af = to_compute(a, dt).astype(np.float64)
-    bf = to_compute(b, dt).astype(np.float64)
-    acc = np.matmul(af, bf)
-    out = np.float64(alpha) * acc
-    if c is not None and beta != 0:
-        out = out + np.float64(beta) * to_compute(c, dt).astype(np.float64)
+    out = gemm_f64(a, b, dt, c, alpha, beta)
     return round_to(out.astype(np.float32) if dt != "f64" else out, dt)
 
 

@@ -3,8 +3,16 @@
 Mirrors tests/test_{mm,bmm,addmm,matmul}.py of the reference (m, n, k in
 [1, 1024], fp32 and fp16, bmm batch in [4, 16], addmm with gauss alpha/beta,
 matmul batch in {None, 1, 2, 3}) with bf16, all four operand layouts, row
-bias broadcast, and the three GEMM configs at full size (oracle on sampled
-rows plus a checksum over every output element)."""
+bias broadcast, every instantiation of the large-tile kernel, and the three
+GEMM configs at full size (oracle on rows in every tile band, exact
+small-integer checksums over every output element).
+
+16-bit results are held to tests.helpers.assert_gemm_ulp: every element
+within one ulp plus the fp32 summation bound of the exact value, and at most
+1 % of elements off the correctly rounded value -- tight enough that a
+dropped or repeated K slice fails.  fp32 results use the fp32 reduction
+tolerance with an atol scaled by sqrt(k), the typical magnitude of a sum of
+k unit-variance products."""
 
 import random
 
@@ -13,8 +21,9 @@ import pytest
 import torch
 
 import ntops_amd
+from ntops_amd import _lib
 from oracle import ops as O
-from tests.helpers import DT_NAME, TOL_GEMM, assert_close, from_np, to_np
+from tests.helpers import DT_NAME, TOL_GEMM, assert_close, assert_gemm_ulp, from_np, tile_rows, to_np
 
 pytestmark = [
     pytest.mark.gpu,
@@ -28,9 +37,39 @@ def rand_sizes():
     return [(random.randint(1, 1024), random.randint(1, 1024), random.randint(1, 1024), dt) for dt in DTYPES]
 
 
-def tol(dtype, k):
-    rtol, atol = TOL_GEMM[DT_NAME[dtype]]
-    return rtol, atol
+def expected16(m, n, k, layout, batch=1):
+    """Family of the kernel that serves a 16-bit GEMM of fresh (16-byte
+    aligned) operands in `layout` ("N" = row-major, "T" = transposed view):
+    the matrix-core kernels need one unit-stride axis per operand with 8-element
+    multiples, and an output with N % 4 == 0."""
+    if m == 1:  # a transposed (1, k) view keeps the row-major strides
+        layout = "N" + layout[1]
+    a_k = layout[0] == "N" and k % 8 == 0
+    a_m = layout[0] == "T" and m % 8 == 0
+    b_n = layout[1] == "N" and n % 8 == 0
+    b_k = layout[1] == "T" and k % 8 == 0
+    if k == 0 or not (a_k or a_m) or not (b_k or b_n) or n % 4:
+        return "gemm_generic"
+    if a_k and m <= 64:
+        return "gemm_skinny "
+    if k <= 128 and m % 128 == 0 and n % 128 == 0:
+        return "gemm_panel "
+    if -(-m // 256) * -(-n // 256) * batch >= 240 and k > 256:
+        return "gemm_mfma 256x256 "
+    return "gemm_mfma 128x128 "
+
+
+def check(got, a, b, dtype, c=None, alpha=1.0, beta=0.0, what=""):
+    """The oracle's result for (a, b[, c]): the ulp guard for 16-bit dtypes,
+    rtol 1e-5 and atol 1e-5 * sqrt(k) for fp32 (unit-variance operands)."""
+    dt = DT_NAME[dtype]
+    if dt in ("bf16", "f16"):
+        assert_gemm_ulp(got, a, b, dt, c, alpha, beta, what)
+        return
+    k = a.shape[-1]
+    exp = from_np(O.gemm(to_np(a), to_np(b), dt, None if c is None else to_np(c), alpha, beta), dt)
+    rtol, atol = TOL_GEMM[dt]
+    assert_close(got, exp, rtol, atol * max(1.0, k**0.5), what)
 
 
 @pytest.mark.parametrize("m, n, k, dtype", rand_sizes())
@@ -38,11 +77,7 @@ def test_mm(m, n, k, dtype):
     a = torch.randn(m, k).to(dtype)
     b = torch.randn(k, n).to(dtype)
     got = ntops_amd.torch.mm(a.cuda(), b.cuda())
-    dt = DT_NAME[dtype]
-    exp = from_np(O.gemm(to_np(a), to_np(b), dt), dt)
-    # randn operands: |c| ~ sqrt(k); scale atol with it
-    rtol, atol = tol(dtype, k)
-    assert_close(got, exp, rtol, atol * max(1.0, k**0.5), "mm")
+    check(got, a, b, dtype, what="mm")
 
 
 @pytest.mark.parametrize("layout", ("NN", "NT", "TN", "TT"))
@@ -54,8 +89,37 @@ def test_mm_layouts(m, n, k, dtype, layout):
     ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
     bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
     got = ntops_amd.torch.mm(ag, bg)
-    dt = DT_NAME[dtype]
-    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), dt), dt), 1.6e-2, 1.6e-2, f"mm {layout}")
+    assert _lib.last_kernel().startswith(expected16(m, n, k, layout))
+    check(got, a, b, dtype, what=f"mm {layout}")
+
+
+# The 256 x 256 tile kernel (>= 240 tiles, K > 256): every instantiation --
+# bf16 and fp16, K-major or M-major A, N-major or K-major B, even edges
+# (M, N multiples of 256, K of 32) and ragged ones (all three off that grid;
+# multiples of 8 so that every layout qualifies) -- each as mm and as addmm
+# with a row-broadcast bias and alpha, beta != 1.
+TILE256 = {"even": (4096, 4352, 512), "ragged": (4104, 4112, 520)}
+
+
+@pytest.mark.parametrize("edges", sorted(TILE256))
+@pytest.mark.parametrize("layout", ("NN", "NT", "TN", "TT"))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_mm_256_tiles(dtype, layout, edges):
+    m, n, k = TILE256[edges]
+    g = torch.Generator().manual_seed(2 * ("NN", "NT", "TN", "TT").index(layout) + (edges == "ragged"))
+    a = (0.1 * torch.randn(m, k, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(k, n, generator=g)).to(dtype)
+    bias = torch.randn(n, generator=g).to(dtype)
+    ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
+    bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
+    kernel = (f"gemm_mfma 256x256 s4 {'A:K' if layout[0] == 'N' else 'A:M'} "
+              f"{'B:N' if layout[1] == 'N' else 'B:K'} {edges}")
+    got = ntops_amd.torch.mm(ag, bg)
+    assert _lib.last_kernel() == kernel
+    check(got, a, b, dtype, what=f"mm 256 {layout} {edges}")
+    got = ntops_amd.torch.addmm(bias.cuda(), ag, bg, beta=0.5, alpha=2.0)
+    assert _lib.last_kernel() == kernel
+    assert_gemm_ulp(got, a, b, DT_NAME[dtype], bias, 2.0, 0.5, f"addmm 256 {layout} {edges}", rows=tile_rows(m))
 
 
 # Small M (decode shapes): the skinny kernel for a K-major A with either B
@@ -87,9 +151,8 @@ def test_mm_small_m(m, n, k, dtype, layout):
     ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
     bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
     got = ntops_amd.torch.mm(ag, bg)
-    dt = DT_NAME[dtype]
-    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), dt), dt), 1.6e-2, 1.6e-2 * max(1.0, (k / 100) ** 0.5),
-                 f"mm small m {layout}")
+    assert _lib.last_kernel().startswith(expected16(m, n, k, layout))
+    check(got, a, b, dtype, what=f"mm small m {layout}")
 
 
 @pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
@@ -102,9 +165,7 @@ def test_mm_small_m_f32(m, n, k, layout):
     ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
     bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
     got = ntops_amd.torch.mm(ag, bg)
-    rtol, atol = tol(torch.float32, k)
-    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), rtol, atol * max(1.0, k**0.5),
-                 f"mm f32 small m {layout}")
+    check(got, a, b, torch.float32, what=f"mm f32 small m {layout}")
 
 
 @pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
@@ -117,9 +178,7 @@ def test_mm_f32_tiles(m, n, k, layout):
     ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
     bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
     got = ntops_amd.torch.mm(ag, bg)
-    rtol, atol = tol(torch.float32, k)
-    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), rtol, atol * max(1.0, k**0.5),
-                 f"mm f32 tiles {layout}")
+    check(got, a, b, torch.float32, what=f"mm f32 tiles {layout}")
 
 
 def test_addmm_and_bmm_f32_tiles():
@@ -140,12 +199,12 @@ def test_addmm_and_bmm_small_m():
     x = (0.1 * torch.randn(7, 512)).bfloat16()
     w = (0.1 * torch.randn(1000, 512)).bfloat16()  # F.linear-style weight: B = w.t() is K-major
     got = ntops_amd.torch.addmm(bias.cuda(), x.cuda(), w.cuda().t(), beta=0.5, alpha=2.0)
-    exp = from_np(O.gemm(to_np(x), to_np(w.t().contiguous()), "bf16", to_np(bias), 2.0, 0.5), "bf16")
-    assert_close(got, exp, 1.6e-2, 1.6e-2, "addmm small m")
+    assert _lib.last_kernel().startswith("gemm_skinny ")
+    check(got, x, w.t().contiguous(), torch.bfloat16, bias, 2.0, 0.5, "addmm small m")
     q = (0.1 * torch.randn(12, 1, 128)).bfloat16()
     kt = (0.1 * torch.randn(12, 128, 777 + 7)).bfloat16()
     got = ntops_amd.torch.bmm(q.cuda(), kt.cuda())
-    assert_close(got, from_np(O.gemm(to_np(q), to_np(kt), "bf16"), "bf16"), 1.6e-2, 1.6e-2, "bmm small m")
+    check(got, q, kt, torch.bfloat16, what="bmm small m")
 
 
 def test_mm_small_integers_exact():
@@ -165,9 +224,7 @@ def test_bmm(m, n, k, dtype):
     a = torch.randn(bsz, m, k).to(dtype)
     b = torch.randn(bsz, k, n).to(dtype)
     got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
-    dt = DT_NAME[dtype]
-    rtol, atol = tol(dtype, k)
-    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), dt), dt), rtol, atol * max(1.0, k**0.5), "bmm")
+    check(got, a, b, dtype, what="bmm")
 
 
 @pytest.mark.parametrize("m, n, k, dtype", rand_sizes())
@@ -177,10 +234,7 @@ def test_addmm(m, n, k, dtype):
     y = torch.randn(k, n).to(dtype)
     beta, alpha = random.gauss(0, 1), random.gauss(0, 1)
     got = ntops_amd.torch.addmm(inp.cuda(), x.cuda(), y.cuda(), beta=beta, alpha=alpha)
-    dt = DT_NAME[dtype]
-    exp = from_np(O.gemm(to_np(x), to_np(y), dt, to_np(inp), alpha, beta), dt)
-    rtol, atol = tol(dtype, k)
-    assert_close(got, exp, rtol, atol * max(1.0, k**0.5), "addmm")
+    check(got, x, y, dtype, inp, alpha, beta, "addmm")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -191,11 +245,11 @@ def test_addmm_bias_and_beta_zero(dtype):
     y = (0.1 * torch.randn(k, n)).to(dtype)
     dt = DT_NAME[dtype]
     got = ntops_amd.torch.addmm(bias.cuda(), x.cuda(), y.cuda())
-    assert_close(got, from_np(O.gemm(to_np(x), to_np(y), dt, to_np(bias), 1.0, 1.0), dt), *TOL_GEMM[dt], "bias")
+    check(got, x, y, dtype, bias, 1.0, 1.0, "bias")
     nan_c = torch.full((m, n), float("nan"), dtype=dtype)
     got = ntops_amd.torch.addmm(nan_c.cuda(), x.cuda(), y.cuda(), beta=0, alpha=2)
     assert not torch.isnan(got).any()
-    assert_close(got, from_np(O.gemm(to_np(x), to_np(y), dt, None, 2.0, 0.0), dt), *TOL_GEMM[dt], "beta=0")
+    check(got, x, y, dtype, None, 2.0, 0.0, "beta=0")
 
 
 # Short-K shapes (K <= 128, M and N multiples of 128): the persistent panel
@@ -223,8 +277,8 @@ def test_bmm_short_k(bsz, m, n, k, layout):
     ag = a.cuda() if layout[0] == "N" else a.transpose(1, 2).contiguous().cuda().transpose(1, 2)
     bg = b.cuda() if layout[1] == "N" else b.transpose(1, 2).contiguous().cuda().transpose(1, 2)
     got = ntops_amd.torch.bmm(ag, bg)
-    dt = DT_NAME[dtype]
-    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), dt), dt), 1.6e-2, 1.6e-2, f"bmm short-k {layout}")
+    assert _lib.last_kernel().startswith("gemm_panel ")
+    check(got, a, b, dtype, what=f"bmm short-k {layout}")
 
 
 def test_addmm_short_k_bias():
@@ -233,8 +287,8 @@ def test_addmm_short_k_bias():
     x = (0.1 * torch.randn(m, k)).bfloat16()
     y = (0.1 * torch.randn(k, n)).bfloat16()
     got = ntops_amd.torch.addmm(bias.cuda(), x.cuda(), y.cuda(), beta=0.5, alpha=2.0)
-    exp = from_np(O.gemm(to_np(x), to_np(y), "bf16", to_np(bias), 2.0, 0.5), "bf16")
-    assert_close(got, exp, 1.6e-2, 1.6e-2, "addmm short-k bias")
+    assert _lib.last_kernel().startswith("gemm_panel ")
+    check(got, x, y, torch.bfloat16, bias, 2.0, 0.5, "addmm short-k bias")
 
 
 def test_gemm_k_zero_strided_views():
@@ -258,25 +312,10 @@ def test_matmul(b, m, n, k, dtype):
     a = torch.randn(a_shape).to(dtype)
     o = torch.randn(o_shape).to(dtype)
     got = ntops_amd.torch.matmul(a.cuda(), o.cuda())
-    dt = DT_NAME[dtype]
-    rtol, atol = tol(dtype, k)
-    assert_close(got, from_np(O.gemm(to_np(a), to_np(o), dt), dt), rtol, atol * max(1.0, k**0.5), "matmul")
+    check(got, a, o, dtype, what="matmul")
     if b is not None:
         got = ntops_amd.torch.matmul(a[0].cuda(), o.cuda())  # broadcast batch
-        assert_close(got, from_np(O.gemm(to_np(a[0])[None], to_np(o), dt), dt), rtol, atol * max(1.0, k**0.5), "bcast")
-
-
-def _checksum(got, a, b, bias=None):
-    """Row sums of the GPU result against A @ (B @ 1) (+ N * bias mean) in
-    fp64: covers every output element with a size-independent bound."""
-    ones = torch.ones(b.shape[-1], 1, dtype=torch.float64)
-    ref = a.double() @ (b.double() @ ones)
-    if bias is not None:
-        ref = ref + bias.double().sum()
-    got_sum = got.double().sum(-1, keepdim=True).cpu()
-    # each of N outputs carries <= 1/2 bf16 ulp of rounding: bound the sum
-    bound = 2.0**-8 * got.double().abs().sum(-1, keepdim=True).cpu() + 1e-3
-    assert ((got_sum - ref).abs() <= bound).all(), "checksum"
+        check(got, a[0].expand(b, m, k), o, dtype, what="bcast")
 
 
 def _config_mm():
@@ -287,26 +326,65 @@ def _config_mm():
     return a, b, bias
 
 
+CONFIG_KERNEL = "gemm_mfma 256x256 s4 A:K B:N even"
+
+
 def test_mm_and_addmm_config_full_size():
     """bf16 (8192 x 4096) . (4096 x 14336), fp32 accumulation; addmm with a
-    (14336,) bias, beta = alpha = 1."""
+    (14336,) bias, beta = alpha = 1: the ulp guard on two rows of every
+    256-row tile band (all columns, so every output tile is checked)."""
     a, b, bias = _config_mm()
     ag, bg = a.cuda(), b.cuda()
-    rows = torch.randint(0, 8192, (48,))
-    bn = to_np(b)
-    for name, fn, bias_ in (
-        ("mm", lambda: ntops_amd.torch.mm(ag, bg), None),
-        ("addmm", lambda: ntops_amd.torch.addmm(bias.cuda(), ag, bg), bias),
-    ):
-        got = fn()
-        sub = got[rows.cuda()]
-        exp = from_np(
-            O.gemm(to_np(a[rows]), bn, "bf16", None if bias_ is None else to_np(bias_), 1.0, 0.0 if bias_ is None else 1.0),
-            "bf16",
-        )
-        assert_close(sub, exp, 1.6e-2, 1.6e-2, f"{name} sampled rows")
-        _checksum(got, a, b, bias_)
-        del got
+    rows = tile_rows(8192)
+    got = ntops_amd.torch.mm(ag, bg)
+    assert _lib.last_kernel() == CONFIG_KERNEL
+    assert_gemm_ulp(got, a, b, "bf16", what="mm config", rows=rows)
+    del got
+    got = ntops_amd.torch.addmm(bias.cuda(), ag, bg)
+    assert _lib.last_kernel() == CONFIG_KERNEL
+    assert_gemm_ulp(got, a, b, "bf16", bias, 1.0, 1.0, "addmm config", rows=rows)
+
+
+def _bf16_rounding_bound(r):
+    """Per-element bound on |bf16(v) - v| for integer v, given r = bf16(v) in
+    float64: 0 where |r| <= 256 (integers are exact there), else half an
+    ulp at |r|."""
+    e = torch.floor(torch.log2(r.abs().clamp_min(1.0)))
+    return torch.where(r.abs() > 256, 0.5 * torch.exp2(e - 7), torch.zeros_like(r))
+
+
+def test_mm_config_exact_small_integers():
+    """The mm / addmm config shapes with operands in {-1, 0, 1} and an integer
+    bias: fp32 accumulation is exact, so every output is bf16(exact integer).
+    Rows in every tile band must match the oracle bit for bit, and the row
+    and column sums of ALL outputs must equal those of the exact product to
+    within the rounding of the few outputs above 256 -- a dropped, repeated or
+    misplaced K slice or tile anywhere changes them."""
+    g = torch.Generator().manual_seed(1)
+    a = torch.randint(-1, 2, (8192, 4096), generator=g).bfloat16()
+    b = torch.randint(-1, 2, (4096, 14336), generator=g).bfloat16()
+    bias = torch.randint(-2, 3, (14336,), generator=g).bfloat16()
+    ad, bd = a.double(), b.double()
+    rows = tile_rows(8192)
+    exact_rows = ad @ bd.sum(1)
+    exact_cols = ad.sum(0) @ bd
+    for name, c in (("mm", None), ("addmm", bias)):
+        if c is None:
+            got = ntops_amd.torch.mm(a.cuda(), b.cuda())
+        else:
+            got = ntops_amd.torch.addmm(c.cuda(), a.cuda(), b.cuda())
+        assert _lib.last_kernel() == CONFIG_KERNEL
+        exp = from_np(O.gemm(to_np(a[rows]), to_np(b), "bf16", None if c is None else to_np(c), 1.0, 1.0), "bf16")
+        assert torch.equal(got[torch.tensor(rows).cuda()].cpu(), exp), f"{name}: tile-band rows differ"
+        r = got.double()
+        slack = _bf16_rounding_bound(r)
+        er = exact_rows + (0.0 if c is None else c.double().sum())
+        ec = exact_cols + (0.0 if c is None else 8192 * c.double())
+        dr = (r.sum(1).cpu() - er).abs()
+        dc = (r.sum(0).cpu() - ec).abs()
+        assert (dr <= slack.sum(1).cpu()).all(), f"{name}: row sums off in {(dr > slack.sum(1).cpu()).sum()} rows"
+        assert (dc <= slack.sum(0).cpu()).all(), f"{name}: column sums off in {(dc > slack.sum(0).cpu()).sum()} cols"
+        del got, r, slack
 
 
 def test_bmm_config_full_size():
@@ -315,6 +393,6 @@ def test_bmm_config_full_size():
     a = (0.02 * torch.randn(32, 2048, 128, generator=g)).bfloat16()
     b = (0.02 * torch.randn(32, 128, 2048, generator=g)).bfloat16()
     got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
+    assert _lib.last_kernel().startswith("gemm_panel A:K B:N")
     for i in range(0, 32, 4):
-        exp = from_np(O.gemm(to_np(a[i : i + 4]), to_np(b[i : i + 4]), "bf16"), "bf16")
-        assert_close(got[i : i + 4], exp, 1.6e-2, 1.6e-2, f"bmm batch {i}")
+        assert_gemm_ulp(got[i : i + 4], a[i : i + 4], b[i : i + 4], "bf16", what=f"bmm batch {i}")
