@@ -298,10 +298,17 @@ int64_t col_bytes_per_image(const ConvArgs& a, int dt) {
 // Rows of each shifted plane of the implicit path.
 int64_t shift_rows(const ConvArgs& a) { return static_cast<int64_t>(a.P) + static_cast<int64_t>(a.R - 1) * a.dh; }
 
-// Whether the implicit GEMM applies (on top of use_gemm).
+// Whether the implicit GEMM applies (on top of use_gemm): stride 1, 16-bit
+// data, output rows of a multiple of 8 pixels, operands inside the 2 GiB
+// buffer range, and an output whose channel and image strides are multiples
+// of 4 elements at an 8-byte aligned address (the epilogue's store width);
+// anything else takes the unfold + GEMM path.
 bool use_implicit(const ConvArgs& a, int dt) {
   const int64_t elems = static_cast<int64_t>(a.S) * a.C * shift_rows(a) * a.Q;
-  return (dt == NTOPS_BF16 || dt == NTOPS_F16) && a.sh == 1 && a.sw == 1 && a.Q % 8 == 0 && elems * 2 < (int64_t(1) << 31);
+  const int64_t crs = static_cast<int64_t>(a.C) * a.R * a.S;
+  const bool out_ok = a.os[1] % 4 == 0 && a.os[0] % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 7u) == 0;
+  return (dt == NTOPS_BF16 || dt == NTOPS_F16) && a.sh == 1 && a.sw == 1 && a.Q % 8 == 0 &&
+         elems * 2 < (int64_t(1) << 31) && (256 * a.ws[0] + crs) * 2 < (int64_t(1) << 31) && out_ok;
 }
 
 // Workspace bytes per image of the chosen GEMM path.

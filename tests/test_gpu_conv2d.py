@@ -167,3 +167,33 @@ def test_conv2d_workload_full_size():
         exp = oracle(x[img:img + 1], wt[ch], b[ch], 1, 1, 1)
         assert_close(got[img:img + 1, ch], exp, 1.6e-2, 1.6e-2, f"image {img}")
     assert torch.isfinite(got).all()
+
+
+@pytest.mark.parametrize("form", ("misaligned", "padded channel stride"))
+def test_conv2d_output_views_the_implicit_gemm_cannot_store(form):
+    """Outputs the implicit GEMM's 8-byte stores cannot serve -- an address
+    2 bytes past alignment, or a channel stride that is not a multiple of 4
+    elements -- take the unfold + GEMM path instead of failing."""
+    dtype = torch.bfloat16
+    n, c, h, k = 2, 64, 16, 64
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(n, c, h, h, generator=g).to(dtype)
+    wt = (torch.randn(k, c, 3, 3, generator=g) / 24).to(dtype)
+    b = torch.randn(k, generator=g).to(dtype)
+    if form == "misaligned":
+        buf = torch.empty(n * k * h * h + 1, dtype=dtype, device="cuda")
+        out = buf[1:].view(n, k, h, h)
+    else:
+        buf = torch.empty(n, k, h * h + 2, dtype=dtype, device="cuda")
+        out = buf[:, :, : h * h].view(n, k, h, h)
+    lib = _lib.load()
+    st = lambda t: _lib.i64_array(t.stride())  # noqa: E731
+    geo = (n, c, h, h, k, 3, 3, h, h, 1, 1, 1, 1, 1, 1)
+    ws_bytes = lib.ntops_conv2d_workspace(_lib.BF16, *geo, st(wt), st(out)) * 16  # room for the unfold path
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    xg, wg, bg = x.cuda(), wt.cuda(), b.cuda()
+    rc = lib.ntops_conv2d(_lib.BF16, *geo, xg.data_ptr(), st(xg), wg.data_ptr(), st(wg), bg.data_ptr(), 1,
+                          out.data_ptr(), st(out), ws.data_ptr(), ws_bytes, _lib.stream_of(out))
+    _lib.check(rc, f"conv2d into a {form} output")
+    assert _lib.last_kernel().startswith("gemm_") and not _lib.last_kernel().endswith(" conv")
+    assert_close(out, oracle(x, wt, b, 1, 1, 1), 1.6e-2, 1.6e-2, form)
