@@ -329,6 +329,26 @@ NTOPS_API int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t W
                void* out, const int64_t* out_strides,
                void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ntops_conv2d without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No ntops counterpart.  The workspace is a
+ * fixed scratch array inside the library, NTOPS_CONV2D_NOALLOC_MAX_SCRATCH
+ * bytes on each GPU it runs on, held until the process ends; images run in
+ * chunks that fit it, and a problem whose single image needs more is
+ * rejected with NTOPS_ERR_UNSUPPORTED.  Nothing is allocated or freed by the
+ * call.  Every call on one GPU shares that GPU's scratch: calls that overlap
+ * on one GPU (concurrent streams or host threads) race.  Arguments and
+ * results otherwise as ntops_conv2d. */
+#define NTOPS_CONV2D_NOALLOC_MAX_SCRATCH ((int64_t)64 << 20)
+NTOPS_API int ntops_conv2d_noalloc(int dtype, int64_t N, int64_t C, int64_t H, int64_t W,
+               int64_t K, int64_t R, int64_t S, int64_t P, int64_t Q,
+               int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+               int64_t dil_h, int64_t dil_w,
+               const void* x, const int64_t* x_strides,
+               const void* w, const int64_t* w_strides,
+               const void* bias, int64_t bias_stride,
+               void* out, const int64_t* out_strides, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

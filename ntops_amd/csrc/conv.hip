@@ -26,10 +26,43 @@
 //    FMA GEMM.
 //  * direct path (small channel counts, any strides): one thread per output
 //    element, fp32 accumulation.
+#include <atomic>
+
 #include "gemm.h"
 
 namespace ntops {
 namespace {
+
+// Scratch of ntops_conv2d_noalloc: stands in for the caller's workspace (the
+// shifted planes or the unfolded input of a chunk of images).  Each GPU holds
+// its own copy at its own address for the life of the process; host code
+// reaches it only through conv_scratch(), never through the symbol's name
+// (which on the host is a stand-in, not a device address).  Every byte a call
+// reads is written by the same call's shift / unfold kernel first, so no
+// clearing is needed; calls that overlap on one GPU share it and race.
+constexpr int64_t kConvScratchBytes = NTOPS_CONV2D_NOALLOC_MAX_SCRATCH;
+static __device__ __align__(256) char scratch[kConvScratchBytes];
+
+// Device address of this device's scratch (looked up once per device with
+// that device current), or nullptr with the error recorded.
+void* conv_scratch() {
+  static std::atomic<void*> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error(NTOPS_ERR_HIP, "conv2d_noalloc: no current HIP device");
+    return nullptr;
+  }
+  void* p = cache[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error(NTOPS_ERR_HIP, "conv2d_noalloc: scratch address lookup failed: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    cache[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
 
 struct ConvArgs {
   const void* x;
@@ -459,4 +492,28 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
     if (rc != NTOPS_OK) return rc;
   }
   return NTOPS_OK;
+}
+
+extern "C" int ntops_conv2d_noalloc(int dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R,
+                                    int64_t S, int64_t P, int64_t Q, int64_t stride_h, int64_t stride_w,
+                                    int64_t pad_h, int64_t pad_w, int64_t dil_h, int64_t dil_w, const void* x,
+                                    const int64_t* x_strides, const void* w, const int64_t* w_strides,
+                                    const void* bias, int64_t bias_stride, void* out, const int64_t* out_strides,
+                                    void* stream) {
+  // Bytes one image takes on the workspace path (0 when the problem runs
+  // without one); images are processed in chunks that fit the scratch.
+  const int64_t per_image = ntops_conv2d_workspace(dtype, 1, C, H, W, K, R, S, P, Q, stride_h, stride_w, pad_h,
+                                                   pad_w, dil_h, dil_w, w_strides, out_strides);
+  if (per_image > kConvScratchBytes)
+    return set_error(NTOPS_ERR_UNSUPPORTED,
+                     "conv2d_noalloc: one image needs %lld bytes of scratch, more than the %lld-byte maximum",
+                     static_cast<long long>(per_image), static_cast<long long>(kConvScratchBytes));
+  void* ws = nullptr;
+  if (per_image > 0 && N > 0 && K > 0 && P > 0 && Q > 0) {
+    ws = conv_scratch();
+    if (ws == nullptr) return NTOPS_ERR_HIP;
+  }
+  return ntops_conv2d(dtype, N, C, H, W, K, R, S, P, Q, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, x,
+                      x_strides, w, w_strides, bias, bias_stride, out, out_strides, ws, ws ? kConvScratchBytes : 0,
+                      stream);
 }
