@@ -43,6 +43,7 @@
  *   ntops_rope_qk     <- no ntops counterpart: two calls of
  *                        torch/rotary_position_embedding.py:7-29 (q and k with
  *                        the same tables) in one launch
+ *   ntops_im2col      <- src/ntops/torch/im2col.py:44-135, kernels/im2col.py:10-80
  *   ntops_conv2d_workspace <- no ntops counterpart (Triton tiles the unfolded
  *                        input on the fly); sizes the caller-owned buffer that
  *                        the GEMM path of ntops_conv2d unfolds into
@@ -328,6 +329,20 @@ NTOPS_API int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t W
                const void* bias, int64_t bias_stride,
                void* out, const int64_t* out_strides,
                void* workspace, int64_t workspace_bytes, void* stream);
+
+/* out (N, C * kernel_h * kernel_w, oh * ow) = the unfolded input x
+ * (N, C, H, W): out[n, (c * kernel_h + r) * kernel_w + s, p * ow + q] =
+ * x[n, c, p * stride_h - pad_h + r * dil_h, q * stride_w - pad_w + s * dil_w],
+ * zero outside the image, with oh = (H + 2 pad_h - dil_h (kernel_h - 1) - 1)
+ * / stride_h + 1 (ow alike).  x and out are described by their 4 and 3
+ * element strides.  Any dtype (pure data movement, bit-exact).  kernel,
+ * dilation and stride >= 1, padding >= 0, and an output size of at least
+ * one, else NTOPS_ERR_INVALID. */
+NTOPS_API int ntops_im2col(int dtype, int64_t N, int64_t C, int64_t H, int64_t W,
+               int64_t kernel_h, int64_t kernel_w, int64_t dil_h, int64_t dil_w,
+               int64_t pad_h, int64_t pad_w, int64_t stride_h, int64_t stride_w,
+               const void* x, const int64_t* x_strides,
+               void* out, const int64_t* out_strides, void* stream);
 
 /* ntops_conv2d without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops,

@@ -98,6 +98,10 @@ _SIGNATURES = {
         _i,
         [_i] + [_i64] * 15 + [_vp, _c_i64p, _vp, _c_i64p, _vp, _i64, _vp, _c_i64p, _vp],
     ),
+    "ntops_im2col": (
+        _i,
+        [_i] + [_i64] * 12 + [_vp, _c_i64p, _vp, _c_i64p, _vp],
+    ),
     "ntops_gemm": (
         _i,
         [_i, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _d, _vp, _c_i64p, _vp],

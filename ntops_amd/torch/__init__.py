@@ -19,6 +19,7 @@ from ntops_amd.torch.exp import exp
 from ntops_amd.torch.ge import ge
 from ntops_amd.torch.gelu import gelu
 from ntops_amd.torch.gt import gt
+from ntops_amd.torch.im2col import im2col
 from ntops_amd.torch.isinf import isinf
 from ntops_amd.torch.isnan import isnan
 from ntops_amd.torch.layer_norm import layer_norm
@@ -61,6 +62,7 @@ __all__ = [
     "ge",
     "gelu",
     "gt",
+    "im2col",
     "isinf",
     "isnan",
     "layer_norm",

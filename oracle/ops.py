@@ -757,6 +757,35 @@ def conv2d(x, w, dt, bias=None, stride=(1, 1), pad=(0, 0), dilation=(1, 1), out_
     return round_to(out.astype(np.float32) if dt != "f64" else out, dt)
 
 
+def im2col(x, kernel_size, dilation=(1, 1), padding=(0, 0), stride=(1, 1)):
+    """kernels/im2col.py:10-80 (the input padded by `padding` on both sides
+    of each spatial axis, tiled into kernel_size windows with the given
+    strides and dilation in floor mode, each window's (c, r, s) elements
+    laid out along the output's middle axis) with the output size of
+    torch/im2col.py:28-31:
+
+        out[n, (c * kh + r) * kw + s, p * ow + q]
+            = xpad[n, c, p * sh + r * dh, q * sw + s * dw]
+
+    where xpad is x with ph zero rows above and below and pw zero columns left
+    and right.  Pure data movement: any dtype, bf16 as its uint16 bits."""
+    x = np.asarray(x)
+    N, C, H, W = x.shape
+    kh, kw = kernel_size
+    dh, dw = dilation
+    ph, pw = padding
+    sh, sw = stride
+    oh = (H + 2 * ph - dh * (kh - 1) - 1) // sh + 1
+    ow = (W + 2 * pw - dw * (kw - 1) - 1) // sw + 1
+    xp = np.zeros((N, C, H + 2 * ph, W + 2 * pw), dtype=x.dtype)
+    xp[:, :, ph:ph + H, pw:pw + W] = x
+    out = np.empty((N, C, kh, kw, oh, ow), dtype=x.dtype)
+    for r in range(kh):
+        for s in range(kw):
+            out[:, :, r, s] = xp[:, :, r * dh: r * dh + sh * (oh - 1) + 1: sh, s * dw: s * dw + sw * (ow - 1) + 1: sw]
+    return out.reshape(N, C * kh * kw, oh * ow)
+
+
 def add_rms_norm(x, residual, dt, cols, weight=None, eps=None, w_dt=None):
     """No ntops counterpart: the composition add (kernels/add.py:10, alpha 1)
     then rms_norm (kernels/rms_norm.py:10-20) that the fused kernel computes in

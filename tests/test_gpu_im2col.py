@@ -1,0 +1,155 @@
+"""GPU parity: im2col through the C ABI against the oracle, bit for bit.
+
+Mirrors the reference's tests/test_im2col.py -- its six (shape, kernel,
+dilation, padding, stride) cases x fp32 / fp16 / bf16 / fp64 / bool / int32 /
+int64 x contiguous and transposed (non-contiguous) input, and the empty
+output shape rejection -- plus int8 / uint8 / int16, the torch CPU golden
+vectors, every kernel variant (LDS-staged and direct planes, vector and
+element stores, 1- to 8-byte elements), 1-element argument iterables, the
+argument checks, and a conv-sized (32, 256, 56, 56) bf16 unfold on sampled
+images."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import ntops_amd
+from ntops_amd import _lib
+from oracle import ops as O
+from tests.helpers import DT_NAME, TORCH_DT, from_np, to_np
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+
+im2col = ntops_amd.torch.im2col
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+REF_CASES = (
+    ((2, 3, 8, 8), (3, 3), 1, 0, 1),
+    ((1, 4, 10, 12), (5, 3), 1, 1, (2, 1)),
+    ((2, 2, 16, 16), (4, 4), 1, 0, (4, 4)),
+    ((3, 6, 7, 9), (3, 2), 1, 0, (1, 1)),
+    ((1, 8, 9, 11), (2, 3), 1, 1, (1, 2)),
+    ((2, 5, 12, 6), (3, 3), 2, (2, 1), (2, 1)),
+)
+DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.float64, torch.bool, torch.int32, torch.int64,
+          torch.int8, torch.uint8, torch.int16)
+
+
+def pair(v):
+    if isinstance(v, int):
+        return (v, v)
+    v = tuple(v)
+    return (v[0], v[0]) if len(v) == 1 else v
+
+
+def make_input(shape, dtype, g):
+    if dtype == torch.bool:
+        return torch.randint(0, 2, shape, generator=g).bool()
+    if dtype.is_floating_point:
+        return torch.randn(shape, generator=g).to(dtype)
+    return torch.randint(-100, 100, shape, generator=g).to(dtype)
+
+
+def expect(x, ks, dil, pad, st):
+    return from_np(O.im2col(to_np(x), pair(ks), pair(dil), pair(pad), pair(st)), DT_NAME[x.dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("noncontiguous", (False, True))
+@pytest.mark.parametrize("shape, ks, dil, pad, st", REF_CASES)
+def test_im2col_reference_grid(shape, ks, dil, pad, st, noncontiguous, dtype):
+    g = torch.Generator().manual_seed(sum(shape))
+    x = make_input(shape, dtype, g)
+    xg = x.cuda()
+    if noncontiguous:  # the reference's transposed input
+        x = x.transpose(2, 3)
+        xg = xg.transpose(2, 3)
+    got = im2col(xg, kernel_size=ks, dilation=dil, padding=pad, stride=st)
+    assert got.dtype == dtype
+    assert torch.equal(got.cpu(), expect(x, ks, dil, pad, st))
+
+
+def test_im2col_golden_vectors():
+    gold = np.load(os.path.join(HERE, "golden", "golden_im2col.npz"))
+    cases = {
+        "k33": ((3, 3), 1, 0, 1), "k53_p1_s21": ((5, 3), 1, 1, (2, 1)), "k44_s44": ((4, 4), 1, 0, (4, 4)),
+        "k32": ((3, 2), 1, 0, (1, 1)), "k23_p1_s12": ((2, 3), 1, 1, (1, 2)),
+        "k33_d2_p21_s21": ((3, 3), 2, (2, 1), (2, 1)), "k11_d3": ((1, 1), 3, 0, 1),
+        "k33_d23_p32": ((3, 3), (2, 3), (3, 2), 1),
+    }
+    for name, (ks, dil, pad, st) in cases.items():
+        for dt in ("f32", "f16", "bf16", "f64", "bool", "i32", "i64"):
+            x = from_np(gold[f"{name}_x_{dt}"], dt).cuda()
+            got = im2col(x, ks, dil, pad, st)
+            assert torch.equal(got.cpu(), from_np(gold[f"{name}_y_{dt}"], dt)), f"{name} {dt}"
+
+
+# (shape, kernel, padding, stride, dtype, expected kernel): planes up to 64
+# KiB are staged in LDS, larger ones gathered from global memory; rows whose
+# length keeps every row start on the run's byte size take vector stores.
+VARIANTS = (
+    ((2, 3, 20, 20), 3, 1, 1, torch.bfloat16, "im2col_lds es2 vec"),        # L = 400
+    ((2, 3, 20, 21), 3, 1, 1, torch.bfloat16, "im2col_lds es2 scalar"),     # L = 420
+    ((2, 3, 20, 20), 3, 1, 1, torch.uint8, "im2col_lds es1 vec"),
+    ((1, 2, 10, 14), 2, 0, 1, torch.int8, "im2col_lds es1 scalar"),       # L = 117
+    ((2, 4, 16, 16), 3, 1, 1, torch.float32, "im2col_lds es4 vec"),
+    ((2, 4, 16, 16), 3, 1, 1, torch.float64, "im2col_lds es8 vec"),
+    ((1, 2, 7, 7), 3, 0, 1, torch.float64, "im2col_lds es8 scalar"),
+    ((1, 2, 130, 130), 3, 1, 1, torch.float32, "im2col_direct es4 vec"),    # 66 KiB plane
+    ((1, 2, 181, 183), 5, 2, 2, torch.bfloat16, "im2col_direct es2 scalar"),
+    ((1, 1, 91, 91), 2, 0, 2, torch.int64, "im2col_direct es8 scalar"),   # L = 2025
+    ((2, 1, 260, 264), 3, 1, 1, torch.uint8, "im2col_direct es1 vec"),
+)
+
+
+@pytest.mark.parametrize("shape, ks, pad, st, dtype, kernel", VARIANTS)
+def test_im2col_kernel_variants(shape, ks, pad, st, dtype, kernel):
+    g = torch.Generator().manual_seed(7)
+    x = make_input(shape, dtype, g)
+    got = im2col(x.cuda(), ks, 1, pad, st)
+    assert _lib.last_kernel() == kernel
+    assert torch.equal(got.cpu(), expect(x, ks, 1, pad, st))
+
+
+def test_im2col_argument_forms_and_checks():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(1, 2, 9, 10, generator=g)
+    xg = x.cuda()
+    got = im2col(xg, (3,), dilation=[2], padding=(1,), stride=[2])
+    assert torch.equal(got.cpu(), expect(x, 3, 2, 1, 2))
+    with pytest.raises(RuntimeError):
+        im2col(torch.randn((1, 1, 2, 2), device="cuda"), kernel_size=(3, 3), padding=0, stride=1)
+    with pytest.raises(RuntimeError):
+        im2col(xg[0], 3)
+    for bad in ({"kernel_size": 0}, {"kernel_size": 3, "dilation": 0}, {"kernel_size": 3, "stride": (1, 0)},
+                {"kernel_size": 3, "padding": -1}):
+        with pytest.raises(RuntimeError):
+            im2col(xg, **bad)
+    with pytest.raises(TypeError):
+        im2col(xg, (3, 3, 3))
+    with pytest.raises(RuntimeError):
+        im2col(x, 3)  # CPU tensor: no fallback
+    empty = im2col(torch.empty(0, 3, 8, 8, device="cuda"), 3)
+    assert empty.shape == (0, 27, 36)
+
+
+def test_im2col_conv_sized():
+    """bf16 (32, 256, 56, 56), 3x3, padding 1 (the conv2d workload's
+    unfold): images 0, 17 and 31 against the oracle bit for bit, and the
+    padding zeros counted over the whole output."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(32, 256, 56, 56, generator=g).bfloat16()
+    got = im2col(x.cuda(), 3, padding=1)
+    assert got.shape == (32, 256 * 9, 3136)
+    for n in (0, 17, 31):
+        assert torch.equal(got[n:n + 1].cpu(), expect(x[n:n + 1], 3, 1, 1, 1)), f"image {n}"
+    # the border taps read padding: per channel, 8 of 9 taps lose one row or
+    # column of 56 pixels (corners two), 4 * 56 + 4 * (2 * 56 - 1) = 668 zeros
+    # (randn inputs are never exactly zero)
+    zeros = (got == 0).sum().item()
+    assert zeros == 32 * 256 * 668
