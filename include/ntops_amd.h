@@ -93,8 +93,9 @@ enum ntops_status {
 NTOPS_API int ntops_abi_version(void);
 /* Message of this thread's most recent failed call ("" if none). */
 NTOPS_API const char* ntops_last_error(void);
-/* Name of the kernel that this thread's most recent GEMM-family call
- * launched (e.g. "gemm_mfma 256x256 s4 A:K B:N even"), "" before the first.
+/* Name of the kernel that this thread's most recent GEMM-family, attention
+ * or im2col call launched (e.g. "gemm_mfma 256x256 s4 A:K B:N even"), ""
+ * before the first.
  * No ntops counterpart (Triton picks its kernel inside ninetoothed.make); it
  * lets callers and tests check which path served a call. */
 NTOPS_API const char* ntops_last_kernel(void);

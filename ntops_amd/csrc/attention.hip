@@ -921,6 +921,8 @@ int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
   // items of equal or unequal length (same-box A/B, non-causal
   // (4, 32, 2048, 128): 903 against 865 TFLOP/s for one workgroup per item)
   const int64_t grid = std::min<int64_t>(total, cu_count_cached());
+  note_kernel("sdpa_flash d%d %s items%lld grid%lld", D, CAUSAL ? (a.causal == 2 ? "causal_lr" : "causal_ul") : "full",
+              static_cast<long long>(total), static_cast<long long>(grid));
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kFaWaves * 64), kLds, st, a, nqb);
   return check_launch("sdpa");
 }
@@ -963,6 +965,7 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
       const int mm = a.mask_dtype < 0 ? 0
                      : (a.ms[2] % 4 == 0 && a.ms[1] % 4 == 0 && a.ms[0] % 4 == 0 && mp % (4 * esz) == 0) ? 1 : 2;
       const dim3 grid(static_cast<unsigned>(total)), block(256);
+      note_kernel("sdpa_fwd d%d mask%d es%d", a.D, mm, esz);
 #define NTOPS_FWD(DD, MM, ES) hipLaunchKernelGGL((k_flash_fwd<T, DD, MM, ES>), grid, block, 0, st, a, nqb, static_cast<int>(total))
 #define NTOPS_FWD_D(DD)                         \
   if (mm == 0) NTOPS_FWD(DD, 0, 1);             \
@@ -984,6 +987,7 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
   }
   const int64_t rows = static_cast<int64_t>(a.B) * a.Hq * a.Sq;
   if (rows > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many rows");
+  note_kernel("sdpa_generic");
   hipLaunchKernelGGL((k_attn_generic<T>), dim3(static_cast<unsigned>(rows)), dim3(64), 0, st, a);
   return check_launch("sdpa");
 }

@@ -207,3 +207,52 @@ def test_sdpa_mask_load_paths(skv, mask_dtype, d):
             mask = torch.where(r > 0.3, torch.randn(shape) * 0.5, torch.tensor(float("-inf"))).to(mask_dtype)
         got = sdpa(q.cuda(), k.cuda(), v.cuda(), attn_mask=mask.cuda())
         assert_close(got, oracle(q, k, v, mask), *TOL[dtype], f"mask {mask_dtype} {tuple(shape)}")
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_sdpa_lower_right_more_queries_than_keys(dtype):
+    """Lower-right causal with Sq - Skv = 400: query row i sees keys
+    j <= i + Skv - Sq, so rows 0..399 see none and give 0 (torch's CPU
+    kernel and the oracle); the flash kernel's first 256-row query block has
+    zero key tiles and the second starts inside the fully masked rows.  The
+    same pattern as an explicit bool mask runs the masked kernel."""
+    from ntops_amd import _lib
+
+    g = torch.Generator().manual_seed(700)
+    b, h, sq, skv, d = 2, 4, 700, 300, 128
+    q, k, v = (torch.randn(b, h, s, d, generator=g).to(dtype) for s in (sq, skv, skv))
+    qg, kg, vg = q.cuda(), k.cuda(), v.cuda()
+    got = sdpa(qg, kg, vg, is_causal=True, causal_variant=CausalVariant.LOWER_RIGHT)
+    assert _lib.last_kernel().startswith("sdpa_flash d128 causal_lr")
+    assert (got[:, :, : sq - skv] == 0).all()
+    assert_close(got, oracle(q, k, v, None, 2), *TOL[dtype], "lower-right, Sq > Skv")
+    m = torch.ones(sq, skv, dtype=torch.bool).tril(skv - sq)
+    got_m = sdpa(qg, kg, vg, attn_mask=m.cuda())
+    assert _lib.last_kernel().startswith("sdpa_fwd d128")
+    assert (got_m[:, :, : sq - skv] == 0).all()
+    assert_close(got_m, oracle(q, k, v, m), *TOL[dtype], "bool mask, fully masked leading rows")
+
+
+def test_sdpa_lower_right_chained_zero_tile_items():
+    """More work items than CUs (3 x 32 heads x 4 query blocks), lower-right
+    causal with Sq - Skv = 512: every head's first two query blocks have no
+    key tile and are chained with blocks that do.  All masked rows are 0;
+    sampled heads (GQA, 4 query heads per key head) match the oracle."""
+    from ntops_amd import _lib
+
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(1024)
+    b, hq, hkv, sq, skv, d = 3, 32, 8, 1024, 512, 128
+    q = torch.randn(b, hq, sq, d, generator=g).to(dtype)
+    k = torch.randn(b, hkv, skv, d, generator=g).to(dtype)
+    v = torch.randn(b, hkv, skv, d, generator=g).to(dtype)
+    got = sdpa(q.cuda(), k.cuda(), v.cuda(), is_causal=True, enable_gqa=True,
+               causal_variant=CausalVariant.LOWER_RIGHT)
+    name = _lib.last_kernel()
+    assert name.startswith("sdpa_flash d128 causal_lr items384 grid")
+    assert int(name.split("grid")[1]) < 384, name
+    assert (got[:, :, : sq - skv] == 0).all()
+    for bi, h0 in ((0, 0), (1, 12), (2, 28)):
+        exp = oracle(q[bi:bi + 1, h0:h0 + 4], k[bi:bi + 1, h0 // 4:h0 // 4 + 1], v[bi:bi + 1, h0 // 4:h0 // 4 + 1],
+                     None, 2)
+        assert_close(got[bi:bi + 1, h0:h0 + 4], exp, *TOL[dtype], f"batch {bi} heads {h0}..{h0 + 3}")
