@@ -299,11 +299,11 @@ def make_workloads():
         return {"x": x, "w": w, "b": b, "y": torch.empty_like(x)}
 
     def rms_step(s):
-        check(lib.ntops_rms_norm(_lib.BF16, R, C, s["x"].data_ptr(), C, s["w"].data_ptr(), _lib.BF16, 1e-6,
+        check(lib.ntops_rms_norm(_lib.BF16, R, C, s["x"].data_ptr(), C, s["w"].data_ptr(), 0, _lib.BF16, 1e-6,
                                  s["y"].data_ptr(), C, stream()), "rms_norm")
 
     def ln_step(s):
-        check(lib.ntops_layer_norm(_lib.BF16, R, C, s["x"].data_ptr(), C, s["w"].data_ptr(), s["b"].data_ptr(),
+        check(lib.ntops_layer_norm(_lib.BF16, R, C, s["x"].data_ptr(), C, s["w"].data_ptr(), s["b"].data_ptr(), 0,
                                    _lib.BF16, 1e-5, s["y"].data_ptr(), C, stream()), "layer_norm")
 
     def norm_cpu_inputs():
@@ -419,7 +419,7 @@ def make_workloads():
 
     def arn_step(s):
         check(lib.ntops_add_rms_norm(_lib.BF16, R, C, s["x"].data_ptr(), C, s["r"].data_ptr(), C, s["w"].data_ptr(),
-                                     _lib.BF16, 1e-6, s["y"].data_ptr(), C, s["ro"].data_ptr(), C, stream()),
+                                     0, _lib.BF16, 1e-6, s["y"].data_ptr(), C, s["ro"].data_ptr(), C, stream()),
               "add_rms_norm")
 
     def arn_cpu():

@@ -203,20 +203,25 @@ NTOPS_API int ntops_cast(int src_dtype, int dst_dtype, int ndim, const int64_t* 
                void* y, const int64_t* y_strides, void* stream);
 
 /* ---- row reductions --------------------------------------------------- */
-/* y[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * w   (fp32 accumulate,
- * one rounding to dtype).  x and y are rows x cols with unit column stride
- * and the given row strides; w (may be NULL = ones) is cols contiguous
- * elements of w_dtype, which is dtype or F32.  dtype in {F32, F16, BF16}. */
+/* y[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * w[r, :]   (fp32
+ * accumulate, one rounding to dtype).  x and y are rows x cols with unit
+ * column stride and the given row strides; w (may be NULL = ones) holds rows
+ * of cols contiguous elements of w_dtype (dtype or F32) w_row_stride apart --
+ * 0 for one weight row shared by every row (the usual case; a non-zero
+ * stride, a weight that differs per row, runs a slower looped kernel).
+ * dtype in {F32, F16, BF16}. */
 NTOPS_API int ntops_rms_norm(int dtype, int64_t rows, int64_t cols,
                    const void* x, int64_t x_row_stride,
-                   const void* w, int w_dtype, double eps,
+                   const void* w, int64_t w_row_stride, int w_dtype, double eps,
                    void* y, int64_t y_row_stride, void* stream);
 
-/* y[r, :] = (x - mean) * rsqrt(var + eps) * w + b, biased variance, fp32
- * moments.  w and b may each be NULL (ones / zeros). */
+/* y[r, :] = (x - mean) * rsqrt(var + eps) * w[r, :] + b[r, :], biased
+ * variance, fp32 moments.  w and b may each be NULL (ones / zeros); both
+ * have rows wb_row_stride apart, 0 when shared by every row (as for
+ * ntops_rms_norm). */
 NTOPS_API int ntops_layer_norm(int dtype, int64_t rows, int64_t cols,
                      const void* x, int64_t x_row_stride,
-                     const void* w, const void* b, int wb_dtype, double eps,
+                     const void* w, const void* b, int64_t wb_row_stride, int wb_dtype, double eps,
                      void* y, int64_t y_row_stride, void* stream);
 
 /* Softmax over the middle axis of an (outer, dim_size, inner) view.
@@ -288,7 +293,7 @@ NTOPS_API int ntops_sdpa(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t 
 NTOPS_API int ntops_add_rms_norm(int dtype, int64_t rows, int64_t cols,
                const void* x, int64_t x_row_stride,
                const void* residual, int64_t residual_row_stride,
-               const void* w, int w_dtype, double eps,
+               const void* w, int64_t w_row_stride, int w_dtype, double eps,
                void* y, int64_t y_row_stride,
                void* residual_out, int64_t residual_out_row_stride, void* stream);
 

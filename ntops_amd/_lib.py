@@ -65,8 +65,8 @@ _SIGNATURES = {
          _vp, _c_i64p, _vp],
     ),
     "ntops_cast": (_i, [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp]),
-    "ntops_rms_norm": (_i, [_i, _i64, _i64, _vp, _i64, _vp, _i, _d, _vp, _i64, _vp]),
-    "ntops_layer_norm": (_i, [_i, _i64, _i64, _vp, _i64, _vp, _vp, _i, _d, _vp, _i64, _vp]),
+    "ntops_rms_norm": (_i, [_i, _i64, _i64, _vp, _i64, _vp, _i64, _i, _d, _vp, _i64, _vp]),
+    "ntops_layer_norm": (_i, [_i, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i, _d, _vp, _i64, _vp]),
     "ntops_softmax": (_i, [_i, _i, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp]),
     "ntops_rope": (
         _i,
@@ -79,7 +79,7 @@ _SIGNATURES = {
     ),
     "ntops_add_rms_norm": (
         _i,
-        [_i, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i, _d, _vp, _i64, _vp, _i64, _vp],
+        [_i, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i, _d, _vp, _i64, _vp, _i64, _vp],
     ),
     "ntops_rope_qk": (
         _i,

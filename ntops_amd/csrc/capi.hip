@@ -47,7 +47,7 @@ int cu_count_cached() {
 
 }  // namespace ntops
 
-extern "C" int ntops_abi_version(void) { return 1; }
+extern "C" int ntops_abi_version(void) { return 2; }
 
 extern "C" const char* ntops_last_error(void) { return ntops::g_last_error; }
 

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_vec(
 }
 
 template <typename T, typename W>
-__global__ __launch_bounds__(256) void k_rms_loop(const T* x, int64_t xs, const W* w, T* y,
+__global__ __launch_bounds__(256) void k_rms_loop(const T* x, int64_t xs, const W* w, int64_t wrs, T* y,
                                                    int64_t ys, int64_t cols, float eps) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
@@ -90,8 +90,9 @@ __global__ __launch_bounds__(256) void k_rms_loop(const T* x, int64_t xs, const 
   ss = block_sum256(ss, red);
   const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
   T* yr = y + row * ys;
+  const W* wr = w != nullptr ? w + row * wrs : nullptr;
   for (int64_t j = threadIdx.x; j < cols; j += 256) {
-    const float wv = w != nullptr ? static_cast<float>(w[j]) : 1.0f;
+    const float wv = wr != nullptr ? static_cast<float>(wr[j]) : 1.0f;
     yr[j] = static_cast<T>(mul_nc(mul_nc(to_f(xr[j]), rstd), wv));
   }
 }
@@ -168,8 +169,8 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
 
 template <typename T, typename W>
 __global__ __launch_bounds__(256) void k_add_rms_loop(const T* x, int64_t xs, const T* res, int64_t rs,
-                                                       const W* w, T* y, int64_t ys, T* ro, int64_t ros,
-                                                       int64_t cols, float eps) {
+                                                       const W* w, int64_t wrs, T* y, int64_t ys, T* ro,
+                                                       int64_t ros, int64_t cols, float eps) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   float ss = 0.f;
@@ -181,8 +182,9 @@ __global__ __launch_bounds__(256) void k_add_rms_loop(const T* x, int64_t xs, co
   }
   ss = block_sum256(ss, red);
   const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+  const W* wr = w != nullptr ? w + row * wrs : nullptr;
   for (int64_t j = threadIdx.x; j < cols; j += 256) {
-    const float wv = w != nullptr ? static_cast<float>(w[j]) : 1.0f;
+    const float wv = wr != nullptr ? static_cast<float>(wr[j]) : 1.0f;
     y[row * ys + j] = static_cast<T>(mul_nc(mul_nc(to_f(ro[row * ros + j]), rstd), wv));
   }
 }
@@ -255,7 +257,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_ln_vec(
 }
 
 template <typename T, typename W>
-__global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W* w, const W* b,
+__global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W* w, const W* b, int64_t wrs,
                                                   T* y, int64_t ys, int64_t cols, float eps) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
@@ -272,9 +274,11 @@ __global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W
   const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
   const float shift = -rstd * mean;
   T* yr = y + row * ys;
+  const W* wr = w != nullptr ? w + row * wrs : nullptr;
+  const W* br = b != nullptr ? b + row * wrs : nullptr;
   for (int64_t j = threadIdx.x; j < cols; j += 256) {
-    const float wv = w != nullptr ? static_cast<float>(w[j]) : 1.0f;
-    const float bv = b != nullptr ? static_cast<float>(b[j]) : 0.0f;
+    const float wv = wr != nullptr ? static_cast<float>(wr[j]) : 1.0f;
+    const float bv = br != nullptr ? static_cast<float>(br[j]) : 0.0f;
     const float n = add_nc(mul_nc(to_f(xr[j]), rstd), shift);
     yr[j] = static_cast<T>(add_nc(mul_nc(n, wv), bv));
   }
@@ -282,15 +286,16 @@ __global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W
 
 // -------------------------------------------------------------- dispatch --
 template <typename T, typename W>
-int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* wv, double eps,
+int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* wv, int64_t wrs, double eps,
             void* yv, int64_t ys, hipStream_t st) {
   const T* x = static_cast<const T*>(xv);
   const W* w = static_cast<const W*>(wv);
   T* y = static_cast<T*>(yv);
   constexpr int V = Pack16<T>::N;
   VecCfg cfg;
+  // a weight that differs per row (wrs != 0) takes the looped kernel
   const bool vec = (cols % V == 0) && (xs % V == 0) && (ys % V == 0) && aligned16(x) &&
-                   aligned16(y) && (w == nullptr || aligned16(w)) && pick_row_cfg(cols / V, &cfg);
+                   aligned16(y) && (w == nullptr || (aligned16(w) && wrs == 0)) && pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
   if (vec) {
 #define NTOPS_RMS_CASE(CH, WP)                                                                    \
@@ -303,13 +308,13 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
     NTOPS_ROW_CASES(NTOPS_RMS_CASE)
 #undef NTOPS_RMS_CASE
   }
-  hipLaunchKernelGGL((k_rms_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, y, ys, cols, feps);
+  hipLaunchKernelGGL((k_rms_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, wrs, y, ys, cols, feps);
   return check_launch("rms_norm");
 }
 
 template <typename T, typename W>
 int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* wv,
-           const void* bv, double eps, void* yv, int64_t ys, hipStream_t st) {
+           const void* bv, int64_t wrs, double eps, void* yv, int64_t ys, hipStream_t st) {
   const T* x = static_cast<const T*>(xv);
   const W* w = static_cast<const W*>(wv);
   const W* b = static_cast<const W*>(bv);
@@ -318,7 +323,8 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
   VecCfg cfg;
   const bool vec = (cols % V == 0) && (xs % V == 0) && (ys % V == 0) && aligned16(x) &&
                    aligned16(y) && (w == nullptr || aligned16(w)) &&
-                   (b == nullptr || aligned16(b)) && pick_row_cfg(cols / V, &cfg);
+                   (b == nullptr || aligned16(b)) && (wrs == 0 || (w == nullptr && b == nullptr)) &&
+                   pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
   if (vec) {
 #define NTOPS_LN_CASE(CH, WP)                                                                     \
@@ -331,14 +337,15 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
     NTOPS_ROW_CASES(NTOPS_LN_CASE)
 #undef NTOPS_LN_CASE
   }
-  hipLaunchKernelGGL((k_ln_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, b, y, ys, cols,
+  hipLaunchKernelGGL((k_ln_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, b, wrs, y, ys, cols,
                      feps);
   return check_launch("layer_norm");
 }
 
 template <typename T, typename W>
 int run_add_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* rv, int64_t rs,
-                const void* wv, double eps, void* yv, int64_t ys, void* rov, int64_t ros, hipStream_t st) {
+                const void* wv, int64_t wrs, double eps, void* yv, int64_t ys, void* rov, int64_t ros,
+                hipStream_t st) {
   const T* x = static_cast<const T*>(xv);
   const T* r = static_cast<const T*>(rv);
   const W* w = static_cast<const W*>(wv);
@@ -347,8 +354,8 @@ int run_add_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const vo
   constexpr int V = Pack16<T>::N;
   VecCfg cfg;
   const bool vec = (cols % V == 0) && (xs % V == 0) && (rs % V == 0) && (ys % V == 0) && (ros % V == 0) &&
-                   aligned16(x) && aligned16(r) && aligned16(y) && aligned16(ro) && (w == nullptr || aligned16(w)) &&
-                   pick_row_cfg(cols / V, &cfg);
+                   aligned16(x) && aligned16(r) && aligned16(y) && aligned16(ro) &&
+                   (w == nullptr || (aligned16(w) && wrs == 0)) && pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
   if (vec) {
 #define NTOPS_ADD_RMS_CASE(CH, WP)                                                                \
@@ -361,8 +368,8 @@ int run_add_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const vo
     NTOPS_ROW_CASES(NTOPS_ADD_RMS_CASE)
 #undef NTOPS_ADD_RMS_CASE
   }
-  hipLaunchKernelGGL((k_add_rms_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, r, rs, w, y, ys, ro, ros, cols,
-                     feps);
+  hipLaunchKernelGGL((k_add_rms_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, r, rs, w, wrs, y, ys, ro, ros,
+                     cols, feps);
   return check_launch("add_rms_norm");
 }
 
@@ -380,8 +387,8 @@ int check_rows(const char* what, int64_t rows, int64_t cols, const void* x, cons
 using namespace ntops;
 
 extern "C" int ntops_rms_norm(int dtype, int64_t rows, int64_t cols, const void* x,
-                              int64_t x_row_stride, const void* w, int w_dtype, double eps,
-                              void* y, int64_t y_row_stride, void* stream) {
+                              int64_t x_row_stride, const void* w, int64_t w_row_stride, int w_dtype,
+                              double eps, void* y, int64_t y_row_stride, void* stream) {
   if (int e = check_rows("rms_norm", rows, cols, x, y)) return e;
   if (rows == 0 || cols == 0) return NTOPS_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -390,14 +397,14 @@ extern "C" int ntops_rms_norm(int dtype, int64_t rows, int64_t cols, const void*
   return dispatch_float16_32(dtype, "rms_norm", [&](auto tag) {
     using T = decltype(tag);
     if (w != nullptr && w_dtype == NTOPS_F32 && dtype != NTOPS_F32)
-      return run_rms<T, float>(rows, cols, x, x_row_stride, w, eps, y, y_row_stride, st);
-    return run_rms<T, T>(rows, cols, x, x_row_stride, w, eps, y, y_row_stride, st);
+      return run_rms<T, float>(rows, cols, x, x_row_stride, w, w_row_stride, eps, y, y_row_stride, st);
+    return run_rms<T, T>(rows, cols, x, x_row_stride, w, w_row_stride, eps, y, y_row_stride, st);
   });
 }
 
 extern "C" int ntops_layer_norm(int dtype, int64_t rows, int64_t cols, const void* x,
-                                int64_t x_row_stride, const void* w, const void* b, int wb_dtype,
-                                double eps, void* y, int64_t y_row_stride, void* stream) {
+                                int64_t x_row_stride, const void* w, const void* b, int64_t wb_row_stride,
+                                int wb_dtype, double eps, void* y, int64_t y_row_stride, void* stream) {
   if (int e = check_rows("layer_norm", rows, cols, x, y)) return e;
   if (rows == 0 || cols == 0) return NTOPS_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -407,14 +414,15 @@ extern "C" int ntops_layer_norm(int dtype, int64_t rows, int64_t cols, const voi
   return dispatch_float16_32(dtype, "layer_norm", [&](auto tag) {
     using T = decltype(tag);
     if ((w != nullptr || b != nullptr) && wb_dtype == NTOPS_F32 && dtype != NTOPS_F32)
-      return run_ln<T, float>(rows, cols, x, x_row_stride, w, b, eps, y, y_row_stride, st);
-    return run_ln<T, T>(rows, cols, x, x_row_stride, w, b, eps, y, y_row_stride, st);
+      return run_ln<T, float>(rows, cols, x, x_row_stride, w, b, wb_row_stride, eps, y, y_row_stride, st);
+    return run_ln<T, T>(rows, cols, x, x_row_stride, w, b, wb_row_stride, eps, y, y_row_stride, st);
   });
 }
 
 extern "C" int ntops_add_rms_norm(int dtype, int64_t rows, int64_t cols, const void* x, int64_t x_row_stride,
-                                  const void* residual, int64_t residual_row_stride, const void* w, int w_dtype,
-                                  double eps, void* y, int64_t y_row_stride, void* residual_out,
+                                  const void* residual, int64_t residual_row_stride, const void* w,
+                                  int64_t w_row_stride, int w_dtype, double eps, void* y, int64_t y_row_stride,
+                                  void* residual_out,
                                   int64_t residual_out_row_stride, void* stream) {
   if (int e = check_rows("add_rms_norm", rows, cols, x, y)) return e;
   if (rows == 0 || cols == 0) return NTOPS_OK;
@@ -426,9 +434,9 @@ extern "C" int ntops_add_rms_norm(int dtype, int64_t rows, int64_t cols, const v
   return dispatch_float16_32(dtype, "add_rms_norm", [&](auto tag) {
     using T = decltype(tag);
     if (w != nullptr && w_dtype == NTOPS_F32 && dtype != NTOPS_F32)
-      return run_add_rms<T, float>(rows, cols, x, x_row_stride, residual, residual_row_stride, w, eps, y,
-                                   y_row_stride, residual_out, residual_out_row_stride, st);
-    return run_add_rms<T, T>(rows, cols, x, x_row_stride, residual, residual_row_stride, w, eps, y, y_row_stride,
-                             residual_out, residual_out_row_stride, st);
+      return run_add_rms<T, float>(rows, cols, x, x_row_stride, residual, residual_row_stride, w, w_row_stride,
+                                   eps, y, y_row_stride, residual_out, residual_out_row_stride, st);
+    return run_add_rms<T, T>(rows, cols, x, x_row_stride, residual, residual_row_stride, w, w_row_stride, eps, y,
+                             y_row_stride, residual_out, residual_out_row_stride, st);
   });
 }

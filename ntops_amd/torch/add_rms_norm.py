@@ -15,7 +15,7 @@ import math
 import torch
 
 from ntops_amd import _lib
-from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _to_dtype
+from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _norm_param
 
 
 def add_rms_norm(input, residual, normalized_shape, weight=None, eps=None, *, inplace=False):
@@ -46,19 +46,17 @@ def add_rms_norm(input, residual, normalized_shape, weight=None, eps=None, *, in
         x, res = _contiguous(input), _contiguous(residual)
         output, new_residual = torch.empty_like(x), torch.empty_like(x)
 
-    w_ptr, w_code = None, _lib.dtype_code(input.dtype)
+    w_ptr, w_rs, w_code = None, 0, _lib.dtype_code(input.dtype)
     if weight is not None:
-        if tuple(weight.shape) != normalized_shape:
-            raise RuntimeError("add_rms_norm: weight shape must equal normalized_shape")
-        if weight.dtype not in (input.dtype, torch.float32):
-            weight = _to_dtype(weight, input.dtype)
-        weight = _contiguous(weight)
-        w_ptr, w_code = weight.data_ptr(), _lib.dtype_code(weight.dtype)
+        w_dtype = weight.dtype if weight.dtype in (input.dtype, torch.float32) else input.dtype
+        weight, w_rs = _norm_param(weight, input, len(normalized_shape), w_dtype)
+        if weight is not None:
+            w_ptr, w_code = weight.data_ptr(), _lib.dtype_code(w_dtype)
 
     lib = _lib.load()
     with _DeviceGuard(dev):
         rc = lib.ntops_add_rms_norm(
-            _lib.dtype_code(input.dtype), rows, cols, x.data_ptr(), cols, res.data_ptr(), cols, w_ptr, w_code,
+            _lib.dtype_code(input.dtype), rows, cols, x.data_ptr(), cols, res.data_ptr(), cols, w_ptr, w_rs, w_code,
             float(eps), output.data_ptr(), cols, new_residual.data_ptr(), cols, _lib.stream_of(output))
     _lib.check(rc, "ntops_amd.add_rms_norm")
     return output, new_residual

@@ -6,7 +6,7 @@ import math
 import torch
 
 from ntops_amd import _lib
-from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _to_dtype
+from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _norm_param
 
 
 def layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
@@ -28,18 +28,19 @@ def layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
     x = _contiguous(input)
     output = torch.empty_like(x)
 
-    # weight and bias share one dtype: the input's, or fp32 for both.
+    # weight and bias share one dtype (the input's, or fp32 for both) and
+    # one row stride: each is expanded like the reference's
+    # `expand_as(input)`; if either differs per row, both are laid out per row.
     params = [p for p in (weight, bias) if p is not None]
-    for p in params:
-        if tuple(p.shape) != normalized_shape:
-            raise RuntimeError("layer_norm: weight/bias shape must equal normalized_shape")
     wb_dtype = input.dtype
     if params and all(p.dtype == torch.float32 for p in params):
         wb_dtype = torch.float32
-    if weight is not None:
-        weight = _contiguous(_to_dtype(weight, wb_dtype))
-    if bias is not None:
-        bias = _contiguous(_to_dtype(bias, wb_dtype))
+    laid = [_norm_param(p, input, nd, wb_dtype) if p is not None else (None, 0) for p in (weight, bias)]
+    wb_rs = max(rs for _, rs in laid)
+    if wb_rs:
+        laid = [_norm_param(p, input, nd, wb_dtype, per_row=True) if p is not None else (None, 0)
+                for p in (weight, bias)]
+    (weight, _), (bias, _) = laid
 
     lib = _lib.load()
     with _DeviceGuard(dev):
@@ -51,6 +52,7 @@ def layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
             cols,
             weight.data_ptr() if weight is not None else None,
             bias.data_ptr() if bias is not None else None,
+            wb_rs,
             _lib.dtype_code(wb_dtype),
             float(eps),
             output.data_ptr(),

@@ -1,17 +1,20 @@
 """rms_norm -- mirror of src/ntops/torch/rms_norm.py:9-31
 (math: kernels/rms_norm.py:10-20).
 
-Semantic deltas from ntops, following torch (the parity reference):
-`eps=None` uses torch.finfo(torch.float32).eps (what torch 2.10's fused CPU
-kernel uses for fp32/fp16/bf16 inputs), and the weight is applied in fp32
-before the single rounding of each output element."""
+The weight is expanded like the reference's `weight.expand_as(input)`: any
+shape that broadcasts to the input is accepted.  Semantic deltas from ntops,
+following torch (the parity reference the reference's own test compares
+against): `eps=None` uses torch.finfo(torch.float32).eps (what torch 2.10's
+fused CPU kernel uses for fp32/fp16/bf16 inputs; ntops takes the input
+dtype's eps, 7.8e-3 for bf16), and the weight is applied in fp32 before the
+single rounding of each output element."""
 
 import math
 
 import torch
 
 from ntops_amd import _lib
-from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _to_dtype
+from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _norm_param
 
 
 def rms_norm(input, normalized_shape, weight=None, eps=None):
@@ -36,14 +39,12 @@ def rms_norm(input, normalized_shape, weight=None, eps=None):
     x = _contiguous(input)
     output = torch.empty_like(x)
 
-    w_ptr, w_code = None, _lib.dtype_code(input.dtype)
+    w_ptr, w_rs, w_code = None, 0, _lib.dtype_code(input.dtype)
     if weight is not None:
-        if tuple(weight.shape) != normalized_shape:
-            raise RuntimeError("rms_norm: weight shape must equal normalized_shape")
-        if weight.dtype not in (input.dtype, torch.float32):
-            weight = _to_dtype(weight, input.dtype)
-        weight = _contiguous(weight)
-        w_ptr, w_code = weight.data_ptr(), _lib.dtype_code(weight.dtype)
+        w_dtype = weight.dtype if weight.dtype in (input.dtype, torch.float32) else input.dtype
+        weight, w_rs = _norm_param(weight, input, nd, w_dtype)
+        if weight is not None:
+            w_ptr, w_code = weight.data_ptr(), _lib.dtype_code(w_dtype)
 
     lib = _lib.load()
     with _DeviceGuard(dev):
@@ -54,6 +55,7 @@ def rms_norm(input, normalized_shape, weight=None, eps=None):
             x.data_ptr(),
             cols,
             w_ptr,
+            w_rs,
             w_code,
             float(eps),
             output.data_ptr(),

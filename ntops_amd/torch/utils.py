@@ -120,6 +120,29 @@ def _contiguous(t):
     return _cast_into(t, out)
 
 
+def _norm_param(param, input, nd, dtype, per_row=False):
+    """A norm's weight or bias as the reference passes it to its kernel,
+    `param.expand_as(input)` (src/ntops/torch/rms_norm.py:17-18,
+    layer_norm.py:17-25; a shape that does not broadcast raises there too),
+    cast to `dtype` by the native kernel and laid out for the C ABI: one
+    contiguous row of the normalized elements and row stride 0 when every
+    row of the expanded parameter is the same (the usual case, incl.
+    broadcasting inside the normalized dims), else a contiguous copy of all
+    rows and row stride cols (always so with per_row).  Returns (tensor,
+    row_stride); (None, 0) for an empty input."""
+    pe = param.expand_as(input)
+    if input.numel() == 0:
+        return None, 0
+    lead = input.dim() - nd
+    if not per_row and all(pe.shape[i] == 1 or pe.stride(i) == 0 for i in range(lead)):
+        row = pe[(0,) * lead] if lead else pe
+        return _contiguous(_to_dtype(row, dtype)), 0
+    cols = 1
+    for n in input.shape[lead:]:
+        cols *= n
+    return _contiguous(_to_dtype(pe, dtype)), cols
+
+
 def _prepare_out(out, shape, dtype, device, like=None):
     """Output tensor for an elementwise result.
 

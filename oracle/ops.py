@@ -544,8 +544,15 @@ def rms_norm(x, dt, cols, weight=None, eps=None, w_dt=None):
     rstd = np.float32(1) / np.sqrt(ss / np.float32(cols) + np.float32(eps))
     y = xf * rstd[:, None]
     if weight is not None:
-        y = y * to_compute(weight, w_dt or dt).reshape(1, cols).astype(np.float32)
+        y = y * _expanded_rows(weight, w_dt or dt, shape, cols)
     return round_to(y, dt).reshape(shape)
+
+
+def _expanded_rows(param, dt, shape, cols):
+    """A norm parameter as the reference's `param.expand_as(input)`
+    (torch/rms_norm.py:17-18, torch/layer_norm.py:17-25): broadcast to the
+    input's shape, as fp32 rows of the normalized elements."""
+    return np.broadcast_to(to_compute(param, dt).astype(np.float32), shape).reshape(-1, cols)
 
 
 @_with_errstate
@@ -561,9 +568,9 @@ def layer_norm(x, dt, cols, weight=None, bias=None, eps=1e-5, wb_dt=None):
     rstd = np.float32(1) / np.sqrt(np.maximum(var, np.float32(0)) + np.float32(eps))
     y = xf * rstd[:, None] + (-rstd * mean)[:, None]
     if weight is not None:
-        y = y * to_compute(weight, wb_dt or dt).reshape(1, cols).astype(np.float32)
+        y = y * _expanded_rows(weight, wb_dt or dt, shape, cols)
     if bias is not None:
-        y = y + to_compute(bias, wb_dt or dt).reshape(1, cols).astype(np.float32)
+        y = y + _expanded_rows(bias, wb_dt or dt, shape, cols)
     return round_to(y, dt).reshape(shape)
 
 

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().ntops_abi_version() == 1
+    assert _lib.load().ntops_abi_version() == 2
 
 
 def _err(lib):
@@ -69,7 +69,7 @@ def test_empty_tensors_launch_nothing():
     st = _arr(5, 1)
     # numel == 0 returns before any HIP call, so this is safe without a GPU
     assert lib.ntops_unary(_lib.UNARY_EXP, _lib.F32, 2, shape, ctypes.c_void_p(16), st, ctypes.c_void_p(16), st, None) == 0
-    assert lib.ntops_rms_norm(_lib.BF16, 0, 4096, None, 4096, None, _lib.BF16, 1e-6, None, 4096, None) == 0
+    assert lib.ntops_rms_norm(_lib.BF16, 0, 4096, None, 4096, None, 0, _lib.BF16, 1e-6, None, 4096, None) == 0
     assert lib.ntops_softmax(_lib.F32, _lib.F32, 0, 3, 1, None, st, None, st, None) == 0
     assert lib.ntops_gemm(_lib.BF16, 1, 0, 4, 4, None, _arr(0, 4, 1), None, _arr(0, 4, 1), None, None, 1.0, 0.0, None, _arr(0, 4, 1), None) == 0
 
@@ -88,10 +88,10 @@ def test_more_than_max_dims_rejected():
 def test_rows_and_rope_and_gemm_validation():
     lib = _lib.load()
     p = ctypes.c_void_p(256)
-    assert lib.ntops_rms_norm(_lib.BF16, -1, 8, p, 8, None, _lib.BF16, 1e-6, p, 8, None) == 1
-    assert lib.ntops_rms_norm(_lib.BF16, 2, 8, p, 8, p, _lib.F16, 1e-6, p, 8, None) == 2
+    assert lib.ntops_rms_norm(_lib.BF16, -1, 8, p, 8, None, 0, _lib.BF16, 1e-6, p, 8, None) == 1
+    assert lib.ntops_rms_norm(_lib.BF16, 2, 8, p, 8, p, 0, _lib.F16, 1e-6, p, 8, None) == 2
     assert "weight dtype" in _err(lib)
-    assert lib.ntops_layer_norm(_lib.F64, 2, 8, p, 8, None, None, _lib.F64, 1e-5, p, 8, None) == 2
+    assert lib.ntops_layer_norm(_lib.F64, 2, 8, p, 8, None, None, 0, _lib.F64, 1e-5, p, 8, None) == 2
     st4 = _arr(8, 8, 8, 1)
     assert lib.ntops_rope(_lib.BF16, 1, 1, 1, 7, p, st4, p, p, 7, 7, 0, p, st4, None) == 1
     assert "even" in _err(lib)

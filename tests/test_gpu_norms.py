@@ -128,6 +128,49 @@ def test_norm_noncontiguous_input_and_fp32_weight():
     assert_close(got, exp, 1.6e-2, 1.6e-2, "ln fp32 weight")
 
 
+# (weight shape, normalized_shape) over a (4, 6, 64) input: the reference
+# expands the weight with `weight.expand_as(input)`, so any broadcastable
+# shape is legal -- shared rows (incl. broadcast inside a 2-D normalized
+# shape) take the vector kernels, weights that differ per row the looped ones.
+WEIGHT_FORMS = (
+    ((64,), (64,)),
+    ((1, 1, 64), (64,)),
+    ((64,), (6, 64)),
+    ((6, 1), (64,)),
+    ((1, 6, 64), (64,)),
+    ((4, 6, 64), (64,)),
+)
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float32))
+@pytest.mark.parametrize("w_shape, nshape", WEIGHT_FORMS)
+def test_norm_weight_broadcast_forms(w_shape, nshape, dtype):
+    dt = DT_NAME[dtype]
+    g = torch.Generator().manual_seed(len(w_shape) * 10 + len(nshape))
+    x = torch.randn(4, 6, 64, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(w_shape, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(w_shape, generator=g)).to(dtype)
+    cols = int(np.prod(nshape))
+    rtol, atol = TOL_REDUCTION[dt]
+    got = ntops_amd.torch.rms_norm(x.cuda(), nshape, w.cuda(), 1e-6)
+    assert_close(got, from_np(O.rms_norm(to_np(x), dt, cols, to_np(w), 1e-6), dt), rtol, atol, f"rms {w_shape}")
+    got = ntops_amd.torch.layer_norm(x.cuda(), nshape, w.cuda(), b.cuda(), 1e-5)
+    assert_close(got, from_np(O.layer_norm(to_np(x), dt, cols, to_np(w), to_np(b), 1e-5), dt), rtol, atol,
+                 f"ln {w_shape}")
+    # mixed: a shared weight with a bias that differs per row (both laid out per row)
+    b_rows = (0.1 * torch.randn(4, 6, 1, generator=g)).to(dtype)
+    got = ntops_amd.torch.layer_norm(x.cuda(), nshape, w.cuda(), b_rows.cuda(), 1e-5)
+    assert_close(got, from_np(O.layer_norm(to_np(x), dt, cols, to_np(w), to_np(b_rows), 1e-5), dt), rtol, atol,
+                 f"ln {w_shape} + per-row bias")
+    r = torch.randn(4, 6, 64, generator=g).to(dtype)
+    y, h = ntops_amd.torch.add_rms_norm(x.cuda(), r.cuda(), nshape, w.cuda(), 1e-6)
+    ey, eh = O.add_rms_norm(to_np(x), to_np(r), dt, cols, to_np(w), 1e-6)
+    assert torch.equal(h.cpu(), from_np(eh, dt))
+    assert_close(y, from_np(ey, dt), rtol, atol, f"add_rms {w_shape}")
+    with pytest.raises(RuntimeError):
+        ntops_amd.torch.rms_norm(x.cuda(), nshape, torch.ones(5, device="cuda", dtype=dtype))
+
+
 def _config_inputs():
     g = torch.Generator().manual_seed(0)
     x = torch.randn(16384, 4096, generator=g).bfloat16()

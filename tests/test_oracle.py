@@ -380,3 +380,37 @@ def _mutant_add_alpha_on_a(a, b, dt, alpha=1):
 )
 def test_planted_mistakes_are_caught(name, mutant):
     assert not PINS[name](mutant), f"a planted mistake in {name} went unnoticed"
+
+
+@pytest.mark.parametrize("dt", ("f32", "bf16"))
+def test_norm_params_expand_like_the_reference(dt):
+    """Weights / biases broadcast against the input (the reference's
+    `expand_as(input)`): each row must equal the one-row computation (pinned
+    by the golden vectors above) with that row of the expanded parameter --
+    a per-row weight, a (6, 1) weight constant along the row, and a (32,)
+    weight broadcast inside a 2-D normalized shape."""
+    rng = np.random.default_rng(11)
+
+    def arr(*shape, scale=1.0, shift=0.0):
+        return O.round_to(rng.standard_normal(shape).astype(np.float32) * scale + shift, dt)
+
+    x = arr(4, 6, 32)
+    cases = (arr(4, 6, 32, scale=0.1, shift=1.0), arr(6, 1, scale=0.1, shift=1.0), arr(1, 6, 32, scale=0.1))
+    for w in cases:
+        wf = np.broadcast_to(O.to_compute(w, dt), x.shape)
+        got = O.rms_norm(x, dt, 32, w, 1e-6).reshape(24, 32)
+        b = arr(6, 1, scale=0.1)
+        got_ln = O.layer_norm(x, dt, 32, w, b, 1e-5).reshape(24, 32)
+        bf = np.broadcast_to(O.to_compute(b, dt), x.shape)
+        for i in range(4):
+            for j in range(6):
+                wr = O.round_to(wf[i, j], dt)
+                np.testing.assert_array_equal(got[6 * i + j], O.rms_norm(x[i, j][None], dt, 32, wr, 1e-6)[0])
+                br = O.round_to(bf[i, j], dt)
+                np.testing.assert_array_equal(got_ln[6 * i + j], O.layer_norm(x[i, j][None], dt, 32, wr, br, 1e-5)[0])
+    # a (32,) weight over normalized_shape (6, 32): the same 32 values in every
+    # 32-element run of each 192-element row
+    w = arr(32, scale=0.1, shift=1.0)
+    got = O.rms_norm(x, dt, 192, w, 1e-6)
+    tiled = O.round_to(np.tile(O.to_compute(w, dt), 6), dt)
+    np.testing.assert_array_equal(got.reshape(4, 192), O.rms_norm(x.reshape(4, 192), dt, 192, tiled, 1e-6))
