@@ -9,13 +9,18 @@ below), inputs resident in HBM.  The headline line is rms_norm on bf16
 JSON line carries every other workload under "ops".
 
 Timing: W eager warmup steps, then K steps captured in one HIP graph (so host
-launch overhead does not pad ~35 us kernels) and replayed between HIP events
-recorded on the launch stream; three input/output buffer sets rotate so the
-256 MB MALL cannot serve a step from the previous one.  Achieved bandwidth
-uses algorithmic bytes (every compulsory byte counted once); GEMMs report
-algorithmic flops.  cpu_baseline times PyTorch's CPU implementation of the
-same op (the reference the configs name) on a bounded sample of the workload
-on this host's cores.
+launch overhead does not pad ~35 us kernels), replayed R times (--replays,
+default 5) back to back between HIP events recorded on the launch stream;
+the reported time per step is the median over the R replays (each replay's
+figure and the spread are in the line too).  Three input/output buffer sets
+rotate so the 256 MB MALL cannot serve a step from the previous one.
+Achieved bandwidth uses algorithmic bytes (every compulsory byte counted
+once); GEMMs report algorithmic flops.  A plain streaming copy (ntops_cast
+f32 -> f32) runs as its own workload and gives each bandwidth-bound op its
+fraction of the measured ceiling; torch.mm / torch.bmm (hipBLASLt, eager) are
+timed at the GEMM configs as a same-box yardstick.  cpu_baseline times
+PyTorch's CPU implementation of the same op (the reference the configs name)
+on a bounded sample of the workload on this host's cores.
 """
 
 import argparse
@@ -42,6 +47,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--replays", type=int, default=5, help="timed replays of the K-step graph (median reported)")
     p.add_argument("--ops", default="all")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     p.add_argument("--eager", action="store_true", help="time eager wrapper calls instead of a graph")
@@ -53,6 +59,11 @@ def parse_args():
                         "DIR/<workload>_{FETCH,WRITE}_SIZE/ and DIR/cal_{FETCH,WRITE}_SIZE/")
     p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic.json"),
                    help="measured HBM bytes per launch used to fill roofline.traffic")
+    p.add_argument("--mfma", metavar="DIR",
+                   help="print MFMA utilisation per GEMM workload (JSON) from rocprofv3 --pmc databases in "
+                        "DIR/<workload>_<counter>/")
+    p.add_argument("--mfma-file", default=os.path.join(ROOT, "profiles", "mfma.json"),
+                   help="measured MFMA utilisation used to fill roofline.mfma_busy")
     return p.parse_args()
 
 
@@ -119,8 +130,8 @@ def traffic(directory):
     """HBM bytes per launch of each workload's kernel: FETCH_SIZE and
     WRITE_SIZE (KiB per dispatch) each scaled by true_bytes / counter_bytes of
     a plain 128 MiB copy kernel (the calibration run)."""
-    cal_f = _counter_for(_one_db(os.path.join(directory, "cal_FETCH_SIZE")), "FETCH_SIZE", "k_cast_dense")
-    cal_w = _counter_for(_one_db(os.path.join(directory, "cal_WRITE_SIZE")), "WRITE_SIZE", "k_cast_dense")
+    cal_f = _counter_for(_one_db(os.path.join(directory, "cal_FETCH_SIZE")), "FETCH_SIZE", "k_cast_pack")
+    cal_w = _counter_for(_one_db(os.path.join(directory, "cal_WRITE_SIZE")), "WRITE_SIZE", "k_cast_pack")
     fetch_factor = COPY_CAL_BYTES / (cal_f * 1024)
     write_factor = COPY_CAL_BYTES / (cal_w * 1024)
     out = {"fetch_factor": round(fetch_factor, 4), "write_factor": round(write_factor, 4), "kernels": {}}
@@ -138,9 +149,62 @@ def traffic(directory):
     print(json.dumps(out, indent=1))
 
 
+def _gpu_agent(db):
+    """(num_xcc, cu_count) of the GPU agent recorded in a rocprofv3 database."""
+    for (ext,) in _db_rows(db, "select extdata from rocpd_info_agent where type = 'GPU'"):
+        info = json.loads(ext)
+        return int(info.get("num_xcc", 8)), int(info.get("cu_count", 256))
+    return 8, 256
+
+
+def mfma_report(directory):
+    """Matrix-core utilisation of each matrix workload's kernel from one
+    rocprofv3 pass of SQ_INSTS_VALU_MFMA_MOPS_BF16, SQ_VALU_MFMA_BUSY_CYCLES
+    and GRBM_GUI_ACTIVE in DIR/<workload>_mfma/.  flops = MOPS * 512 (checked
+    against the algorithmic count); busy = MFMA busy cycles / (active cycles
+    per XCD * 4 SIMDs * CUs); clock = active cycles per XCD / kernel time."""
+    out = {"kernels": {}}
+    for name in ("mm", "addmm", "bmm", "sdpa", "conv2d", "mfma_ceiling"):
+        d = os.path.join(directory, f"{name}_mfma")
+        if not os.path.isdir(d):
+            continue
+        db = _one_db(d)
+        nxcc, cus = _gpu_agent(db)
+        pattern = KERNEL_OF[name]
+        per = {}
+        for kname, cname, v, disp, dur in _db_rows(
+                db, "select kernel_name, counter_name, value, dispatch_id, duration from counters_collection"):
+            if pattern in _kernel_key(kname):
+                per.setdefault(disp, {"duration": dur})[cname] = v
+        rows = [r for r in per.values() if {"SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES",
+                                            "GRBM_GUI_ACTIVE"} <= set(r)]
+        if not rows:
+            continue
+        busy = [r["SQ_VALU_MFMA_BUSY_CYCLES"] / (r["GRBM_GUI_ACTIVE"] / nxcc * 4 * cus) for r in rows]
+        clock = [r["GRBM_GUI_ACTIVE"] / nxcc / r["duration"] for r in rows]
+        out["kernels"][name] = {
+            "kernel": pattern,
+            "dispatches": len(rows),
+            "flops": round(statistics.median(r["SQ_INSTS_VALU_MFMA_MOPS_BF16"] for r in rows) * 512),
+            "busy": round(statistics.median(busy), 4),
+            "clock_ghz": round(statistics.median(clock), 3),
+            "kernel_us": round(statistics.median(r["duration"] for r in rows) / 1e3, 2),
+        }
+    print(json.dumps(out, indent=1))
+
+
 # kernel symbol fragment of each workload's dominant kernel
 KERNEL_OF = {
+    "copy": "k_cast_pack",
+    "mfma_ceiling": "k_mfma_probe",
     "silu": "k_unary_dense",
+    "add": "k_binary_dense",
+    "gelu_f32": "k_unary_dense",
+    "gelu_bf16": "k_unary_dense",
+    "exp_f32": "k_unary_dense",
+    "exp_bf16": "k_unary_dense",
+    "bitwise_and": "k_binary_dense",
+    "im2col": "k_im2col",
     "div": "k_binary_dense",
     "eq": "k_binary_dense",
     "clamp": "k_clamp_dense",
@@ -174,7 +238,7 @@ def copy_calibration():
                                   ys[i % NSETS].data_ptr(), st,
                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "copy")
     torch.cuda.synchronize()
-    print(f"copy calibration: 10 x {COPY_CAL_BYTES} B (ntops_cast f32 -> f32, k_cast_dense<float, float>)")
+    print(f"copy calibration: 10 x {COPY_CAL_BYTES} B (ntops_cast f32 -> f32, k_cast_pack<float, float>)")
 
 
 def load_traffic(path):
@@ -287,6 +351,91 @@ def make_workloads():
                       16 * EN[0] * EN[1], 1, lambda i: ew_build(i, 3), clamp_step,
                       ew_cpu(torch.clamp, 3, 16, "torch.clamp fp32 (2048, 4096), tensor bounds = 1/4 of the workload"),
                       "f32"))
+
+    # the rest of the hot-path elementwise rows at (8192, 4096): add (three
+    # bf16 streams), gelu and exp in fp32 and bf16, bitwise_and on int32
+    def ew_dt_build(i, n_in, dtype):
+        g = _gen(60 + i)
+        if dtype == torch.int32:
+            ts = [torch.randint(-2**31, 2**31 - 1, EN, device="cuda", generator=g, dtype=torch.int32)
+                  for _ in range(n_in)]
+        else:
+            ts = [torch.randn(*EN, device="cuda", generator=g).to(dtype) for _ in range(n_in)]
+        return {"in": ts, "y": torch.empty(*EN, device="cuda", dtype=dtype)}
+
+    def unary_step(op, code):
+        def step(s):
+            check(lib.ntops_unary(op, code, 2, en_shape, s["in"][0].data_ptr(), en_strides, s["y"].data_ptr(),
+                                  en_strides, stream()), "unary")
+        return step
+
+    def binary_step(op, code):
+        def step(s):
+            a, b = s["in"]
+            check(lib.ntops_binary(op, code, 2, en_shape, a.data_ptr(), en_strides, b.data_ptr(), en_strides,
+                                   0.0, 0, 1.0, 1, s["y"].data_ptr(), en_strides, stream()), "binary")
+        return step
+
+    def ew_dt_cpu(fn, n_in, dtype, bytes_per_el, desc):
+        def make():
+            g = _cpu_gen()
+            if dtype == torch.int32:
+                ts = [torch.randint(-2**31, 2**31 - 1, (2048, 4096), generator=g, dtype=torch.int32)
+                      for _ in range(n_in)]
+            else:
+                ts = [torch.randn(2048, 4096, generator=g).to(dtype) for _ in range(n_in)]
+            return (lambda: fn(*ts)), 2048 * 4096 * bytes_per_el, desc + " (2048, 4096) = 1/4 of the workload"
+        return make
+
+    n_el = EN[0] * EN[1]
+    W.append(Workload("add", "add bf16 (8192, 4096) + (8192, 4096), alpha 1", "GB/s", "hbm", 6 * n_el, 1,
+                      lambda i: ew_dt_build(i, 2, torch.bfloat16), binary_step(_lib.BINARY_ADD, _lib.BF16),
+                      ew_dt_cpu(torch.add, 2, torch.bfloat16, 6, "torch.add bf16"), "bf16"))
+    for nm, op, fn in (("gelu", _lib.UNARY_GELU, F.gelu), ("exp", _lib.UNARY_EXP, torch.exp)):
+        for dtype, code, tag, esz in ((torch.float32, _lib.F32, "f32", 4), (torch.bfloat16, _lib.BF16, "bf16", 2)):
+            W.append(Workload(f"{nm}_{tag}", f"{nm} {'fp32' if tag == 'f32' else 'bf16'} (8192, 4096)", "GB/s", "hbm",
+                              2 * esz * n_el, 1, (lambda dt: lambda i: ew_dt_build(i, 1, dt))(dtype),
+                              unary_step(op, code), ew_dt_cpu(fn, 1, dtype, 2 * esz, f"{fn.__name__} {tag}"), tag))
+    W.append(Workload("bitwise_and", "bitwise_and int32 (8192, 4096) & (8192, 4096)", "GB/s", "hbm", 12 * n_el, 1,
+                      lambda i: ew_dt_build(i, 2, torch.int32), binary_step(_lib.BINARY_BITWISE_AND, _lib.I32),
+                      ew_dt_cpu(torch.bitwise_and, 2, torch.int32, 12, "torch.bitwise_and int32"), "int32"))
+
+    # streaming copy (ntops_cast f32 -> f32, 128 MiB in and out per step):
+    # the measured ceiling of the bandwidth-bound kernels
+    CN_ = 32 << 20
+    cp_shape, cp_st = _lib.i64_array((CN_,)), _lib.i64_array((1,))
+
+    def copy_build(i):
+        x = torch.randn(CN_, device="cuda", generator=_gen(80 + i))
+        return {"x": x, "y": torch.empty_like(x)}
+
+    def copy_step(s):
+        check(lib.ntops_cast(_lib.F32, _lib.F32, 1, cp_shape, s["x"].data_ptr(), cp_st, s["y"].data_ptr(), cp_st,
+                             stream()), "copy")
+
+    def copy_cpu():
+        x = torch.randn(CN_ // 4, generator=_cpu_gen())
+        y = torch.empty_like(x)
+        return (lambda: y.copy_(x)), 2 * x.numel() * 4, "Tensor.copy_ fp32 32 MiB = 1/4 of the workload"
+
+    W.append(Workload("copy", "streaming copy fp32 128 MiB -> 128 MiB (ntops_cast): measured HBM ceiling", "GB/s",
+                      "hbm", 2 * CN_ * 4, 1, copy_build, copy_step, copy_cpu, "f32"))
+    W[-1].yardstick = (lambda s: s["y"].copy_(s["x"]), "torch Tensor.copy_ (device-to-device), eager")
+
+    # matrix-core rate probe: full-chip bf16 MFMAs on register operands, the
+    # measured ceiling of the matrix-bound kernels
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    PROBE_ITERS = 5600
+
+    def probe_build(i):
+        return {"out": torch.empty(cus * 4, device="cuda")}
+
+    def probe_step(s):
+        check(lib.ntops_mfma_rate_probe(cus, PROBE_ITERS, s["out"].data_ptr(), stream()), "mfma probe")
+
+    W.append(Workload("mfma_ceiling", f"bf16 MFMA rate probe: {cus} workgroups x 4 waves x {PROBE_ITERS} rounds of "
+                      "8 v_mfma_f32_32x32x16_bf16 on register operands: measured matrix-core ceiling", "TFLOP/s",
+                      "mfma", cus * 4 * PROBE_ITERS * 8 * 32768, 1, probe_build, probe_step, None, "bf16"))
 
     # rms_norm / layer_norm bf16 (16384, 4096)
     R, C = 16384, 4096
@@ -444,7 +593,8 @@ def make_workloads():
         a = (0.02 * torch.randn(M, K, device="cuda", generator=g)).bfloat16()
         b = (0.02 * torch.randn(K, N, device="cuda", generator=g)).bfloat16()
         bias = (0.02 * torch.randn(N, device="cuda", generator=g)).bfloat16()
-        return {"a": a, "b": b, "bias": bias.expand(M, N), "out": torch.empty(M, N, dtype=torch.bfloat16, device="cuda")}
+        return {"a": a, "b": b, "bias": bias.expand(M, N), "bias1": bias,
+                "out": torch.empty(M, N, dtype=torch.bfloat16, device="cuda")}
 
     def mm_step(s):
         gemm(s["a"], s["b"], s["out"])
@@ -471,9 +621,12 @@ def make_workloads():
     W.append(Workload("mm", "mm bf16 (8192 x 4096).(4096 x 14336), fp32 accumulate", "TFLOP/s", "mfma",
                       2 * M * N * K, 1, mm_build, mm_step, mm_cpu, "bf16"))
     W[-1].bytes = (M * K + K * N + M * N) * 2
+    W[-1].yardstick = (lambda s: torch.mm(s["a"], s["b"], out=s["out"]), "torch.mm (hipBLASLt), eager")
     W.append(Workload("addmm", "addmm bf16 bias (14336,) + (8192 x 4096).(4096 x 14336), beta = alpha = 1",
                       "TFLOP/s", "mfma", 2 * M * N * K, 1, mm_build, addmm_step, addmm_cpu, "bf16"))
     W[-1].bytes = (M * K + K * N + M * N + N) * 2
+    W[-1].yardstick = (lambda s: torch.addmm(s["bias1"], s["a"], s["b"], out=s["out"]),
+                       "torch.addmm (hipBLASLt), eager")
 
     BB, BM, BK, BN = 32, 2048, 128, 2048
 
@@ -497,6 +650,7 @@ def make_workloads():
     W.append(Workload("bmm", "bmm bf16 32 x (2048 x 128).(128 x 2048), fp32 accumulate", "GB/s", "hbm",
                       (BB * BM * BK + BB * BK * BN + BB * BM * BN) * 2, 1, bmm_build, bmm_step, bmm_cpu, "bf16"))
     W[-1].flops = 2 * BB * BM * BN * BK
+    W[-1].yardstick = (lambda s: torch.bmm(s["a"], s["b"], out=s["out"]), "torch.bmm (hipBLASLt), eager")
 
     # scaled_dot_product_attention bf16 causal, (4, 32, 2048, 128): the
     # algorithmic flops are those of the unmasked (q, kv) pairs, S (S + 1) / 2
@@ -547,6 +701,21 @@ def make_workloads():
         return (lambda: F.conv2d(x, w, b, padding=1)), 2 * 2 * CK * CC * 9 * CH * CH, \
             "torch conv2d bf16 (2, 256, 56, 56) * (256, 256, 3, 3) = 1/16 of the workload"
 
+    # im2col bf16 (32, 256, 56, 56), 3x3, padding 1: the conv workload's
+    # unfold as the public op (reads the input once, writes 9x it)
+    i2c = ntops_amd.torch.im2col
+
+    def i2c_step(s):
+        i2c(s["x"], 3, padding=1)
+
+    def i2c_cpu():
+        x = torch.randn(2, CC, CH, CH, generator=_cpu_gen()).bfloat16()
+        return (lambda: F.unfold(x, 3, padding=1)), 2 * (x.numel() + 2 * CC * 9 * CH * CH), \
+            "F.unfold bf16 (2, 256, 56, 56), 3x3, padding 1 = 1/16 of the workload"
+
+    W.append(Workload("im2col", "im2col bf16 (32, 256, 56, 56), kernel 3x3, padding 1 -> (32, 2304, 3136)", "GB/s",
+                      "hbm", 2 * (CN * CC * CH * CH + CN * CC * 9 * CH * CH), 1, conv_build, i2c_step, i2c_cpu, "bf16"))
+
     W.append(Workload("conv2d", "conv2d bf16 (32, 256, 56, 56) * (256, 256, 3, 3) + bias, padding 1 "
                       "(unfold + MFMA GEMM)", "TFLOP/s", "mfma", 2 * CN * CK * CC * 9 * CH * CH, 1, conv_build,
                       conv_step, conv_cpu, "bf16"))
@@ -557,20 +726,22 @@ def make_workloads():
 # -------------------------------------------------------------- timing ----
 
 
-def time_gpu(w, steps, warmup, eager):
+def time_gpu(w, steps, warmup, eager, replays):
+    """Per-step milliseconds of each of `replays` timed runs of `steps` steps
+    (a captured K-step graph replayed back to back, or eager launches)."""
     sets = [w.build(i) for i in range(NSETS)]
     torch.cuda.synchronize()
     for i in range(max(1, warmup)):  # >= 1: one-time kernel attributes are set outside capture
         w.step(sets[i % NSETS])
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
     if eager:
         torch.cuda.synchronize()
-        start.record()
-        for i in range(steps):
-            w.step(sets[i % NSETS])
-        end.record()
+        events[0].record()
+        for r in range(replays):
+            for i in range(steps):
+                w.step(sets[i % NSETS])
+            events[r + 1].record()
         torch.cuda.synchronize()
     else:
         graph = torch.cuda.CUDAGraph()
@@ -579,15 +750,38 @@ def time_gpu(w, steps, warmup, eager):
                 w.step(sets[i % NSETS])
         graph.replay()  # one untimed replay (the graph's first launch)
         torch.cuda.synchronize()
-        start.record()
-        graph.replay()
-        end.record()
+        graph.replay()  # keeps the GPU busy while the timed replays are queued
+        events[0].record()
+        for r in range(replays):
+            graph.replay()
+            events[r + 1].record()
         torch.cuda.synchronize()
         del graph
-    ms = start.elapsed_time(end) / steps
+    ms = [events[r].elapsed_time(events[r + 1]) / steps for r in range(replays)]
     del sets
     torch.cuda.empty_cache()
     return ms
+
+
+def time_yardstick(fn, build, steps, replays):
+    """Eager per-step milliseconds (median of `replays` runs of `steps`
+    calls over the rotating buffer sets) of a library call; kept out of
+    graph capture, which library calls are not guaranteed to survive."""
+    sets = [build(i) for i in range(NSETS)]
+    for i in range(3):
+        fn(sets[i % NSETS])
+    torch.cuda.synchronize()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+    events[0].record()
+    for r in range(replays):
+        for i in range(steps):
+            fn(sets[i % NSETS])
+        events[r + 1].record()
+    torch.cuda.synchronize()
+    ms = [events[r].elapsed_time(events[r + 1]) / steps for r in range(replays)]
+    del sets
+    torch.cuda.empty_cache()
+    return statistics.median(ms)
 
 
 def cpu_threads():
@@ -625,7 +819,8 @@ def time_cpu(w):
                       f"{cpu_model()}"}
 
 
-def result_for(w, ms, measured_traffic):
+def result_for(w, ms_list, measured_traffic, measured_mfma):
+    ms = statistics.median(ms_list)
     sec = ms / 1e3
     if w.unit == "TFLOP/s":
         value = w.work / sec / 1e12
@@ -641,6 +836,8 @@ def result_for(w, ms, measured_traffic):
         "unit": unit,
         "ms_per_step": round(ms, 5),
         "kernel_ms": round(per_kernel_ms, 5),
+        "replay_ms_per_step": [round(m, 5) for m in ms_list],
+        "replay_spread": round((max(ms_list) - min(ms_list)) / ms, 4),
         "roofline": {"bound": w.bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4), "traffic": None},
     }
@@ -650,9 +847,22 @@ def result_for(w, ms, measured_traffic):
         out["roofline"]["traffic"] = t["bytes"]
         out["roofline"]["algorithmic_bytes_per_launch"] = (
             w.work // w.kernels_per_step if unit == "GB/s" else getattr(w, "bytes", None))
+    m = measured_mfma.get(w.name)
+    if m:
+        # matrix-core busy fraction of the kernel (profiles/mfma.json)
+        out["roofline"]["mfma_busy"] = m["busy"]
+        out["roofline"]["mfma_flops_per_launch"] = m.get("flops")
     if getattr(w, "flops", None):
         out["tflops"] = round(w.flops / sec / 1e12, 3)
     return out
+
+
+def load_json_kernels(path):
+    try:
+        with open(path) as f:
+            return json.load(f).get("kernels", {})
+    except (OSError, ValueError):
+        return {}
 
 
 def main():
@@ -662,6 +872,9 @@ def main():
         return
     if args.traffic:
         traffic(args.traffic)
+        return
+    if args.mfma:
+        mfma_report(args.mfma)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -673,8 +886,12 @@ def main():
     if args.copy_calibration:
         copy_calibration()
         return
+    if args.replays < 1 or args.steps < 1:
+        print("bench.py: --steps and --replays must be >= 1", file=sys.stderr)
+        sys.exit(2)
     torch.set_num_threads(cpu_threads())
     measured_traffic = load_traffic(args.traffic_file)
+    measured_mfma = load_json_kernels(args.mfma_file)
     workloads = make_workloads()
     names = list(workloads) if args.ops == "all" else args.ops.split(",")
     headline = "rms_norm" if "rms_norm" in names else names[0]
@@ -683,13 +900,35 @@ def main():
     results = {}
     for n in names:
         w = workloads[n]
-        ms = time_gpu(w, args.steps, args.warmup, args.eager)
-        r = result_for(w, ms, measured_traffic)
-        if not args.no_cpu:
+        ms = time_gpu(w, args.steps, args.warmup, args.eager, args.replays)
+        r = result_for(w, ms, measured_traffic, measured_mfma)
+        y = getattr(w, "yardstick", None)
+        if y is not None:
+            fn, lib_desc = y
+            y_ms = time_yardstick(fn, w.build, args.steps, args.replays)
+            y_val = w.work / (y_ms / 1e3) / (1e12 if w.unit == "TFLOP/s" else 1e9)
+            r["yardstick"] = {"library": lib_desc, "ms_per_step": round(y_ms, 5), "value": round(y_val, 3),
+                              "unit": w.unit, "ratio": round(r["value"] / y_val, 4)}
+        if not args.no_cpu and w.cpu is not None:
             r["cpu_baseline"] = time_cpu(w)
         results[n] = r
         print(f"# {n}: {r['value']} {r['unit']} ({r['kernel_ms'] * 1e3:.1f} us/kernel, "
-              f"{100 * r['roofline']['frac']:.1f}% of roofline)", file=sys.stderr, flush=True)
+              f"{100 * r['roofline']['frac']:.1f}% of roofline, replay spread {100 * r['replay_spread']:.1f}%"
+              + (f"; {r['yardstick']['library']}: {r['yardstick']['value']} {w.unit}" if "yardstick" in r else "")
+              + ")", file=sys.stderr, flush=True)
+    ceiling = mceiling = None
+    if "copy" in results:
+        # every bandwidth-bound kernel against the measured streaming ceiling
+        ceiling = results["copy"]["roofline"]["achieved"]
+        for r in results.values():
+            if r["unit"] == "GB/s":
+                r["roofline"]["frac_of_copy"] = round(r["roofline"]["achieved"] / ceiling, 4)
+    if "mfma_ceiling" in results:
+        # every matrix-bound kernel against the measured matrix-core rate
+        mceiling = results["mfma_ceiling"]["roofline"]["achieved"]
+        for n, r in results.items():
+            if r["unit"] == "TFLOP/s" and n != "mfma_ceiling":
+                r["roofline"]["frac_of_mfma_ceiling"] = round(r["roofline"]["achieved"] / mceiling, 4)
 
     h = results[headline]
     line = {
@@ -705,10 +944,18 @@ def main():
         "vs_baseline": None,
         "dtype": workloads[headline].dtype,
         "data": "synthetic (seeded torch.randn of the configured shapes, resident in HBM)",
-        "config": {"workload": h["workload"], "timing": "eager" if args.eager else "hip-graph of K steps",
+        "config": {"workload": h["workload"],
+                   "timing": ("eager" if args.eager else "hip-graph of K steps") +
+                             f", median of {args.replays} timed replays",
                    "buffer_sets": NSETS},
         "roofline": h["roofline"],
         "cpu_baseline": h.get("cpu_baseline"),
+        "hbm_ceiling": None if ceiling is None else {
+            "copy_gbs": round(ceiling, 3), "frac_of_peak": round(ceiling / HBM_PEAK_GBS, 4),
+            "kernel": "ntops_cast fp32 -> fp32, 128 MiB in + 128 MiB out per step (k_cast_pack)"},
+        "mfma_ceiling": None if mceiling is None else {
+            "tflops": round(mceiling, 3), "frac_of_peak": round(mceiling / MFMA_BF16_PEAK_TFLOPS, 4),
+            "kernel": "ntops_mfma_rate_probe (k_mfma_probe), bf16 32x32x16 MFMAs on register operands"},
         "ops": {n: r for n, r in results.items() if n != headline},
     }
     print(json.dumps(line))

@@ -350,6 +350,14 @@ NTOPS_API int ntops_im2col(int dtype, int64_t N, int64_t C, int64_t H, int64_t W
                const void* x, const int64_t* x_strides,
                void* out, const int64_t* out_strides, void* stream);
 
+/* ---- measurement ---------------------------------------------------------- */
+/* Matrix-core rate probe (no ntops counterpart; the ceiling bench.py reports
+ * for the matrix-bound kernels): `workgroups` workgroups of 4 waves, each
+ * wave running `iters` (even) rounds of 8 v_mfma_f32_32x32x16_bf16 on
+ * register operands, i.e. workgroups * 4 * iters * 8 * 32768 flops, and
+ * writing one checksum float per wave to out (workgroups * 4 floats). */
+NTOPS_API int ntops_mfma_rate_probe(int64_t workgroups, int64_t iters, float* out, void* stream);
+
 /* ntops_conv2d without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc).  No ntops counterpart.  The workspace is a

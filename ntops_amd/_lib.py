@@ -102,6 +102,7 @@ _SIGNATURES = {
         _i,
         [_i] + [_i64] * 12 + [_vp, _c_i64p, _vp, _c_i64p, _vp],
     ),
+    "ntops_mfma_rate_probe": (_i, [_i64, _i64, _vp, _vp]),
     "ntops_gemm": (
         _i,
         [_i, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _d, _vp, _c_i64p, _vp],

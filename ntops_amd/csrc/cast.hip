@@ -2,6 +2,8 @@
 // promotion (operands converted to the common dtype before an elementwise
 // op) and to materialise contiguous copies of views the row kernels cannot
 // address, so no data movement falls back to torch.
+#include <algorithm>
+
 #include "dispatch.h"
 
 namespace ntops {
@@ -23,6 +25,27 @@ __global__ __launch_bounds__(kThreads) void k_cast_dense(const S* x, D* y, int64
   for (int u = 0; u < kPerThread; ++u) {
     const int64_t i = base + u * kThreads;
     if (i < n) y[i] = convert<D>(r[u]);
+  }
+}
+
+// Dense conversion between element types of one size (incl. the plain copy
+// S == D): one 16-byte pack per thread, non-temporal loads and stores (the
+// data streams through once), block 0 converts the tail.
+template <typename S, typename D>
+__global__ __launch_bounds__(kThreads) void k_cast_pack(const S* x, D* y, int64_t npack, int64_t n) {
+  static_assert(sizeof(S) == sizeof(D), "same-size element types");
+  constexpr int V = Pack16<S>::N;
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (p < npack) {
+    const Pack16<S> r = load16_nt(x + p * V);
+    Pack16<D> o;
+#pragma unroll
+    for (int i = 0; i < V; ++i) o.v[i] = convert<D>(r.v[i]);
+    store16_nt(y + p * V, o);
+  }
+  if (blockIdx.x == 0) {
+    const int64_t i = npack * V + threadIdx.x;
+    if (threadIdx.x < V && i < n) y[i] = convert<D>(x[i]);
   }
 }
 
@@ -50,6 +73,15 @@ int launch_cast(int ndim, const int64_t* shape, const void* xv, const int64_t* x
   const S* x = static_cast<const S*>(xv);
   D* y = static_cast<D*>(yv);
   const bool dense = sp.ndim == 0 || (sp.ndim == 1 && sp.stride[0][0] == 1 && sp.stride[1][0] == 1);
+  if constexpr (sizeof(S) == sizeof(D) && sizeof(S) <= 16) {
+    if (dense && aligned16(x) && aligned16(y)) {
+      constexpr int V = 16 / sizeof(S);
+      const int64_t npack = n / V;
+      const int64_t blocks = std::max<int64_t>(1, ceil_div(npack, static_cast<int64_t>(kThreads)));
+      hipLaunchKernelGGL((k_cast_pack<S, D>), dim3(blocks), dim3(kThreads), 0, st, x, y, npack, n);
+      return check_launch("ntops_cast");
+    }
+  }
   if (dense) {
     const int64_t blocks = ceil_div(n, static_cast<int64_t>(kThreads) * kPerThread);
     hipLaunchKernelGGL((k_cast_dense<S, D>), dim3(blocks), dim3(kThreads), 0, st, x, y, n);
