@@ -62,6 +62,10 @@ def parse_args():
     p.add_argument("--mfma", metavar="DIR",
                    help="print MFMA utilisation per GEMM workload (JSON) from rocprofv3 --pmc databases in "
                         "DIR/<workload>_<counter>/")
+    p.add_argument("--counters", metavar="DB",
+                   help="print, per kernel of a rocprofv3 --pmc database, the median of each counter and its "
+                        "rate per CU per active cycle (markdown); --kernels limits the kernels by name fragment")
+    p.add_argument("--kernels", default="", help="comma-separated kernel name fragments for --counters")
     p.add_argument("--mfma-file", default=os.path.join(ROOT, "profiles", "mfma.json"),
                    help="measured MFMA utilisation used to fill roofline.mfma_busy")
     return p.parse_args()
@@ -155,6 +159,39 @@ def _gpu_agent(db):
         info = json.loads(ext)
         return int(info.get("num_xcc", 8)), int(info.get("cu_count", 256))
     return 8, 256
+
+
+def counter_table(db, fragments):
+    """Markdown table of a --pmc database: per kernel (matched by name
+    fragment), the median over dispatches of each counter, its value per CU
+    per active cycle (GRBM_GUI_ACTIVE per XCD), the kernel time and the clock
+    those imply."""
+    nxcc, cus = _gpu_agent(db)
+    frags = [f for f in fragments.split(",") if f] or [""]
+    per = {}
+    for kname, cname, v, disp, dur in _db_rows(
+            db, "select kernel_name, counter_name, value, dispatch_id, duration from counters_collection"):
+        key = _kernel_key(kname)
+        f = next((f for f in frags if f in key), None)
+        if f is None:
+            continue
+        per.setdefault((key, f), {}).setdefault(disp, {"duration": dur})[cname] = v
+    for (key, f), disps in sorted(per.items(), key=lambda kv: kv[0][1]):
+        rows = list(disps.values())
+        counters = sorted({c for r in rows for c in r if c != "duration"})
+        med = {c: statistics.median(r[c] for r in rows if c in r) for c in counters}
+        dur = statistics.median(r["duration"] for r in rows)
+        gui = med.get("GRBM_GUI_ACTIVE")
+        head = f"`{key[:90]}`: {len(rows)} dispatches, {dur / 1e3:.1f} us"
+        if gui:
+            head += f", {gui / nxcc:.0f} active cycles per XCD, {gui / nxcc / dur:.2f} GHz"
+        print(f"{head}\n\n| counter | median per dispatch | per CU per active cycle |\n|---|---|---|")
+        for c in counters:
+            if c == "GRBM_GUI_ACTIVE":
+                continue
+            rate = f"{med[c] / (gui / nxcc * cus):.3f}" if gui else ""
+            print(f"| {c} | {med[c]:.0f} | {rate} |")
+        print()
 
 
 def mfma_report(directory):
@@ -875,6 +912,9 @@ def main():
         return
     if args.mfma:
         mfma_report(args.mfma)
+        return
+    if args.counters:
+        counter_table(args.counters, args.kernels)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
