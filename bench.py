@@ -12,7 +12,12 @@ Timing: W eager warmup steps, then K steps captured in one HIP graph (so host
 launch overhead does not pad ~35 us kernels), replayed R times (--replays,
 default 5) back to back between HIP events recorded on the launch stream;
 the reported time per step is the median over the R replays (each replay's
-figure and the spread are in the line too).  Three input/output buffer sets
+figure and the spread are in the line too).  Before the timed replays the
+graph is replayed untimed for --settle-ms of wall time (default 100): the
+part's clocks take ~10 ms to settle after a change of load (bmm bf16
+32 x (2048 x 128)(128 x 2048) ran 63-88 us per step in the first replays
+after an MFMA-heavy workload or an idle second, 53-58 us once settled), so
+without it the short workloads were timed inside that transient.  Three input/output buffer sets
 rotate so the 256 MB MALL cannot serve a step from the previous one.
 Achieved bandwidth uses algorithmic bytes (every compulsory byte counted
 once); GEMMs report algorithmic flops.  A plain streaming copy (ntops_cast
@@ -48,6 +53,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--replays", type=int, default=5, help="timed replays of the K-step graph (median reported)")
+    p.add_argument("--settle-ms", type=float, default=100.0,
+                   help="untimed replays of the captured steps for this much wall time before timing")
     p.add_argument("--ops", default="all")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     p.add_argument("--eager", action="store_true", help="time eager wrapper calls instead of a graph")
@@ -763,17 +770,34 @@ def make_workloads():
 # -------------------------------------------------------------- timing ----
 
 
-def time_gpu(w, steps, warmup, eager, replays):
+def settle(run_once, settle_ms):
+    """Runs `run_once` (untimed) until `settle_ms` of wall time has passed, so
+    the timed runs start with the part's clocks settled for this load."""
+    t_end = time.perf_counter() + settle_ms / 1e3
+    while True:
+        run_once()
+        torch.cuda.synchronize()
+        if time.perf_counter() >= t_end:
+            return
+
+
+def time_gpu(w, steps, warmup, eager, replays, settle_ms=0.0):
     """Per-step milliseconds of each of `replays` timed runs of `steps` steps
-    (a captured K-step graph replayed back to back, or eager launches)."""
+    (a captured K-step graph replayed back to back, or eager launches), after
+    `warmup` eager steps and `settle_ms` of untimed runs of the same steps."""
     sets = [w.build(i) for i in range(NSETS)]
     torch.cuda.synchronize()
     for i in range(max(1, warmup)):  # >= 1: one-time kernel attributes are set outside capture
         w.step(sets[i % NSETS])
     torch.cuda.synchronize()
     events = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+
+    def eager_steps():
+        for i in range(steps):
+            w.step(sets[i % NSETS])
+
     if eager:
-        torch.cuda.synchronize()
+        settle(eager_steps, settle_ms)
         events[0].record()
         for r in range(replays):
             for i in range(steps):
@@ -787,6 +811,7 @@ def time_gpu(w, steps, warmup, eager, replays):
                 w.step(sets[i % NSETS])
         graph.replay()  # one untimed replay (the graph's first launch)
         torch.cuda.synchronize()
+        settle(graph.replay, settle_ms)
         graph.replay()  # keeps the GPU busy while the timed replays are queued
         events[0].record()
         for r in range(replays):
@@ -800,14 +825,21 @@ def time_gpu(w, steps, warmup, eager, replays):
     return ms
 
 
-def time_yardstick(fn, build, steps, replays):
+def time_yardstick(fn, build, steps, replays, settle_ms=0.0):
     """Eager per-step milliseconds (median of `replays` runs of `steps`
-    calls over the rotating buffer sets) of a library call; kept out of
-    graph capture, which library calls are not guaranteed to survive."""
+    calls over the rotating buffer sets) of a library call, after the same
+    settling as the workload's own timing; kept out of graph capture, which
+    library calls are not guaranteed to survive."""
     sets = [build(i) for i in range(NSETS)]
     for i in range(3):
         fn(sets[i % NSETS])
     torch.cuda.synchronize()
+
+    def eager_steps():
+        for i in range(steps):
+            fn(sets[i % NSETS])
+
+    settle(eager_steps, settle_ms)
     events = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
     events[0].record()
     for r in range(replays):
@@ -940,12 +972,12 @@ def main():
     results = {}
     for n in names:
         w = workloads[n]
-        ms = time_gpu(w, args.steps, args.warmup, args.eager, args.replays)
+        ms = time_gpu(w, args.steps, args.warmup, args.eager, args.replays, args.settle_ms)
         r = result_for(w, ms, measured_traffic, measured_mfma)
         y = getattr(w, "yardstick", None)
         if y is not None:
             fn, lib_desc = y
-            y_ms = time_yardstick(fn, w.build, args.steps, args.replays)
+            y_ms = time_yardstick(fn, w.build, args.steps, args.replays, args.settle_ms)
             y_val = w.work / (y_ms / 1e3) / (1e12 if w.unit == "TFLOP/s" else 1e9)
             r["yardstick"] = {"library": lib_desc, "ms_per_step": round(y_ms, 5), "value": round(y_val, 3),
                               "unit": w.unit, "ratio": round(r["value"] / y_val, 4)}
@@ -987,6 +1019,7 @@ def main():
         "config": {"workload": h["workload"],
                    "timing": ("eager" if args.eager else "hip-graph of K steps") +
                              f", median of {args.replays} timed replays",
+                   "settle_ms": args.settle_ms,
                    "buffer_sets": NSETS},
         "roofline": h["roofline"],
         "cpu_baseline": h.get("cpu_baseline"),

@@ -64,6 +64,7 @@ struct GemmArgs {
   int M, N, K, batch;
   float alpha, beta;
   int use_c;
+  int c_mode;  // epilogue's C access (kCNone / kCStrided / kCVec4 / kCRow), set by set_c_mode
   int staged;  // out is 16-byte aligned with unit column stride and N % 8 == 0
   // Implicit convolution operand (used only by the CONV instantiation): B's
   // k-row kg = (c * R + r) * S + s starts at element
@@ -268,14 +269,42 @@ __device__ __forceinline__ u32x4 load_frag(const char* tile, int row0, int ks, i
 // row  m = l & 31  and columns  n = 8q + 4(l >> 5) + 0..3  in
 // acc[i][j][4q .. 4q+3].  alpha / beta are applied in fp32 and each value is
 // rounded once.  (mw, nw) is the wave tile's origin in the output; D and Cp
-// already point at the batch's matrices.  HAS_C is a template parameter so
-// the C test is not a branch per element.
-template <typename T, bool HAS_C, int TM, int TN>
-__device__ __forceinline__ float final_value(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
-                                             const T* Cp, int i, int j, int q, int e, int m,
-                                             int n) {
+// already point at the batch's matrices.  The C access mode CM is a template
+// parameter so the C test is not a branch per element:
+//   kCNone     no C;
+//   kCStrided  one load per element (any strides);
+//   kCVec4     unit column stride, rows and batches 8-byte aligned: a lane's
+//              4 consecutive columns in one 8-byte load (addmm's bias row
+//              and full C matrices);
+//   kCRow      column stride 0: one value per row (conv2d's bias).
+constexpr int kCNone = 0, kCStrided = 1, kCVec4 = 2, kCRow = 3;
+
+// beta * C at (m, n .. n + 3) in fp32 (zeros where `ok` is false, i.e.
+// past the output's edge: no load is issued there).
+template <typename T, int CM>
+__device__ __forceinline__ void c_values(const GemmArgs& g, const T* Cp, int m, int n, bool ok, float (&c)[4]) {
+  if constexpr (CM == kCVec4) {
+    u32x2 raw = {0u, 0u};
+    if (ok) raw = *reinterpret_cast<const u32x2*>(Cp + static_cast<int64_t>(m) * g.sc_m + n);
+    const T* t = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c[e] = g.beta * static_cast<float>(t[e]);
+  } else if constexpr (CM == kCRow) {
+    const float v = ok ? g.beta * static_cast<float>(Cp[static_cast<int64_t>(m) * g.sc_m]) : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c[e] = v;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      c[e] = (CM == kCStrided && ok) ? g.beta * static_cast<float>(Cp[m * g.sc_m + (n + e) * g.sc_n]) : 0.f;
+  }
+}
+
+template <typename T, int CM, int TM, int TN>
+__device__ __forceinline__ float final_value(const GemmArgs& g, const f32x16 (&acc)[TM][TN], const float (&c)[4],
+                                             int i, int j, int q, int e) {
   float v = g.alpha * acc[i][j][4 * q + e];
-  if constexpr (HAS_C) v += g.beta * static_cast<float>(Cp[m * g.sc_m + (n + e) * g.sc_n]);
+  if constexpr (CM != kCNone) v += c[e];
   return v;
 }
 
@@ -285,7 +314,7 @@ __device__ __forceinline__ float final_value(const GemmArgs& g, const f32x16 (&a
 // it out with 16-byte stores, 8 lanes per 128-byte row segment, so every L2
 // write request is a full line instead of 16 bytes (store_rows: exactly
 // WTM / 8 store instructions when EVEN).
-template <typename T, bool HAS_C, int TM, int TN, int WTM, int WTN, bool EVEN>
+template <typename T, int CM, int TM, int TN, int WTM, int WTN, bool EVEN>
 __device__ __forceinline__ void stage_tile(const GemmArgs& g, const f32x16 (&acc)[TM][TN], char* ep,
                                            const T* Cp, int mw, int nw, int lane,
                                            u32x4 (&rows)[WTM / 8]) {
@@ -301,10 +330,13 @@ __device__ __forceinline__ void stage_tile(const GemmArgs& g, const f32x16 (&acc
         const int col = j * 32 + q * 8 + (lane >> 5) * 4;
         const int n = nw + col;
         T o[4];
+        // N % 4 == 0 on this path, so columns n .. n + 3 are all in or all out
+        float cv[4];
+        c_values<T, CM>(g, Cp, m, n, EVEN || (m < g.M && n < g.N), cv);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const bool ok = EVEN || (m < g.M && n + e < g.N);
-          o[e] = static_cast<T>(ok ? final_value<T, HAS_C>(g, acc, Cp, i, j, q, e, m, n) : 0.f);
+          o[e] = static_cast<T>(ok ? final_value<T, CM>(g, acc, cv, i, j, q, e) : 0.f);
         }
         const int c = col >> 3, half = (col >> 2) & 1;
         *reinterpret_cast<u32x2*>(ep + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + half * 8) =
@@ -338,18 +370,18 @@ __device__ __forceinline__ void store_rows(const GemmArgs& g, const u32x4 (&rows
   }
 }
 
-template <typename T, bool HAS_C, int TM, int TN, int WTM, int WTN, bool EVEN, bool NT>
+template <typename T, int CM, int TM, int TN, int WTM, int WTN, bool EVEN, bool NT>
 __device__ __forceinline__ void store_tile_staged(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
                                                   char* ep, T* D, const T* Cp, int mw, int nw,
                                                   int lane) {
   u32x4 rows[WTM / 8];
-  stage_tile<T, HAS_C, TM, TN, WTM, WTN, EVEN>(g, acc, ep, Cp, mw, nw, lane, rows);
+  stage_tile<T, CM, TM, TN, WTM, WTN, EVEN>(g, acc, ep, Cp, mw, nw, lane, rows);
   store_rows<T, WTM, EVEN, NT>(g, rows, D, mw, nw, lane);
 }
 
 // Direct store: 8-byte stores of each lane's 4 consecutive columns (any
 // output row stride that keeps 8-byte alignment), element stores at the edge.
-template <typename T, bool HAS_C, int TM, int TN, bool EVEN>
+template <typename T, int CM, int TM, int TN, bool EVEN>
 __device__ __forceinline__ void store_tile_direct(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
                                                   T* D, const T* Cp, int mw, int nw, int lane) {
 #pragma unroll
@@ -360,19 +392,15 @@ __device__ __forceinline__ void store_tile_direct(const GemmArgs& g, const f32x1
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = nw + j * 32 + q * 8 + (lane >> 5) * 4;
+        // N % 4 == 0 on this path, so columns n .. n + 3 are all in or all out
         if (EVEN || (m < g.M && n + 3 < g.N)) {
+          float cv[4];
+          c_values<T, CM>(g, Cp, m, n, true, cv);
           T o[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            o[e] = static_cast<T>(final_value<T, HAS_C>(g, acc, Cp, i, j, q, e, m, n));
+          for (int e = 0; e < 4; ++e) o[e] = static_cast<T>(final_value<T, CM>(g, acc, cv, i, j, q, e));
           *reinterpret_cast<u32x2*>(D + static_cast<int64_t>(m) * g.sd_m + n) =
               __builtin_bit_cast(u32x2, o);
-        } else if (m < g.M) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < g.N)
-              D[static_cast<int64_t>(m) * g.sd_m + n + e] =
-                  static_cast<T>(final_value<T, HAS_C>(g, acc, Cp, i, j, q, e, m, n));
         }
       }
     }
@@ -504,16 +532,18 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
   const T* Cp = g.use_c ? static_cast<const T*>(g.C) + bat * g.sc_b : nullptr;
   const int mw = m0 + wm * WTM, nw = n0 + wn * WTN;
   char* ep = smem + wave * (WTM * WTN * 2);
-  if (g.staged) {
-    if (Cp != nullptr)
-      store_tile_staged<T, true, TM, TN, WTM, WTN, EVEN, kStreamOutMfma>(g, acc, ep, D, Cp, mw, nw, lane);
+  auto store = [&](auto cm_tag) {
+    constexpr int CM = decltype(cm_tag)::value;
+    if (g.staged)
+      store_tile_staged<T, CM, TM, TN, WTM, WTN, EVEN, kStreamOutMfma>(g, acc, ep, D, Cp, mw, nw, lane);
     else
-      store_tile_staged<T, false, TM, TN, WTM, WTN, EVEN, kStreamOutMfma>(g, acc, ep, D, Cp, mw, nw, lane);
-  } else {
-    if (Cp != nullptr)
-      store_tile_direct<T, true, TM, TN, EVEN>(g, acc, D, Cp, mw, nw, lane);
-    else
-      store_tile_direct<T, false, TM, TN, EVEN>(g, acc, D, Cp, mw, nw, lane);
+      store_tile_direct<T, CM, TM, TN, EVEN>(g, acc, D, Cp, mw, nw, lane);
+  };
+  switch (Cp == nullptr ? kCNone : g.c_mode) {
+    case kCNone: store(std::integral_constant<int, kCNone>{}); break;
+    case kCVec4: store(std::integral_constant<int, kCVec4>{}); break;
+    case kCRow: store(std::integral_constant<int, kCRow>{}); break;
+    default: store(std::integral_constant<int, kCStrided>{}); break;
   }
 }
 
@@ -649,10 +679,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_panel(GemmArgs g, int seg) {
     const int mw = c.m0 + wm * WTM, nw = c.n0 + wn * WTN;
     u32x4 rows[WTM / 8];
     if (g.use_c)
-      stage_tile<T, true, TM, TN, WTM, WTN, true>(g, acc, ep, static_cast<const T*>(g.C) + c.bat * g.sc_b,
-                                                   mw, nw, lane, rows);
+      stage_tile<T, kCStrided, TM, TN, WTM, WTN, true>(g, acc, ep, static_cast<const T*>(g.C) + c.bat * g.sc_b,
+                                                        mw, nw, lane, rows);
     else
-      stage_tile<T, false, TM, TN, WTM, WTN, true>(g, acc, ep, nullptr, mw, nw, lane, rows);
+      stage_tile<T, kCNone, TM, TN, WTM, WTN, true>(g, acc, ep, nullptr, mw, nw, lane, rows);
     wait_lgkmcnt0();
     // Every wave holds its rows: the panels may be refilled.  The next
     // tile's DMA is queued ahead of this tile's stores.
@@ -1229,6 +1259,19 @@ int launch_mfma(const GemmArgs& g, hipStream_t st) {
   return check_launch("gemm");
 }
 
+// Picks the epilogue's C access (see c_values) from C's strides and alignment.
+void set_c_mode(GemmArgs& g) {
+  if (!g.use_c)
+    g.c_mode = kCNone;
+  else if (g.sc_n == 0)
+    g.c_mode = kCRow;
+  else if (g.sc_n == 1 && g.sc_m % 4 == 0 && (g.batch == 1 || g.sc_b % 4 == 0) &&
+           (reinterpret_cast<uintptr_t>(g.C) & 7u) == 0)
+    g.c_mode = kCVec4;
+  else
+    g.c_mode = kCStrided;
+}
+
 // Number of CUs of the current device (queried once per device).
 int cu_count() {
   static int cache[64] = {0};
@@ -1412,6 +1455,7 @@ int gemm_implicit_conv(int dtype, int batch, int M, int N, int K, const void* w,
   g.sc_b = 0;
   g.sc_m = bias ? bias_stride : 0;
   g.sc_n = 0;
+  set_c_mode(g);
   g.staged = (out_ld % 8 == 0 && (batch == 1 || out_batch % 8 == 0) && N % 8 == 0 &&
               (reinterpret_cast<uintptr_t>(out) & 15u) == 0)
                  ? 1
@@ -1484,6 +1528,7 @@ extern "C" int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_
   } else {
     g.sc_b = g.sc_m = g.sc_n = 0;
   }
+  set_c_mode(g);
   hipStream_t st = static_cast<hipStream_t>(stream);
   return dispatch_float16_32(dtype, "gemm", [&](auto tag) {
     using T = decltype(tag);
