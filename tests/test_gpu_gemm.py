@@ -252,6 +252,59 @@ def test_addmm_bias_and_beta_zero(dtype):
     check(got, x, y, dtype, None, 2.0, 0.0, "beta=0")
 
 
+# Every form of addmm's C operand reaches its own epilogue access: a row bias
+# and a full contiguous C are read 4 columns per 8-byte load, a transposed or
+# misaligned C element by element, a column (or scalar) C once per row --
+# on the 128 x 128 kernel with staged and direct stores and on the 256 x 256
+# kernel with ragged edges.
+C_FORMS = ("row_bias", "full", "transposed", "column", "scalar", "misaligned")
+# "direct": the output is a view 8 bytes past a 16-byte boundary, which the
+# staged (16-byte) stores cannot serve
+C_SHAPES = {"128 staged": (200, 136, 96), "128 direct": (200, 136, 96), "256 ragged": (4104, 4112, 520)}
+
+
+def c_operand(form, m, n, dtype, g):
+    """(CPU C in the oracle's broadcastable form, GPU C as addmm receives it)."""
+    if form == "row_bias":
+        c = torch.randn(n, generator=g).to(dtype)
+        return c, c.cuda()
+    if form == "column":
+        c = torch.randn(m, 1, generator=g).to(dtype)
+        return c, c.cuda()
+    if form == "scalar":
+        c = torch.randn(1, 1, generator=g).to(dtype)
+        return c, c.cuda()
+    c = torch.randn(m, n, generator=g).to(dtype)
+    if form == "full":
+        return c, c.cuda()
+    if form == "transposed":
+        return c, c.t().contiguous().cuda().t()
+    buf = torch.empty(m * n + 1, dtype=dtype, device="cuda")
+    cg = buf[1:].view(m, n)
+    cg.copy_(c.cuda())
+    assert cg.data_ptr() % 8 != 0
+    return c, cg
+
+
+@pytest.mark.parametrize("shape", sorted(C_SHAPES))
+@pytest.mark.parametrize("form", C_FORMS)
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_addmm_c_forms(dtype, form, shape):
+    m, n, k = C_SHAPES[shape]
+    g = torch.Generator().manual_seed(C_FORMS.index(form) * 7 + sorted(C_SHAPES).index(shape))
+    a = (0.1 * torch.randn(m, k, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(k, n, generator=g)).to(dtype)
+    c, cg = c_operand(form, m, n, dtype, g)
+    out = None
+    if shape.endswith("direct"):
+        out = torch.empty(m * n + 4, dtype=dtype, device="cuda")[4:].view(m, n)
+        assert out.data_ptr() % 16 == 8
+    got = ntops_amd.torch.addmm(cg, a.cuda(), b.cuda(), beta=0.75, alpha=1.5, out=out)
+    assert _lib.last_kernel().startswith("gemm_mfma " + shape.split()[0])
+    rows = tile_rows(m) if m > 1024 else None
+    assert_gemm_ulp(got, a, b, DT_NAME[dtype], c, 1.5, 0.75, f"addmm C {form} {shape}", rows=rows)
+
+
 # Short-K shapes (K <= 128, M and N multiples of 128): the persistent panel
 # kernel.  Tile counts below, at and above one block per CU, divisible by 8
 # or not (XCD remap on / off), K below the 128-wide panel (zero-filled tail),
