@@ -7,8 +7,21 @@
 // lines 102-104), torch/conv2d.py:8-53 (argument forms, output size from
 // torch/pooling.py:4-19, groups == 1).
 //
-// Three paths:
-//  * implicit GEMM (stride 1, bf16 / fp16, output rows of a multiple of 8
+// Four paths:
+//  * channels-last implicit GEMM (bf16 / fp16, C a multiple of 32, any
+//    stride and dilation): the weights are reordered once per call to
+//    wt[k][((cb * R + r) * S + s) * 32 + ci] (c = 32 cb + ci: the taps of a
+//    32-channel block are consecutive in k, so the GEMM's consecutive K
+//    tiles re-read the same pixels while they are in L2) and each image is
+//    copied once into a
+//    caller-owned workspace as a zero-padded channels-last image
+//    xt[hh][ww][c] = x[c][hh - ph][ww - pw] of Hp = (P - 1) sh + (R - 1) dh + 1
+//    rows of Wp = (Q - 1) sw + (S - 1) dw + 1 pixels, so that output pixel
+//    (p, q) under tap (r, s) reads the C contiguous channels at
+//    xt[p sh + r dh][q sw + s dw]: the GEMM's B operand is K-major with one
+//    row per output pixel (its base fixed for the tile) and one scalar offset
+//    per 32-channel K tile, with no bounds tests (the padding is in the copy);
+//  * implicit GEMM over shifted planes (stride 1, bf16 / fp16, output rows of a multiple of 8
 //    pixels): each image is copied once into a caller-owned workspace as S
 //    column-shifted, zero-padded planes xs[s][c][row][q] =
 //    x[c][row - ph][q + s * dw - pw] with Hp = P + (R - 1) * dh rows of Q
@@ -302,6 +315,125 @@ __global__ __launch_bounds__(256) void k_conv_shift_plane(ConvArgs a, T* xs, int
   }
 }
 
+// Padded channels-last copy of images n0 .. n0 + nb - 1:
+// xt[b][hh][ww][c] = x[n0 + b][c][hh - ph][ww - pw], zero outside the image.
+// One thread per pixel and 8 channels: 8 loads of one channel row each
+// (neighbouring threads read neighbouring pixels of it) and one 16-byte
+// store of the channels.
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_to_cl(ConvArgs a, T* xt, int n0, int nb, int hp, int wp) {
+  const int c8 = a.C / 8;
+  const int64_t total = static_cast<int64_t>(nb) * hp * c8 * wp;
+  const T* x = static_cast<const T*>(a.x);
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int ww = static_cast<int>(i % wp);
+    int64_t t = i / wp;
+    const int j = static_cast<int>(t % c8);
+    t /= c8;
+    const int hh = static_cast<int>(t % hp);
+    const int b = static_cast<int>(t / hp);
+    const int ih = hh - a.ph, iw = ww - a.pw;
+    T v[8];
+    if (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) && static_cast<unsigned>(iw) < static_cast<unsigned>(a.W)) {
+      const T* src = x + (n0 + b) * a.xs[0] + static_cast<int64_t>(j * 8) * a.xs[1] + ih * a.xs[2] + iw * a.xs[3];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = src[e * a.xs[1]];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = static_cast<T>(0.f);
+    }
+    *reinterpret_cast<u32x4*>(xt + ((static_cast<int64_t>(b) * hp + hh) * wp + ww) * a.C + j * 8) =
+        __builtin_bit_cast(u32x4, v);
+  }
+}
+
+// Same output as k_conv_to_cl for contiguous 16-byte aligned input rows of a
+// multiple of 8 pixels that fit the padded row (pw + W <= wp): a thread
+// moves an 8 x 8 block -- 8 pixels of 8 channels -- with eight 16-byte loads
+// along the pixels of each channel, a transpose in registers and eight
+// 16-byte stores along the channels of each pixel; neighbouring threads take
+// neighbouring channel groups, so each pixel's C channels are written as
+// one contiguous run.  Threads past the blocks zero the padding columns.
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_to_cl8(ConvArgs a, T* xt, int n0, int nb, int hp, int wp) {
+  const int c8 = a.C / 8, w8 = a.W / 8, npad = wp - a.W;
+  const int64_t body = static_cast<int64_t>(nb) * hp * w8 * c8;
+  const int64_t total = body + static_cast<int64_t>(nb) * hp * npad * c8;
+  const T* x = static_cast<const T*>(a.x);
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (i < body) {
+      const int j = static_cast<int>(i % c8);
+      int64_t t = i / c8;
+      const int pg = static_cast<int>(t % w8);
+      t /= w8;
+      const int hh = static_cast<int>(t % hp);
+      const int b = static_cast<int>(t / hp);
+      const int ih = hh - a.ph;
+      T* dst = xt + ((static_cast<int64_t>(b) * hp + hh) * wp + a.pw + pg * 8) * a.C + j * 8;
+      u32x4 out[8];
+      if (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H)) {
+        const T* src = x + (n0 + b) * a.xs[0] + static_cast<int64_t>(j * 8) * a.xs[1] + ih * a.xs[2] + pg * 8;
+        u32x4 in[8];  // in[e]: pixels 0..7 of channel 8j + e, two per word
+#pragma unroll
+        for (int e = 0; e < 8; ++e) in[e] = *reinterpret_cast<const u32x4*>(src + e * a.xs[1]);
+        // out[f] word k: channels 2k (low half) and 2k + 1 (high half) of pixel f
+#pragma unroll
+        for (int f = 0; f < 8; ++f)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = in[2 * k][f / 2], hi = in[2 * k + 1][f / 2];
+            out[f][k] = (f & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+          }
+      } else {
+#pragma unroll
+        for (int f = 0; f < 8; ++f) out[f] = u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int f = 0; f < 8; ++f) *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(f) * a.C) = out[f];
+    } else {
+      const int64_t k = i - body;
+      const int j = static_cast<int>(k % c8);
+      int64_t t = k / c8;
+      const int pp = static_cast<int>(t % npad);
+      t /= npad;
+      const int hh = static_cast<int>(t % hp);
+      const int b = static_cast<int>(t / hp);
+      const int ww = pp < a.pw ? pp : a.W + pp;  // padding columns [0, pw) and [pw + W, wp)
+      *reinterpret_cast<u32x4*>(xt + ((static_cast<int64_t>(b) * hp + hh) * wp + ww) * a.C + j * 8) =
+          u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+// Weights in the channels-last GEMM's k order (32-channel blocks, then
+// taps, then the block's channels): wt[k][((cb * R + r) * S + s) * 32 + ci]
+// = w[k][32 cb + ci][r][s].  One thread per 8 channels: 8 loads, one
+// 16-byte store.
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_weights_cl(ConvArgs a, T* wt) {
+  const int64_t crs = static_cast<int64_t>(a.C) * a.R * a.S;
+  const int64_t total = static_cast<int64_t>(a.K) * crs / 8;
+  const T* w = static_cast<const T*>(a.w);
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int ci8 = static_cast<int>(i % 4) * 8;  // the 8 channels' offset in the block
+    int64_t t = i / 4;
+    const int s = static_cast<int>(t % a.S);
+    t /= a.S;
+    const int r = static_cast<int>(t % a.R);
+    t /= a.R;
+    const int cb = static_cast<int>(t % (a.C / 32));
+    const int k = static_cast<int>(t / (a.C / 32));
+    const T* src = w + k * a.ws[0] + static_cast<int64_t>(cb * 32 + ci8) * a.ws[1] + r * a.ws[2] + s * a.ws[3];
+    T v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = src[e * a.ws[1]];
+    *reinterpret_cast<u32x4*>(wt + i * 8) = __builtin_bit_cast(u32x4, v);
+  }
+}
+
 unsigned grid_for(int64_t work, int per_block) {
   int64_t g = (work + per_block - 1) / per_block;
   if (g > 65536) g = 65536;  // grid-stride loops cover the rest
@@ -344,10 +476,36 @@ bool use_implicit(const ConvArgs& a, int dt) {
          elems * 2 < (int64_t(1) << 31) && (256 * a.ws[0] + crs) * 2 < (int64_t(1) << 31) && out_ok;
 }
 
+// Rows and pixels per row of the channels-last padded copy.
+int64_t cl_rows(const ConvArgs& a) { return static_cast<int64_t>(a.P - 1) * a.sh + static_cast<int64_t>(a.R - 1) * a.dh + 1; }
+int64_t cl_cols(const ConvArgs& a) { return static_cast<int64_t>(a.Q - 1) * a.sw + static_cast<int64_t>(a.S - 1) * a.dw + 1; }
+
+// Whether the channels-last implicit GEMM applies (on top of use_gemm):
+// 16-bit data, C a multiple of the GEMM's 32-channel K tile, P * Q a
+// multiple of 4 with the output channel and image strides multiples of 4
+// elements at an 8-byte aligned address (the epilogue's store width), and
+// each padded image and the weight matrix inside the 2 GiB buffer range.
+bool use_channels_last(const ConvArgs& a, int dt) {
+  const int64_t crs = static_cast<int64_t>(a.C) * a.R * a.S;
+  const int64_t pq = static_cast<int64_t>(a.P) * a.Q;
+  const bool out_ok = a.os[1] % 4 == 0 && a.os[0] % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 7u) == 0;
+  return (dt == NTOPS_BF16 || dt == NTOPS_F16) && a.C % 32 == 0 && pq % 4 == 0 && out_ok &&
+         cl_rows(a) * cl_cols(a) * a.C * 2 < (int64_t(1) << 31) && 257 * crs * 2 < (int64_t(1) << 31) &&
+         crs <= 0x7fffffffLL && pq <= 0x7fffffffLL;
+}
+
 // Workspace bytes per image of the chosen GEMM path.
 int64_t ws_bytes_per_image(const ConvArgs& a, int dt) {
+  if (use_channels_last(a, dt)) return cl_rows(a) * cl_cols(a) * a.C * dtype_size(dt);
   if (use_implicit(a, dt)) return static_cast<int64_t>(a.S) * a.C * shift_rows(a) * a.Q * dtype_size(dt);
   return col_bytes_per_image(a, dt);
+}
+
+// Workspace bytes the chosen GEMM path needs once per call, ahead of the
+// images' (the channels-last path's reordered weights, rounded up to 256).
+int64_t ws_bytes_fixed(const ConvArgs& a, int dt) {
+  if (!use_channels_last(a, dt)) return 0;
+  return (static_cast<int64_t>(a.K) * a.C * a.R * a.S * dtype_size(dt) + 255) / 256 * 256;
 }
 
 int fill_args(ConvArgs& a, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
@@ -391,8 +549,9 @@ extern "C" int64_t ntops_conv2d_workspace(int dtype, int64_t N, int64_t C, int64
     a.os[i] = out_strides[i];
   }
   a.w = nullptr;  // alignment is checked again on the call
+  a.out = nullptr;
   if (!use_gemm(a, dtype)) return 0;
-  return ws_bytes_per_image(a, dtype) * N;
+  return ws_bytes_fixed(a, dtype) + ws_bytes_per_image(a, dtype) * N;
 }
 
 extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R,
@@ -420,8 +579,9 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t per_image = dtype_size(dtype) ? ws_bytes_per_image(a, dtype) : 0;
+  const int64_t fixed = dtype_size(dtype) ? ws_bytes_fixed(a, dtype) : 0;
   const bool gemm = dtype_size(dtype) && use_gemm(a, dtype) && workspace && per_image > 0 &&
-                    workspace_bytes >= per_image && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0;
+                    workspace_bytes >= fixed + per_image && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0;
   if (!gemm) {
     return dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
       using T = decltype(tag);
@@ -431,6 +591,56 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
     });
   }
   const int64_t crs = C * R * S;
+  if (use_channels_last(a, dtype)) {
+    // channels-last implicit GEMM: weights reordered into the workspace's
+    // first `fixed` bytes, then chunks of images that fit the rest
+    const int64_t hp = cl_rows(a), wp = cl_cols(a);
+    const int64_t img = hp * wp * C;  // elements of one padded image
+    const int64_t nb_max = std::min<int64_t>(N, (workspace_bytes - fixed) / per_image);
+    void* wt = workspace;
+    void* xt = static_cast<char*>(workspace) + fixed;
+    rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
+      using T = decltype(tag);
+      if constexpr (sizeof(T) != 2) {
+        return set_error(NTOPS_ERR_INVALID, "conv2d: the channels-last path needs 16-bit data");
+      } else {
+        hipLaunchKernelGGL(k_conv_weights_cl<T>, dim3(grid_for(K * crs / 8, 256)), dim3(256), 0, st, a,
+                           static_cast<T*>(wt));
+        return check_launch("conv2d");
+      }
+    });
+    if (rc != NTOPS_OK) return rc;
+    for (int64_t n0 = 0; n0 < N; n0 += nb_max) {
+      const int64_t nb = std::min(nb_max, N - n0);
+      rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
+        using T = decltype(tag);
+        if constexpr (sizeof(T) != 2) {
+          return set_error(NTOPS_ERR_INVALID, "conv2d: the channels-last path needs 16-bit data");
+        } else {
+          const bool rows16 = a.xs[3] == 1 && a.xs[2] % 8 == 0 && a.xs[1] % 8 == 0 && a.xs[0] % 8 == 0 &&
+                              W % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && pad_w + W <= wp;
+          if (rows16)
+            hipLaunchKernelGGL(k_conv_to_cl8<T>, dim3(grid_for(nb * hp * (C / 8) * (W / 8 + wp - W), 256)),
+                               dim3(256), 0, st, a, static_cast<T*>(xt), static_cast<int>(n0), static_cast<int>(nb),
+                               static_cast<int>(hp), static_cast<int>(wp));
+          else
+            hipLaunchKernelGGL(k_conv_to_cl<T>, dim3(grid_for(nb * hp * (C / 8) * wp, 256)), dim3(256), 0, st, a,
+                               static_cast<T*>(xt), static_cast<int>(n0), static_cast<int>(nb), static_cast<int>(hp),
+                               static_cast<int>(wp));
+          return check_launch("conv2d");
+        }
+      });
+      if (rc != NTOPS_OK) return rc;
+      void* dst = static_cast<char*>(out) + n0 * out_strides[0] * dtype_size(dtype);
+      rc = gemm_conv_channels_last(dtype, static_cast<int>(nb), static_cast<int>(K), static_cast<int>(P * Q),
+                                   static_cast<int>(crs), wt, xt, img, static_cast<int>(R), static_cast<int>(S),
+                                   static_cast<int>(C), static_cast<int>(Q), static_cast<int>(stride_h),
+                                   static_cast<int>(stride_w), static_cast<int>(wp), static_cast<int>(dil_h),
+                                   static_cast<int>(dil_w), bias, bias_stride, dst, out_strides[0], out_strides[1], st);
+      if (rc != NTOPS_OK) return rc;
+    }
+    return NTOPS_OK;
+  }
   if (use_implicit(a, dtype)) {
     // implicit GEMM, in chunks of images that fit the workspace
     const int64_t hp = shift_rows(a);

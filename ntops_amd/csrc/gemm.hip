@@ -73,6 +73,16 @@ struct GemmArgs {
   int cv_rs, cv_r, cv_s;
   int cv_ds, cv_dr, cv_dc;  // BK k-rows expressed as (s, r, c) steps: BK = (dc * R + dr) * S + ds
   int64_t cv_per_s, cv_per_c, cv_per_r;
+  // Channels-last convolution operand (CONV == 2): B is K-major with one row
+  // per output pixel n of the batch's image, p = n / cl_q, q = n % cl_q,
+  // starting at element (p * cl_sh * cl_wp + q * cl_sw) * cl_c of the
+  // batch's zero-padded (rows of cl_wp pixels, cl_c channels each) image.
+  // k runs over 32-channel blocks, then taps, then the block's channels:
+  // k = ((cb * cv_r + r) * cv_s + s) * 32 + ci adds (r * cl_dh * cl_wp +
+  // s * cl_dw) * cl_c + 32 * cb + ci, so one K tile is one (block, tap) and
+  // the R * S tiles of a block, which read overlapping pixels, follow each
+  // other (the reuse stays within L2).
+  int cl_q, cl_sh, cl_sw, cl_wp, cl_c, cl_dh, cl_dw;
 };
 
 
@@ -115,9 +125,13 @@ __device__ __forceinline__ void tile_of(int pid, int nblocks, int tm_count, int 
 // One operand's global -> LDS stream for a tile of R rows/columns x BK k.
 // The tile is R * BK * 2 bytes: R * BK / 512 one-KiB load instructions,
 // spread evenly over the NW waves of the block.
-template <int R, bool KMAJ, int NW, bool EVEN, int BK, bool CONV = false>
+// CONV: 0 a plain operand; 1 the shifted-plane convolution operand (N-major,
+// per-lane k-row bases); 2 the channels-last convolution operand (K-major,
+// per-lane pixel bases plus one scalar offset per K tile).
+template <int R, bool KMAJ, int NW, bool EVEN, int BK, int CONV = 0>
 struct TileLoader {
-  static_assert(!CONV || !KMAJ, "the implicit convolution operand is N-major");
+  static_assert(CONV != 1 || !KMAJ, "the shifted-plane convolution operand is N-major");
+  static_assert(CONV != 2 || KMAJ, "the channels-last convolution operand is K-major");
   static constexpr int kInst = R * BK / 512 / NW;
   static_assert(kInst * NW * 512 == R * BK, "tile must split evenly over the waves");
   static constexpr int kCprK = BK / 8;  // chunks per row (K-major)
@@ -130,7 +144,10 @@ struct TileLoader {
   int lds_base;           // first instruction's LDS offset inside the operand tile
   // implicit convolution (CONV): this lane's k-row of each instruction for
   // the next tile to issue, as (c, r, s) -- advanced by BK per tile
-  int cv_c[CONV ? kInst : 1], cv_r[CONV ? kInst : 1], cv_s[CONV ? kInst : 1];
+  int cv_c[CONV == 1 ? kInst : 1], cv_r[CONV == 1 ? kInst : 1], cv_s[CONV == 1 ? kInst : 1];
+  // channels-last convolution (CONV == 2): the tap (r, s) and first channel
+  // c0 of the next K tile to issue
+  int cl_r = 0, cl_s = 0, cl_c0 = 0;
 
   // base: element pointer at the tile origin; ld: row stride (K-major) or
   // k-row stride (M/N-major), in elements; extent_bytes: readable bytes.
@@ -165,9 +182,25 @@ struct TileLoader {
         const int q = wave * kInst + i;
         const int krow = q * rows_per_inst + lane / kCprMN;
         const int c = mnslot(krow, lane % kCprMN);
-        voff[i] = static_cast<uint32_t>((CONV ? 0 : krow * ld * 2) + c * 16);
+        voff[i] = static_cast<uint32_t>((CONV == 1 ? 0 : krow * ld * 2) + c * 16);
         lim_row[i] = krow;
         lim_col[i] = c * 8;
+      }
+    }
+  }
+
+  // Channels-last convolution: each instruction's row is output pixel
+  // n0 + row; its offset becomes that pixel's element in the padded image
+  // (rows past the image's last pixel keep a valid offset and are rejected
+  // by lim_row when !EVEN).
+  __device__ __forceinline__ void conv_cl_init(const GemmArgs& g, int n0) {
+    if constexpr (CONV == 2) {
+#pragma unroll
+      for (int i = 0; i < kInst; ++i) {
+        const int n = min(n0 + lim_row[i], g.N - 1);
+        const int p = n / g.cl_q, q = n - p * g.cl_q;
+        const int64_t pix = (static_cast<int64_t>(p) * g.cl_sh * g.cl_wp + static_cast<int64_t>(q) * g.cl_sw) * g.cl_c;
+        voff[i] = static_cast<uint32_t>(pix * 2 + lim_col[i] * 2);
       }
     }
   }
@@ -175,7 +208,7 @@ struct TileLoader {
   // Implicit convolution: the (c, r, s) of each instruction's k-row at
   // k0 = 0 (k-row kg = (c * R + r) * S + s).
   __device__ __forceinline__ void conv_init(const GemmArgs& g) {
-    if constexpr (CONV) {
+    if constexpr (CONV == 1) {
 #pragma unroll
       for (int i = 0; i < kInst; ++i) {
         const int kg = lim_row[i];
@@ -201,10 +234,25 @@ struct TileLoader {
   // CONV: tiles must be issued in order k0 = 0, BK, 2 BK, ... (each call
   // advances the (c, r, s) state by BK k-rows).
   __device__ __forceinline__ void issue(char* lds, int k0, int valid, int K, const GemmArgs* cv = nullptr) {
+    // channels-last: the tile's (channel block, tap) offset in bytes, then
+    // advance to the next K tile's: the next tap, after the last tap the
+    // next block
+    uint32_t cl_off = 0;
+    if constexpr (CONV == 2) {
+      static_assert(BK == 32, "one K tile is one 32-channel block under one tap");
+      cl_off = static_cast<uint32_t>(((cl_r * cv->cl_dh * cv->cl_wp + cl_s * cv->cl_dw) * cv->cl_c + cl_c0) * 2);
+      if (++cl_s >= cv->cv_s) {
+        cl_s = 0;
+        if (++cl_r >= cv->cv_r) {
+          cl_r = 0;
+          cl_c0 += BK;
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
       uint32_t off;
-      if constexpr (CONV) {
+      if constexpr (CONV == 1) {
         // row base of k-row (c, r, s), then advance it by BK k-rows
         const int64_t base = cv_s[i] * cv->cv_per_s + cv_c[i] * cv->cv_per_c + cv_r[i] * cv->cv_per_r;
         off = voff[i] + static_cast<uint32_t>(base * 2);
@@ -215,6 +263,8 @@ struct TileLoader {
         const int cr = cv_r[i] >= cv->cv_r ? 1 : 0;
         cv_r[i] -= cr * cv->cv_r;
         cv_c[i] += cv->cv_dc + cr;
+      } else if constexpr (CONV == 2) {
+        off = voff[i] + cl_off;
       } else {
         off = voff[i] + static_cast<uint32_t>(k0) * k_stride_bytes;
       }
@@ -416,7 +466,7 @@ constexpr bool kStreamOutPanel = true;
 // kt + STAGES - 1 are issued right after the barrier that opens tile kt, so
 // an operand fetch that misses L2 has STAGES - 1 tiles of MFMA work to land.
 template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN,
-          bool CONV = false>
+          int CONV = 0>
 __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
@@ -449,9 +499,12 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
             (static_cast<int64_t>(m_valid - 1) * g.sa_m + g.K) * 2, wave, lane);
   else
     la.init(A + m0, g.sa_k, (static_cast<int64_t>(g.K - 1) * g.sa_k + m_valid) * 2, wave, lane);
-  if constexpr (CONV) {
+  if constexpr (CONV == 1) {
     lb.init(B + n0, 0, (g.sb_b - n0) * 2, wave, lane);  // the batch's whole buffer
     lb.conv_init(g);
+  } else if constexpr (CONV == 2) {
+    lb.init(B, 0, g.sb_b * 2, wave, lane);  // the batch's whole padded image
+    lb.conv_cl_init(g, n0);
   }
   else if constexpr (BKM)
     lb.init(B + static_cast<int64_t>(n0) * g.sb_n, g.sb_n,
@@ -1239,7 +1292,7 @@ __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
 
 // ---- host dispatch ---------------------------------------------------------
 template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN,
-          bool CONV = false>
+          int CONV = 0>
 int launch_mfma(const GemmArgs& g, hipStream_t st) {
   constexpr int NT = WM * WN * 64;
   constexpr int kLds = STAGES * (BM + BN) * BK * 2;
@@ -1254,7 +1307,7 @@ int launch_mfma(const GemmArgs& g, hipStream_t st) {
   const int64_t tiles = static_cast<int64_t>((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN) * g.batch;
   if (tiles > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "gemm: too many tiles");
   note_kernel("gemm_mfma %dx%d s%d %s %s %s%s", BM, BN, STAGES, AK ? "A:K" : "A:M", BKM ? "B:K" : "B:N",
-              EVEN ? "even" : "ragged", CONV ? " conv" : "");
+              EVEN ? "even" : "ragged", CONV == 1 ? " conv" : CONV == 2 ? " conv_cl" : "");
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles)), dim3(NT), kLds, st, g);
   return check_launch("gemm");
 }
@@ -1405,18 +1458,20 @@ int run_gemm(GemmArgs g, hipStream_t st) {
   return check_launch("gemm");
 }
 
-template <typename T>
+// CONV 1: shifted planes (B N-major); CONV 2: channels-last (B K-major).
+template <typename T, int CONV>
 int run_implicit_conv(const GemmArgs& g, hipStream_t st) {
   constexpr int kBK = 32, kStages = 4;
+  constexpr bool BKM = CONV == 2;
   const int64_t big_tiles = static_cast<int64_t>((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
   if (big_tiles >= 240 && g.K > 256) {
     if (g.M % 256 == 0 && g.N % 256 == 0 && g.K % kBK == 0)
-      return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, true, false, true, true>(g, st);
-    return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, true, false, false, true>(g, st);
+      return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, true, BKM, true, CONV>(g, st);
+    return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, true, BKM, false, CONV>(g, st);
   }
   if (g.M % 128 == 0 && g.N % 128 == 0 && g.K % kBK == 0)
-    return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, true, false, true, true>(g, st);
-  return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, true, false, false, true>(g, st);
+    return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, true, BKM, true, CONV>(g, st);
+  return launch_mfma<T, 128, 128, 2, 2, kBK, kStages, true, BKM, false, CONV>(g, st);
 }
 
 }  // namespace
@@ -1471,9 +1526,64 @@ int gemm_implicit_conv(int dtype, int batch, int M, int N, int K, const void* w,
   g.cv_per_c = per_c;
   g.cv_per_r = per_r;
   switch (dtype) {
-    case NTOPS_BF16: return run_implicit_conv<__bf16>(g, st);
-    case NTOPS_F16: return run_implicit_conv<_Float16>(g, st);
+    case NTOPS_BF16: return run_implicit_conv<__bf16, 1>(g, st);
+    case NTOPS_F16: return run_implicit_conv<_Float16, 1>(g, st);
     default: return set_error(NTOPS_ERR_UNSUPPORTED, "conv2d: the implicit GEMM needs BF16 or F16");
+  }
+}
+
+int gemm_conv_channels_last(int dtype, int batch, int M, int N, int K, const void* w, const void* xt,
+                            int64_t img_elems, int R, int S, int C, int Q, int sh, int sw, int wp, int dh,
+                            int dw, const void* bias, int64_t bias_stride, void* out, int64_t out_batch,
+                            int64_t out_ld, hipStream_t st) {
+  if (batch <= 0 || M <= 0 || N <= 0 || K <= 0) return NTOPS_OK;
+  if (!aligned16(w) || !aligned16(xt) || C % 32 || K != R * S * C || N % 4 || img_elems % 8 || out_ld % 4 ||
+      out_batch % 4 || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return set_error(NTOPS_ERR_UNSUPPORTED, "conv2d: operand layout unsuited to the channels-last GEMM");
+  if (img_elems * 2 >= (int64_t(1) << 31) || (257 * static_cast<int64_t>(K)) * 2 >= (int64_t(1) << 31))
+    return set_error(NTOPS_ERR_UNSUPPORTED, "conv2d: operand exceeds the 2 GiB buffer range");
+  GemmArgs g{};
+  g.A = w;
+  g.B = xt;
+  g.D = out;
+  g.sa_b = 0;
+  g.sa_m = K;
+  g.sa_k = 1;
+  g.sb_b = img_elems;
+  g.sb_k = 1;
+  g.sb_n = 0;  // rows come from the convolution geometry
+  g.sd_b = out_batch;
+  g.sd_m = out_ld;
+  g.sd_n = 1;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.batch = batch;
+  g.alpha = 1.f;
+  g.beta = bias ? 1.f : 0.f;
+  g.use_c = bias ? 1 : 0;
+  g.C = bias;
+  g.sc_b = 0;
+  g.sc_m = bias ? bias_stride : 0;
+  g.sc_n = 0;
+  set_c_mode(g);
+  g.staged = (out_ld % 8 == 0 && (batch == 1 || out_batch % 8 == 0) && N % 8 == 0 &&
+              (reinterpret_cast<uintptr_t>(out) & 15u) == 0)
+                 ? 1
+                 : 0;
+  g.cv_r = R;
+  g.cv_s = S;
+  g.cl_q = Q;
+  g.cl_sh = sh;
+  g.cl_sw = sw;
+  g.cl_wp = wp;
+  g.cl_c = C;
+  g.cl_dh = dh;
+  g.cl_dw = dw;
+  switch (dtype) {
+    case NTOPS_BF16: return run_implicit_conv<__bf16, 2>(g, st);
+    case NTOPS_F16: return run_implicit_conv<_Float16, 2>(g, st);
+    default: return set_error(NTOPS_ERR_UNSUPPORTED, "conv2d: the channels-last GEMM needs BF16 or F16");
   }
 }
 

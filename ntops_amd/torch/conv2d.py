@@ -75,8 +75,10 @@ def conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
     ws_bytes = lib.ntops_conv2d_workspace(dt, *geometry, _strides(weight), _strides(output))
     workspace = None
     if ws_bytes > 0:
-        per_image = ws_bytes // n
-        size = max(per_image, min(ws_bytes, _WORKSPACE_CAP // per_image * per_image))
+        # the whole batch in one pass if it fits the cap, else chunks: at
+        # least what one image needs (its bytes plus any per-call part)
+        one = lib.ntops_conv2d_workspace(dt, 1, *geometry[1:], _strides(weight), _strides(output))
+        size = min(ws_bytes, max(one, _WORKSPACE_CAP))
         workspace = torch.empty(size, dtype=torch.uint8, device=dev)
     with _DeviceGuard(dev):
         rc = lib.ntops_conv2d(

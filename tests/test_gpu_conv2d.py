@@ -61,7 +61,22 @@ GEMM_CASES = [
     (2, 64, 20, 21, 40, 3, 3, (2, 3), (2, 3), (2, 3), False),
     (1, 128, 14, 14, 256, 1, 1, 1, 0, 1, True),
     (2, 16, 31, 29, 64, 5, 5, 1, 2, 1, True),
+    (2, 48, 16, 16, 64, 3, 3, 1, 1, 1, True),
+    (1, 128, 16, 16, 256, 1, 1, 1, 0, 1, True),
+    (2, 32, 33, 22, 64, 3, 3, (2, 1), (1, 2), (2, 3), True),
 ]
+
+
+def expected_path(dtype, c, p, q, stride):
+    """Kernel family of the GEMM paths: the channels-last implicit GEMM for
+    16-bit data with C % 32 == 0 and P * Q % 4 == 0, the implicit GEMM over
+    shifted planes for the rest of the 16-bit stride-1 problems with
+    Q % 8 == 0, otherwise unfold + GEMM."""
+    if dtype != torch.float32 and c % 32 == 0 and (p * q) % 4 == 0:
+        return " conv_cl"
+    if dtype != torch.float32 and pair(stride) == (1, 1) and q % 8 == 0:
+        return " conv"
+    return ""
 
 
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
@@ -80,14 +95,36 @@ def test_conv2d_gemm_path(case, dtype):
     assert ws > 0, "expected the GEMM path"
     got = conv2d(x.cuda(), wt.cuda(), bias=None if b is None else b.cuda(), stride=stride, padding=padding,
                  dilation=dilation)
+    kern = _lib.last_kernel()
+    want = expected_path(dtype, c, P, Q, stride)
+    assert kern.startswith("gemm_") and (kern.endswith(want) if want else not kern.endswith("conv") and
+                                         not kern.endswith("conv_cl")), kern
     exp = oracle(x, wt, b, stride, padding, dilation)
     tol = (2e-5, 2e-5) if dtype == torch.float32 else TOL[dtype]
     assert_close(got, exp, *tol, "conv2d gemm path")
 
 
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_conv2d_channels_last_256_tiles(dtype):
+    """240 images of 16 x 16 pixels into 256 channels: 240 full 256 x 256
+    tiles, the channels-last implicit GEMM's even large-tile kernel (K = 288);
+    images at both ends and in the middle against the oracle."""
+    g = torch.Generator().manual_seed(17)
+    n, c, h, k = 240, 32, 16, 256
+    x = torch.randn(n, c, h, h, generator=g).to(dtype)
+    wt = (torch.randn(k, c, 3, 3, generator=g) / 17).to(dtype)
+    b = torch.randn(k, generator=g).to(dtype)
+    got = conv2d(x.cuda(), wt.cuda(), b.cuda(), padding=1)
+    assert _lib.last_kernel() == "gemm_mfma 256x256 s4 A:K B:K even conv_cl"
+    for img in (0, 119, 239):
+        exp = oracle(x[img:img + 1], wt, b, 1, 1, 1)
+        assert_close(got[img:img + 1], exp, *TOL[dtype], f"image {img}")
+
+
 def test_conv2d_workspace_chunks():
-    """One image per chunk (workspace of exactly one image), and a workspace
-    too small for one image (direct kernel): both equal the one-chunk run."""
+    """One image per chunk (workspace of exactly what one image needs), and a
+    workspace too small for one image (direct kernel): both equal the
+    one-chunk run."""
     dtype = torch.bfloat16
     n, c, h, w, k = 5, 64, 18, 18, 64
     g = torch.Generator().manual_seed(9)
@@ -99,8 +136,10 @@ def test_conv2d_workspace_chunks():
     geo = (n, c, h, w, k, 3, 3, h, w, 1, 1, 1, 1, 1, 1)
     st = lambda t: _lib.i64_array(t.stride())  # noqa: E731
     total = lib.ntops_conv2d_workspace(_lib.dtype_code(dtype), *geo, st(wt), st(full))
-    assert total > 0 and total % n == 0
-    for ws_bytes in (total // n, total // n - 16):
+    one = lib.ntops_conv2d_workspace(_lib.dtype_code(dtype), 1, *geo[1:], st(wt), st(full))
+    # the bytes of every image plus a per-call part (the reordered weights)
+    assert 0 < one < total and (total - one) % (n - 1) == 0
+    for ws_bytes in (one, one - 16):
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
         out = torch.empty_like(full)
         rc = lib.ntops_conv2d(_lib.dtype_code(dtype), *geo, x.data_ptr(), st(x), wt.data_ptr(), st(wt), b.data_ptr(), 1,

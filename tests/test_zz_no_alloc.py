@@ -63,12 +63,12 @@ def _inputs(n, c, h, k, r, dtype, seed):
 
 
 def test_conv2d_noalloc_matches_workspace_entry():
-    # 1) bf16 (32, 256, 56, 56) * (256, 256, 3, 3), padding 1: the implicit
-    #    GEMM over shifted planes; 5.0 MB per image, so the 64 MiB scratch
-    #    runs it in three chunks (13 + 13 + 6 images) where the workspace
-    #    entry runs one.
+    # 1) bf16 (32, 256, 56, 56) * (256, 256, 3, 3), padding 1: the
+    #    channels-last implicit GEMM, 1.7 MB per padded image plus 1.2 MB of
+    #    reordered weights, all in the scratch at once.
     # 2) fp16 (3, 64, 21, 21) * (96, 64, 3, 3), stride 2, padding 1: the
-    #    unfold + GEMM path, smaller, over scratch holding call 1's planes.
+    #    unfold + GEMM path (11 x 11 output pixels), smaller, over scratch
+    #    holding call 1's padded images.
     cases = [
         ((32, 256, 56, 256, 3, torch.bfloat16, 0), 1, 1),
         ((3, 64, 21, 96, 3, torch.float16, 1), 2, 1),
@@ -94,7 +94,7 @@ def test_conv2d_noalloc_rejects_images_beyond_the_scratch():
     """One image needing more than the scratch holds: an error naming the
     limit, before any launch (pointers are never dereferenced)."""
     lib = _lib.load()
-    n, c, h, k = 1, 256, 256, 64
+    n, c, h, k = 1, 256, 400, 64
     geo = (n, c, h, h, k, 3, 3, h, h, 1, 1, 1, 1, 1, 1)
     wst = _lib.i64_array((c * 9, 9, 3, 1))
     ost = _lib.i64_array((k * h * h, h * h, h, 1))
