@@ -317,10 +317,13 @@ NTOPS_API int ntops_rope_qk(int dtype, int64_t B, int64_t S, int64_t Hq, int64_t
  * described by its 4 element strides; bias may be NULL (bias_stride is its
  * element stride).  fp32 accumulation, one rounding to dtype (BF16, F16,
  * F32).  workspace (device memory of workspace_bytes, 16-byte aligned, may
- * be NULL) lets large problems run as an unfold + matrix-core GEMM over
- * chunks of images; ntops_conv2d_workspace returns the bytes that cover the
- * whole batch in one chunk (0 when the problem runs without a workspace).
- * Without enough workspace for one image the direct kernel runs. */
+ * be NULL) lets large problems run as a matrix-core GEMM over a rearranged
+ * copy of the input (padded channels-last images, shifted planes or the
+ * unfold), in chunks of images; ntops_conv2d_workspace returns the bytes
+ * that cover the whole batch in one chunk (0 when the problem runs without a
+ * workspace): a per-call part plus a part per image, so its value for N = 1
+ * is what one chunk of one image needs.  With less than that the direct
+ * kernel runs. */
 NTOPS_API int64_t ntops_conv2d_workspace(int dtype, int64_t N, int64_t C, int64_t H, int64_t W,
                int64_t K, int64_t R, int64_t S, int64_t P, int64_t Q,
                int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
