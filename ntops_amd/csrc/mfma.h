@@ -31,14 +31,17 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
 }
 
 // Chunk slot of 16-byte chunk `c` of row `r` in a K-major tile whose rows
-// hold BK k values (BK / 8 chunks); conflict-free for the fragment reads
-// (16 lanes per pass, rows r .. r + 15).
+// hold BK k values (BK / 8 chunks).  Every form is an involution and gives
+// zero SQ_LDS_BANK_CONFLICT for the fragment reads (ds_read_b128, lanes
+// 0-31 rows r0 .. r0 + 31 at chunk c, lanes 32-63 the same rows at c + 1,
+// c even); for BK = 64, c ^ ((r >> 1 + r >> 4) & 7), c ^ (r & 7) and
+// c ^ ((r >> 2) & 7) each conflict on every read (256 vs 414 B per clock).
 template <int BK>
 __device__ __forceinline__ int kslot(int r, int c) {
   if constexpr (BK == 128)
     return c ^ (r & 15);
   else if constexpr (BK == 64)
-    return c ^ (((r >> 1) + (r >> 4)) & 7);
+    return c ^ ((r >> 1) & 7);
   else
     return c ^ ((r >> 2) & 3);
 }
