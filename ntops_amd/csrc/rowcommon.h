@@ -106,72 +106,26 @@ inline bool pick_row_cfg(int64_t npk, VecCfg* cfg) {
   MACRO(4, 16)                 \
   MACRO(8, 16)
 
+// Group g's packs of this lane (block g holds rows g * RPB ..); zeros past
+// the row end or past `rows` (buffer loads against the row's extent: no
+// branches).  Each block handles one row group: a persistent grid with one
+// group of register prefetch (weight and bias held for all the block's
+// rows) measured 2 % slower on layer_norm bf16 (16384, 4096) and ~2 %
+// slower on rms_norm.
+template <int WPR, typename T, int CHUNKS>
+__device__ __forceinline__ void load_row_packs(Pack16<T> (&r)[CHUNKS], const T* base, int64_t stride,
+                                               int64_t rows, const RowPos& p, int npk, int64_t g) {
+  const int64_t row = g * RowShape<WPR>::kRowsPerBlock + p.row_in_block;
+  const bool ok = row < rows;
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(base + (ok ? row : 0) * stride, ok ? npk * 16u : 0u);
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) r[c] = buffer_load16_nt<T>(rs, pack_of<WPR>(p, c) * 16u);
+}
+
 // The V per-column parameters (weight or bias, type W) that go with one
 // 16-byte pack of the row, kept in their own type from load to use
 // (V * sizeof(W) bytes: one 16-byte load for W == T, two for float with a
 // 16-bit T).
-// Row-group loop.  A block handles row groups (the RPB rows it holds at
-// once) g0, g0 + G, g0 + 2G, ...  Kernels with a long reduction phase
-// (layer_norm: two dependent reductions) run it streaming (STREAM): the grid
-// is the number of blocks resident at once and the block carries one group
-// of register prefetch, so while group g is reduced and written, group
-// g + G's loads are in flight and each CU keeps HBM reads outstanding
-// through the reduction and store phases; per-column parameters (weight,
-// bias) are then loaded once per block, since every row a lane touches uses
-// the same packs.  Measured on MI355X this lifts layer_norm bf16
-// (16384, 4096) from 63% to 69% of HBM peak, while rms_norm, whose
-// reduction is short, loses ~2% to it: those kernels run one group per block
-// (grid = groups) and load parameters at the point of use.  The 1024-thread
-// shapes (16 waves per row) never stream: a second group or resident
-// parameters would cost occupancy or spill.
-template <int CHUNKS, int WPR>
-constexpr bool kCanStream = CHUNKS * WPR <= 16;
-
-// Group stride of the loop.  Without streaming the grid is `groups`, and a
-// stride of `groups` lets the compiler see the single trip and keep the
-// register allocation of a straight-line kernel.
-template <bool STREAM>
-__device__ __forceinline__ int64_t row_step(int64_t groups) {
-  return STREAM ? static_cast<int64_t>(gridDim.x) : groups;
-}
-
-template <typename T, int CHUNKS, int WPR, bool STREAM>
-struct RowLoader {
-  static constexpr int V = Pack16<T>::N;
-  static constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
-  const T* base;
-  int64_t stride, rows;
-  RowPos p;
-  int npk;
-  Pack16<T> buf[CHUNKS];
-
-  __device__ __forceinline__ RowLoader(const T* b, int64_t s, int64_t nrows, const RowPos& pos, int n)
-      : base(b), stride(s), rows(nrows), p(pos), npk(n) {}
-
-  // Group g's packs of this lane; zeros past the row end or past `rows`
-  // (buffer loads against the row's extent: no branches).
-  __device__ __forceinline__ void load(Pack16<T> (&r)[CHUNKS], int64_t g) const {
-    const int64_t row = g * RPB + p.row_in_block;
-    const bool ok = row < rows;
-    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(base + (ok ? row : 0) * stride, ok ? npk * 16u : 0u);
-#pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) r[c] = buffer_load16_nt<T>(rs, pack_of<WPR>(p, c) * 16u);
-  }
-  __device__ __forceinline__ void start(int64_t g) {
-    if constexpr (STREAM) load(buf, g);
-  }
-  // Hands back group g and (streaming) issues group gn's loads.
-  __device__ __forceinline__ void next(Pack16<T> (&r)[CHUNKS], int64_t g, int64_t gn) {
-    if constexpr (STREAM) {
-#pragma unroll
-      for (int c = 0; c < CHUNKS; ++c) r[c] = buf[c];
-      load(buf, gn);
-    } else {
-      load(r, g);
-    }
-  }
-};
-
 template <typename W, int V>
 struct ParamPack {
   static constexpr int kPer = Pack16<W>::N;
@@ -184,34 +138,6 @@ struct ParamPack {
   }
   __device__ __forceinline__ float get(int i) const { return static_cast<float>(q[i / kPer].v[i % kPer]); }
 };
-
-template <int WPR, typename W, int V, int CHUNKS>
-__device__ __forceinline__ void load_params(ParamPack<W, V> (&q)[CHUNKS], const W* w, const RowPos& p,
-                                            int npk) {
-#pragma unroll
-  for (int c = 0; c < CHUNKS; ++c)
-    if (pack_of<WPR>(p, c) < npk) q[c].load(w + pack_of<WPR>(p, c) * V);
-}
-
-// Grid of a vec row kernel K of WPR waves per row over `rows` rows: with
-// STREAM the number of blocks resident at once (K's occupancy, queried once
-// per kernel, times the CU count) capped by the group count, else one block
-// per group.
-template <auto K, bool STREAM, int WPR>
-int64_t row_grid(int64_t rows) {
-  constexpr int kThreads = RowShape<WPR>::kThreads;
-  const int64_t groups = ceil_div(rows, RowShape<WPR>::kRowsPerBlock);
-  if constexpr (!STREAM) {
-    return groups;
-  } else {
-    static const int per_cu = [] {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K, kThreads, 0) != hipSuccess || n <= 0) n = 1;
-      return n;
-    }();
-    return std::min<int64_t>(groups, static_cast<int64_t>(per_cu) * cu_count_cached());
-  }
-}
 
 // Block-wide sum for the looped (any width) kernels: 256 threads.
 template <typename C>

@@ -16,8 +16,7 @@
 //              element, to the two separate kernels, in one pass.
 //
 // Vector path: one HBM read + one HBM write per element, row held in VGPRs
-// (see rowcommon.h); layer_norm runs it streaming (persistent blocks with
-// one row group of register prefetch), rms_norm one row group per block.  Looped path (unaligned rows, or rows wider than 64K
+// (see rowcommon.h), one row group per block.  Looped path (unaligned rows, or rows wider than 64K
 // 16-bit elements): one 256-thread block per row, scalar strided accesses,
 // re-reading the row from L2 for the second / third pass.
 #include "dispatch.h"
@@ -38,41 +37,37 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_vec(
     int64_t rows, int cols, float eps) {
   constexpr int V = Pack16<T>::N;
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
-  __shared__ float red[2][RPB * WPR];
+  __shared__ float red[RPB * WPR];
   const RowPos p = row_pos<WPR>();
   const int npk = cols / V;
-  const int64_t groups = (rows + RPB - 1) / RPB;
-  const int64_t step = row_step<false>(groups);
-  RowLoader<T, CHUNKS, WPR, false> in(x, xs, rows, p, npk);
-  for (int64_t g = blockIdx.x, it = 0; g < groups; g += step, ++it) {
-    Pack16<T> r[CHUNKS];
-    in.next(r, g, g + step);
-    float ss = 0.f;
+  const int64_t g = blockIdx.x;
+  Pack16<T> r[CHUNKS];
+  load_row_packs<WPR>(r, x, xs, rows, p, npk, g);
+  float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < CHUNKS; ++c)
+  for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float f = to_f(r[c].v[i]);
-        ss += f * f;
-      }
-    ss = row_sum<WPR>(ss, red[it & 1], p);
-    const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
-    const int64_t row = g * RPB + p.row_in_block;
-    const bool row_ok = row < rows;
-    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
-#pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-      const int pk = pack_of<WPR>(p, c);
-      ParamPack<W, V> wq;
-      if (w != nullptr && pk < npk) wq.load(w + pk * V);
-      Pack16<T> o;
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float wv = w != nullptr ? wq.get(i) : 1.0f;
-        o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(r[c].v[i]), rstd), wv));
-      }
-      buffer_store16_nt(out, pk * 16u, o);
+    for (int i = 0; i < V; ++i) {
+      const float f = to_f(r[c].v[i]);
+      ss += f * f;
     }
+  ss = row_sum<WPR>(ss, red, p);
+  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+  const int64_t row = g * RPB + p.row_in_block;
+  const bool row_ok = row < rows;
+  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int pk = pack_of<WPR>(p, c);
+    ParamPack<W, V> wq;
+    if (w != nullptr && pk < npk) wq.load(w + pk * V);
+    Pack16<T> o;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float wv = w != nullptr ? wq.get(i) : 1.0f;
+      o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(r[c].v[i]), rstd), wv));
+    }
+    buffer_store16_nt(out, pk * 16u, o);
   }
 }
 
@@ -190,69 +185,77 @@ __global__ __launch_bounds__(256) void k_add_rms_loop(const T* x, int64_t xs, co
 }
 
 // ------------------------------------------------------------ layer_norm --
+// Each element is converted to fp32 once and the row stays in fp32 VGPRs
+// through both reductions and the write.  Packs past the row end load as
+// zeros; the variance pass sums each pack's squares apart and adds the sum
+// only for packs inside the row (one select per pack, not per element;
+// subtracting the pads' known share n_pad * mean^2 instead loses the
+// variance to cancellation when |mean| >> std).  The output is
+// fma(fma(x, rstd, -mean * rstd), w, b): torch's CPU expression with the two
+// products contracted (a different bf16 rounding only within ~2 fp32 ulps
+// of a rounding boundary).
 template <typename T, typename W, int CHUNKS, int WPR>
 __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_ln_vec(
     const T* __restrict__ x, int64_t xs, const W* __restrict__ w, const W* __restrict__ b,
     T* __restrict__ y, int64_t ys, int64_t rows, int cols, float eps) {
   constexpr int V = Pack16<T>::N;
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
-  __shared__ float red0[2][RPB * WPR];
-  __shared__ float red1[2][RPB * WPR];
+  __shared__ float red0[RPB * WPR];
+  __shared__ float red1[RPB * WPR];
   const RowPos p = row_pos<WPR>();
   const int npk = cols / V;
-  const int64_t groups = (rows + RPB - 1) / RPB;
-  constexpr bool kStream = kCanStream<CHUNKS, WPR>;
-  const int64_t step = row_step<kStream>(groups);
-  ParamPack<W, V> wq[CHUNKS], bq[CHUNKS];
-  if constexpr (kStream) {
-    if (w != nullptr) load_params<WPR>(wq, w, p, npk);
-    if (b != nullptr) load_params<WPR>(bq, b, p, npk);
-  }
-  RowLoader<T, CHUNKS, WPR, kStream> in(x, xs, rows, p, npk);
-  in.start(blockIdx.x);
-  for (int64_t g = blockIdx.x, it = 0; g < groups; g += step, ++it) {
+  const int64_t g = blockIdx.x;
+  float f[CHUNKS][V];
+  {
     Pack16<T> r[CHUNKS];
-    in.next(r, g, g + step);
-    float s = 0.f;
+    load_row_packs<WPR>(r, x, xs, rows, p, npk, g);
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
-      for (int i = 0; i < V; ++i) s += to_f(r[c].v[i]);
-    const float mean = row_sum<WPR>(s, red0[it & 1], p) / static_cast<float>(cols);
-    float q = 0.f;
+      for (int i = 0; i < V; ++i) f[c][i] = to_f(r[c].v[i]);
+  }
+  float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-      const bool ok = pack_of<WPR>(p, c) < npk;
+  for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float d = ok ? to_f(r[c].v[i]) - mean : 0.f;
-        q += d * d;
-      }
+    for (int i = 0; i < V; i += 2) {
+      s0 += f[c][i];
+      s1 += f[c][i + 1];
     }
-    const float var = row_sum<WPR>(q, red1[it & 1], p) / static_cast<float>(cols);
-    const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
-    const float shift = -rstd * mean;
-    const int64_t row = g * RPB + p.row_in_block;
-    const bool row_ok = row < rows;
-    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
+  // divided, not scaled by 1 / cols: a constant row's mean must come out exact
+  const float mean = row_sum<WPR>(s0 + s1, red0, p) / static_cast<float>(cols);
+  float q = 0.f;
 #pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-      const int pk = pack_of<WPR>(p, c);
-      if constexpr (!kStream)
-        if (pk < npk) {
-          if (w != nullptr) wq[c].load(w + pk * V);
-          if (b != nullptr) bq[c].load(b + pk * V);
-        }
-      Pack16<T> o;
+  for (int c = 0; c < CHUNKS; ++c) {
+    float q0 = 0.f, q1 = 0.f;
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float wv = w != nullptr ? wq[c].get(i) : 1.0f;
-        const float bv = b != nullptr ? bq[c].get(i) : 0.0f;
-        const float n = add_nc(mul_nc(to_f(r[c].v[i]), rstd), shift);
-        o.v[i] = static_cast<T>(add_nc(mul_nc(n, wv), bv));
-      }
-      buffer_store16_nt(out, pk * 16u, o);
+    for (int i = 0; i < V; i += 2) {
+      const float d0 = f[c][i] - mean, d1 = f[c][i + 1] - mean;
+      q0 = fmaf(d0, d0, q0);
+      q1 = fmaf(d1, d1, q1);
     }
+    q += pack_of<WPR>(p, c) < npk ? q0 + q1 : 0.f;
+  }
+  const float var = row_sum<WPR>(q, red1, p) * (1.0f / static_cast<float>(cols));
+  const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
+  const float shift = -rstd * mean;
+  const int64_t row = g * RPB + p.row_in_block;
+  const bool row_ok = row < rows;
+  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int pk = pack_of<WPR>(p, c);
+    ParamPack<W, V> wq, bq;
+    if (w != nullptr && pk < npk) wq.load(w + pk * V);
+    if (b != nullptr && pk < npk) bq.load(b + pk * V);
+    Pack16<T> o;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float wv = w != nullptr ? wq.get(i) : 1.0f;
+      const float bv = b != nullptr ? bq.get(i) : 0.0f;
+      o.v[i] = static_cast<T>(fmaf(fmaf(f[c][i], rstd, shift), wv, bv));
+    }
+    buffer_store16_nt(out, pk * 16u, o);
   }
 }
 
@@ -300,7 +303,7 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
   if (vec) {
 #define NTOPS_RMS_CASE(CH, WP)                                                                    \
   if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
-    hipLaunchKernelGGL((k_rms_vec<T, W, CH, WP>), dim3(row_grid<k_rms_vec<T, W, CH, WP>, false, WP>(rows)), \
+    hipLaunchKernelGGL((k_rms_vec<T, W, CH, WP>), dim3(ceil_div(rows, RowShape<WP>::kRowsPerBlock)),      \
                        dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, y, ys, rows,                \
                        static_cast<int>(cols), feps);                                             \
     return check_launch("rms_norm");                                                              \
@@ -329,7 +332,7 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
   if (vec) {
 #define NTOPS_LN_CASE(CH, WP)                                                                     \
   if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
-    hipLaunchKernelGGL((k_ln_vec<T, W, CH, WP>), dim3(row_grid<k_ln_vec<T, W, CH, WP>, kCanStream<CH, WP>, WP>(rows)), \
+    hipLaunchKernelGGL((k_ln_vec<T, W, CH, WP>), dim3(ceil_div(rows, RowShape<WP>::kRowsPerBlock)),       \
                        dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, b, y, ys, rows,             \
                        static_cast<int>(cols), feps);                                             \
     return check_launch("layer_norm");                                                            \
