@@ -348,90 +348,123 @@ __global__ __launch_bounds__(256) void k_conv_to_cl(ConvArgs a, T* xt, int n0, i
   }
 }
 
-// Same output as k_conv_to_cl for contiguous 16-byte aligned input rows of a
-// multiple of 8 pixels that fit the padded row (pw + W <= wp): a thread
-// moves an 8 x 8 block -- 8 pixels of 8 channels -- with eight 16-byte loads
-// along the pixels of each channel, a transpose in registers and eight
-// 16-byte stores along the channels of each pixel; neighbouring threads take
-// neighbouring channel groups, so each pixel's C channels are written as
-// one contiguous run.  Threads past the blocks zero the padding columns.
+// Weights in the channels-last GEMM's k order (32-channel blocks, then
+// taps, then the block's channels): wt[k][((cb * R + r) * S + s) * 32 + ci]
+// = w[k][32 cb + ci][r][s].  Item i (of K C R S / 8) is 8 channels: 8
+// loads, one 16-byte store.
 template <typename T>
-__global__ __launch_bounds__(256) void k_conv_to_cl8(ConvArgs a, T* xt, int n0, int nb, int hp, int wp) {
-  const int c8 = a.C / 8, w8 = a.W / 8, npad = wp - a.W;
-  const int64_t body = static_cast<int64_t>(nb) * hp * w8 * c8;
-  const int64_t total = body + static_cast<int64_t>(nb) * hp * npad * c8;
+__device__ __forceinline__ void conv_weight_pack(const ConvArgs& a, T* wt, int64_t i) {
+  const T* w = static_cast<const T*>(a.w);
+  const int ci8 = static_cast<int>(i % 4) * 8;  // the 8 channels' offset in the block
+  int64_t t = i / 4;
+  const int s = static_cast<int>(t % a.S);
+  t /= a.S;
+  const int r = static_cast<int>(t % a.R);
+  t /= a.R;
+  const int cb = static_cast<int>(t % (a.C / 32));
+  const int k = static_cast<int>(t / (a.C / 32));
+  const T* src = w + k * a.ws[0] + static_cast<int64_t>(cb * 32 + ci8) * a.ws[1] + r * a.ws[2] + s * a.ws[3];
+  T v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = src[e * a.ws[1]];
+  *reinterpret_cast<u32x4*>(wt + i * 8) = __builtin_bit_cast(u32x4, v);
+}
+
+// Same output as k_conv_to_cl for 16-byte aligned input rows of a multiple
+// of 8 pixels that fit the padded row (pw + W <= wp).  A wave moves 64
+// channels x 64 consecutive pixels of the channel planes: lane 8 j + g loads
+// 8 pixels (one 16-byte run, inside one image row) of each of the channels
+// 8 j .. 8 j + 7 -- eight lanes read 128 contiguous bytes of a plane --,
+// transposes the 8 x 8 block in registers and stores 8 channels of each of
+// its 8 pixels -- eight lanes write 128 contiguous bytes of a pixel.  Waves
+// past the interior zero the border (rows above and below it, columns beside
+// it), 16 bytes per lane.  (32, 256, 56, 56) bf16: 18.9 us, 5.6 TB/s, where
+// lanes taking neighbouring channel groups of one pixel group ran 25.0 us.
+// With wt set, the launch's first waves also reorder the weights
+// (conv_weight_pack), which a launch of their own left serialised ahead of
+// the copy.
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_to_cl8(ConvArgs a, T* xt, int n0, int nb, int hp, int wp, T* wt) {
+  const int lane = threadIdx.x & 63;
+  const int64_t witems = wt != nullptr ? static_cast<int64_t>(a.K) * a.C * a.R * a.S / 8 : 0;
+  const int64_t wwaves = (witems + 63) / 64;
+  const int64_t hw = static_cast<int64_t>(a.H) * a.W;
+  const int cb = (a.C + 63) / 64;                        // 64-channel blocks
+  const int64_t pb = (hw + 63) / 64;                     // 64-pixel blocks
+  const int64_t units = static_cast<int64_t>(nb) * cb * pb;
+  const int top = min(a.ph, hp);                         // zero rows above the interior
+  const int mid = max(0, min(hp, a.ph + a.H) - a.ph);    // interior rows
+  const int bot = hp - top - mid;                        // zero rows below it
+  const int side = wp - a.W;                             // zero columns per interior row
+  const int64_t border = static_cast<int64_t>(top + bot) * wp + static_cast<int64_t>(mid) * side;
+  const int c8 = a.C / 8;
+  const int64_t pads = static_cast<int64_t>(nb) * border * c8;
+  const int64_t waves = wwaves + units + (pads + 63) / 64;
   const T* x = static_cast<const T*>(a.x);
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    if (i < body) {
-      const int j = static_cast<int>(i % c8);
-      int64_t t = i / c8;
-      const int pg = static_cast<int>(t % w8);
-      t /= w8;
-      const int hh = static_cast<int>(t % hp);
-      const int b = static_cast<int>(t / hp);
-      const int ih = hh - a.ph;
-      T* dst = xt + ((static_cast<int64_t>(b) * hp + hh) * wp + a.pw + pg * 8) * a.C + j * 8;
-      u32x4 out[8];
-      if (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H)) {
-        const T* src = x + (n0 + b) * a.xs[0] + static_cast<int64_t>(j * 8) * a.xs[1] + ih * a.xs[2] + pg * 8;
-        u32x4 in[8];  // in[e]: pixels 0..7 of channel 8j + e, two per word
+  for (int64_t v = blockIdx.x * 4ll + (threadIdx.x >> 6); v < waves; v += static_cast<int64_t>(gridDim.x) * 4) {
+    if (v < wwaves) {
+      const int64_t i = v * 64 + lane;
+      if (i < witems) conv_weight_pack(a, wt, i);
+      continue;
+    }
+    const int64_t u = v - wwaves;
+    if (u < units) {
+      const int64_t g = u % pb;
+      const int64_t t = u / pb;
+      const int c0 = static_cast<int>(t % cb) * 64 + (lane >> 3) * 8;
+      const int b = static_cast<int>(t / cb);
+      const int64_t p0 = g * 64 + (lane & 7) * 8;
+      if (c0 >= a.C || p0 >= hw) continue;
+      const int ih = static_cast<int>(p0 / a.W), iw = static_cast<int>(p0 % a.W);
+      const int hh = a.ph + ih;
+      if (hh >= hp) continue;  // input row the convolution never reads
+      const T* src = x + (n0 + b) * a.xs[0] + c0 * a.xs[1] + ih * a.xs[2] + iw;
+      u32x4 in[8];  // in[e]: pixels 0..7 of channel c0 + e, two per word
 #pragma unroll
-        for (int e = 0; e < 8; ++e) in[e] = *reinterpret_cast<const u32x4*>(src + e * a.xs[1]);
-        // out[f] word k: channels 2k (low half) and 2k + 1 (high half) of pixel f
+      for (int e = 0; e < 8; ++e) in[e] = *reinterpret_cast<const u32x4*>(src + e * a.xs[1]);
+      u32x4 out[8];  // out[f] word k: channels 2k (low half) and 2k + 1 (high half) of pixel f
 #pragma unroll
-        for (int f = 0; f < 8; ++f)
+      for (int f = 0; f < 8; ++f)
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const uint32_t lo = in[2 * k][f / 2], hi = in[2 * k + 1][f / 2];
-            out[f][k] = (f & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-          }
-      } else {
-#pragma unroll
-        for (int f = 0; f < 8; ++f) out[f] = u32x4{0u, 0u, 0u, 0u};
-      }
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t lo = in[2 * k][f / 2], hi = in[2 * k + 1][f / 2];
+          out[f][k] = (f & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+        }
+      T* dst = xt + ((static_cast<int64_t>(b) * hp + hh) * wp + a.pw + iw) * a.C + c0;
 #pragma unroll
       for (int f = 0; f < 8; ++f) *reinterpret_cast<u32x4*>(dst + static_cast<int64_t>(f) * a.C) = out[f];
     } else {
-      const int64_t k = i - body;
+      const int64_t k = (u - units) * 64 + lane;
+      if (k >= pads) continue;
       const int j = static_cast<int>(k % c8);
-      int64_t t = k / c8;
-      const int pp = static_cast<int>(t % npad);
-      t /= npad;
-      const int hh = static_cast<int>(t % hp);
-      const int b = static_cast<int>(t / hp);
-      const int ww = pp < a.pw ? pp : a.W + pp;  // padding columns [0, pw) and [pw + W, wp)
+      int64_t q = k / c8;
+      const int b = static_cast<int>(q / border);
+      q %= border;
+      int hh, ww;
+      if (q < static_cast<int64_t>(top) * wp) {
+        hh = static_cast<int>(q / wp);
+        ww = static_cast<int>(q % wp);
+      } else if ((q -= static_cast<int64_t>(top) * wp) < static_cast<int64_t>(bot) * wp) {
+        hh = top + mid + static_cast<int>(q / wp);
+        ww = static_cast<int>(q % wp);
+      } else {
+        q -= static_cast<int64_t>(bot) * wp;
+        hh = a.ph + static_cast<int>(q / side);
+        const int c = static_cast<int>(q % side);
+        ww = c < a.pw ? c : a.W + c;  // columns [0, pw) and [pw + W, wp)
+      }
       *reinterpret_cast<u32x4*>(xt + ((static_cast<int64_t>(b) * hp + hh) * wp + ww) * a.C + j * 8) =
           u32x4{0u, 0u, 0u, 0u};
     }
   }
 }
 
-// Weights in the channels-last GEMM's k order (32-channel blocks, then
-// taps, then the block's channels): wt[k][((cb * R + r) * S + s) * 32 + ci]
-// = w[k][32 cb + ci][r][s].  One thread per 8 channels: 8 loads, one
-// 16-byte store.
 template <typename T>
 __global__ __launch_bounds__(256) void k_conv_weights_cl(ConvArgs a, T* wt) {
-  const int64_t crs = static_cast<int64_t>(a.C) * a.R * a.S;
-  const int64_t total = static_cast<int64_t>(a.K) * crs / 8;
-  const T* w = static_cast<const T*>(a.w);
+  const int64_t total = static_cast<int64_t>(a.K) * a.C * a.R * a.S / 8;
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int ci8 = static_cast<int>(i % 4) * 8;  // the 8 channels' offset in the block
-    int64_t t = i / 4;
-    const int s = static_cast<int>(t % a.S);
-    t /= a.S;
-    const int r = static_cast<int>(t % a.R);
-    t /= a.R;
-    const int cb = static_cast<int>(t % (a.C / 32));
-    const int k = static_cast<int>(t / (a.C / 32));
-    const T* src = w + k * a.ws[0] + static_cast<int64_t>(cb * 32 + ci8) * a.ws[1] + r * a.ws[2] + s * a.ws[3];
-    T v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = src[e * a.ws[1]];
-    *reinterpret_cast<u32x4*>(wt + i * 8) = __builtin_bit_cast(u32x4, v);
-  }
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    conv_weight_pack(a, wt, i);
 }
 
 unsigned grid_for(int64_t work, int per_block) {
@@ -479,6 +512,17 @@ bool use_implicit(const ConvArgs& a, int dt) {
 // Rows and pixels per row of the channels-last padded copy.
 int64_t cl_rows(const ConvArgs& a) { return static_cast<int64_t>(a.P - 1) * a.sh + static_cast<int64_t>(a.R - 1) * a.dh + 1; }
 int64_t cl_cols(const ConvArgs& a) { return static_cast<int64_t>(a.Q - 1) * a.sw + static_cast<int64_t>(a.S - 1) * a.dw + 1; }
+
+// Waves of k_conv_to_cl8 for nb images: the weight items (if any), 64 per
+// wave, 64-channel x 64-pixel blocks of the input, then the border's
+// 16-byte chunks, 64 per wave.
+int64_t cl8_waves(const ConvArgs& a, int64_t nb, int64_t hp, int64_t wp, bool weights) {
+  const int64_t hw = static_cast<int64_t>(a.H) * a.W;
+  const int64_t mid = std::max<int64_t>(0, std::min<int64_t>(hp, a.ph + a.H) - a.ph);  // interior rows
+  const int64_t border = (hp - mid) * wp + mid * (wp - a.W);
+  const int64_t witems = weights ? static_cast<int64_t>(a.K) * a.C * a.R * a.S / 8 : 0;
+  return (witems + 63) / 64 + nb * ((a.C + 63) / 64) * ((hw + 63) / 64) + (nb * border * (a.C / 8) + 63) / 64;
+}
 
 // Whether the channels-last implicit GEMM applies (on top of use_gemm):
 // 16-bit data, C a multiple of the GEMM's 32-channel K tile, P * Q a
@@ -599,17 +643,23 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
     const int64_t nb_max = std::min<int64_t>(N, (workspace_bytes - fixed) / per_image);
     void* wt = workspace;
     void* xt = static_cast<char*>(workspace) + fixed;
-    rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
-      using T = decltype(tag);
-      if constexpr (sizeof(T) != 2) {
-        return set_error(NTOPS_ERR_INVALID, "conv2d: the channels-last path needs 16-bit data");
-      } else {
-        hipLaunchKernelGGL(k_conv_weights_cl<T>, dim3(grid_for(K * crs / 8, 256)), dim3(256), 0, st, a,
-                           static_cast<T*>(wt));
-        return check_launch("conv2d");
-      }
-    });
-    if (rc != NTOPS_OK) return rc;
+    // 16-byte input rows: the block copy, which also reorders the weights
+    // (with the first chunk); otherwise the element copy after a weight launch
+    const bool rows16 = a.xs[3] == 1 && a.xs[2] % 8 == 0 && a.xs[1] % 8 == 0 && a.xs[0] % 8 == 0 &&
+                        W % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && pad_w + W <= wp;
+    if (!rows16) {
+      rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
+        using T = decltype(tag);
+        if constexpr (sizeof(T) != 2) {
+          return set_error(NTOPS_ERR_INVALID, "conv2d: the channels-last path needs 16-bit data");
+        } else {
+          hipLaunchKernelGGL(k_conv_weights_cl<T>, dim3(grid_for(K * crs / 8, 256)), dim3(256), 0, st, a,
+                             static_cast<T*>(wt));
+          return check_launch("conv2d");
+        }
+      });
+      if (rc != NTOPS_OK) return rc;
+    }
     for (int64_t n0 = 0; n0 < N; n0 += nb_max) {
       const int64_t nb = std::min(nb_max, N - n0);
       rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
@@ -617,12 +667,10 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
         if constexpr (sizeof(T) != 2) {
           return set_error(NTOPS_ERR_INVALID, "conv2d: the channels-last path needs 16-bit data");
         } else {
-          const bool rows16 = a.xs[3] == 1 && a.xs[2] % 8 == 0 && a.xs[1] % 8 == 0 && a.xs[0] % 8 == 0 &&
-                              W % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && pad_w + W <= wp;
           if (rows16)
-            hipLaunchKernelGGL(k_conv_to_cl8<T>, dim3(grid_for(nb * hp * (C / 8) * (W / 8 + wp - W), 256)),
+            hipLaunchKernelGGL(k_conv_to_cl8<T>, dim3(grid_for(cl8_waves(a, nb, hp, wp, n0 == 0) * 64, 256)),
                                dim3(256), 0, st, a, static_cast<T*>(xt), static_cast<int>(n0), static_cast<int>(nb),
-                               static_cast<int>(hp), static_cast<int>(wp));
+                               static_cast<int>(hp), static_cast<int>(wp), n0 == 0 ? static_cast<T*>(wt) : nullptr);
           else
             hipLaunchKernelGGL(k_conv_to_cl<T>, dim3(grid_for(nb * hp * (C / 8) * wp, 256)), dim3(256), 0, st, a,
                                static_cast<T*>(xt), static_cast<int>(n0), static_cast<int>(nb), static_cast<int>(hp),
