@@ -18,8 +18,16 @@
 //  * direct kernel (larger planes): a grid-stride loop over (image, channel,
 //    run) items whose taps gather from global memory (L2).
 // When every output row starts on a multiple of the run's byte size (capped
-// at 16 bytes), whole runs are written with full-width vector stores;
+// at 16 bytes), whole runs are written with full-width non-temporal vector
+// stores (the output is written once and is kh * kw times the input: on the
+// (32, 256, 56, 56) 3x3 bf16 unfold they move 86 instead of 99 us);
 // otherwise (and for a row's last, partial run) element by element.
+//  * stride-1 kernel (16-bit elements, stride and dilation 1, output rows a
+//    multiple of 8 pixels, vector stores): the plane is staged in LDS with
+//    its zero padding around it, so a run's 8 + kw - 1 input elements under
+//    kernel row r are one aligned 32-byte LDS read and the kw taps are
+//    register selections (even taps) or 16-bit funnel shifts (odd taps) of
+//    it -- no per-element bounds tests or gathers.
 #include "dispatch.h"
 
 namespace ntops {
@@ -68,14 +76,14 @@ __device__ __forceinline__ void store_run(const Im2colArgs& a, char* row, int j0
     if (j0 + kRun <= a.L) {
       char* dst = row + static_cast<int64_t>(j0) * ES;
       if constexpr (ES == 1) {
-        *reinterpret_cast<uint64_t*>(dst) = __builtin_bit_cast(uint64_t, v);
+        __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, v), reinterpret_cast<uint64_t*>(dst));
       } else {
         struct Chunks {
           u32x4 c[ES * kRun / 16];
         };
         const Chunks ch = __builtin_bit_cast(Chunks, v);
 #pragma unroll
-        for (int i = 0; i < ES * kRun / 16; ++i) reinterpret_cast<u32x4*>(dst)[i] = ch.c[i];
+        for (int i = 0; i < ES * kRun / 16; ++i) __builtin_nontemporal_store(ch.c[i], reinterpret_cast<u32x4*>(dst) + i);
       }
       return;
     }
@@ -144,10 +152,111 @@ __global__ __launch_bounds__(256) void k_im2col_direct(Im2colArgs a, int64_t ite
   }
 }
 
+
+// Stride 1, dilation 1, ES == 2, ow % 8 == 0, KW <= 9, VEC stores.  LDS holds
+// the plane zero-padded: row ih + ph, column iw + pw, `pitch` (a multiple of
+// 8, >= ow + 8) elements per row, H + 2 ph rows.  Output pixel (p, q) under
+// tap (r, s) is padded element (p + r, q + s), so the run at (p, q0) reads
+// padded row p + r, columns q0 .. q0 + 15 (two 16-byte reads; q0 and pitch
+// are multiples of 8) and tap s takes elements s .. s + 7 of them.
+template <int KW>
+__global__ __launch_bounds__(512) void k_im2col_s1(Im2colArgs a, int pitch, int vec_in) {
+  extern __shared__ __attribute__((aligned(16))) char sm[];
+  uint16_t* plane = reinterpret_cast<uint16_t*>(sm);
+  const int n = blockIdx.x / a.C;
+  const int c = blockIdx.x - n * a.C;
+  const int hp = a.H + 2 * a.ph;
+  for (int i = threadIdx.x; i < hp * pitch / 8; i += blockDim.x) reinterpret_cast<u32x4*>(sm)[i] = u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();
+  const uint16_t* x = static_cast<const uint16_t*>(a.x) + n * a.xs[0] + c * a.xs[1];
+  if (vec_in) {  // unit column stride, rows of a multiple of 8 elements, 16-byte aligned
+    const int w8 = a.W / 8;
+    for (int i = threadIdx.x; i < a.H * w8; i += blockDim.x) {
+      const int ih = i / w8, iw = (i - ih * w8) * 8;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(x + ih * a.xs[2] + iw);
+      // 2-byte stores kept apart (relaxed atomic stores are not merged): with
+      // pw odd the destination is only 2-byte aligned, and merged they would
+      // form a misaligned 16-byte LDS store
+      uint16_t* d = plane + (ih + a.ph) * pitch + iw + a.pw;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        __hip_atomic_store(d + 2 * k, static_cast<uint16_t>(v[k]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_store(d + 2 * k + 1, static_cast<uint16_t>(v[k] >> 16), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < a.H * a.W; i += blockDim.x) {
+      const int ih = i / a.W, iw = i - ih * a.W;
+      plane[(ih + a.ph) * pitch + iw + a.pw] = x[ih * a.xs[2] + iw * a.xs[3]];
+    }
+  }
+  __syncthreads();
+  char* out = static_cast<char*>(a.out) + (static_cast<int64_t>(n) * a.os[0] +
+                                           static_cast<int64_t>(c) * a.kh * KW * a.os[1]) * 2;
+  for (int run = threadIdx.x; run < a.runs; run += blockDim.x) {
+    const int j0 = run * kRun;
+    const int p = j0 / a.ow, q0 = j0 - p * a.ow;
+    for (int r = 0; r < a.kh; ++r) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(plane + (p + r) * pitch + q0);
+      const u32x4 lo = src[0], hi = src[1];
+      const uint32_t d[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};  // elements 2k, 2k + 1
+#pragma unroll
+      for (int s = 0; s < KW; ++s) {
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          o[k] = (s & 1) ? __builtin_amdgcn_alignbit(d[s / 2 + k + 1], d[s / 2 + k], 16) : d[s / 2 + k];
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(out + (static_cast<int64_t>(r * KW + s) * a.os[1] + j0) * 2));
+      }
+    }
+  }
+}
+
+// Row pitch (elements) of the stride-1 kernel's padded plane, or 0 when the
+// problem is not one it handles (including a padded plane over 64 KiB).
+int s1_pitch(const Im2colArgs& a) {
+  if (a.sh != 1 || a.sw != 1 || a.dh != 1 || a.dw != 1 || a.ow % kRun != 0 || a.kw > 9) return 0;
+  const int64_t w = std::max<int64_t>(static_cast<int64_t>(a.W) + 2 * a.pw, static_cast<int64_t>(a.ow) + 8);
+  const int64_t pitch = (w + 7) / 8 * 8;
+  if ((static_cast<int64_t>(a.H) + 2 * a.ph) * pitch * 2 > kIm2colPlaneLds) return 0;
+  return static_cast<int>(pitch);
+}
+
+template <int KW>
+int launch_s1(const Im2colArgs& a, int pitch, hipStream_t st) {
+  const bool vec_in = a.xs[3] == 1 && a.W % 8 == 0 && a.xs[2] % 8 == 0 && a.xs[1] % 8 == 0 && a.xs[0] % 8 == 0 &&
+                      (reinterpret_cast<uintptr_t>(a.x) & 15u) == 0;
+  const int threads = static_cast<int>(std::min<int64_t>(512, (std::max(a.runs, 64) + 63) / 64 * 64));
+  const unsigned lds = static_cast<unsigned>((static_cast<int64_t>(a.H) + 2 * a.ph) * pitch * 2);
+  note_kernel("im2col_s1 kw%d", KW);
+  hipLaunchKernelGGL(k_im2col_s1<KW>, dim3(static_cast<unsigned>(static_cast<int64_t>(a.N) * a.C)), dim3(threads),
+                     lds, st, a, pitch, vec_in ? 1 : 0);
+  return check_launch("im2col");
+}
+
+int run_s1(const Im2colArgs& a, int pitch, hipStream_t st) {
+  switch (a.kw) {
+    case 1: return launch_s1<1>(a, pitch, st);
+    case 2: return launch_s1<2>(a, pitch, st);
+    case 3: return launch_s1<3>(a, pitch, st);
+    case 4: return launch_s1<4>(a, pitch, st);
+    case 5: return launch_s1<5>(a, pitch, st);
+    case 6: return launch_s1<6>(a, pitch, st);
+    case 7: return launch_s1<7>(a, pitch, st);
+    case 8: return launch_s1<8>(a, pitch, st);
+    default: return launch_s1<9>(a, pitch, st);
+  }
+}
+
 template <int ES, bool VEC>
 int launch_im2col(const Im2colArgs& a, hipStream_t st) {
   const int64_t planes = static_cast<int64_t>(a.N) * a.C;
   const int64_t plane_bytes = static_cast<int64_t>(a.H) * a.W * ES;
+  if constexpr (ES == 2 && VEC) {
+    const int pitch = s1_pitch(a);
+    if (pitch > 0 && planes <= 0x7fffffffLL) return run_s1(a, pitch, st);
+  }
   if (plane_bytes <= kIm2colPlaneLds && planes <= 0x7fffffffLL) {
     note_kernel("im2col_lds es%d %s", ES, VEC ? "vec" : "scalar");
     hipLaunchKernelGGL((k_im2col_lds<ES, VEC>), dim3(static_cast<unsigned>(planes)), dim3(256),

@@ -91,8 +91,15 @@ def test_im2col_golden_vectors():
 
 # (shape, kernel, padding, stride, dtype, expected kernel): planes up to 64
 # KiB are staged in LDS, larger ones gathered from global memory; rows whose
-# length keeps every row start on the run's byte size take vector stores.
+# length keeps every row start on the run's byte size take vector stores;
+# 16-bit stride-1 problems with output rows of a multiple of 8 pixels take
+# the zero-padded LDS plane with register-selected taps (kernel widths 1-9;
+# plane loaded by 16-byte rows, or element by element when W % 8 != 0).
 VARIANTS = (
+    ((2, 3, 18, 24), 3, 1, 1, torch.bfloat16, "im2col_s1 kw3"),
+    ((1, 2, 12, 16), 5, 2, 1, torch.float16, "im2col_s1 kw5"),
+    ((1, 3, 9, 9), 2, 0, 1, torch.bfloat16, "im2col_s1 kw2"),
+    ((1, 2, 8, 16), 1, 0, 1, torch.bfloat16, "im2col_s1 kw1"),
     ((2, 3, 20, 20), 3, 1, 1, torch.bfloat16, "im2col_lds es2 vec"),        # L = 400
     ((2, 3, 20, 21), 3, 1, 1, torch.bfloat16, "im2col_lds es2 scalar"),     # L = 420
     ((2, 3, 20, 20), 3, 1, 1, torch.uint8, "im2col_lds es1 vec"),
