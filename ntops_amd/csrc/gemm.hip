@@ -457,8 +457,10 @@ __device__ __forceinline__ void store_tile_direct(const GemmArgs& g, const f32x1
   }
 }
 
-// Output stores marked non-temporal (streamed past L2) per kernel.
-constexpr bool kStreamOutMfma = false;
+// Output stores marked non-temporal (streamed past L2) per kernel: both
+// kernels write their output once (mm 8192 x 14336 bf16: 767 -> 762 us,
+// conv2d's implicit GEMM 155.5 -> 152.6 us with them).
+constexpr bool kStreamOutMfma = true;
 constexpr bool kStreamOutPanel = true;
 
 // ---- MFMA kernel -----------------------------------------------------------
