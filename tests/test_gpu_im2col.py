@@ -100,6 +100,9 @@ VARIANTS = (
     ((1, 2, 12, 16), 5, 2, 1, torch.float16, "im2col_s1 kw5"),
     ((1, 3, 9, 9), 2, 0, 1, torch.bfloat16, "im2col_s1 kw2"),
     ((1, 2, 8, 16), 1, 0, 1, torch.bfloat16, "im2col_s1 kw1"),
+    ((1, 2, 10, 16), 7, 3, 1, torch.bfloat16, "im2col_s1 kw7"),
+    ((2, 1, 9, 8), 9, 4, 1, torch.float16, "im2col_s1 kw9"),
+    ((1, 2, 6, 17), 4, 1, 1, torch.bfloat16, "im2col_s1 kw4"),          # ow = 16, W % 8 != 0
     ((2, 3, 20, 20), 3, 1, 1, torch.bfloat16, "im2col_lds es2 vec"),        # L = 400
     ((2, 3, 20, 21), 3, 1, 1, torch.bfloat16, "im2col_lds es2 scalar"),     # L = 420
     ((2, 3, 20, 20), 3, 1, 1, torch.uint8, "im2col_lds es1 vec"),
@@ -121,6 +124,17 @@ def test_im2col_kernel_variants(shape, ks, pad, st, dtype, kernel):
     got = im2col(x.cuda(), ks, 1, pad, st)
     assert _lib.last_kernel() == kernel
     assert torch.equal(got.cpu(), expect(x, ks, 1, pad, st))
+
+
+def test_im2col_stride1_strided_input():
+    """The stride-1 16-bit kernel on a channels-last view (column stride C):
+    the plane is loaded element by element, the taps as for a contiguous one."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 16, 16, 5, generator=g).bfloat16()  # N, H, W, C
+    xv = x.cuda().permute(0, 3, 1, 2)                         # (2, 5, 16, 16), strides (1280, 1, 80, 5)
+    got = im2col(xv, 3, 1, 1, 1)
+    assert _lib.last_kernel() == "im2col_s1 kw3"
+    assert torch.equal(got.cpu(), expect(x.permute(0, 3, 1, 2).contiguous(), 3, 1, 1, 1))
 
 
 def test_im2col_argument_forms_and_checks():
