@@ -991,8 +991,8 @@ def main():
             fn, lib_desc = y
             try:
                 y_ms = time_yardstick(fn, w.build, args.steps, args.replays, args.settle_ms)
-            except RuntimeError as e:  # a library backend missing on this install
-                r["yardstick"] = {"library": lib_desc, "error": str(e)[:200]}
+            except Exception as e:  # a library backend missing on this install
+                r["yardstick"] = {"library": lib_desc, "error": f"{type(e).__name__}: {str(e)[:200]}"}
             else:
                 y_val = w.work / (y_ms / 1e3) / (1e12 if w.unit == "TFLOP/s" else 1e9)
                 r["yardstick"] = {"library": lib_desc, "ms_per_step": round(y_ms, 5), "value": round(y_val, 3),
