@@ -22,8 +22,10 @@ rotate so the 256 MB MALL cannot serve a step from the previous one.
 Achieved bandwidth uses algorithmic bytes (every compulsory byte counted
 once); GEMMs report algorithmic flops.  A plain streaming copy (ntops_cast
 f32 -> f32) runs as its own workload and gives each bandwidth-bound op its
-fraction of the measured ceiling; torch.mm / torch.bmm (hipBLASLt, eager) are
-timed at the GEMM configs as a same-box yardstick.  cpu_baseline times
+fraction of the measured ceiling; torch.mm / torch.bmm (hipBLASLt, eager),
+torch's GPU scaled_dot_product_attention (flash / memory-efficient backends)
+and conv2d (MIOpen) are timed at their configs as same-box yardsticks, and
+Tensor.copy_ beside the copy.  cpu_baseline times
 PyTorch's CPU implementation of the same op (the reference the configs name)
 on a bounded sample of the workload on this host's cores.
 """
