@@ -80,15 +80,20 @@ __device__ __forceinline__ C row_max(C v, C* red, const RowPos& p) {
 // more waves per row measured faster on MI355X than deep per-lane unrolling
 // (e.g. 4096 bf16: 2 packs x 4 waves reaches ~5.9 TB/s, 8 packs x 1 wave
 // ~4.9 TB/s): more rows are in flight per CU and the per-row reduction is
-// shorter.  Rows wider than 8 packs x 16 waves use the looped kernels.
+// shorter.  `deep` picks 4 packs x 2 waves for rows of 257-512 packs instead
+// (layer_norm, whose two dependent reductions gain from the longer per-lane
+// runs: bf16 (16384, 4096) 47.5 -> 45.9 us, where rms_norm and add_rms_norm
+// lose 1-4 % with it).  Rows wider than 8 packs x 16 waves use the looped
+// kernels.
 struct VecCfg {
   int chunks, wpr;
 };
-inline bool pick_row_cfg(int64_t npk, VecCfg* cfg) {
+inline bool pick_row_cfg(int64_t npk, VecCfg* cfg, bool deep = false) {
   static const VecCfg table[] = {{1, 1}, {2, 1}, {2, 2}, {2, 4}, {2, 8}, {2, 16}, {4, 16}, {8, 16}};
   for (const VecCfg& c : table) {
     if (static_cast<int64_t>(c.chunks) * c.wpr * 64 >= npk) {
       *cfg = c;
+      if (deep && c.chunks == 2 && c.wpr == 4) *cfg = VecCfg{4, 2};
       return true;
     }
   }
@@ -105,6 +110,10 @@ inline bool pick_row_cfg(int64_t npk, VecCfg* cfg) {
   MACRO(2, 16)                 \
   MACRO(4, 16)                 \
   MACRO(8, 16)
+// ... and the extra shape of pick_row_cfg(.., deep = true).
+#define NTOPS_DEEP_ROW_CASES(MACRO) \
+  NTOPS_ROW_CASES(MACRO)            \
+  MACRO(4, 2)
 
 // Group g's packs of this lane (block g holds rows g * RPB ..); zeros past
 // the row end or past `rows` (buffer loads against the row's extent: no

@@ -327,7 +327,7 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
   const bool vec = (cols % V == 0) && (xs % V == 0) && (ys % V == 0) && aligned16(x) &&
                    aligned16(y) && (w == nullptr || aligned16(w)) &&
                    (b == nullptr || aligned16(b)) && (wrs == 0 || (w == nullptr && b == nullptr)) &&
-                   pick_row_cfg(cols / V, &cfg);
+                   pick_row_cfg(cols / V, &cfg, true);
   const float feps = static_cast<float>(eps);
   if (vec) {
 #define NTOPS_LN_CASE(CH, WP)                                                                     \
@@ -337,7 +337,7 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
                        static_cast<int>(cols), feps);                                             \
     return check_launch("layer_norm");                                                            \
   }
-    NTOPS_ROW_CASES(NTOPS_LN_CASE)
+    NTOPS_DEEP_ROW_CASES(NTOPS_LN_CASE)
 #undef NTOPS_LN_CASE
   }
   hipLaunchKernelGGL((k_ln_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, b, wrs, y, ys, cols,
