@@ -343,5 +343,14 @@ bool build_space(int ndim, const int64_t* shape, const int64_t* const strides[NO
 }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// n > 0 blocks as an x * y grid (x <= 65536): a dispatch counts each
+// dimension's work-items in 32 bits, so a one-dimensional grid of 256-thread
+// blocks would end at 2^24 blocks.  Kernels index blocks with block_id() and
+// ignore ids >= n (the tail of the last grid row).
+inline dim3 blocks_2d(int64_t n) {
+  const int64_t x = n < 65536 ? n : 65536;
+  return dim3(static_cast<unsigned>(x), static_cast<unsigned>((n + x - 1) / x));
+}
+__device__ __forceinline__ int64_t block_id() { return blockIdx.x + static_cast<int64_t>(blockIdx.y) * gridDim.x; }
 
 }  // namespace ntops

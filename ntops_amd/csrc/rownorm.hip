@@ -40,7 +40,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_vec(
   __shared__ float red[RPB * WPR];
   const RowPos p = row_pos<WPR>();
   const int npk = cols / V;
-  const int64_t g = blockIdx.x;
+  const int64_t g = block_id();  // past the last group: loads read 0, stores are dropped
   Pack16<T> r[CHUNKS];
   load_row_packs<WPR>(r, x, xs, rows, p, npk, g);
   float ss = 0.f;
@@ -73,9 +73,10 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_vec(
 
 template <typename T, typename W>
 __global__ __launch_bounds__(256) void k_rms_loop(const T* x, int64_t xs, const W* w, int64_t wrs, T* y,
-                                                   int64_t ys, int64_t cols, float eps) {
+                                                   int64_t ys, int64_t rows, int64_t cols, float eps) {
   __shared__ float red[4];
-  const int64_t row = blockIdx.x;
+  const int64_t row = block_id();
+  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
   const T* xr = x + row * xs;
   float ss = 0.f;
   for (int64_t j = threadIdx.x; j < cols; j += 256) {
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
   __shared__ float red[RPB * WPR];
   const RowPos p = row_pos<WPR>();
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + p.row_in_block;
+  const int64_t row = block_id() * RPB + p.row_in_block;
   const bool row_ok = row < rows;
   const int npk = cols / V;
   const uint32_t extent = row_ok ? npk * 16u : 0u;  // past the row end: loads give 0, stores dropped
@@ -165,9 +166,10 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
 template <typename T, typename W>
 __global__ __launch_bounds__(256) void k_add_rms_loop(const T* x, int64_t xs, const T* res, int64_t rs,
                                                        const W* w, int64_t wrs, T* y, int64_t ys, T* ro,
-                                                       int64_t ros, int64_t cols, float eps) {
+                                                       int64_t ros, int64_t rows, int64_t cols, float eps) {
   __shared__ float red[4];
-  const int64_t row = blockIdx.x;
+  const int64_t row = block_id();
+  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
   float ss = 0.f;
   for (int64_t j = threadIdx.x; j < cols; j += 256) {
     const T hv = static_cast<T>(add_nc(to_f(x[row * xs + j]), to_f(res[row * rs + j])));
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_ln_vec(
   __shared__ float red1[RPB * WPR];
   const RowPos p = row_pos<WPR>();
   const int npk = cols / V;
-  const int64_t g = blockIdx.x;
+  const int64_t g = block_id();  // past the last group: loads read 0, stores are dropped
   float f[CHUNKS][V];
   {
     Pack16<T> r[CHUNKS];
@@ -261,9 +263,10 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_ln_vec(
 
 template <typename T, typename W>
 __global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W* w, const W* b, int64_t wrs,
-                                                  T* y, int64_t ys, int64_t cols, float eps) {
+                                                  T* y, int64_t ys, int64_t rows, int64_t cols, float eps) {
   __shared__ float red[4];
-  const int64_t row = blockIdx.x;
+  const int64_t row = block_id();
+  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
   const T* xr = x + row * xs;
   float s = 0.f;
   for (int64_t j = threadIdx.x; j < cols; j += 256) s += to_f(xr[j]);
@@ -303,7 +306,7 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
   if (vec) {
 #define NTOPS_RMS_CASE(CH, WP)                                                                    \
   if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
-    hipLaunchKernelGGL((k_rms_vec<T, W, CH, WP>), dim3(ceil_div(rows, RowShape<WP>::kRowsPerBlock)),      \
+    hipLaunchKernelGGL((k_rms_vec<T, W, CH, WP>), blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
                        dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, y, ys, rows,                \
                        static_cast<int>(cols), feps);                                             \
     return check_launch("rms_norm");                                                              \
@@ -311,7 +314,7 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
     NTOPS_ROW_CASES(NTOPS_RMS_CASE)
 #undef NTOPS_RMS_CASE
   }
-  hipLaunchKernelGGL((k_rms_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, wrs, y, ys, cols, feps);
+  hipLaunchKernelGGL((k_rms_loop<T, W>), blocks_2d(rows), dim3(256), 0, st, x, xs, w, wrs, y, ys, rows, cols, feps);
   return check_launch("rms_norm");
 }
 
@@ -332,7 +335,7 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
   if (vec) {
 #define NTOPS_LN_CASE(CH, WP)                                                                     \
   if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
-    hipLaunchKernelGGL((k_ln_vec<T, W, CH, WP>), dim3(ceil_div(rows, RowShape<WP>::kRowsPerBlock)),       \
+    hipLaunchKernelGGL((k_ln_vec<T, W, CH, WP>), blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
                        dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, b, y, ys, rows,             \
                        static_cast<int>(cols), feps);                                             \
     return check_launch("layer_norm");                                                            \
@@ -340,7 +343,7 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
     NTOPS_DEEP_ROW_CASES(NTOPS_LN_CASE)
 #undef NTOPS_LN_CASE
   }
-  hipLaunchKernelGGL((k_ln_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, w, b, wrs, y, ys, cols,
+  hipLaunchKernelGGL((k_ln_loop<T, W>), blocks_2d(rows), dim3(256), 0, st, x, xs, w, b, wrs, y, ys, rows, cols,
                      feps);
   return check_launch("layer_norm");
 }
@@ -363,7 +366,7 @@ int run_add_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const vo
   if (vec) {
 #define NTOPS_ADD_RMS_CASE(CH, WP)                                                                \
   if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
-    hipLaunchKernelGGL((k_add_rms_vec<T, W, CH, WP>), dim3(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
+    hipLaunchKernelGGL((k_add_rms_vec<T, W, CH, WP>), blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
                        dim3(RowShape<WP>::kThreads), 0, st, x, xs, r, rs, w, y, ys, ro, ros,      \
                        rows, static_cast<int>(cols), feps);                                       \
     return check_launch("add_rms_norm");                                                          \
@@ -371,8 +374,8 @@ int run_add_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const vo
     NTOPS_ROW_CASES(NTOPS_ADD_RMS_CASE)
 #undef NTOPS_ADD_RMS_CASE
   }
-  hipLaunchKernelGGL((k_add_rms_loop<T, W>), dim3(rows), dim3(256), 0, st, x, xs, r, rs, w, wrs, y, ys, ro, ros,
-                     cols, feps);
+  hipLaunchKernelGGL((k_add_rms_loop<T, W>), blocks_2d(rows), dim3(256), 0, st, x, xs, r, rs, w, wrs, y, ys, ro, ros,
+                     rows, cols, feps);
   return check_launch("add_rms_norm");
 }
 

@@ -199,3 +199,26 @@ def test_layer_norm_config_full_size():
     assert_close(got, exp, 1.6e-2, 1.6e-2, "layer_norm config")
     mism = (got.cpu() != exp).float().mean().item()
     assert mism < 1e-3, f"bit mismatch fraction {mism}"
+
+
+@pytest.mark.parametrize("cols", (8, 7))
+def test_norms_many_rows(cols):
+    """200003 rows: more row groups than one grid dimension holds (the
+    blocks form a 2-D grid whose last row has ids past the end), on the
+    register-resident kernels (8 bf16 columns) and the looped ones (7)."""
+    g = torch.Generator().manual_seed(cols)
+    rows = 200003
+    x = (torch.randn(rows, cols, generator=g) + 0.5).bfloat16()
+    w = (1 + 0.1 * torch.randn(cols, generator=g)).bfloat16()
+    b = (0.1 * torch.randn(cols, generator=g)).bfloat16()
+    rtol, atol = TOL_REDUCTION["bf16"]
+    got = ntops_amd.torch.rms_norm(x.cuda(), (cols,), w.cuda(), 1e-6)
+    assert_close(got, from_np(O.rms_norm(to_np(x), "bf16", cols, to_np(w), 1e-6), "bf16"), rtol, atol, "rms_norm")
+    got = ntops_amd.torch.layer_norm(x.cuda(), (cols,), w.cuda(), b.cuda(), 1e-5)
+    assert_close(got, from_np(O.layer_norm(to_np(x), "bf16", cols, to_np(w), to_np(b), 1e-5), "bf16"), rtol, atol,
+                 "layer_norm")
+    r = torch.randn(rows, cols, generator=g).bfloat16()
+    y, h = ntops_amd.torch.add_rms_norm(x.cuda(), r.cuda(), (cols,), w.cuda(), 1e-6)
+    ey, eh = O.add_rms_norm(to_np(x), to_np(r), "bf16", cols, to_np(w), 1e-6, "bf16")
+    assert torch.equal(h.cpu(), from_np(eh, "bf16")), "add_rms_norm residual"
+    assert_close(y, from_np(ey, "bf16"), rtol, atol, "add_rms_norm")

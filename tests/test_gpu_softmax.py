@@ -103,3 +103,12 @@ def test_softmax_config_full_size():
     assert torch.allclose(sums, torch.ones_like(sums), atol=2e-2), "row sums"
     assert (got.masked_select(mask.cuda().expand(B, H, S, S)) == 0).all(), "causal zeros"
     assert (got[:, :, 0, 0] == 1).all(), "row 0 is one-hot"
+
+
+@pytest.mark.parametrize("cols", (8, 7))
+def test_softmax_many_rows(cols):
+    """200003 rows: the register-resident (8 bf16 columns) and looped (7)
+    kernels on a 2-D grid of blocks whose last row has ids past the end."""
+    x = (torch.randn(200003, cols, generator=torch.Generator().manual_seed(cols)) * 3).bfloat16()
+    got = ntops_amd.torch.softmax(x.cuda(), -1)
+    assert_close(got, from_np(O.softmax(to_np(x), -1, "bf16"), "bf16"), *TOL_REDUCTION["bf16"], "softmax")
