@@ -234,6 +234,12 @@ struct TileLoader {
   // CONV: tiles must be issued in order k0 = 0, BK, 2 BK, ... (each call
   // advances the (c, r, s) state by BK k-rows).
   __device__ __forceinline__ void issue(char* lds, int k0, int valid, int K, const GemmArgs* cv = nullptr) {
+    issue(lds_addr(lds), k0, valid, K, cv);
+  }
+  // The same with the tile's 32-bit LDS address (the kernels form it from
+  // the LDS base once: a generic -> LDS pointer cast per load instruction
+  // carries a null test, 3-4 scalar instructions each).
+  __device__ __forceinline__ void issue(uint32_t lds, int k0, int valid, int K, const GemmArgs* cv = nullptr) {
     // channels-last: the tile's (channel block, tap) offset in bytes, then
     // advance to the next K tile's: the next tap, after the last tap the
     // next block
@@ -276,9 +282,7 @@ struct TileLoader {
           ok = k0 + lim_row[i] < K && lim_col[i] < valid;
         off = ok ? off : kOOB;
       }
-      const uint32_t dst = __builtin_amdgcn_readfirstlane(
-          static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds + lds_base + i * 1024))));
-      dma16(rsrc, dst, off);
+      dma16(rsrc, lds + static_cast<uint32_t>(lds_base + i * 1024), off);
     }
   }
 };
@@ -514,8 +518,9 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
   else
     lb.init(B + n0, g.sb_k, (static_cast<int64_t>(g.K - 1) * g.sb_k + n_valid) * 2, wave, lane);
 
+  const uint32_t smem_addr = lds_addr(smem);
   auto issue = [&](int stage, int k0) {
-    char* base = smem + stage * kStage;
+    const uint32_t base = smem_addr + static_cast<uint32_t>(stage * kStage);
     la.issue(base, k0, m_valid, g.K);
     lb.issue(base + kATile, k0, n_valid, g.K, &g);
   };

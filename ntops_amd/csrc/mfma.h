@@ -84,6 +84,11 @@ __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_dst, uint32_t vof
                : "memory");
 }
 
+// 32-bit LDS address of a pointer into the block's LDS (wave-uniform).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)p)));
+}
+
 // Packs 8 fp32 values into an MFMA operand of 8 T elements (one rounding).
 template <typename T>
 __device__ __forceinline__ u32x4 pack8(const float* v) {
