@@ -151,7 +151,7 @@ struct KvDma {
     rsrc.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32) & 0xffffu);
     rsrc.z = __builtin_amdgcn_readfirstlane(extent);
     rsrc.w = 0x00020000u;
-    lds_off = wave * kInst * 1024;
+    lds_off = __builtin_amdgcn_readfirstlane(wave * kInst * 1024);
     constexpr int cpr = D / 8;
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
@@ -173,11 +173,12 @@ struct KvDma {
     return r;
   }
 
-  // Loads tile t into `tile` (its LDS home) through resource r (this
-  // operand's own by default); a tile past the end loads nothing but still
-  // counts once per instruction in vmcnt.
-  __device__ __forceinline__ void issue(char* tile, int t, bool valid) const { issue(rsrc, tile, t, valid); }
-  __device__ __forceinline__ void issue(u32x4 r, char* tile, int t, bool valid) const {
+  // Loads tile t into LDS at the 32-bit LDS address `tile` through resource
+  // r; a tile past the end loads nothing but still counts once per
+  // instruction in vmcnt.  Kernels form the address from the LDS base once:
+  // a generic -> LDS pointer cast per load instruction carries a null test,
+  // 3-4 scalar instructions each.
+  __device__ __forceinline__ void issue(u32x4 r, uint32_t tile, int t, bool valid) const {
     // t passes through an empty asm so that the offsets of tiles issued at
     // fixed points (an item's first and last tiles) are computed here, not
     // hoisted out of the item loop to sit in registers for the whole kernel
@@ -185,9 +186,7 @@ struct KvDma {
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
       const uint32_t off = valid ? voff[i] + static_cast<uint32_t>(t) * tile_bytes : kOOB;
-      const uint32_t dst = __builtin_amdgcn_readfirstlane(
-          static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(tile + lds_off + i * 1024))));
-      dma16(r, dst, off);
+      dma16(r, tile + static_cast<uint32_t>(lds_off + i * 1024), off);
     }
   }
 };
@@ -317,10 +316,11 @@ __global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int t
   KvDma<D, true, 4> vd;
   kd.init(K, a.ks[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane);
   vd.init(V, a.vs[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane);
+  const uint32_t smem_addr = lds_addr(smem);
   auto dma = [&](int t) {
-    char* st = smem + (t & 1) * 2 * kTile;
-    kd.issue(st, t, true);
-    vd.issue(st + kTile, t, true);
+    const uint32_t st = smem_addr + static_cast<uint32_t>((t & 1) * 2 * kTile);
+    kd.issue(kd.rsrc, st, t, true);
+    vd.issue(vd.rsrc, st + kTile, t, true);
   };
 
   f32x16 o[DT];
@@ -615,8 +615,9 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb) {
   // Slot g of the load stream: this item's tile g, then the next item's
   // tiles 0 and 1 (empty loads when there is no next item, so that every
   // period issues L instructions until the last one), then nothing.
+  const uint32_t smem_addr = lds_addr(smem);
   auto dma = [&](int g) {
-    char* st = smem + ((base + g) & 3) * kStage;
+    const uint32_t st = smem_addr + static_cast<uint32_t>(((base + g) & 3) * kStage);
     if (g < nkv) {
       kd.issue(rk, st, g, true);
       vd.issue(rv, st + kTile, g, true);
