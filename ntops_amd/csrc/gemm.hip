@@ -555,10 +555,15 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
   // with one extra barrier so every wave executes the same number.
   if (grp == 1) block_barrier();
   u32x4 af[KS][TM], bf[KS][TN];
-  for (int k = 0; k < ktiles; ++k) {
+  // One K tile.  STEADY: tile k + STAGES - 1 exists, so the refill is
+  // unconditional and the wait for tile k + 1 a constant (the loop over
+  // these tiles carries no per-tile branches); the last STAGES - 1 tiles
+  // take the general form.
+  auto tile = [&](int k, auto steady_tag) {
+    constexpr bool STEADY = decltype(steady_tag)::value;
     // memory phase: refill the stage of tile k - 1 with tile k + STAGES - 1,
     // then read all of tile k's fragments.
-    if (k + STAGES - 1 < ktiles) issue((k + STAGES - 1) % STAGES, (k + STAGES - 1) * BK);
+    if (STEADY || k + STAGES - 1 < ktiles) issue((k + STAGES - 1) % STAGES, (k + STAGES - 1) * BK);
     const char* sa = smem + (k % STAGES) * kStage;
     const char* sb = sa + kATile;
 #pragma unroll
@@ -572,7 +577,10 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
     // this wave's share of tile k + 1 has landed before the barrier that
     // opens the next memory phase of either group.
     wait_lgkmcnt0();
-    if (k + 1 < ktiles) wait_tile(min(STAGES - 2, ktiles - 2 - k), kLoadsPerTile);
+    if constexpr (STEADY)
+      wait_vmcnt<(STAGES - 2) * kLoadsPerTile>();
+    else if (k + 1 < ktiles)
+      wait_tile(min(STAGES - 2, ktiles - 2 - k), kLoadsPerTile);
     block_barrier();
     // MFMA phase, at raised wave priority so the SIMD's arbiter issues the
     // matrix wave ahead of its memory-phase partner (+0.8 % on mm).
@@ -585,7 +593,10 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[ks][j], af[ks][i], acc[i][j]);
     __builtin_amdgcn_s_setprio(0);
     block_barrier();
-  }
+  };
+  int k = 0;
+  for (; k + STAGES - 1 < ktiles; ++k) tile(k, std::true_type{});
+  for (; k < ktiles; ++k) tile(k, std::false_type{});
   if (grp == 0) block_barrier();
 
   T* D = static_cast<T*>(g.D) + bat * g.sd_b;
