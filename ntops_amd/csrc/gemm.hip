@@ -228,17 +228,14 @@ struct TileLoader {
     rsrc.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32) & 0xffffu);
   }
 
-  // Issues the loads of the K tile starting at k0 into `lds` (this operand's
-  // tile in one LDS stage).  `valid` is the number of valid tile rows
-  // (K-major) or tile columns (M/N-major); K bounds the k axis.
+  // Issues the loads of the K tile starting at k0 into LDS at the 32-bit
+  // LDS address `lds` (this operand's tile in one LDS stage; the kernels
+  // form it from the LDS base once: a generic -> LDS pointer cast per load
+  // instruction carries a null test, 3-4 scalar instructions each).
+  // `valid` is the number of valid tile rows (K-major) or tile columns
+  // (M/N-major); K bounds the k axis.
   // CONV: tiles must be issued in order k0 = 0, BK, 2 BK, ... (each call
   // advances the (c, r, s) state by BK k-rows).
-  __device__ __forceinline__ void issue(char* lds, int k0, int valid, int K, const GemmArgs* cv = nullptr) {
-    issue(lds_addr(lds), k0, valid, K, cv);
-  }
-  // The same with the tile's 32-bit LDS address (the kernels form it from
-  // the LDS base once: a generic -> LDS pointer cast per load instruction
-  // carries a null test, 3-4 scalar instructions each).
   __device__ __forceinline__ void issue(uint32_t lds, int k0, int valid, int K, const GemmArgs* cv = nullptr) {
     // channels-last: the tile's (channel block, tap) offset in bytes, then
     // advance to the next K tile's: the next tap, after the last tap the
@@ -702,12 +699,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_panel(GemmArgs g, int seg) {
     c.first = j == 0;
     return c;
   };
+  const uint32_t smem_addr = lds_addr(smem);
   auto issue = [&](const Coord& c) {
     la.rebase(A0 + c.bat * g.sa_b + (AK ? static_cast<int64_t>(c.m0) * g.sa_m : c.m0));
-    la.issue(smem + kOffA, 0, BM, g.K);
+    la.issue(smem_addr + kOffA, 0, BM, g.K);
     if (c.first) {
       lb.rebase(B0 + c.bat * g.sb_b + (BKM ? static_cast<int64_t>(c.n0) * g.sb_n : c.n0));
-      lb.issue(smem + kOffB, 0, BN, g.K);
+      lb.issue(smem_addr + kOffB, 0, BN, g.K);
     }
   };
 
