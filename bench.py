@@ -963,8 +963,8 @@ def main():
         counter_table(args.counters, args.kernels)
         return
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(every op runs on a single MI355X; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: this library measures one GPU; --gpus {args.gpus} is not supported "
+              "(every op runs on a single MI355X; the ops are not sharded across GPUs)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
