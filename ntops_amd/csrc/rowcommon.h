@@ -80,7 +80,8 @@ __device__ __forceinline__ C row_max(C v, C* red, const RowPos& p) {
 // more waves per row measured faster on MI355X than deep per-lane unrolling
 // (e.g. 4096 bf16: 2 packs x 4 waves reaches ~5.9 TB/s, 8 packs x 1 wave
 // ~4.9 TB/s): more rows are in flight per CU and the per-row reduction is
-// shorter.  `deep` picks 4 packs x 2 waves for rows of 257-512 packs instead
+// shorter.  One pack per lane goes too far (rms_norm bf16 (16384, 4096) with
+// 1 pack x 8 waves: 48.3 against 44.0 us).  `deep` picks 4 packs x 2 waves for rows of 257-512 packs instead
 // (layer_norm, whose two dependent reductions gain from the longer per-lane
 // runs: bf16 (16384, 4096) 47.5 -> 45.9 us, where rms_norm and add_rms_norm
 // lose 1-4 % with it).  Rows wider than 8 packs x 16 waves use the looped
