@@ -87,6 +87,19 @@ struct ConvArgs {
   int sh, sw, ph, pw, dh, dw;
 };
 
+// Output plane rows of pq pixels from rows of ld pixels (image i, channel
+// k: src[(i K + k) ld + p] -> dst[i os0 + k os1 + p]), one element per
+// thread.
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_rows_out(const T* src, int64_t ld, T* dst, int64_t os0,
+                                                       int64_t os1, int64_t K, int64_t pq, int64_t total) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= total) return;
+  const int64_t p = e % pq, r = e / pq;  // r = i K + k
+  const int64_t i = r / K, k = r - i * K;
+  dst[i * os0 + k * os1 + p] = src[r * ld + p];
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_conv_direct(ConvArgs a, int64_t total) {
   using O = typename OpMath<T>::T_;
@@ -476,21 +489,31 @@ unsigned grid_for(int64_t work, int per_block) {
 // Pixels per unfolded row (a multiple of 8, so rows stay 16-byte aligned).
 int64_t col_ld(const ConvArgs& a) { return (static_cast<int64_t>(a.P) * a.Q + 7) / 8 * 8; }
 
-// Whether the GEMM path applies: enough reduction depth and output channels
-// to feed the matrix cores, unit-stride weight rows of a multiple of 8
-// elements, and pixel planes of the output that are contiguous.
+// Whether the GEMM path applies: enough reduction depth, output channels and
+// output pixels to feed the matrix cores, unit-stride weight rows of a
+// multiple of 8 elements, and pixel planes of the output that are
+// contiguous.
 bool use_gemm(const ConvArgs& a, int dt) {
   const int64_t crs = static_cast<int64_t>(a.C) * a.R * a.S;
   const int64_t pq = static_cast<int64_t>(a.P) * a.Q;
   const bool w_rows = a.ws[3] == 1 && a.ws[2] == a.S && a.ws[1] == static_cast<int64_t>(a.R) * a.S &&
                       a.ws[0] % 8 == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15u) == 0;
   const bool out_plane = a.os[3] == 1 && a.os[2] == a.Q;
-  return dt != NTOPS_F64 && crs >= 64 && crs % 8 == 0 && a.K >= 32 && pq >= 64 && w_rows && out_plane &&
+  return dt != NTOPS_F64 && crs >= 64 && crs % 8 == 0 && a.K >= 32 && pq >= 16 && w_rows && out_plane &&
          crs * col_ld(a) <= 0x7fffffffLL;
 }
 
 int64_t col_bytes_per_image(const ConvArgs& a, int dt) {
   return static_cast<int64_t>(a.C) * a.R * a.S * col_ld(a) * dtype_size(dt);
+}
+
+// Output planes whose pixel count is not a multiple of 8 are computed at
+// the unfold's padded width (the matrix-core GEMM's N-major operand and
+// vector stores need it) into the workspace, then copied out: bytes per
+// image of that staging (0 when the plane is written directly).
+int64_t padded_out_bytes_per_image(const ConvArgs& a, int dt) {
+  const int64_t pq = static_cast<int64_t>(a.P) * a.Q;
+  return pq % 8 ? static_cast<int64_t>(a.K) * col_ld(a) * dtype_size(dt) : 0;
 }
 
 // Rows of each shifted plane of the implicit path.
@@ -542,7 +565,7 @@ bool use_channels_last(const ConvArgs& a, int dt) {
 int64_t ws_bytes_per_image(const ConvArgs& a, int dt) {
   if (use_channels_last(a, dt)) return cl_rows(a) * cl_cols(a) * a.C * dtype_size(dt);
   if (use_implicit(a, dt)) return static_cast<int64_t>(a.S) * a.C * shift_rows(a) * a.Q * dtype_size(dt);
-  return col_bytes_per_image(a, dt);
+  return col_bytes_per_image(a, dt) + padded_out_bytes_per_image(a, dt);
 }
 
 // Workspace bytes the chosen GEMM path needs once per call, ahead of the
@@ -730,6 +753,11 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
   const int64_t c_str[3] = {0, bias_stride, 0};
   const int64_t d_str[3] = {out_strides[0], out_strides[1], 1};
   const int es = dtype_size(dtype);
+  // planes of P Q % 8 != 0 pixels: the GEMM writes rows of ld pixels into
+  // the workspace after the unfold, then k_conv_rows_out copies them out
+  const bool padded = padded_out_bytes_per_image(a, dtype) > 0;
+  void* staged = static_cast<char*>(workspace) + nb_max * crs * ld * es;
+  const int64_t s_str[3] = {K * ld, ld, 1};
   for (int64_t n0 = 0; n0 < N; n0 += nb_max) {
     const int64_t nb = std::min(nb_max, N - n0);
     rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
@@ -745,9 +773,21 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
     });
     if (rc != NTOPS_OK) return rc;
     void* dst = static_cast<char*>(out) + n0 * out_strides[0] * es;
-    rc = ntops_gemm(dtype, nb, K, P * Q, crs, w, a_str, workspace, b_str, bias, bias ? c_str : nullptr, 1.0,
-                    bias ? 1.0 : 0.0, dst, d_str, stream);
+    rc = ntops_gemm(dtype, nb, K, padded ? ld : P * Q, crs, w, a_str, workspace, b_str, bias,
+                    bias ? c_str : nullptr, 1.0, bias ? 1.0 : 0.0, padded ? staged : dst, padded ? s_str : d_str,
+                    stream);
     if (rc != NTOPS_OK) return rc;
+    if (padded) {
+      rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
+        using T = decltype(tag);
+        const int64_t total = nb * K * P * Q;
+        hipLaunchKernelGGL(k_conv_rows_out<T>, dim3(grid_for(total, 256)), dim3(256), 0, st,
+                           static_cast<const T*>(staged), ld, static_cast<T*>(dst), out_strides[0],
+                           out_strides[1], K, P * Q, total);
+        return check_launch("conv2d");
+      });
+      if (rc != NTOPS_OK) return rc;
+    }
   }
   return NTOPS_OK;
 }

@@ -64,6 +64,10 @@ GEMM_CASES = [
     (2, 48, 16, 16, 64, 3, 3, 1, 1, 1, True),
     (1, 128, 16, 16, 256, 1, 1, 1, 0, 1, True),
     (2, 32, 33, 22, 64, 3, 3, (2, 1), (1, 2), (2, 3), True),
+    # output planes of P Q % 8 != 0 pixels (7 x 7, 9 x 9): unfold + GEMM at the
+    # padded width, then the planes copied out
+    (4, 64, 7, 7, 64, 3, 3, 1, 1, 1, True),
+    (3, 32, 9, 9, 40, 3, 3, 1, 1, 1, False),
 ]
 
 
