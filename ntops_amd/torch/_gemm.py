@@ -3,7 +3,7 @@
 import torch
 
 from ntops_amd import _lib
-from ntops_amd.torch.utils import _DeviceGuard
+from ntops_amd.torch.utils import _DeviceGuard, _cast_into
 
 _GEMM_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 
@@ -13,6 +13,19 @@ def _strides3(t):
     if t.dim() == 2:
         return (0, t.stride(0), t.stride(1))
     return (t.stride(0) if t.shape[0] > 1 else 0, t.stride(1), t.stride(2))
+
+
+def _padded_width(a, b, n):
+    """Column count to run the GEMM at when n columns would send it to the
+    generic kernel (None otherwise): the matrix-core kernels load an N-major
+    B in 16-byte row pieces (16-bit: N % 8 == 0; fp32: N % 4 == 0) and store
+    4-column runs (N % 4 == 0)."""
+    unit = 4 if a.dtype == torch.float32 else 8
+    if n <= unit or n % unit == 0 or a.shape[-1] == 0 or a.shape[-2] == 0:
+        return None
+    if n % 4 == 0 and b.stride(-2) == 1 and b.stride(-1) != 1:  # K-major B: N is free
+        return None
+    return (n + unit - 1) // unit * unit
 
 
 def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, what="ntops_amd.mm"):
@@ -26,6 +39,29 @@ def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, what="ntops_amd.mm"):
                 f"{what}: expected all operands to have dtype {a.dtype}, got {t.dtype}"
             )
     dev = _lib.require_cuda(a, b, out, c)
+    n = b.shape[-1]
+    np_ = _padded_width(a, b, n)
+    if np_ is not None:
+        # B (and C) copied into rows of np_ columns, the product computed at
+        # that width, its first n columns copied out (the extra columns only
+        # ever meet the extra columns of B and C)
+        with _DeviceGuard(dev):
+            bp = torch.empty(b.shape[:-1] + (np_,), dtype=b.dtype, device=b.device)
+            _cast_into(b, bp[..., :n])
+            cp = None
+            if c is not None:
+                if all(s == 0 for s in c.stride()[:-1]):  # one row broadcast (a bias)
+                    row = torch.empty(np_, dtype=c.dtype, device=c.device)
+                    _cast_into(c[(0,) * (c.dim() - 1)], row[:n])
+                    cp = row.expand(out.shape[:-1] + (np_,))
+                else:
+                    cp = torch.empty(out.shape[:-1] + (np_,), dtype=c.dtype, device=c.device)
+                    _cast_into(c, cp[..., :n])
+            op = torch.empty(out.shape[:-1] + (np_,), dtype=out.dtype, device=out.device)
+        gemm(a, bp, op, cp, alpha, beta, what)
+        with _DeviceGuard(dev):
+            _cast_into(op[..., :n], out)
+        return out
     batch = a.shape[0] if a.dim() == 3 else 1
     m, k = a.shape[-2], a.shape[-1]
     n = b.shape[-1]

@@ -41,9 +41,14 @@ def expected16(m, n, k, layout, batch=1):
     """Family of the kernel that serves a 16-bit GEMM of fresh (16-byte
     aligned) operands in `layout` ("N" = row-major, "T" = transposed view):
     the matrix-core kernels need one unit-stride axis per operand with 8-element
-    multiples, and an output with N % 4 == 0."""
+    multiples, and an output with N % 4 == 0 (an N that would break either is
+    rounded up to 8 columns by the wrapper, B copied N-major)."""
     if m == 1:  # a transposed (1, k) view keeps the row-major strides
         layout = "N" + layout[1]
+    if n > 8 and n % 8 and (n % 4 or layout[1] == "N") and k > 0:
+        # the wrapper runs the product at the width rounded up to 8 columns,
+        # B copied N-major
+        n, layout = (n + 7) // 8 * 8, layout[0] + "N"
     a_k = layout[0] == "N" and k % 8 == 0
     a_m = layout[0] == "T" and m % 8 == 0
     b_n = layout[1] == "N" and n % 8 == 0
@@ -153,6 +158,42 @@ def test_mm_small_m(m, n, k, dtype, layout):
     got = ntops_amd.torch.mm(ag, bg)
     assert _lib.last_kernel().startswith(expected16(m, n, k, layout))
     check(got, a, b, dtype, what=f"mm small m {layout}")
+
+
+# N not a multiple of 8 (or of 4): the product runs at the padded width on
+# the matrix cores (a vocabulary-sized projection among them), as mm, as
+# addmm with a row bias and as bmm, every element against the oracle.
+ODD_N = [(300, 1001, 256), (2048, 50257, 768), (40, 1003, 520), (512, 100, 1024), (256, 13, 512)]
+
+
+@pytest.mark.parametrize("layout", ("NN", "NT"))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("m, n, k", ODD_N)
+def test_mm_odd_n(m, n, k, dtype, layout):
+    g = torch.Generator().manual_seed(m + n + k)
+    a = (0.1 * torch.randn(m, k, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(k, n, generator=g)).to(dtype)
+    bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
+    rows = tile_rows(m) if m > 1024 else list(range(m))
+    got = ntops_amd.torch.mm(a.cuda(), bg)
+    if dtype != torch.float32:
+        assert _lib.last_kernel().startswith(expected16(m, n, k, "N" + layout[1])), _lib.last_kernel()
+        assert not _lib.last_kernel().startswith("gemm_generic")
+    check(got[rows], a[rows], b, dtype, what=f"mm odd n {layout}")
+    bias = (0.1 * torch.randn(n, generator=g)).to(dtype)
+    got = ntops_amd.torch.addmm(bias.cuda(), a.cuda(), bg, beta=0.5, alpha=2.0)
+    check(got[rows], a[rows], b, dtype, c=bias.expand(len(rows), n), alpha=2.0, beta=0.5,
+          what=f"addmm odd n {layout}")
+
+
+def test_bmm_odd_n():
+    g = torch.Generator().manual_seed(5)
+    a = (0.1 * torch.randn(3, 200, 264, generator=g)).bfloat16()
+    b = (0.1 * torch.randn(3, 264, 203, generator=g)).bfloat16()
+    got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
+    assert not _lib.last_kernel().startswith("gemm_generic"), _lib.last_kernel()
+    for i in range(3):
+        check(got[i], a[i], b[i], torch.bfloat16, what="bmm odd n")
 
 
 @pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
