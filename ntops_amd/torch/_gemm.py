@@ -28,6 +28,33 @@ def _padded_width(a, b, n):
     return (n + unit - 1) // unit * unit
 
 
+def _padded_depth(a, b, k):
+    """Depth to run the GEMM at when a K-major operand's rows of k elements
+    would send it to the generic kernel (None otherwise)."""
+    unit = 4 if a.dtype == torch.float32 else 8
+    if k <= unit or k % unit == 0 or a.shape[-2] == 0 or b.shape[-1] == 0:
+        return None
+    a_kmajor = a.stride(-1) == 1
+    b_kmajor = b.stride(-2) == 1 and b.stride(-1) != 1
+    if not (a_kmajor or b_kmajor):
+        return None
+    return (k + unit - 1) // unit * unit
+
+
+def _pad_last_two(t, rows, cols):
+    """A new tensor of t's batch shape x (rows, cols) holding t in its leading
+    corner and zeros elsewhere (copies and fills by the native cast kernel)."""
+    p = torch.empty(t.shape[:-2] + (rows, cols), dtype=t.dtype, device=t.device)
+    zero = torch.zeros((), dtype=t.dtype, device=t.device)
+    r, c = t.shape[-2], t.shape[-1]
+    _cast_into(t, p[..., :r, :c])
+    if cols > c:
+        _cast_into(zero.expand(p[..., :, c:].shape), p[..., :, c:])
+    if rows > r:
+        _cast_into(zero.expand(p[..., r:, :c].shape), p[..., r:, :c])
+    return p
+
+
 def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, what="ntops_amd.mm"):
     """out = alpha * (a @ b) + beta * c for 2-D (mm) or 3-D (bmm) operands;
     c is already expanded to out's shape (stride 0 where broadcast)."""
@@ -39,6 +66,15 @@ def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, what="ntops_amd.mm"):
                 f"{what}: expected all operands to have dtype {a.dtype}, got {t.dtype}"
             )
     dev = _lib.require_cuda(a, b, out, c)
+    k = a.shape[-1]
+    kp = _padded_depth(a, b, k)
+    if kp is not None:
+        # A's rows and B's columns extended with zeros to depth kp (the
+        # products they add are exact zeros)
+        with _DeviceGuard(dev):
+            ap = _pad_last_two(a, a.shape[-2], kp)
+            bp = _pad_last_two(b, kp, b.shape[-1])
+        return gemm(ap, bp, out, c, alpha, beta, what)
     n = b.shape[-1]
     np_ = _padded_width(a, b, n)
     if np_ is not None:

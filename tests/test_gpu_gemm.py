@@ -45,6 +45,10 @@ def expected16(m, n, k, layout, batch=1):
     rounded up to 8 columns by the wrapper, B copied N-major)."""
     if m == 1:  # a transposed (1, k) view keeps the row-major strides
         layout = "N" + layout[1]
+    if k > 8 and k % 8 and (layout[0] == "N" or layout[1] == "T") and n > 0:
+        # the wrapper zero-extends K to a multiple of 8, both operands copied
+        # into fresh row-major tensors
+        k, layout = (k + 7) // 8 * 8, "NN"
     if n > 8 and n % 8 and (n % 4 or layout[1] == "N") and k > 0:
         # the wrapper runs the product at the width rounded up to 8 columns,
         # B copied N-major
@@ -184,6 +188,27 @@ def test_mm_odd_n(m, n, k, dtype, layout):
     got = ntops_amd.torch.addmm(bias.cuda(), a.cuda(), bg, beta=0.5, alpha=2.0)
     check(got[rows], a[rows], b, dtype, c=bias.expand(len(rows), n), alpha=2.0, beta=0.5,
           what=f"addmm odd n {layout}")
+
+
+# K not a multiple of 8 (or of 4): A's rows and B's columns zero-extended so
+# the matrix cores take the product.
+ODD_K = [(300, 256, 100), (1000, 1024, 1001), (40, 512, 77), (2048, 2048, 4095)]
+
+
+@pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("m, n, k", ODD_K)
+def test_mm_odd_k(m, n, k, dtype, layout):
+    g = torch.Generator().manual_seed(m + 3 * n + k)
+    a = (0.1 * torch.randn(m, k, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(k, n, generator=g)).to(dtype)
+    ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
+    bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
+    rows = tile_rows(m) if m > 1024 else list(range(m))
+    got = ntops_amd.torch.mm(ag, bg)
+    if dtype != torch.float32:
+        assert _lib.last_kernel().startswith(expected16(m, n, k, layout)), _lib.last_kernel()
+    check(got[rows], a[rows], b, dtype, what=f"mm odd k {layout}")
 
 
 def test_bmm_odd_n():
