@@ -91,7 +91,7 @@ def test_sdpa(b, hq, sq, d, hkv, skv, mask_type, is_causal, scale, variant, kv_c
 
 
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
-@pytest.mark.parametrize("d", (64, 128))
+@pytest.mark.parametrize("d", (64, 128, 80, 96))  # 80, 96: zero-extended to 128 for 16-bit data
 def test_sdpa_edges(dtype, d):
     g = torch.Generator().manual_seed(d)
     rt = lambda *s: torch.randn(*s, generator=g).to(dtype)  # noqa: E731
