@@ -159,6 +159,63 @@ __global__ __launch_bounds__(256) void k_softmax_loop(const Ti* x, int64_t xs0, 
     yr[j * ys1] = convert<To>(ex(static_cast<C>(convert<To>(xr[j * xs1])) - m) * inv);
 }
 
+// The same over unit-stride rows of any width and alignment when input and
+// output share a dtype: each row as a scalar head up to its first 16-byte
+// boundary, 16-byte packs, a scalar tail (a vocabulary-wide row of 50257
+// bf16 elements is 16-byte aligned on at most one row in eight); the output
+// in packs too when its row has the input row's alignment (contiguous
+// tensors), else element by element.
+template <typename T, typename C>
+__global__ __launch_bounds__(256) void k_softmax_loop_v(const T* x, int64_t xs0, T* y, int64_t ys0,
+                                                        int64_t rows, int64_t cols) {
+  constexpr int V = Pack16<T>::N;
+  __shared__ C red[4];
+  const int64_t row = block_id();
+  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
+  const T* xr = x + row * xs0;
+  T* yr = y + row * ys0;
+  const int mis = static_cast<int>((reinterpret_cast<uintptr_t>(xr) & 15u) / sizeof(T));
+  const int64_t head = mis ? (V - mis < cols ? V - mis : cols) : 0;
+  const int64_t packs = (cols - head) / V;
+  const int64_t tail = head + packs * V;
+  const T* xb = xr + head;  // 16-byte aligned
+  const int t = threadIdx.x;
+  C m = -__builtin_huge_val();
+  if (t < head) m = static_cast<C>(xr[t]);
+  for (int64_t p = t; p < packs; p += 256) {
+    const Pack16<T> v = load16(xb + p * V);
+#pragma unroll
+    for (int e = 0; e < V; ++e) m = cmax(m, static_cast<C>(v.v[e]));
+  }
+  for (int64_t j = tail + t; j < cols; j += 256) m = cmax(m, static_cast<C>(xr[j]));
+  m = block_max256(m, red);
+  C s = 0;
+  if (t < head) s = ex(static_cast<C>(xr[t]) - m);
+  for (int64_t p = t; p < packs; p += 256) {
+    const Pack16<T> v = load16(xb + p * V);
+#pragma unroll
+    for (int e = 0; e < V; ++e) s += ex(static_cast<C>(v.v[e]) - m);
+  }
+  for (int64_t j = tail + t; j < cols; j += 256) s += ex(static_cast<C>(xr[j]) - m);
+  s = block_sum256(s, red);
+  const C inv = C(1) / s;
+  if (t < head) yr[t] = convert<T>(ex(static_cast<C>(xr[t]) - m) * inv);
+  const bool packed_out = ((reinterpret_cast<uintptr_t>(yr) ^ reinterpret_cast<uintptr_t>(xr)) & 15u) == 0;
+  for (int64_t p = t; p < packs; p += 256) {
+    const Pack16<T> v = load16(xb + p * V);
+    Pack16<T> o;
+#pragma unroll
+    for (int e = 0; e < V; ++e) o.v[e] = convert<T>(ex(static_cast<C>(v.v[e]) - m) * inv);
+    if (packed_out) {
+      store16(yr + head + p * V, o);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) yr[head + p * V + e] = o.v[e];
+    }
+  }
+  for (int64_t j = tail + t; j < cols; j += 256) yr[j] = convert<T>(ex(static_cast<C>(xr[j]) - m) * inv);
+}
+
 // One thread per (outer, inner) column.
 template <typename Ti, typename To, typename C>
 __global__ __launch_bounds__(256) void k_softmax_col(const Ti* x, int64_t xs0, int64_t xs1,
@@ -206,6 +263,11 @@ int run_softmax(int64_t outer, int64_t dim, int64_t inner, const void* xv, const
   }
         NTOPS_ROW_CASES(NTOPS_SM_CASE)
 #undef NTOPS_SM_CASE
+      }
+      if (xs[1] == 1 && ys[1] == 1 && outer <= 0x7fffffffLL) {
+        hipLaunchKernelGGL((k_softmax_loop_v<To, C>), blocks_2d(outer), dim3(256), 0, st, x, xs[0], y, ys[0],
+                           outer, dim);
+        return check_launch("softmax");
       }
     }
     if (outer > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "softmax: too many rows");

@@ -56,6 +56,23 @@ def test_softmax_widths(cols, dtype):
     assert_close(got, exp, *TOL_REDUCTION[dt], f"softmax width {cols}")
 
 
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("cols", (50257, 1001, 13, 7))
+def test_softmax_odd_width_row_views(cols, dtype):
+    """Rows whose width is no multiple of a 16-byte pack, read through views
+    that start at different offsets (so each row has its own head / pack /
+    tail split, and the output rows -- contiguous -- are aligned unlike the
+    input rows, the element-store branch)."""
+    g = torch.Generator().manual_seed(cols)
+    x = (torch.randn(37, cols + 3, generator=g) * 3).to(dtype)
+    xg = x.cuda()
+    dt = DT_NAME[dtype]
+    for lo in (0, 1, 3):
+        got = ntops_amd.torch.softmax(xg[:, lo:lo + cols], -1)
+        exp = from_np(O.softmax(to_np(x[:, lo:lo + cols].contiguous()), -1, dt), dt)
+        assert_close(got, exp, *TOL_REDUCTION[dt], f"softmax row views offset {lo}")
+
+
 def test_softmax_special_rows():
     x = torch.randn(4, 64)
     x[1] = float("-inf")  # all -inf -> NaN, like torch
