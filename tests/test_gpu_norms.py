@@ -116,6 +116,24 @@ def test_layer_norm_offset_rows(cols, dtype):
     assert_close(got, exp, rtol, atol, f"ln offset rows {cols}")
 
 
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("cols", (4100, 1001, 13))
+def test_rms_norm_odd_width_row_views(cols, dtype):
+    """rms_norm on rows that are no multiple of a 16-byte pack, through views
+    starting at different offsets (the looped kernel, rows at every 16-byte
+    alignment)."""
+    g = torch.Generator().manual_seed(cols)
+    x = torch.randn(29, cols + 3, generator=g).to(dtype)
+    w = (1 + 0.02 * torch.randn(cols, generator=g)).to(dtype)
+    xg = x.cuda()
+    dt = DT_NAME[dtype]
+    rtol, atol = TOL_REDUCTION[dt]
+    for lo in (0, 1, 3):
+        got = ntops_amd.torch.rms_norm(xg[:, lo:lo + cols], (cols,), w.cuda(), 1e-6)
+        exp = from_np(O.rms_norm(to_np(x[:, lo:lo + cols].contiguous()), dt, cols, to_np(w), 1e-6), dt)
+        assert_close(got, exp, rtol, atol, f"rms_norm row views offset {lo}")
+
+
 def test_norm_noncontiguous_input_and_fp32_weight():
     x = torch.randn(64, 96).bfloat16()
     xg = x.cuda().t()  # (96, 64) non-contiguous
