@@ -68,6 +68,11 @@ GEMM_CASES = [
     # padded width, then the planes copied out
     (4, 64, 7, 7, 64, 3, 3, 1, 1, 1, True),
     (3, 32, 9, 9, 40, 3, 3, 1, 1, 1, False),
+    # 16-63 output pixels, which the GEMM paths take from 16 on: 4 x 4 and
+    # 6 x 6 planes (channels-last), 5 x 5 with C % 32 != 0 (padded unfold)
+    (8, 64, 4, 4, 64, 3, 3, 1, 1, 1, True),
+    (4, 64, 6, 6, 96, 3, 3, 1, 1, 1, False),
+    (4, 48, 5, 5, 64, 3, 3, 1, 1, 1, True),
 ]
 
 
