@@ -89,15 +89,16 @@ struct ConvArgs {
 
 // Output plane rows of pq pixels from rows of ld pixels (image i, channel
 // k: src[(i K + k) ld + p] -> dst[i os0 + k os1 + p]), one element per
-// thread.
+// thread per step of a grid-stride loop (the grid is capped by grid_for).
 template <typename T>
 __global__ __launch_bounds__(256) void k_conv_rows_out(const T* src, int64_t ld, T* dst, int64_t os0,
                                                        int64_t os1, int64_t K, int64_t pq, int64_t total) {
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (e >= total) return;
-  const int64_t p = e % pq, r = e / pq;  // r = i K + k
-  const int64_t i = r / K, k = r - i * K;
-  dst[i * os0 + k * os1 + p] = src[r * ld + p];
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t p = e % pq, r = e / pq;  // r = i K + k
+    const int64_t i = r / K, k = r - i * K;
+    dst[i * os0 + k * os1 + p] = src[r * ld + p];
+  }
 }
 
 template <typename T>
@@ -210,11 +211,13 @@ __device__ __forceinline__ void stage_plane(const ConvArgs& a, const T* xc, T* p
 constexpr int kPlaneLds = 64 * 1024;
 
 template <typename T>
-__global__ __launch_bounds__(256) void k_im2col_plane(ConvArgs a, T* col, int n0, int64_t ld) {
+__global__ __launch_bounds__(256) void k_im2col_plane(ConvArgs a, T* col, int n0, int nb, int64_t ld) {
   extern __shared__ __attribute__((aligned(16))) char sm[];  // H * W elements
   T* plane = reinterpret_cast<T*>(sm);
-  const int b = blockIdx.x / a.C;
-  const int c = blockIdx.x - b * a.C;
+  const int64_t id = block_id();  // (image, channel) plane; blocks_2d grid
+  if (id >= static_cast<int64_t>(nb) * a.C) return;  // the tail of the grid (the whole block)
+  const int b = static_cast<int>(id / a.C);
+  const int c = static_cast<int>(id - static_cast<int64_t>(b) * a.C);
   stage_plane<T>(a, static_cast<const T*>(a.x) + (n0 + b) * a.xs[0] + c * a.xs[1], plane);
   __syncthreads();
   const int rs = a.R * a.S;
@@ -297,11 +300,13 @@ __global__ __launch_bounds__(256) void k_conv_shift(ConvArgs a, T* xs, int n0, i
 // input plane staged in LDS (read from HBM once); a thread then writes the
 // same 8-pixel run of every shifted plane.
 template <typename T>
-__global__ __launch_bounds__(256) void k_conv_shift_plane(ConvArgs a, T* xs, int n0, int hp) {
+__global__ __launch_bounds__(256) void k_conv_shift_plane(ConvArgs a, T* xs, int n0, int nb, int hp) {
   extern __shared__ __attribute__((aligned(16))) char sm[];  // H * W elements
   T* plane = reinterpret_cast<T*>(sm);
-  const int b = blockIdx.x / a.C;
-  const int c = blockIdx.x - b * a.C;
+  const int64_t id = block_id();  // (image, channel) plane; blocks_2d grid
+  if (id >= static_cast<int64_t>(nb) * a.C) return;  // the tail of the grid (the whole block)
+  const int b = static_cast<int>(id / a.C);
+  const int c = static_cast<int>(id - static_cast<int64_t>(b) * a.C);
   stage_plane<T>(a, static_cast<const T*>(a.x) + (n0 + b) * a.xs[0] + c * a.xs[1], plane);
   __syncthreads();
   const int q8 = a.Q / 8;
@@ -724,10 +729,10 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
         if constexpr (sizeof(T) != 2) {
           return set_error(NTOPS_ERR_INVALID, "conv2d: the implicit path needs 16-bit data");
         } else {
-          if (H * W * static_cast<int64_t>(sizeof(T)) <= kPlaneLds && nb * C <= 0x7fffffffLL)
-            hipLaunchKernelGGL(k_conv_shift_plane<T>, dim3(static_cast<unsigned>(nb * C)), dim3(256),
+          if (H * W * static_cast<int64_t>(sizeof(T)) <= kPlaneLds)
+            hipLaunchKernelGGL(k_conv_shift_plane<T>, blocks_2d(nb * C), dim3(256),
                                static_cast<unsigned>(H * W * sizeof(T)), st, a, static_cast<T*>(workspace),
-                               static_cast<int>(n0), static_cast<int>(hp));
+                               static_cast<int>(n0), static_cast<int>(nb), static_cast<int>(hp));
           else
             hipLaunchKernelGGL(k_conv_shift<T>, dim3(grid_for(nb * S * C * hp * (Q / 8), 256)), dim3(256), 0, st, a,
                                static_cast<T*>(workspace), static_cast<int>(n0), static_cast<int>(nb),
@@ -762,10 +767,10 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
     const int64_t nb = std::min(nb_max, N - n0);
     rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
       using T = decltype(tag);
-      if (static_cast<int64_t>(H) * W * static_cast<int64_t>(sizeof(T)) <= kPlaneLds && nb * C <= 0x7fffffffLL)
-        hipLaunchKernelGGL(k_im2col_plane<T>, dim3(static_cast<unsigned>(nb * C)), dim3(256),
+      if (static_cast<int64_t>(H) * W * static_cast<int64_t>(sizeof(T)) <= kPlaneLds)
+        hipLaunchKernelGGL(k_im2col_plane<T>, blocks_2d(nb * C), dim3(256),
                            static_cast<unsigned>(H * W * sizeof(T)), st, a, static_cast<T*>(workspace),
-                           static_cast<int>(n0), ld);
+                           static_cast<int>(n0), static_cast<int>(nb), ld);
       else
         hipLaunchKernelGGL(k_im2col<T>, dim3(grid_for(nb * crs * (ld / 8), 256)), dim3(256), 0, st, a,
                            static_cast<T*>(workspace), static_cast<int>(n0), static_cast<int>(nb), ld);

@@ -124,8 +124,10 @@ __global__ __launch_bounds__(256) void k_im2col_lds(Im2colArgs a) {
   using U = typename Bits<ES>::U;
   extern __shared__ __attribute__((aligned(16))) char sm[];
   U* plane = reinterpret_cast<U*>(sm);
-  const int n = blockIdx.x / a.C;
-  const int c = blockIdx.x - n * a.C;
+  const int64_t id = block_id();  // (image, channel) plane; blocks_2d grid
+  if (id >= static_cast<int64_t>(a.N) * a.C) return;  // the tail of the grid (the whole block)
+  const int n = static_cast<int>(id / a.C);
+  const int c = static_cast<int>(id - static_cast<int64_t>(n) * a.C);
   const U* x = static_cast<const U*>(a.x) + n * a.xs[0] + c * a.xs[1];
   const int hw = a.H * a.W;
   for (int i = threadIdx.x; i < hw; i += blockDim.x) {
@@ -163,8 +165,10 @@ template <int KW>
 __global__ __launch_bounds__(512) void k_im2col_s1(Im2colArgs a, int pitch, int vec_in) {
   extern __shared__ __attribute__((aligned(16))) char sm[];
   uint16_t* plane = reinterpret_cast<uint16_t*>(sm);
-  const int n = blockIdx.x / a.C;
-  const int c = blockIdx.x - n * a.C;
+  const int64_t id = block_id();  // (image, channel) plane; blocks_2d grid
+  if (id >= static_cast<int64_t>(a.N) * a.C) return;  // the tail of the grid (the whole block)
+  const int n = static_cast<int>(id / a.C);
+  const int c = static_cast<int>(id - static_cast<int64_t>(n) * a.C);
   const int hp = a.H + 2 * a.ph;
   for (int i = threadIdx.x; i < hp * pitch / 8; i += blockDim.x) reinterpret_cast<u32x4*>(sm)[i] = u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
@@ -230,7 +234,7 @@ int launch_s1(const Im2colArgs& a, int pitch, hipStream_t st) {
   const int threads = static_cast<int>(std::min<int64_t>(512, (std::max(a.runs, 64) + 63) / 64 * 64));
   const unsigned lds = static_cast<unsigned>((static_cast<int64_t>(a.H) + 2 * a.ph) * pitch * 2);
   note_kernel("im2col_s1 kw%d", KW);
-  hipLaunchKernelGGL(k_im2col_s1<KW>, dim3(static_cast<unsigned>(static_cast<int64_t>(a.N) * a.C)), dim3(threads),
+  hipLaunchKernelGGL(k_im2col_s1<KW>, blocks_2d(static_cast<int64_t>(a.N) * a.C), dim3(threads),
                      lds, st, a, pitch, vec_in ? 1 : 0);
   return check_launch("im2col");
 }
@@ -255,11 +259,11 @@ int launch_im2col(const Im2colArgs& a, hipStream_t st) {
   const int64_t plane_bytes = static_cast<int64_t>(a.H) * a.W * ES;
   if constexpr (ES == 2 && VEC) {
     const int pitch = s1_pitch(a);
-    if (pitch > 0 && planes <= 0x7fffffffLL) return run_s1(a, pitch, st);
+    if (pitch > 0) return run_s1(a, pitch, st);
   }
-  if (plane_bytes <= kIm2colPlaneLds && planes <= 0x7fffffffLL) {
+  if (plane_bytes <= kIm2colPlaneLds) {
     note_kernel("im2col_lds es%d %s", ES, VEC ? "vec" : "scalar");
-    hipLaunchKernelGGL((k_im2col_lds<ES, VEC>), dim3(static_cast<unsigned>(planes)), dim3(256),
+    hipLaunchKernelGGL((k_im2col_lds<ES, VEC>), blocks_2d(planes), dim3(256),
                        static_cast<unsigned>(plane_bytes), st, a);
     return check_launch("im2col");
   }

@@ -113,6 +113,39 @@ def test_conv2d_gemm_path(case, dtype):
     assert_close(got, exp, *tol, "conv2d gemm path")
 
 
+def test_conv2d_padded_unfold_past_2_24_outputs():
+    """bf16 (256, 512, 7, 7) * (2048, 512, 1, 1): 49-pixel output planes take
+    the unfold + GEMM at the padded width, whose planes are then copied out of
+    the workspace; 256 x 2048 x 49 = 25.7M outputs, more than the copy's
+    capped grid covers in one pass (2^24 threads), so the copy must loop.
+    Images at both ends and in the middle against the oracle, and the output
+    must hold no element the copy skipped (the output is pre-filled with NaN)."""
+    g = torch.Generator().manual_seed(29)
+    n, c, h, k = 256, 512, 7, 2048
+    x = torch.randn(n, c, h, h, generator=g).bfloat16()
+    wt = (torch.randn(k, c, 1, 1, generator=g) / c ** 0.5).bfloat16()
+    b = torch.randn(k, generator=g).bfloat16()
+    out = torch.full((n, k, h, h), float("nan"), dtype=torch.bfloat16, device="cuda")
+    lib = _lib.load()
+    geo = (n, c, h, h, k, 1, 1, h, h, 1, 1, 0, 0, 1, 1)
+    st = lambda t: _lib.i64_array(t.stride())  # noqa: E731
+    need = lib.ntops_conv2d_workspace(_lib.BF16, *geo, st(wt), st(out))
+    assert 0 < need <= 1 << 28  # every image in one chunk
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    xg, wg, bg = x.cuda(), wt.cuda(), b.cuda()
+    rc = lib.ntops_conv2d(_lib.BF16, *geo, xg.data_ptr(), st(xg), wg.data_ptr(), st(wg), bg.data_ptr(), 1,
+                          out.data_ptr(), st(out), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.ntops_last_error()
+    assert not _lib.last_kernel().endswith("conv_cl"), _lib.last_kernel()
+    torch.cuda.synchronize()
+    assert n * k * h * h > 1 << 24
+    assert not torch.isnan(out).any().item(), "output elements left unwritten"
+    got = out.cpu()
+    for img in (0, 128, 255):
+        exp = oracle(x[img:img + 1], wt, b, 1, 0, 1)
+        assert_close(got[img:img + 1], exp, *TOL[torch.bfloat16], f"image {img}")
+
+
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
 def test_conv2d_channels_last_256_tiles(dtype):
     """240 images of 16 x 16 pixels into 256 channels: 240 full 256 x 256

@@ -174,3 +174,24 @@ def test_im2col_conv_sized():
     # (randn inputs are never exactly zero)
     zeros = (got == 0).sum().item()
     assert zeros == 32 * 256 * 668
+
+
+@pytest.mark.parametrize("dtype, hw, ks, kernel", [
+    (torch.float32, (2, 2), (2, 2), "im2col_lds"),  # 256-thread blocks: 2^24 planes fill one grid dimension
+    (torch.bfloat16, (1, 8), (1, 1), "im2col_s1"),
+])
+def test_im2col_more_than_2_24_planes(dtype, hw, ks, kernel):
+    """2^24 + 37 (image, channel) planes, one workgroup each: the grid is two
+    dimensional (one dimension's work-item count is 32-bit).  A kernel that
+    covers a whole plane unfolds it into one output column run, so the
+    expected output is a reshape of the input."""
+    c = (1 << 24) + 37
+    x = torch.randn(1, c, *hw, device="cuda").to(dtype)
+    got = im2col(x, ks)
+    assert _lib.last_kernel().startswith(kernel), _lib.last_kernel()
+    oh, ow = hw[0] - ks[0] + 1, hw[1] - ks[1] + 1
+    assert got.shape == (1, c * ks[0] * ks[1], oh * ow)
+    exp = x.reshape(1, c, hw[0] * hw[1]) if ks == (1, 1) else x.reshape(1, c * 4, 1)
+    assert torch.equal(got, exp.reshape(got.shape))
+    del got, x, exp
+    torch.cuda.empty_cache()

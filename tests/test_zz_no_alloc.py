@@ -5,7 +5,6 @@ workspace path (so it runs over scratch that still holds the first call's
 data), each checked against the workspace entry point at the bf16 / fp16
 tolerance and the small one also against the oracle."""
 
-import ctypes
 
 import pytest
 import torch
@@ -92,7 +91,9 @@ def test_conv2d_noalloc_matches_workspace_entry():
 
 def test_conv2d_noalloc_rejects_images_beyond_the_scratch():
     """One image needing more than the scratch holds: an error naming the
-    limit, before any launch (pointers are never dereferenced)."""
+    limit, before any launch.  The tensors are null pointers, so a
+    regression in the size check stops at ntops_conv2d's null-pointer check
+    (a different message, the test fails) instead of launching kernels."""
     lib = _lib.load()
     n, c, h, k = 1, 256, 400, 64
     geo = (n, c, h, h, k, 3, 3, h, h, 1, 1, 1, 1, 1, 1)
@@ -100,7 +101,6 @@ def test_conv2d_noalloc_rejects_images_beyond_the_scratch():
     ost = _lib.i64_array((k * h * h, h * h, h, 1))
     need = lib.ntops_conv2d_workspace(_lib.BF16, *geo, wst, ost)
     assert need > MAX_SCRATCH
-    p = ctypes.c_void_p(256)
     xst = _lib.i64_array((c * h * h, h * h, h, 1))
-    rc = lib.ntops_conv2d_noalloc(_lib.BF16, *geo, p, xst, p, wst, None, 0, p, ost, None)
+    rc = lib.ntops_conv2d_noalloc(_lib.BF16, *geo, None, xst, None, wst, None, 0, None, ost, None)
     assert rc == 2 and "maximum" in lib.ntops_last_error().decode()
