@@ -49,6 +49,30 @@ def test_rms_norm(shape, dtype, weight_is_none, eps):
     assert_close(got, ref, rtol, atol, "rms_norm vs torch cpu")
 
 
+@pytest.mark.parametrize("cols", (4096, 1000, 12288, 40))
+@pytest.mark.parametrize("weight_is_none", (False, True))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_rms_norm_eps_none_bits(dtype, weight_is_none, cols):
+    """eps=None resolves to finfo(float32).eps for 16-bit inputs too (ntops'
+    finfo(dtype).eps would change most output bits): the output bits against
+    the oracle's, fewer than 1 in 1000 allowed to differ (fp32 sums in
+    another order may move a rounding boundary), and an input whose mean
+    square is below eps where the default dominates the result."""
+    g = torch.Generator().manual_seed(cols + (7 if weight_is_none else 0))
+    x = torch.randn(256, cols, generator=g).to(dtype)
+    w = None if weight_is_none else (1 + 0.02 * torch.randn(cols, generator=g)).to(dtype)
+    dt = DT_NAME[dtype]
+    got = ntops_amd.torch.rms_norm(x.cuda(), (cols,), None if w is None else w.cuda()).cpu()
+    exp = from_np(O.rms_norm(to_np(x), dt, cols, None if w is None else to_np(w), None), dt)
+    assert_close(got, exp, *TOL_REDUCTION[dt], "rms_norm eps=None")
+    mism = (got.view(torch.int16) != exp.view(torch.int16)).float().mean().item()
+    assert mism < 1e-3, f"bit mismatch fraction {mism}"
+    # mean square 2^-24 < eps = 2^-23: y = 1 / sqrt(3) (finfo(dtype).eps: < 0.01)
+    tiny = torch.full((3, cols), 2.0 ** -12, dtype=dtype, device="cuda")
+    y = ntops_amd.torch.rms_norm(tiny, (cols,)).float()
+    torch.testing.assert_close(y, torch.full_like(y, 3 ** -0.5), rtol=2 ** -8, atol=0)
+
+
 @pytest.mark.parametrize("eps", (1e-8, 1e-5, 1e-3))
 @pytest.mark.parametrize("bias_is_none", (False, True))
 @pytest.mark.parametrize("weight_is_none", (False, True))

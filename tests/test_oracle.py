@@ -95,6 +95,11 @@ def test_golden_norms(dt):
     x, w, b = GOLD[f"norm_{dt}_x"], GOLD[f"norm_{dt}_w"], GOLD[f"norm_{dt}_b"]
     close(O.rms_norm(x, dt, 256, w, 1e-6), GOLD[f"rms_{dt}"], dt, TOL_REDUCTION, "rms_norm")
     close(O.rms_norm(x, dt, 256, None, None), GOLD[f"rms_noweight_epsnone_{dt}"], dt, TOL_REDUCTION, "rms_norm eps=None")
+    if dt != "f32":
+        # the eps=None default (finfo(float32).eps) is visible in the 16-bit
+        # bits: ntops' finfo(dtype).eps changes about three quarters of them
+        equal(O.rms_norm(x, dt, 256, None, None), GOLD[f"rms_noweight_epsnone_{dt}"], dt, "rms_norm eps=None bits")
+        equal(O.rms_norm(x, dt, 256, w, 1e-6), GOLD[f"rms_{dt}"], dt, "rms_norm bits")
     close(O.layer_norm(x, dt, 256, w, b, 1e-5), GOLD[f"ln_{dt}"], dt, TOL_REDUCTION, "layer_norm")
     close(O.layer_norm(x, dt, 256, None, None, 1e-5), GOLD[f"ln_noaffine_{dt}"], dt, TOL_REDUCTION, "layer_norm plain")
 
@@ -197,9 +202,18 @@ def pin_rms(fn):
     const = fn(np.full((1, 64), 0.5, np.float32), "f32", 64, None, 0.25)  # 0.5/sqrt(0.25+0.25)
     w = np.arange(64, dtype=np.float32) / 64
     yw = fn(x, "f32", 64, w, 0.0)
-    return bool(np.array_equal(y1, y2) and np.allclose(rms, 1.0, atol=1e-6)
-                and np.allclose(const, 0.5 / np.sqrt(0.5), rtol=1e-7)
-                and np.allclose(yw, y1 * w, rtol=1e-6, atol=1e-7))
+    ok = bool(np.array_equal(y1, y2) and np.allclose(rms, 1.0, atol=1e-6)
+              and np.allclose(const, 0.5 / np.sqrt(0.5), rtol=1e-7)
+              and np.allclose(yw, y1 * w, rtol=1e-6, atol=1e-7))
+    # eps=None is finfo(float32).eps = 2^-23 for every input dtype: a constant
+    # 16-bit row of 2^-12 has mean square 2^-24, so y = 2^-12 / sqrt(3 * 2^-24)
+    # = 1 / sqrt(3); finfo(bf16).eps (2^-7) or finfo(f16).eps (2^-10) would
+    # give 0.003 or 0.008
+    for dt in ("bf16", "f16"):
+        tiny = O.round_to(np.full((2, 64), 2.0 ** -12, np.float32), dt)
+        yt = O.to_compute(fn(tiny, dt, 64, None, None), dt)
+        ok = ok and bool(np.allclose(yt, 1 / np.sqrt(3), rtol=2.0 ** -8, atol=0))
+    return ok
 
 
 def pin_layer_norm(fn):
@@ -335,6 +349,13 @@ def _mutant_rms_eps_outside(x, dt, cols, weight=None, eps=None, w_dt=None):
     return y + np.float32(eps or 0)
 
 
+def _mutant_rms_eps_of_dtype(x, dt, cols, weight=None, eps=None, w_dt=None):
+    # ntops' own default, finfo(input dtype).eps, in place of finfo(float32).eps
+    if eps is None:
+        eps = {"f32": 2.0 ** -23, "bf16": 2.0 ** -7, "f16": 2.0 ** -10}[dt]
+    return O.rms_norm(x, dt, cols, weight, eps, w_dt)
+
+
 def _mutant_gemm_transposed(a, b, dt, c=None, alpha=1.0, beta=0.0):
     if np.ndim(a) == 2 and a.shape[0] == a.shape[1]:
         a = a.T
@@ -371,6 +392,7 @@ def _mutant_add_alpha_on_a(a, b, dt, alpha=1):
         ("rotary_position_embedding", _mutant_rope_index),
         ("rms_norm", _mutant_rms_no_mean),
         ("rms_norm", _mutant_rms_eps_outside),
+        ("rms_norm", _mutant_rms_eps_of_dtype),
         ("gemm", _mutant_gemm_drop_bias),
         ("softmax", _mutant_softmax_no_max),
         ("layer_norm", _mutant_ln_no_mean),
