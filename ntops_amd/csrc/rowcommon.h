@@ -81,20 +81,16 @@ __device__ __forceinline__ C row_max(C v, C* red, const RowPos& p) {
 // (e.g. 4096 bf16: 2 packs x 4 waves reaches ~5.9 TB/s, 8 packs x 1 wave
 // ~4.9 TB/s): more rows are in flight per CU and the per-row reduction is
 // shorter.  One pack per lane goes too far (rms_norm bf16 (16384, 4096) with
-// 1 pack x 8 waves: 48.3 against 44.0 us).  `deep` picks 4 packs x 2 waves for rows of 257-512 packs instead
-// (layer_norm, whose two dependent reductions gain from the longer per-lane
-// runs: bf16 (16384, 4096) 47.5 -> 45.9 us, where rms_norm and add_rms_norm
-// lose 1-4 % with it).  Rows wider than 8 packs x 16 waves use the looped
-// kernels.
+// 1 pack x 8 waves: 48.3 against 44.0 us).  Rows wider than 8 packs x 16
+// waves use the looped kernels.
 struct VecCfg {
   int chunks, wpr;
 };
-inline bool pick_row_cfg(int64_t npk, VecCfg* cfg, bool deep = false) {
+inline bool pick_row_cfg(int64_t npk, VecCfg* cfg) {
   static const VecCfg table[] = {{1, 1}, {2, 1}, {2, 2}, {2, 4}, {2, 8}, {2, 16}, {4, 16}, {8, 16}};
   for (const VecCfg& c : table) {
     if (static_cast<int64_t>(c.chunks) * c.wpr * 64 >= npk) {
       *cfg = c;
-      if (deep && c.chunks == 2 && c.wpr == 4) *cfg = VecCfg{4, 2};
       return true;
     }
   }
@@ -111,21 +107,13 @@ inline bool pick_row_cfg(int64_t npk, VecCfg* cfg, bool deep = false) {
   MACRO(2, 16)                 \
   MACRO(4, 16)                 \
   MACRO(8, 16)
-// ... and the extra shape of pick_row_cfg(.., deep = true).
-#define NTOPS_DEEP_ROW_CASES(MACRO) \
-  NTOPS_ROW_CASES(MACRO)            \
-  MACRO(4, 2)
 
-// Group g's packs of this lane (block g holds rows g * RPB ..); zeros past
-// the row end or past `rows` (buffer loads against the row's extent: no
-// branches).  Each block handles one row group: a persistent grid with one
-// group of register prefetch (weight and bias held for all the block's
-// rows) measured 2 % slower on layer_norm bf16 (16384, 4096) and ~2 %
-// slower on rms_norm.
+// The packs of one row that this lane holds; zeros past the row end or for
+// rows at or past `rows` (buffer loads against the row's extent: no
+// branches).
 template <int WPR, typename T, int CHUNKS>
-__device__ __forceinline__ void load_row_packs(Pack16<T> (&r)[CHUNKS], const T* base, int64_t stride,
-                                               int64_t rows, const RowPos& p, int npk, int64_t g) {
-  const int64_t row = g * RowShape<WPR>::kRowsPerBlock + p.row_in_block;
+__device__ __forceinline__ void load_row(Pack16<T> (&r)[CHUNKS], const T* base, int64_t stride, int64_t rows,
+                                         const RowPos& p, int npk, int64_t row) {
   const bool ok = row < rows;
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(base + (ok ? row : 0) * stride, ok ? npk * 16u : 0u);
 #pragma unroll
@@ -135,19 +123,52 @@ __device__ __forceinline__ void load_row_packs(Pack16<T> (&r)[CHUNKS], const T* 
 // The V per-column parameters (weight or bias, type W) that go with one
 // 16-byte pack of the row, kept in their own type from load to use
 // (V * sizeof(W) bytes: one 16-byte load for W == T, two for float with a
-// 16-bit T).
+// 16-bit T).  Loads go through a buffer resource over the parameter row
+// (param_rsrc), whose extent is 0 when the parameter is absent: the loads
+// then return zeros without touching memory, and no branch surrounds them.
+// They keep the default cache policy: every row group re-reads them.
 template <typename W, int V>
 struct ParamPack {
   static constexpr int kPer = Pack16<W>::N;
   static constexpr int kLoads = V / kPer;
   static_assert(kLoads >= 1 && V % kPer == 0, "parameter type narrower than the row type");
   Pack16<W> q[kLoads];
-  __device__ __forceinline__ void load(const W* p) {
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int pk) {
 #pragma unroll
-    for (int j = 0; j < kLoads; ++j) q[j] = load16(p + j * kPer);
+    for (int j = 0; j < kLoads; ++j)
+      q[j] = __builtin_bit_cast(Pack16<W>, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rs, (static_cast<uint32_t>(pk) * kLoads + j) * 16u, 0, 0));
   }
   __device__ __forceinline__ float get(int i) const { return static_cast<float>(q[i / kPer].v[i % kPer]); }
 };
+
+// Resource over a parameter row of npk packs of V elements (null: extent 0).
+template <int V, typename W>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t param_rsrc(const W* w, int npk) {
+  return buffer_rsrc(w, w != nullptr ? static_cast<uint32_t>(npk) * V * static_cast<uint32_t>(sizeof(W)) : 0u);
+}
+
+// Sums v[k] over the WPR waves of each of a slot's R rows (one LDS exchange
+// and one barrier for all R); `red` holds R * kRowsPerBlock * WPR floats.
+template <int WPR, int R>
+__device__ __forceinline__ void rows_sum(float (&v)[R], float* red, const RowPos& p) {
+  constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
+#pragma unroll
+  for (int k = 0; k < R; ++k) v[k] = wave_sum(v[k]);
+  if constexpr (WPR > 1) {
+    if (p.lane == 0)
+#pragma unroll
+      for (int k = 0; k < R; ++k) red[(k * RPB + p.row_in_block) * WPR + p.wave_in_row] = v[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < WPR; ++i) s += red[(k * RPB + p.row_in_block) * WPR + i];
+      v[k] = s;
+    }
+  }
+}
 
 // Block-wide sum for the looped (any width) kernels: 256 threads.
 template <typename C>

@@ -19,6 +19,10 @@
 // (see rowcommon.h), one row group per block.  Looped path (unaligned rows, or rows wider than 64K
 // 16-bit elements): one 256-thread block per row, scalar strided accesses,
 // re-reading the row from L2 for the second / third pass.
+//
+// Weight and bias reads are cache traffic of their own: every row re-reads
+// the whole parameter row from L1 / L2.  The kernels share one parameter
+// load between the rows of a wave slot where the registers allow it.
 #include "dispatch.h"
 #include "rowcommon.h"
 
@@ -31,43 +35,63 @@ __device__ __forceinline__ float to_f(T v) {
 }
 
 // -------------------------------------------------------------- rms_norm --
-template <typename T, typename W, int CHUNKS, int WPR>
+// A wave slot owns R consecutive rows (R = 2 for rows of up to 2 packs per
+// lane): the weight packs, loaded once next to the row loads, serve all R
+// (wider shapes keep R = 1 and load the weight at its use, for registers).
+// On MI355X the weight's cache traffic, not its instruction count, is what
+// costs: rms_norm bf16 (16384, 4096) runs 42.2 us with the weight loads
+// issued but returning zeros (extent 0), 44.1 us reading it once per row,
+// 43.6 us once per two rows (same box, eager launches).
+template <typename T, typename W, int CHUNKS, int WPR, int R>
 __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_vec(
     const T* __restrict__ x, int64_t xs, const W* __restrict__ w, T* __restrict__ y, int64_t ys,
     int64_t rows, int cols, float eps) {
   constexpr int V = Pack16<T>::N;
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
-  __shared__ float red[RPB * WPR];
+  constexpr bool kEarly = R > 1;  // one row per slot: weight loaded at its use (fewer VGPRs)
+  __shared__ float red[R * RPB * WPR];
   const RowPos p = row_pos<WPR>();
   const int npk = cols / V;
-  const int64_t g = block_id();  // past the last group: loads read 0, stores are dropped
-  Pack16<T> r[CHUNKS];
-  load_row_packs<WPR>(r, x, xs, rows, p, npk, g);
-  float ss = 0.f;
+  // past the last row: loads read 0, stores are dropped
+  const int64_t row0 = (block_id() * RPB + p.row_in_block) * R;
+  Pack16<T> r[R][CHUNKS];
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c)
+  for (int k = 0; k < R; ++k) load_row<WPR>(r[k], x, xs, rows, p, npk, row0 + k);
+  const __amdgpu_buffer_rsrc_t wr = param_rsrc<V>(w, npk);
+  ParamPack<W, V> wq[CHUNKS];
+  if constexpr (kEarly)
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float f = to_f(r[c].v[i]);
-      ss += f * f;
+    for (int c = 0; c < CHUNKS; ++c) wq[c].load(wr, pack_of<WPR>(p, c));
+  float ss[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    ss[k] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float f = to_f(r[k][c].v[i]);
+        ss[k] += f * f;
+      }
+  }
+  rows_sum<WPR>(ss, red, p);
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const float rstd = 1.0f / __fsqrt_rn(ss[k] / static_cast<float>(cols) + eps);
+    const int64_t row = row0 + k;
+    const bool row_ok = row < rows;
+    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      if constexpr (!kEarly) wq[c].load(wr, pack_of<WPR>(p, c));
+      Pack16<T> o;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float wv = w != nullptr ? wq[c].get(i) : 1.0f;
+        o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(r[k][c].v[i]), rstd), wv));
+      }
+      buffer_store16_nt(out, pack_of<WPR>(p, c) * 16u, o);
     }
-  ss = row_sum<WPR>(ss, red, p);
-  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
-  const int64_t row = g * RPB + p.row_in_block;
-  const bool row_ok = row < rows;
-  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
-#pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int pk = pack_of<WPR>(p, c);
-    ParamPack<W, V> wq;
-    if (w != nullptr && pk < npk) wq.load(w + pk * V);
-    Pack16<T> o;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float wv = w != nullptr ? wq.get(i) : 1.0f;
-      o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(r[c].v[i]), rstd), wv));
-    }
-    buffer_store16_nt(out, pk * 16u, o);
   }
 }
 
@@ -97,12 +121,18 @@ __global__ __launch_bounds__(256) void k_rms_loop(const T* x, int64_t xs, const 
 // Reads x and residual once, writes the rounded sum h (the new residual) and
 // y = rms_norm(h); h stays in VGPRs between the two.  out / res_out may
 // alias x / residual (each element is read and written by one thread).
+// Up to 4 packs per lane, the weight is loaded with the rows and h is
+// stored before the reduction (bf16 (16384, 4096): 88.7 -> 85.7 us, same
+// box), spreading the writes over the kernel; wider shapes keep h packed
+// across the reduction and load the weight after it, to fit the 128 VGPRs
+// of a 1024-thread block.
 template <typename T, typename W, int CHUNKS, int WPR>
 __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
     const T* x, int64_t xs, const T* res, int64_t rs, const W* __restrict__ w, T* y, int64_t ys, T* ro,
     int64_t ros, int64_t rows, int cols, float eps) {
   constexpr int V = Pack16<T>::N;
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
+  constexpr bool kEarly = CHUNKS <= 4;
   __shared__ float red[RPB * WPR];
   const RowPos p = row_pos<WPR>();
   const int64_t row = block_id() * RPB + p.row_in_block;
@@ -113,50 +143,71 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
 
   const __amdgpu_buffer_rsrc_t in_x = buffer_rsrc(x + row_c * xs, extent);
   const __amdgpu_buffer_rsrc_t in_r = buffer_rsrc(res + row_c * rs, extent);
+  const __amdgpu_buffer_rsrc_t wr = param_rsrc<V>(w, npk);
+  const __amdgpu_buffer_rsrc_t out_r = buffer_rsrc(ro + row_c * ros, extent);
   Pack16<T> h[CHUNKS];
+  ParamPack<W, V> wq[CHUNKS];
+  if constexpr (kEarly) {
+    Pack16<T> a[CHUNKS], b[CHUNKS];
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const Pack16<T> a = buffer_load16_nt<T>(in_x, pack_of<WPR>(p, c) * 16u);
-    const Pack16<T> b = buffer_load16_nt<T>(in_r, pack_of<WPR>(p, c) * 16u);
+    for (int c = 0; c < CHUNKS; ++c) {
+      a[c] = buffer_load16_nt<T>(in_x, pack_of<WPR>(p, c) * 16u);
+      b[c] = buffer_load16_nt<T>(in_r, pack_of<WPR>(p, c) * 16u);
+    }
 #pragma unroll
-    for (int i = 0; i < V; ++i) h[c].v[i] = static_cast<T>(add_nc(to_f(a.v[i]), to_f(b.v[i])));
-    // Wide shapes: at most four chunks of both inputs in flight, or the
-    // two inputs plus the sums overflow the 128 VGPRs of a 1024-thread block.
-    if constexpr (CHUNKS > 4)
+    for (int c = 0; c < CHUNKS; ++c) wq[c].load(wr, pack_of<WPR>(p, c));
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+      for (int i = 0; i < V; ++i) h[c].v[i] = static_cast<T>(add_nc(to_f(a[c].v[i]), to_f(b[c].v[i])));
+  } else {
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const Pack16<T> a = buffer_load16_nt<T>(in_x, pack_of<WPR>(p, c) * 16u);
+      const Pack16<T> b = buffer_load16_nt<T>(in_r, pack_of<WPR>(p, c) * 16u);
+#pragma unroll
+      for (int i = 0; i < V; ++i) h[c].v[i] = static_cast<T>(add_nc(to_f(a.v[i]), to_f(b.v[i])));
+      // at most four chunks of both inputs in flight, or the two inputs plus
+      // the sums overflow the 128 VGPRs of a 1024-thread block
       if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
   }
-  float ss = 0.f;
+  float ss[1] = {0.f};
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       const float f = to_f(h[c].v[i]);
-      ss += f * f;
+      ss[0] += f * f;
     }
-  // Wide shapes: keep h packed across the reduction (the fp32 copies the
-  // compiler would otherwise carry do not fit beside it).
-  if constexpr (CHUNKS > 4)
+  if constexpr (kEarly) {
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) buffer_store16_nt(out_r, pack_of<WPR>(p, c) * 16u, h[c]);
+  } else {
+    // keep h packed across the reduction (the fp32 copies the compiler would
+    // otherwise carry do not fit beside it)
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c) {
       u32x4 bits = __builtin_bit_cast(u32x4, h[c]);
       asm volatile("" : "+v"(bits));
       h[c] = __builtin_bit_cast(Pack16<T>, bits);
     }
-  ss = row_sum<WPR>(ss, red, p);
-  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+  }
+  rows_sum<WPR>(ss, red, p);
+  const float rstd = 1.0f / __fsqrt_rn(ss[0] / static_cast<float>(cols) + eps);
 
-  const __amdgpu_buffer_rsrc_t out_r = buffer_rsrc(ro + row_c * ros, extent);
   const __amdgpu_buffer_rsrc_t out_y = buffer_rsrc(y + row_c * ys, extent);
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const int pk = pack_of<WPR>(p, c);
-    buffer_store16_nt(out_r, pk * 16u, h[c]);
-    ParamPack<W, V> wq;
-    if (w != nullptr && pk < npk) wq.load(w + pk * V);
+    if constexpr (!kEarly) {
+      buffer_store16_nt(out_r, pk * 16u, h[c]);
+      wq[c].load(wr, pk);
+    }
     Pack16<T> o;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-      const float wv = w != nullptr ? wq.get(i) : 1.0f;
+      const float wv = w != nullptr ? wq[c].get(i) : 1.0f;
       o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(h[c].v[i]), rstd), wv));
     }
     buffer_store16_nt(out_y, pk * 16u, o);
@@ -196,68 +247,103 @@ __global__ __launch_bounds__(256) void k_add_rms_loop(const T* x, int64_t xs, co
 // fma(fma(x, rstd, -mean * rstd), w, b): torch's CPU expression with the two
 // products contracted (a different bf16 rounding only within ~2 fp32 ulps
 // of a rounding boundary).
-template <typename T, typename W, int CHUNKS, int WPR>
+// R rows per wave slot share the weight and bias packs, which are then
+// loaded with the rows (R = 2 up to 2 packs per lane: bf16 (16384, 4096) on
+// 2 packs x 4 waves 45.3 us, against 46.1 us for one row per slot on 4 x 2
+// with the parameters loaded at their use; loaded early for one row per
+// slot they cost occupancy and measured 48.2 us).
+template <typename T, typename W, int CHUNKS, int WPR, int R>
 __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_ln_vec(
     const T* __restrict__ x, int64_t xs, const W* __restrict__ w, const W* __restrict__ b,
     T* __restrict__ y, int64_t ys, int64_t rows, int cols, float eps) {
   constexpr int V = Pack16<T>::N;
   constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
-  __shared__ float red0[RPB * WPR];
-  __shared__ float red1[RPB * WPR];
+  constexpr bool kEarly = R > 1;
+  __shared__ float red0[R * RPB * WPR];
+  __shared__ float red1[R * RPB * WPR];
   const RowPos p = row_pos<WPR>();
   const int npk = cols / V;
-  const int64_t g = block_id();  // past the last group: loads read 0, stores are dropped
-  float f[CHUNKS][V];
+  // past the last row: loads read 0, stores are dropped
+  const int64_t row0 = (block_id() * RPB + p.row_in_block) * R;
+  const __amdgpu_buffer_rsrc_t wr = param_rsrc<V>(w, npk);
+  const __amdgpu_buffer_rsrc_t br = param_rsrc<V>(b, npk);
+  float f[R][CHUNKS][V];
+  ParamPack<W, V> wq[CHUNKS], bq[CHUNKS];
   {
-    Pack16<T> r[CHUNKS];
-    load_row_packs<WPR>(r, x, xs, rows, p, npk, g);
+    Pack16<T> r[R][CHUNKS];
+#pragma unroll
+    for (int k = 0; k < R; ++k) load_row<WPR>(r[k], x, xs, rows, p, npk, row0 + k);
+    if constexpr (kEarly) {
+#pragma unroll
+      for (int c = 0; c < CHUNKS; ++c) {
+        wq[c].load(wr, pack_of<WPR>(p, c));
+        bq[c].load(br, pack_of<WPR>(p, c));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+      for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+        for (int i = 0; i < V; ++i) f[k][c][i] = to_f(r[k][c].v[i]);
+  }
+  float mean[R], acc[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    float s0 = 0.f, s1 = 0.f;
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
-      for (int i = 0; i < V; ++i) f[c][i] = to_f(r[c].v[i]);
+      for (int i = 0; i < V; i += 2) {
+        s0 += f[k][c][i];
+        s1 += f[k][c][i + 1];
+      }
+    acc[k] = s0 + s1;
   }
-  float s0 = 0.f, s1 = 0.f;
+  rows_sum<WPR>(acc, red0, p);
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c)
+  for (int k = 0; k < R; ++k) {
+    // divided, not scaled by 1 / cols: a constant row's mean must come out exact
+    mean[k] = acc[k] / static_cast<float>(cols);
+    float q = 0.f;
 #pragma unroll
-    for (int i = 0; i < V; i += 2) {
-      s0 += f[c][i];
-      s1 += f[c][i + 1];
+    for (int c = 0; c < CHUNKS; ++c) {
+      float q0 = 0.f, q1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < V; i += 2) {
+        const float d0 = f[k][c][i] - mean[k], d1 = f[k][c][i + 1] - mean[k];
+        q0 = fmaf(d0, d0, q0);
+        q1 = fmaf(d1, d1, q1);
+      }
+      q += pack_of<WPR>(p, c) < npk ? q0 + q1 : 0.f;
     }
-  // divided, not scaled by 1 / cols: a constant row's mean must come out exact
-  const float mean = row_sum<WPR>(s0 + s1, red0, p) / static_cast<float>(cols);
-  float q = 0.f;
-#pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    float q0 = 0.f, q1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < V; i += 2) {
-      const float d0 = f[c][i] - mean, d1 = f[c][i + 1] - mean;
-      q0 = fmaf(d0, d0, q0);
-      q1 = fmaf(d1, d1, q1);
-    }
-    q += pack_of<WPR>(p, c) < npk ? q0 + q1 : 0.f;
+    acc[k] = q;
   }
-  const float var = row_sum<WPR>(q, red1, p) * (1.0f / static_cast<float>(cols));
-  const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
-  const float shift = -rstd * mean;
-  const int64_t row = g * RPB + p.row_in_block;
-  const bool row_ok = row < rows;
-  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
+  rows_sum<WPR>(acc, red1, p);
 #pragma unroll
-  for (int c = 0; c < CHUNKS; ++c) {
-    const int pk = pack_of<WPR>(p, c);
-    ParamPack<W, V> wq, bq;
-    if (w != nullptr && pk < npk) wq.load(w + pk * V);
-    if (b != nullptr && pk < npk) bq.load(b + pk * V);
-    Pack16<T> o;
+  for (int k = 0; k < R; ++k) {
+    const float var = acc[k] * (1.0f / static_cast<float>(cols));
+    const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
+    const float shift = -rstd * mean[k];
+    const int64_t row = row0 + k;
+    const bool row_ok = row < rows;
+    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + (row_ok ? row : 0) * ys, row_ok ? npk * 16u : 0u);
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float wv = w != nullptr ? wq.get(i) : 1.0f;
-      const float bv = b != nullptr ? bq.get(i) : 0.0f;
-      o.v[i] = static_cast<T>(fmaf(fmaf(f[c][i], rstd, shift), wv, bv));
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int pk = pack_of<WPR>(p, c);
+      if constexpr (!kEarly) {
+        wq[c].load(wr, pk);
+        bq[c].load(br, pk);
+      }
+      Pack16<T> o;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float wv = w != nullptr ? wq[c].get(i) : 1.0f;
+        const float bv = b != nullptr ? bq[c].get(i) : 0.0f;
+        o.v[i] = static_cast<T>(fmaf(fmaf(f[k][c][i], rstd, shift), wv, bv));
+      }
+      buffer_store16_nt(out, pk * 16u, o);
     }
-    buffer_store16_nt(out, pk * 16u, o);
   }
 }
 
@@ -306,7 +392,9 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
   if (vec) {
 #define NTOPS_RMS_CASE(CH, WP)                                                                    \
   if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
-    hipLaunchKernelGGL((k_rms_vec<T, W, CH, WP>), blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
+    constexpr int R = CH <= 2 ? 2 : 1;                                                            \
+    hipLaunchKernelGGL((k_rms_vec<T, W, CH, WP, R>),                                              \
+                       blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock * R)),                \
                        dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, y, ys, rows,                \
                        static_cast<int>(cols), feps);                                             \
     return check_launch("rms_norm");                                                              \
@@ -330,17 +418,19 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
   const bool vec = (cols % V == 0) && (xs % V == 0) && (ys % V == 0) && aligned16(x) &&
                    aligned16(y) && (w == nullptr || aligned16(w)) &&
                    (b == nullptr || aligned16(b)) && (wrs == 0 || (w == nullptr && b == nullptr)) &&
-                   pick_row_cfg(cols / V, &cfg, true);
+                   pick_row_cfg(cols / V, &cfg);
   const float feps = static_cast<float>(eps);
   if (vec) {
 #define NTOPS_LN_CASE(CH, WP)                                                                     \
   if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
-    hipLaunchKernelGGL((k_ln_vec<T, W, CH, WP>), blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
+    constexpr int R = CH <= 2 ? 2 : 1;                                                            \
+    hipLaunchKernelGGL((k_ln_vec<T, W, CH, WP, R>),                                               \
+                       blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock * R)),                \
                        dim3(RowShape<WP>::kThreads), 0, st, x, xs, w, b, y, ys, rows,             \
                        static_cast<int>(cols), feps);                                             \
     return check_launch("layer_norm");                                                            \
   }
-    NTOPS_DEEP_ROW_CASES(NTOPS_LN_CASE)
+    NTOPS_ROW_CASES(NTOPS_LN_CASE)
 #undef NTOPS_LN_CASE
   }
   hipLaunchKernelGGL((k_ln_loop<T, W>), blocks_2d(rows), dim3(256), 0, st, x, xs, w, b, wrs, y, ys, rows, cols,
