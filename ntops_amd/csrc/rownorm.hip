@@ -71,7 +71,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_vec(
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const float f = to_f(r[k][c].v[i]);
-        ss[k] += f * f;
+        ss[k] = fmaf(f, f, ss[k]);  // as k_add_rms_vec: one fma per element
       }
   }
   rows_sum<WPR>(ss, red, p);
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       const float f = to_f(h[c].v[i]);
-      ss[0] += f * f;
+      ss[0] = fmaf(f, f, ss[0]);  // as k_rms_vec: one fma per element
     }
   if constexpr (kEarly) {
 #pragma unroll
@@ -211,29 +211,6 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_vec(
       o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(h[c].v[i]), rstd), wv));
     }
     buffer_store16_nt(out_y, pk * 16u, o);
-  }
-}
-
-template <typename T, typename W>
-__global__ __launch_bounds__(256) void k_add_rms_loop(const T* x, int64_t xs, const T* res, int64_t rs,
-                                                       const W* w, int64_t wrs, T* y, int64_t ys, T* ro,
-                                                       int64_t ros, int64_t rows, int64_t cols, float eps) {
-  __shared__ float red[4];
-  const int64_t row = block_id();
-  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
-  float ss = 0.f;
-  for (int64_t j = threadIdx.x; j < cols; j += 256) {
-    const T hv = static_cast<T>(add_nc(to_f(x[row * xs + j]), to_f(res[row * rs + j])));
-    ro[row * ros + j] = hv;
-    const float f = to_f(hv);
-    ss += f * f;
-  }
-  ss = block_sum256(ss, red);
-  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
-  const W* wr = w != nullptr ? w + row * wrs : nullptr;
-  for (int64_t j = threadIdx.x; j < cols; j += 256) {
-    const float wv = wr != nullptr ? static_cast<float>(wr[j]) : 1.0f;
-    y[row * ys + j] = static_cast<T>(mul_nc(mul_nc(to_f(ro[row * ros + j]), rstd), wv));
   }
 }
 
@@ -376,7 +353,271 @@ __global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W
   }
 }
 
+// ------------------------------------------- rows that are not 16-byte runs --
+// Rows whose width or start is not a multiple of 16 bytes (an odd width such
+// as 4100, or a view into wider rows), with the output rows laid out at the
+// same offset within 16 bytes as the input rows: each row splits into a
+// head of `head` elements up to the first 16-byte boundary, `npk` whole
+// packs and a tail (head, tail < V).  The packs travel as in the aligned
+// kernels (register-resident, one HBM read and one write); lanes 0..head-1
+// of the row's first wave hold the head elements and lanes 0..tail-1 of its
+// last wave the tail (element loads and stores through buffer resources
+// whose extent is the head / tail: branch-free, zeros elsewhere).  The
+// weight and bias rows are staged once per block in LDS, where element j is
+// read at any offset: a pack of the row starts `head` elements past a
+// parameter pack boundary.
+struct OddRow {
+  int head, npk, tail;
+};
+template <typename T>
+__device__ __forceinline__ OddRow odd_row(const T* row, int cols) {
+  constexpr int V = Pack16<T>::N;
+  const int off = static_cast<int>((reinterpret_cast<uintptr_t>(row) & 15u) / sizeof(T));
+  const int head = min((V - off) & (V - 1), cols);
+  const int npk = (cols - head) / V;
+  return {head, npk, cols - head - npk * V};
+}
+
+template <typename T>
+__device__ __forceinline__ T buffer_load_elem(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(T) == 2)
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kBufNT));
+  else
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kBufNT));
+}
+template <typename T>
+__device__ __forceinline__ void buffer_store_elem(__amdgpu_buffer_rsrc_t r, uint32_t off, T v) {
+  if constexpr (sizeof(T) == 2)
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, off, 0, kBufNT);
+  else
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, off, 0, kBufNT);
+}
+
+// One row of an odd-layout slot as this lane holds it: the packs, and the
+// head / tail element this lane owns (zero where it owns none).
+template <typename T, int CHUNKS>
+struct OddSlot {
+  Pack16<T> pk[CHUNKS];
+  T hd, tl;
+  bool own_hd, own_tl;
+};
+
+template <int WPR, typename T, int CHUNKS>
+__device__ __forceinline__ void odd_load(OddSlot<T, CHUNKS>& d, const T* row, const OddRow& g, bool row_ok,
+                                         const RowPos& p) {
+  const bool first = p.wave_in_row == 0, last = p.wave_in_row == WPR - 1;
+  const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(row + g.head, row_ok ? g.npk * 16u : 0u);
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) d.pk[c] = buffer_load16_nt<T>(rp, pack_of<WPR>(p, c) * 16u);
+  const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(row, row_ok && first ? g.head * sizeof(T) : 0u);
+  const __amdgpu_buffer_rsrc_t rt =
+      buffer_rsrc(row + g.head + g.npk * Pack16<T>::N, row_ok && last ? g.tail * sizeof(T) : 0u);
+  d.hd = buffer_load_elem<T>(rh, p.lane * sizeof(T));
+  d.tl = buffer_load_elem<T>(rt, p.lane * sizeof(T));
+  d.own_hd = row_ok && first && p.lane < g.head;
+  d.own_tl = row_ok && last && p.lane < g.tail;
+}
+
+// This lane's sum of squares over its elements of the row: head, packs,
+// tail.  rms_norm and add_rms_norm share it, so their outputs agree bit for
+// bit on the same row layout.  The products and sums are spelled as explicit
+// fmas: left to contraction, `hd * hd + p * p` may become fma(p, p, hd * hd)
+// in one kernel and fma(hd, hd, p * p) in the other.
+template <typename T, int CHUNKS>
+__device__ __forceinline__ float odd_sumsq(const OddSlot<T, CHUNKS>& d) {
+  constexpr int V = Pack16<T>::N;
+  float ss = mul_nc(to_f(d.hd), to_f(d.hd));
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float f = to_f(d.pk[c].v[i]);
+      ss = fmaf(f, f, ss);
+    }
+  return fmaf(to_f(d.tl), to_f(d.tl), ss);
+}
+
+// Stages `cols` parameters of type W at `src` into LDS at `dst` (16-byte
+// packs, then the last cols % per-pack elements one by one).
+template <typename W>
+__device__ __forceinline__ void stage_param(W* dst, const W* src, int cols) {
+  constexpr int kPer = Pack16<W>::N;
+  const int full = cols / kPer;
+  for (int q = threadIdx.x; q < full; q += blockDim.x)
+    *reinterpret_cast<u32x4*>(dst + q * kPer) = *reinterpret_cast<const u32x4*>(src + q * kPer);
+  for (int e = full * kPer + threadIdx.x; e < cols; e += blockDim.x) dst[e] = src[e];
+}
+
+// Writes one row's normalised values: packs, head and tail; f(v, j) gives
+// the output for element value v at column j.
+template <int WPR, typename T, int CHUNKS, typename F>
+__device__ __forceinline__ void odd_store(T* row, const OddRow& g, bool row_ok, const RowPos& p,
+                                          const OddSlot<T, CHUNKS>& d, F f) {
+  constexpr int V = Pack16<T>::N;
+  const bool first = p.wave_in_row == 0, last = p.wave_in_row == WPR - 1;
+  const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(row + g.head, row_ok ? g.npk * 16u : 0u);
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int pk = pack_of<WPR>(p, c);
+    const int j0 = g.head + pk * V;
+    Pack16<T> o;
+#pragma unroll
+    for (int i = 0; i < V; ++i) o.v[i] = f(d.pk[c].v[i], pk < g.npk ? j0 + i : 0);
+    buffer_store16_nt(rp, pk * 16u, o);
+  }
+  const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(row, row_ok && first ? g.head * sizeof(T) : 0u);
+  const __amdgpu_buffer_rsrc_t rt =
+      buffer_rsrc(row + g.head + g.npk * V, row_ok && last ? g.tail * sizeof(T) : 0u);
+  buffer_store_elem<T>(rh, p.lane * sizeof(T), f(d.hd, d.own_hd ? p.lane : 0));
+  buffer_store_elem<T>(rt, p.lane * sizeof(T), f(d.tl, d.own_tl ? g.head + g.npk * V + p.lane : 0));
+}
+
+// Bytes of LDS the odd-layout kernels stage per parameter row.
+template <typename W>
+__host__ __device__ inline int64_t odd_param_bytes(int64_t cols) {
+  return (cols * static_cast<int64_t>(sizeof(W)) + 15) / 16 * 16;
+}
+constexpr int64_t kOddLdsMax = 64 * 1024;
+
+template <typename T, typename W, int CHUNKS, int WPR>
+__global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_odd(
+    const T* __restrict__ x, int64_t xs, const W* __restrict__ w, T* __restrict__ y, int64_t ys,
+    int64_t rows, int cols, float eps) {
+  constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
+  __shared__ float red[RPB * WPR];
+  extern __shared__ __attribute__((aligned(16))) char psm[];
+  W* wl = reinterpret_cast<W*>(psm);
+  const RowPos p = row_pos<WPR>();
+  const int64_t row = block_id() * RPB + p.row_in_block;
+  const bool row_ok = row < rows;
+  const T* xr = x + (row_ok ? row : 0) * xs;
+  const OddRow g = odd_row(xr, cols);
+  OddSlot<T, CHUNKS> d;
+  odd_load<WPR>(d, xr, g, row_ok, p);
+  if (w != nullptr) stage_param(wl, w, cols);
+  float ss[1] = {odd_sumsq(d)};
+  __syncthreads();  // the staged weight (and, for one wave per row, nothing else)
+  rows_sum<WPR>(ss, red, p);
+  const float rstd = 1.0f / __fsqrt_rn(ss[0] / static_cast<float>(cols) + eps);
+  odd_store<WPR>(y + (row_ok ? row : 0) * ys, g, row_ok, p, d, [&](T v, int j) {
+    const float wv = w != nullptr ? static_cast<float>(wl[j]) : 1.0f;
+    return static_cast<T>(mul_nc(mul_nc(to_f(v), rstd), wv));
+  });
+}
+
+// x, residual, new residual and output share one layout; h = x + residual
+// is rounded, stored, and normalised exactly as k_rms_odd normalises a row
+// of that layout.
+template <typename T, typename W, int CHUNKS, int WPR>
+__global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_add_rms_odd(
+    const T* x, int64_t xs, const T* res, int64_t rs, const W* __restrict__ w, T* y, int64_t ys, T* ro,
+    int64_t ros, int64_t rows, int cols, float eps) {
+  constexpr int V = Pack16<T>::N;
+  constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
+  __shared__ float red[RPB * WPR];
+  extern __shared__ __attribute__((aligned(16))) char psm[];
+  W* wl = reinterpret_cast<W*>(psm);
+  const RowPos p = row_pos<WPR>();
+  const int64_t row = block_id() * RPB + p.row_in_block;
+  const bool row_ok = row < rows;
+  const int64_t rc = row_ok ? row : 0;
+  const OddRow g = odd_row(x + rc * xs, cols);
+  OddSlot<T, CHUNKS> d, e;
+  odd_load<WPR>(d, x + rc * xs, g, row_ok, p);
+  odd_load<WPR>(e, res + rc * rs, g, row_ok, p);
+  if (w != nullptr) stage_param(wl, w, cols);
+  auto add = [](T a, T b) { return static_cast<T>(add_nc(to_f(a), to_f(b))); };
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+    for (int i = 0; i < V; ++i) d.pk[c].v[i] = add(d.pk[c].v[i], e.pk[c].v[i]);
+  d.hd = add(d.hd, e.hd);
+  d.tl = add(d.tl, e.tl);
+  odd_store<WPR>(ro + rc * ros, g, row_ok, p, d, [](T v, int) { return v; });
+  float ss[1] = {odd_sumsq(d)};
+  __syncthreads();
+  rows_sum<WPR>(ss, red, p);
+  const float rstd = 1.0f / __fsqrt_rn(ss[0] / static_cast<float>(cols) + eps);
+  odd_store<WPR>(y + rc * ys, g, row_ok, p, d, [&](T v, int j) {
+    const float wv = w != nullptr ? static_cast<float>(wl[j]) : 1.0f;
+    return static_cast<T>(mul_nc(mul_nc(to_f(v), rstd), wv));
+  });
+}
+
+template <typename T, typename W, int CHUNKS, int WPR>
+__global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_ln_odd(
+    const T* __restrict__ x, int64_t xs, const W* __restrict__ w, const W* __restrict__ b,
+    T* __restrict__ y, int64_t ys, int64_t rows, int cols, float eps) {
+  constexpr int V = Pack16<T>::N;
+  constexpr int RPB = RowShape<WPR>::kRowsPerBlock;
+  __shared__ float red0[RPB * WPR];
+  __shared__ float red1[RPB * WPR];
+  extern __shared__ __attribute__((aligned(16))) char psm[];
+  W* wl = reinterpret_cast<W*>(psm);
+  W* bl = reinterpret_cast<W*>(psm + odd_param_bytes<W>(cols));
+  const RowPos p = row_pos<WPR>();
+  const int64_t row = block_id() * RPB + p.row_in_block;
+  const bool row_ok = row < rows;
+  const T* xr = x + (row_ok ? row : 0) * xs;
+  const OddRow g = odd_row(xr, cols);
+  OddSlot<T, CHUNKS> d;
+  odd_load<WPR>(d, xr, g, row_ok, p);
+  if (w != nullptr) stage_param(wl, w, cols);
+  if (b != nullptr) stage_param(bl, b, cols);
+  float acc[1];
+  {
+    float s0 = to_f(d.hd), s1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+      for (int i = 0; i < V; i += 2) {
+        s0 += to_f(d.pk[c].v[i]);
+        s1 += to_f(d.pk[c].v[i + 1]);
+      }
+    acc[0] = s0 + s1 + to_f(d.tl);
+  }
+  __syncthreads();
+  rows_sum<WPR>(acc, red0, p);
+  const float mean = acc[0] / static_cast<float>(cols);
+  {
+    const float dh = to_f(d.hd) - mean, dt = to_f(d.tl) - mean;
+    float q = (d.own_hd ? dh * dh : 0.f) + (d.own_tl ? dt * dt : 0.f);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      float q0 = 0.f, q1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < V; i += 2) {
+        const float d0 = to_f(d.pk[c].v[i]) - mean, d1 = to_f(d.pk[c].v[i + 1]) - mean;
+        q0 = fmaf(d0, d0, q0);
+        q1 = fmaf(d1, d1, q1);
+      }
+      q += pack_of<WPR>(p, c) < g.npk ? q0 + q1 : 0.f;
+    }
+    acc[0] = q;
+  }
+  rows_sum<WPR>(acc, red1, p);
+  const float var = acc[0] * (1.0f / static_cast<float>(cols));
+  const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
+  const float shift = -rstd * mean;
+  odd_store<WPR>(y + (row_ok ? row : 0) * ys, g, row_ok, p, d, [&](T v, int j) {
+    const float wv = w != nullptr ? static_cast<float>(wl[j]) : 1.0f;
+    const float bv = b != nullptr ? static_cast<float>(bl[j]) : 0.0f;
+    return static_cast<T>(fmaf(fmaf(to_f(v), rstd, shift), wv, bv));
+  });
+}
+
 // -------------------------------------------------------------- dispatch --
+// Rows of a and b start at the same offset within 16 bytes, row for row.
+template <typename T>
+bool same_layout(const void* a, int64_t as, const void* b, int64_t bs) {
+  return ((reinterpret_cast<uintptr_t>(a) - reinterpret_cast<uintptr_t>(b)) & 15u) == 0 &&
+         (((as - bs) * static_cast<int64_t>(sizeof(T))) & 15) == 0;
+}
+
+// Launch shape of the odd-layout kernels: from the most whole packs a row
+// can hold (at least one pack, for rows shorter than a pack).
+inline bool pick_odd_cfg(int64_t cols, int v, VecCfg* cfg) { return pick_row_cfg(cols / v > 0 ? cols / v : 1, cfg); }
+
 template <typename T, typename W>
 int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* wv, int64_t wrs, double eps,
             void* yv, int64_t ys, hipStream_t st) {
@@ -401,6 +642,19 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
   }
     NTOPS_ROW_CASES(NTOPS_RMS_CASE)
 #undef NTOPS_RMS_CASE
+  }
+  const int64_t lds = w != nullptr ? odd_param_bytes<W>(cols) : 0;
+  if (same_layout<T>(x, xs, y, ys) && (w == nullptr || (aligned16(w) && wrs == 0)) && lds <= kOddLdsMax &&
+      pick_odd_cfg(cols, V, &cfg)) {
+#define NTOPS_RMS_ODD_CASE(CH, WP)                                                                \
+  if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
+    hipLaunchKernelGGL((k_rms_odd<T, W, CH, WP>), blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
+                       dim3(RowShape<WP>::kThreads), static_cast<unsigned>(lds), st, x, xs, w, y, ys,    \
+                       rows, static_cast<int>(cols), feps);                                       \
+    return check_launch("rms_norm");                                                              \
+  }
+    NTOPS_ROW_CASES(NTOPS_RMS_ODD_CASE)
+#undef NTOPS_RMS_ODD_CASE
   }
   hipLaunchKernelGGL((k_rms_loop<T, W>), blocks_2d(rows), dim3(256), 0, st, x, xs, w, wrs, y, ys, rows, cols, feps);
   return check_launch("rms_norm");
@@ -433,10 +687,27 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
     NTOPS_ROW_CASES(NTOPS_LN_CASE)
 #undef NTOPS_LN_CASE
   }
+  const int64_t lds = (w != nullptr || b != nullptr) ? 2 * odd_param_bytes<W>(cols) : 0;
+  if (same_layout<T>(x, xs, y, ys) && (w == nullptr || aligned16(w)) && (b == nullptr || aligned16(b)) &&
+      wrs == 0 && lds <= kOddLdsMax && pick_odd_cfg(cols, V, &cfg)) {
+#define NTOPS_LN_ODD_CASE(CH, WP)                                                                 \
+  if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
+    hipLaunchKernelGGL((k_ln_odd<T, W, CH, WP>), blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
+                       dim3(RowShape<WP>::kThreads), static_cast<unsigned>(lds), st, x, xs, w, b, y, ys, \
+                       rows, static_cast<int>(cols), feps);                                       \
+    return check_launch("layer_norm");                                                            \
+  }
+    NTOPS_ROW_CASES(NTOPS_LN_ODD_CASE)
+#undef NTOPS_LN_ODD_CASE
+  }
   hipLaunchKernelGGL((k_ln_loop<T, W>), blocks_2d(rows), dim3(256), 0, st, x, xs, w, b, wrs, y, ys, rows, cols,
                      feps);
   return check_launch("layer_norm");
 }
+
+// run_add_rms's answer for layouts it leaves to add followed by rms_norm
+// (not a status code).
+constexpr int kComposeAddRms = -1;
 
 template <typename T, typename W>
 int run_add_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* rv, int64_t rs,
@@ -464,9 +735,20 @@ int run_add_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const vo
     NTOPS_ROW_CASES(NTOPS_ADD_RMS_CASE)
 #undef NTOPS_ADD_RMS_CASE
   }
-  hipLaunchKernelGGL((k_add_rms_loop<T, W>), blocks_2d(rows), dim3(256), 0, st, x, xs, r, rs, w, wrs, y, ys, ro, ros,
-                     rows, cols, feps);
-  return check_launch("add_rms_norm");
+  const int64_t lds = w != nullptr ? odd_param_bytes<W>(cols) : 0;
+  if (same_layout<T>(x, xs, y, ys) && same_layout<T>(r, rs, y, ys) && same_layout<T>(ro, ros, y, ys) &&
+      (w == nullptr || (aligned16(w) && wrs == 0)) && lds <= kOddLdsMax && pick_odd_cfg(cols, V, &cfg)) {
+#define NTOPS_ADD_RMS_ODD_CASE(CH, WP)                                                            \
+  if (cfg.chunks == CH && cfg.wpr == WP) {                                                        \
+    hipLaunchKernelGGL((k_add_rms_odd<T, W, CH, WP>), blocks_2d(ceil_div(rows, RowShape<WP>::kRowsPerBlock)), \
+                       dim3(RowShape<WP>::kThreads), static_cast<unsigned>(lds), st, x, xs, r, rs, w, y, ys,   \
+                       ro, ros, rows, static_cast<int>(cols), feps);                              \
+    return check_launch("add_rms_norm");                                                          \
+  }
+    NTOPS_ROW_CASES(NTOPS_ADD_RMS_ODD_CASE)
+#undef NTOPS_ADD_RMS_ODD_CASE
+  }
+  return kComposeAddRms;
 }
 
 int check_rows(const char* what, int64_t rows, int64_t cols, const void* x, const void* y) {
@@ -527,7 +809,7 @@ extern "C" int ntops_add_rms_norm(int dtype, int64_t rows, int64_t cols, const v
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (w != nullptr && w_dtype != dtype && w_dtype != NTOPS_F32)
     return set_error(NTOPS_ERR_UNSUPPORTED, "add_rms_norm: weight dtype must equal input dtype or be F32");
-  return dispatch_float16_32(dtype, "add_rms_norm", [&](auto tag) {
+  const int rc = dispatch_float16_32(dtype, "add_rms_norm", [&](auto tag) {
     using T = decltype(tag);
     if (w != nullptr && w_dtype == NTOPS_F32 && dtype != NTOPS_F32)
       return run_add_rms<T, float>(rows, cols, x, x_row_stride, residual, residual_row_stride, w, w_row_stride,
@@ -535,4 +817,17 @@ extern "C" int ntops_add_rms_norm(int dtype, int64_t rows, int64_t cols, const v
     return run_add_rms<T, T>(rows, cols, x, x_row_stride, residual, residual_row_stride, w, w_row_stride, eps, y,
                              y_row_stride, residual_out, residual_out_row_stride, st);
   });
+  if (rc != kComposeAddRms) return rc;
+  // Layouts the one-pass kernels do not take (operands at different offsets
+  // within 16 bytes, rows wider than the register budget, a weight that
+  // differs per row): the sum through ntops_binary, then ntops_rms_norm over
+  // the new residual -- the very kernels `add` and `rms_norm` run, so the
+  // result is theirs element for element.
+  const int64_t shape[2] = {rows, cols};
+  const int64_t xst[2] = {x_row_stride, 1}, rst[2] = {residual_row_stride, 1}, ost[2] = {residual_out_row_stride, 1};
+  if (int e = ntops_binary(NTOPS_BINARY_ADD, dtype, 2, shape, x, xst, residual, rst, 0.0, 0, 1.0, 1, residual_out,
+                           ost, stream))
+    return e;
+  return ntops_rms_norm(dtype, rows, cols, residual_out, residual_out_row_stride, w, w_row_stride, w_dtype, eps, y,
+                        y_row_stride, stream);
 }
