@@ -25,6 +25,7 @@
 // load between the rows of a wave slot where the registers allow it.
 #include "dispatch.h"
 #include "rowcommon.h"
+#include "rowwide.h"
 
 namespace ntops {
 namespace {
@@ -353,6 +354,121 @@ __global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W
   }
 }
 
+// ------------------------------------------------------------ wide rows --
+// Rows of more than 8192 packs (rowwide.h): the row is read once into VGPRs
+// and LDS, each pass reads it there; the weight and bias are read at their
+// use.  Row = block.
+template <typename T, typename W>
+__global__ __launch_bounds__(kWideThreads) void k_rms_wide(const T* __restrict__ x, int64_t xs,
+                                                           const W* __restrict__ w, T* __restrict__ y,
+                                                           int64_t ys, int64_t rows, int cols, float eps) {
+  constexpr int V = Pack16<T>::N;
+  __shared__ float red[kWideWaves];
+  extern __shared__ __attribute__((aligned(16))) char wsm[];
+  const int64_t row = block_id();
+  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
+  const int npk = cols / V, t = threadIdx.x;
+  WideRow<T> d;
+  wide_load(d, x + row * xs, npk, wsm);
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kWideRegChunks; ++c)
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss = fmaf(to_f(d.r[c].v[i]), to_f(d.r[c].v[i]), ss);
+  for (int q = t; q < d.nl; q += kWideThreads) {
+    const Pack16<T> v = wide_lds_pack(d, q);
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss = fmaf(to_f(v.v[i]), to_f(v.v[i]), ss);
+  }
+  ss = wide_reduce(ss, red, [](float a, float b) { return a + b; });
+  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
+  const __amdgpu_buffer_rsrc_t wr = param_rsrc<V>(w, npk);
+  auto emit = [&](const Pack16<T>& v, int pk) {
+    ParamPack<W, V> wq;
+    wq.load(wr, pk);
+    Pack16<T> o;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float wv = w != nullptr ? wq.get(i) : 1.0f;
+      o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(v.v[i]), rstd), wv));
+    }
+    buffer_store16_nt(out, pk * 16u, o);
+  };
+#pragma unroll
+  for (int c = 0; c < kWideRegChunks; ++c) emit(d.r[c], c * kWideThreads + t);
+  for (int q = t; q < d.nl; q += kWideThreads) emit(wide_lds_pack(d, q), kWideRegPacks + q);
+}
+
+template <typename T, typename W>
+__global__ __launch_bounds__(kWideThreads) void k_ln_wide(const T* __restrict__ x, int64_t xs,
+                                                          const W* __restrict__ w, const W* __restrict__ b,
+                                                          T* __restrict__ y, int64_t ys, int64_t rows, int cols,
+                                                          float eps) {
+  constexpr int V = Pack16<T>::N;
+  __shared__ float red[kWideWaves];
+  extern __shared__ __attribute__((aligned(16))) char wsm[];
+  const int64_t row = block_id();
+  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
+  const int npk = cols / V, t = threadIdx.x;
+  WideRow<T> d;
+  wide_load(d, x + row * xs, npk, wsm);
+  // register packs past the row end hold zeros: they add nothing to the sum
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < kWideRegChunks; ++c)
+#pragma unroll
+    for (int i = 0; i < V; ++i) s += to_f(d.r[c].v[i]);
+  for (int q = t; q < d.nl; q += kWideThreads) {
+    const Pack16<T> v = wide_lds_pack(d, q);
+#pragma unroll
+    for (int i = 0; i < V; ++i) s += to_f(v.v[i]);
+  }
+  const auto sum = [](float a, float b) { return a + b; };
+  const float mean = wide_reduce(s, red, sum) / static_cast<float>(cols);
+  float q2 = 0.f;
+#pragma unroll
+  for (int c = 0; c < kWideRegChunks; ++c) {
+    float qc = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float dv = to_f(d.r[c].v[i]) - mean;
+      qc = fmaf(dv, dv, qc);
+    }
+    q2 += c * kWideThreads + t < npk ? qc : 0.f;
+  }
+  for (int q = t; q < d.nl; q += kWideThreads) {
+    const Pack16<T> v = wide_lds_pack(d, q);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float dv = to_f(v.v[i]) - mean;
+      q2 = fmaf(dv, dv, q2);
+    }
+  }
+  const float var = wide_reduce(q2, red, sum) * (1.0f / static_cast<float>(cols));
+  const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
+  const float shift = -rstd * mean;
+  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
+  const __amdgpu_buffer_rsrc_t wr = param_rsrc<V>(w, npk);
+  const __amdgpu_buffer_rsrc_t br = param_rsrc<V>(b, npk);
+  auto emit = [&](const Pack16<T>& v, int pk) {
+    ParamPack<W, V> wq, bq;
+    wq.load(wr, pk);
+    bq.load(br, pk);
+    Pack16<T> o;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float wv = w != nullptr ? wq.get(i) : 1.0f;
+      const float bv = b != nullptr ? bq.get(i) : 0.0f;
+      o.v[i] = static_cast<T>(fmaf(fmaf(to_f(v.v[i]), rstd, shift), wv, bv));
+    }
+    buffer_store16_nt(out, pk * 16u, o);
+  };
+#pragma unroll
+  for (int c = 0; c < kWideRegChunks; ++c) emit(d.r[c], c * kWideThreads + t);
+  for (int q = t; q < d.nl; q += kWideThreads) emit(wide_lds_pack(d, q), kWideRegPacks + q);
+}
+
 // ------------------------------------------- rows that are not 16-byte runs --
 // Rows whose width or start is not a multiple of 16 bytes (an odd width such
 // as 4100, or a view into wider rows), with the output rows laid out at the
@@ -614,6 +730,13 @@ bool same_layout(const void* a, int64_t as, const void* b, int64_t bs) {
          (((as - bs) * static_cast<int64_t>(sizeof(T))) & 15) == 0;
 }
 
+// Rows of whole 16-byte packs, every row 16-byte aligned, in x and y.
+template <typename T>
+bool aligned16_rows(const void* x, int64_t xs, const void* y, int64_t ys, int64_t cols) {
+  constexpr int V = Pack16<T>::N;
+  return cols % V == 0 && xs % V == 0 && ys % V == 0 && aligned16(x) && aligned16(y);
+}
+
 // Launch shape of the odd-layout kernels: from the most whole packs a row
 // can hold (at least one pack, for rows shorter than a pack).
 inline bool pick_odd_cfg(int64_t cols, int v, VecCfg* cfg) { return pick_row_cfg(cols / v > 0 ? cols / v : 1, cfg); }
@@ -642,6 +765,14 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
   }
     NTOPS_ROW_CASES(NTOPS_RMS_CASE)
 #undef NTOPS_RMS_CASE
+  }
+  if (aligned16_rows<T>(x, xs, y, ys, cols) && (w == nullptr || (aligned16(w) && wrs == 0)) &&
+      wide_row_fits(cols / V)) {
+    static bool lds_set = false;
+    if (int e = wide_lds_attr(k_rms_wide<T, W>, lds_set)) return e;
+    hipLaunchKernelGGL((k_rms_wide<T, W>), blocks_2d(rows), dim3(kWideThreads), wide_lds_bytes(cols / V), st, x, xs,
+                       w, y, ys, rows, static_cast<int>(cols), feps);
+    return check_launch("rms_norm");
   }
   const int64_t lds = w != nullptr ? odd_param_bytes<W>(cols) : 0;
   if (same_layout<T>(x, xs, y, ys) && (w == nullptr || (aligned16(w) && wrs == 0)) && lds <= kOddLdsMax &&
@@ -686,6 +817,14 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
   }
     NTOPS_ROW_CASES(NTOPS_LN_CASE)
 #undef NTOPS_LN_CASE
+  }
+  if (aligned16_rows<T>(x, xs, y, ys, cols) && (w == nullptr || aligned16(w)) && (b == nullptr || aligned16(b)) &&
+      wrs == 0 && wide_row_fits(cols / V)) {
+    static bool lds_set = false;
+    if (int e = wide_lds_attr(k_ln_wide<T, W>, lds_set)) return e;
+    hipLaunchKernelGGL((k_ln_wide<T, W>), blocks_2d(rows), dim3(kWideThreads), wide_lds_bytes(cols / V), st, x, xs, w,
+                       b, y, ys, rows, static_cast<int>(cols), feps);
+    return check_launch("layer_norm");
   }
   const int64_t lds = (w != nullptr || b != nullptr) ? 2 * odd_param_bytes<W>(cols) : 0;
   if (same_layout<T>(x, xs, y, ys) && (w == nullptr || aligned16(w)) && (b == nullptr || aligned16(b)) &&

@@ -15,6 +15,7 @@
 //   threads touch adjacent inner elements, so every pass is coalesced.
 #include "dispatch.h"
 #include "rowcommon.h"
+#include "rowwide.h"
 
 namespace ntops {
 namespace {
@@ -133,6 +134,62 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_softmax_vec(
       store16_nt(yr + pk * V, o);
     }
   }
+}
+
+// Rows of more than 8192 packs (rowwide.h): one block per row, the row read
+// once into VGPRs and LDS; three passes over it there -- the row max, the
+// sum of exp(x - max), the outputs exp(x - max) / sum (the exponential
+// evaluated again rather than kept: the registers hold the row itself).
+template <typename T>
+__global__ __launch_bounds__(kWideThreads) void k_softmax_wide(const T* __restrict__ x, int64_t xs,
+                                                               T* __restrict__ y, int64_t ys, int64_t rows,
+                                                               int cols) {
+  constexpr int V = Pack16<T>::N;
+  __shared__ float red[kWideWaves];
+  extern __shared__ __attribute__((aligned(16))) char wsm[];
+  const int64_t row = block_id();
+  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
+  const int npk = cols / V, t = threadIdx.x;
+  WideRow<T> d;
+  wide_load(d, x + row * xs, npk, wsm);
+  const float ninf = -__builtin_huge_valf();
+  float m = ninf;
+#pragma unroll
+  for (int c = 0; c < kWideRegChunks; ++c)
+    if (c * kWideThreads + t < npk)
+#pragma unroll
+      for (int i = 0; i < V; ++i) m = cmax(m, static_cast<float>(d.r[c].v[i]));
+  for (int q = t; q < d.nl; q += kWideThreads) {
+    const Pack16<T> v = wide_lds_pack(d, q);
+#pragma unroll
+    for (int i = 0; i < V; ++i) m = cmax(m, static_cast<float>(v.v[i]));
+  }
+  m = wide_reduce(m, red, [](float a, float b) { return cmax(a, b); });
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < kWideRegChunks; ++c) {
+    float sc = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) sc += row_exp(static_cast<float>(d.r[c].v[i]) - m);
+    s += c * kWideThreads + t < npk ? sc : 0.f;
+  }
+  for (int q = t; q < d.nl; q += kWideThreads) {
+    const Pack16<T> v = wide_lds_pack(d, q);
+#pragma unroll
+    for (int i = 0; i < V; ++i) s += row_exp(static_cast<float>(v.v[i]) - m);
+  }
+  s = wide_reduce(s, red, [](float a, float b) { return a + b; });
+  const float inv = 1.0f / s;
+  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
+  auto emit = [&](const Pack16<T>& v, int pk) {
+    Pack16<T> o;
+#pragma unroll
+    for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(row_exp(static_cast<float>(v.v[i]) - m) * inv);
+    buffer_store16_nt(out, pk * 16u, o);
+  };
+#pragma unroll
+  for (int c = 0; c < kWideRegChunks; ++c) emit(d.r[c], c * kWideThreads + t);
+  for (int q = t; q < d.nl; q += kWideThreads) emit(wide_lds_pack(d, q), kWideRegPacks + q);
 }
 
 // One block per row, any element stride, input converted to the output dtype
@@ -263,6 +320,16 @@ int run_softmax(int64_t outer, int64_t dim, int64_t inner, const void* xv, const
   }
         NTOPS_ROW_CASES(NTOPS_SM_CASE)
 #undef NTOPS_SM_CASE
+      }
+      if constexpr (sizeof(C) == 4) {
+        if (xs[1] == 1 && ys[1] == 1 && dim % V == 0 && xs[0] % V == 0 && ys[0] % V == 0 && aligned16(x) &&
+            aligned16(y) && wide_row_fits(dim / V) && outer <= 0x7fffffffLL) {
+          static bool lds_set = false;
+          if (int e = wide_lds_attr(k_softmax_wide<To>, lds_set)) return e;
+          hipLaunchKernelGGL((k_softmax_wide<To>), blocks_2d(outer), dim3(kWideThreads), wide_lds_bytes(dim / V), st,
+                             x, xs[0], y, ys[0], outer, static_cast<int>(dim));
+          return check_launch("softmax");
+        }
       }
       if (xs[1] == 1 && ys[1] == 1 && outer <= 0x7fffffffLL) {
         hipLaunchKernelGGL((k_softmax_loop_v<To, C>), blocks_2d(outer), dim3(256), 0, st, x, xs[0], y, ys[0],
