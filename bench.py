@@ -523,6 +523,48 @@ def make_workloads():
     W.append(Workload("layer_norm", "layer_norm bf16 (16384, 4096), weight + bias (4096,), eps 1e-5", "GB/s",
                       "hbm", 2 * R * C * 2 + 2 * C * 2, 1, norm_build, ln_step, ln_cpu, "bf16"))
 
+    # the same norms on rows the register-resident kernels do not take:
+    # an odd width (16384, 4100) -- head / packs / tail, parameters in LDS --
+    # and wide rows (512, 131072) staged in VGPRs + LDS (rms_norm, softmax)
+    RO, CO = 16384, 4100
+    RW, CW = 512, 131072
+
+    def odd_build(i):
+        g = _gen(120 + i)
+        x = torch.randn(RO, CO, device="cuda", generator=g).bfloat16()
+        w = (1 + 0.02 * torch.randn(CO, device="cuda", generator=g)).bfloat16()
+        return {"x": x, "w": w, "y": torch.empty_like(x)}
+
+    def rms_odd_step(s):
+        check(lib.ntops_rms_norm(_lib.BF16, RO, CO, s["x"].data_ptr(), CO, s["w"].data_ptr(), 0, _lib.BF16, 1e-6,
+                                 s["y"].data_ptr(), CO, stream()), "rms_norm")
+
+    def wide_build(i):
+        g = _gen(140 + i)
+        x = torch.randn(RW, CW, device="cuda", generator=g).bfloat16()
+        w = (1 + 0.02 * torch.randn(CW, device="cuda", generator=g)).bfloat16()
+        return {"x": x, "w": w, "y": torch.empty_like(x)}
+
+    def rms_wide_step(s):
+        check(lib.ntops_rms_norm(_lib.BF16, RW, CW, s["x"].data_ptr(), CW, s["w"].data_ptr(), 0, _lib.BF16, 1e-6,
+                                 s["y"].data_ptr(), CW, stream()), "rms_norm")
+
+    wide_strides = _lib.i64_array((CW, 1, 1))
+
+    def sm_wide_step(s):
+        check(lib.ntops_softmax(_lib.BF16, _lib.BF16, RW, CW, 1, s["x"].data_ptr(), wide_strides, s["y"].data_ptr(),
+                                wide_strides, stream()), "softmax")
+
+    W.append(Workload("rms_norm_odd", "rms_norm bf16 (16384, 4100), weight (4100,), eps 1e-6 (rows not 16-byte runs)",
+                      "GB/s", "hbm", 2 * RO * CO * 2 + CO * 2, 1, odd_build, rms_odd_step, None, "bf16"))
+    W[-1].yardstick = (lambda s: F.rms_norm(s["x"], (CO,), s["w"], 1e-6), "torch rms_norm (GPU), eager")
+    W.append(Workload("rms_norm_wide", "rms_norm bf16 (512, 131072), weight (131072,), eps 1e-6 (rows staged in LDS)",
+                      "GB/s", "hbm", 2 * RW * CW * 2 + CW * 2, 1, wide_build, rms_wide_step, None, "bf16"))
+    W[-1].yardstick = (lambda s: F.rms_norm(s["x"], (CW,), s["w"], 1e-6), "torch rms_norm (GPU), eager")
+    W.append(Workload("softmax_wide", "softmax bf16 (512, 131072) dim=-1 (rows staged in LDS)", "GB/s", "hbm",
+                      2 * RW * CW * 2, 1, wide_build, sm_wide_step, None, "bf16"))
+    W[-1].yardstick = (lambda s: torch.softmax(s["x"], -1), "torch softmax (GPU), eager")
+
     # softmax bf16 (4, 32, 2048, 2048) causal
     SB, SH, SS = 4, 32, 2048
 
