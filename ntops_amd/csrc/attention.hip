@@ -8,7 +8,10 @@
 // variants).  Rows whose every score is masked produce 0, as torch's CPU
 // kernel does (the reference would produce NaN).
 //
-// MFMA path (bf16 / f16, head dim 64 or 128, unit stride along D):
+// MFMA path (bf16 / f16, unit stride along D, head dim a multiple of 8 up to
+// 128: kernels for D = 64 and 128, the columns past a smaller head dim read
+// as zero from Q, K and V -- their products add nothing to S, and their O
+// columns are zero and never stored):
 //  * one 4-wave workgroup per (batch, head, 128 query rows); wave w owns 32
 //    rows and keeps their Q fragments in VGPRs for the whole kernel;
 //  * key / value tiles of 64 rows are double-buffered in LDS (the next
@@ -144,8 +147,12 @@ struct KvDma {
   int lds_off;
 
   // base: element pointer of key row 0; ld: row stride in elements;
-  // extent: readable bytes (rows at or past the end read as zero).
-  __device__ __forceinline__ void init(const void* base, int64_t ld, uint32_t extent, int wave, int lane) {
+  // extent: readable bytes (rows at or past the end read as zero); dt: the
+  // head dim of the data (a multiple of 8, at most D): the chunks of columns
+  // dt .. D - 1 read as zero (their offset starts at kOOB, and a tile's
+  // offset added to it stays below 2^32 and past every extent, since the
+  // launch keeps (Skv + 256) * ld * 2 below 2^31).
+  __device__ __forceinline__ void init(const void* base, int64_t ld, uint32_t extent, int wave, int lane, int dt) {
     const uint64_t addr = reinterpret_cast<uint64_t>(base);
     rsrc.x = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
     rsrc.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32) & 0xffffu);
@@ -158,7 +165,7 @@ struct KvDma {
       const int row = (wave * kInst + i) * kRowsPerInst + lane / cpr;
       const int slot = lane % cpr;
       const int c = IS_V ? vslot<D>(row, slot) : kslot<D>(row, slot);  // swizzles are involutions
-      voff[i] = static_cast<uint32_t>(row * ld * 2 + c * 16);
+      voff[i] = c * 8 < dt ? static_cast<uint32_t>(row * ld * 2 + c * 16) : kOOB;
     }
     tile_bytes = static_cast<uint32_t>(64 * ld * 2);
   }
@@ -223,8 +230,9 @@ __global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int t
   u32x4 qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    if (my_q < a.Sq)
-      qf[ks] = *reinterpret_cast<const u32x4*>(Q + my_q * a.qs[2] + ks * 16 + 8 * (lane >> 5));
+    const int d0 = ks * 16 + 8 * (lane >> 5);  // columns past the head dim read as zero
+    if (my_q < a.Sq && d0 < a.D)
+      qf[ks] = *reinterpret_cast<const u32x4*>(Q + my_q * a.qs[2] + d0);
     else
       qf[ks] = u32x4{0, 0, 0, 0};
   }
@@ -314,8 +322,8 @@ __global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int t
   // the end read as zero, keeping 0 * V finite)
   KvDma<D, false, 4> kd;
   KvDma<D, true, 4> vd;
-  kd.init(K, a.ks[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane);
-  vd.init(V, a.vs[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane);
+  kd.init(K, a.ks[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane, a.D);
+  vd.init(V, a.vs[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane, a.D);
   const uint32_t smem_addr = lds_addr(smem);
   auto dma = [&](int t) {
     const uint32_t st = smem_addr + static_cast<uint32_t>((t & 1) * 2 * kTile);
@@ -464,7 +472,9 @@ __global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int t
       T v4[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
-      *reinterpret_cast<u32x2*>(O + t * 32 + 8 * qq + 4 * (lane >> 5)) = __builtin_bit_cast(u32x2, v4);
+      const int col = t * 32 + 8 * qq + 4 * (lane >> 5);
+      if (col < a.D)  // a.D % 8 == 0: the 4 columns are all in or all out
+        *reinterpret_cast<u32x2*>(O + col) = __builtin_bit_cast(u32x2, v4);
     }
 }
 
@@ -520,7 +530,9 @@ __device__ __forceinline__ bool fa_item(int r, int nbh, int nqb, int& bh, int& q
   return true;
 }
 
-template <typename T, int D, bool CAUSAL>
+// TAIL: the head dim a.D is below D (columns a.D .. D - 1 masked); compiled
+// apart so the D-wide kernels carry no column tests.
+template <typename T, int D, bool CAUSAL, bool TAIL>
 __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb) {
   constexpr int BN = 64;
   constexpr int NS = kFaStages;
@@ -564,9 +576,11 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb) {
         buffer_rsrc(Q, static_cast<uint32_t>(static_cast<int64_t>(a.Sq) * a.qs[2] * 2));
     const uint32_t row = static_cast<uint32_t>((qb * kFaRows + wave * 32 + (lane & 31)) * a.qs[2] * 2);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = ks * 16 + 8 * (lane >> 5);  // columns past the head dim read as zero
       qf[ks] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rq, row + ks * 32 + 16 * (lane >> 5), 0, 0));
+                                             rq, !TAIL || d0 < a.D ? row + d0 * 2 : kOOB, 0, 0));
+    }
   };
   // K / V of (batch * head) bh
   auto k_base = [&](int bh) {
@@ -579,8 +593,8 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb) {
   };
   KvDma<D, false, NW> kd;
   KvDma<D, true, NW> vd;
-  kd.init(k_base(0), a.ks[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane);
-  vd.init(v_base(0), a.vs[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane);
+  kd.init(k_base(0), a.ks[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.ks[2] * 2), wave, lane, a.D);
+  vd.init(v_base(0), a.vs[2], static_cast<uint32_t>(static_cast<int64_t>(a.Skv) * a.vs[2] * 2), wave, lane, a.D);
   // Work item (batch * head, query block) of a persistent workgroup (one
   // per CU) walking the items fa_item picks, so that a head's query blocks
   // run together on one XCD (its K and V stay in that L2) and per-workgroup
@@ -828,8 +842,9 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb) {
       T v4[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) v4[e] = static_cast<T>(o[t][4 * qq + e] * inv);
+      const int col = t * 32 + 8 * qq + 4 * (lane >> 5);  // columns past the head dim: dropped
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v4), ro,
-                                            orow + (t * 32 + 8 * qq + 4 * (lane >> 5)) * 2, 0, 0);
+                                            !TAIL || col < a.D ? orow + col * 2 : kOOB, 0, 0);
     }
   base = (base + nkv) & 3;
   };  // item
@@ -904,10 +919,10 @@ __global__ __launch_bounds__(64) void k_attn_generic(AttnArgs a) {
   }
 }
 
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, bool TAIL>
 int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
   constexpr int kLds = kFaStages * 2 * 64 * D * 2;
-  auto kern = k_flash_attn<T, D, CAUSAL>;
+  auto kern = k_flash_attn<T, D, CAUSAL, TAIL>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -930,13 +945,17 @@ int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
 
 template <typename T, int D>
 int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
-  return a.causal ? launch_flash_attn<T, D, true>(a, st) : launch_flash_attn<T, D, false>(a, st);
+  if (a.D < D)
+    return a.causal ? launch_flash_attn<T, D, true, true>(a, st) : launch_flash_attn<T, D, false, true>(a, st);
+  return a.causal ? launch_flash_attn<T, D, true, false>(a, st) : launch_flash_attn<T, D, false, false>(a, st);
 }
 
 template <typename T>
 int run_attention(const AttnArgs& a, hipStream_t st) {
   const auto unit_d = [&](const int64_t* s) { return s[3] == 1 && s[2] % 8 == 0 && s[1] % 8 == 0 && s[0] % 8 == 0; };
-  const bool mfma = !std::is_same<T, float>::value && (a.D == 64 || a.D == 128) && unit_d(a.qs) &&
+  // head dims up to 128 in multiples of 8 run on the D = 64 / 128 kernels,
+  // the columns past the head dim zero in Q, K and V and dropped from O
+  const bool mfma = !std::is_same<T, float>::value && a.D % 8 == 0 && a.D <= 128 && unit_d(a.qs) &&
                     unit_d(a.ks) && unit_d(a.vs) && a.os[3] == 1 && a.os[2] % 4 == 0 &&
                     a.os[1] % 4 == 0 && a.os[0] % 4 == 0 && aligned16(a.q) && aligned16(a.k) &&
                     aligned16(a.v) && (reinterpret_cast<uintptr_t>(a.o) & 7u) == 0;
@@ -950,7 +969,7 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
     const bool dma = mfma && a.mask_dtype < 0 && a.scale_log2 > 0.f && a.Sq > 128 && a.Skv > 0 &&
                      a.ks[2] >= a.D && a.vs[2] >= a.D && (static_cast<int64_t>(a.Skv) + 256) * ld * 2 < 0x7fffffffLL &&
                      (static_cast<int64_t>(a.Sq) + kFaRows) * qo * 2 < 0x7fffffffLL;
-    if (dma) return a.D == 128 ? launch_flash_attn<T, 128>(a, st) : launch_flash_attn<T, 64>(a, st);
+    if (dma) return a.D > 64 ? launch_flash_attn<T, 128>(a, st) : launch_flash_attn<T, 64>(a, st);
     // the masked MFMA kernel takes the mask with contiguous keys through a
     // per-(batch, head) buffer resource (its plane spanning less than 2^31
     // bytes) and folds it into S as mask / scale (scale != 0)
@@ -966,7 +985,7 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
       const int mm = a.mask_dtype < 0 ? 0
                      : (a.ms[2] % 4 == 0 && a.ms[1] % 4 == 0 && a.ms[0] % 4 == 0 && mp % (4 * esz) == 0) ? 1 : 2;
       const dim3 grid(static_cast<unsigned>(total)), block(256);
-      note_kernel("sdpa_fwd d%d mask%d es%d", a.D, mm, esz);
+      note_kernel("sdpa_fwd d%d mask%d es%d", a.D > 64 ? 128 : 64, mm, esz);
 #define NTOPS_FWD(DD, MM, ES) hipLaunchKernelGGL((k_flash_fwd<T, DD, MM, ES>), grid, block, 0, st, a, nqb, static_cast<int>(total))
 #define NTOPS_FWD_D(DD)                         \
   if (mm == 0) NTOPS_FWD(DD, 0, 1);             \
@@ -976,7 +995,7 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
   else if (esz == 1) NTOPS_FWD(DD, 2, 1);       \
   else if (esz == 2) NTOPS_FWD(DD, 2, 2);       \
   else NTOPS_FWD(DD, 2, 4);
-      if (a.D == 128) {
+      if (a.D > 64) {
         NTOPS_FWD_D(128)
       } else {
         NTOPS_FWD_D(64)

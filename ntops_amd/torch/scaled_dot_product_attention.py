@@ -89,38 +89,14 @@ def scaled_dot_product_attention(
     if scale is None:
         scale = 1 / math.sqrt(D)
 
-    # 16-bit head dims below 128 other than 64 run on the matrix-core kernel
-    # at 64 or 128: Q, K and V zero-extended along D (the scores and the
-    # first D output columns are unchanged), the scale kept for D
-    Dk, result = D, None
-    if query.dtype != torch.float32 and D < 128 and D != 64:
-        Dk = 64 if D < 64 else 128
-        with _DeviceGuard(dev):
-            query, key, value = (_zero_extend_last(t, Dk) for t in (query, key, value))
-        result = torch.empty(query.shape[:-1] + (D,), dtype=value.dtype, device=dev)
-
     output = torch.empty(query.shape[:-1] + (value.shape[-1],), dtype=value.dtype, device=dev)
     lib = _lib.load()
     with _DeviceGuard(dev):
         rc = lib.ntops_sdpa(
-            _lib.dtype_code(query.dtype), B, Hq, key.shape[1], Sq, Skv, Dk,
+            _lib.dtype_code(query.dtype), B, Hq, key.shape[1], Sq, Skv, D,
             query.data_ptr(), _strides(query), key.data_ptr(), _strides(key), value.data_ptr(), _strides(value),
             mask_ptr, mask_code, mask_strides, causal, float(scale),
             output.data_ptr(), _strides(output), _lib.stream_of(output),
         )
     _lib.check(rc, "ntops_amd.scaled_dot_product_attention")
-    if result is not None:
-        with _DeviceGuard(dev):
-            output = _cast_into(output[..., :D], result)
     return output.squeeze(0) if squeeze else output
-
-
-def _zero_extend_last(t, width):
-    """A new tensor of t's shape with the last axis `width` long: t, then
-    zeros (copies and fills by the native cast kernel)."""
-    p = torch.empty(t.shape[:-1] + (width,), dtype=t.dtype, device=t.device)
-    d = t.shape[-1]
-    _cast_into(t, p[..., :d])
-    zero = torch.zeros((), dtype=t.dtype, device=t.device)
-    _cast_into(zero.expand(p[..., d:].shape), p[..., d:])
-    return p

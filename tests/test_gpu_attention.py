@@ -20,6 +20,7 @@ import pytest
 import torch
 
 import ntops_amd
+from ntops_amd import _lib
 from ntops_amd.kernels.scaled_dot_product_attention import CausalVariant
 from oracle import ops as O
 from tests.helpers import DT_NAME, assert_close, from_np, to_np
@@ -91,7 +92,9 @@ def test_sdpa(b, hq, sq, d, hkv, skv, mask_type, is_causal, scale, variant, kv_c
 
 
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
-@pytest.mark.parametrize("d", (64, 128, 80, 96))  # 80, 96: zero-extended to 128 for 16-bit data
+# head dims below 64 / 128 (16-bit data): the D = 64 / 128 kernels with the
+# columns past the head dim read as zero and never stored
+@pytest.mark.parametrize("d", (64, 128, 80, 96, 32, 48, 120))
 def test_sdpa_edges(dtype, d):
     g = torch.Generator().manual_seed(d)
     rt = lambda *s: torch.randn(*s, generator=g).to(dtype)  # noqa: E731
@@ -115,6 +118,26 @@ def test_sdpa_edges(dtype, d):
     got3 = sdpa(qs[0].cuda().transpose(0, 1), ks[0].cuda().transpose(0, 1), vs[0].cuda().transpose(0, 1))
     exp3 = oracle(qs[:1].transpose(1, 2), ks[:1].transpose(1, 2), vs[:1].transpose(1, 2))[0]
     assert_close(got3, exp3, *TOL[dtype], "3-D")
+
+
+@pytest.mark.parametrize("d, causal", ((96, 1), (80, 2), (96, 0), (40, 1)))
+def test_sdpa_head_dim_tail_on_matrix_cores(d, causal):
+    """bf16 head dims that are not 64 / 128 run on the matrix-core kernels
+    (asserted by name) with the tail columns zero: against the oracle on
+    every element, for the flash kernel (Sq > 128) and the masked one."""
+    g = torch.Generator().manual_seed(d * 10 + causal)
+    b, h, s = 2, 4, 384
+    q, k, v = (torch.randn(b, h, s, d, generator=g).bfloat16() for _ in range(3))
+    variant = CausalVariant.LOWER_RIGHT if causal == 2 else None
+    got = sdpa(q.cuda(), k.cuda(), v.cuda(), is_causal=causal > 0, causal_variant=variant)
+    dk = 128 if d > 64 else 64
+    assert _lib.last_kernel().startswith(f"sdpa_flash d{dk}"), _lib.last_kernel()
+    assert got.shape == (b, h, s, d)
+    assert_close(got, oracle(q, k, v, None, causal), *TOL[torch.bfloat16], f"d {d}")
+    m = torch.rand(s, s, generator=g) > 0.4
+    got = sdpa(q.cuda(), k.cuda(), v.cuda(), attn_mask=m.cuda())
+    assert _lib.last_kernel().startswith(f"sdpa_fwd d{dk}"), _lib.last_kernel()
+    assert_close(got, oracle(q, k, v, m), *TOL[torch.bfloat16], f"d {d} masked")
 
 
 def test_sdpa_argument_checks():
