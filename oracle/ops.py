@@ -684,7 +684,7 @@ def gemm(a, b, dt, c=None, alpha=1.0, beta=0.0):
 
 
 @_with_errstate
-def scaled_dot_product_attention(q, k, v, dt, mask=None, mask_dt=None, causal=0, scale=None):
+def scaled_dot_product_attention(q, k, v, dt, mask=None, mask_dt=None, causal=0, scale=None, round_p=False):
     """kernels/scaled_dot_product_attention.py:154-201 (an online, base-2
     softmax over key blocks) restated as its closed form, in float64:
     out = softmax(q k^T * scale + mask) v per (batch, query head), with query
@@ -694,7 +694,14 @@ def scaled_dot_product_attention(q, k, v, dt, mask=None, mask_dt=None, causal=0,
     causal: 0 none, 1 upper-left (j <= i), 2 lower-right (j <= i + Skv - Sq).
     scale defaults to 1 / sqrt(D).  A row with every key masked gives 0, as
     torch's CPU kernel does (the reference's loop would give NaN).  Inputs are
-    (B, H, S, D) arrays of dt; the result is rounded to dt once."""
+    (B, H, S, D) arrays of dt; the result is rounded to dt once.
+
+    round_p: the probabilities enter P @ V rounded to dt, as the reference's
+    `ntl.dot(stable_qk.to(value[i].dtype), value[j])` (line 196) and the
+    matrix-core kernels do, while the denominator sums them unrounded (its
+    `lse`, line 198).  They are rounded relative to the row's exact max; a
+    blockwise kernel rounds exp2(s - m) for its running or reference max m,
+    which rounds the same up to a power-of-two rescaling."""
     qf = to_compute(q, dt).astype(np.float64)
     kf = to_compute(k, dt).astype(np.float64)
     vf = to_compute(v, dt).astype(np.float64)
@@ -723,6 +730,8 @@ def scaled_dot_product_attention(q, k, v, dt, mask=None, mask_dt=None, causal=0,
     mx = np.where(np.isfinite(mx), mx, 0.0)
     p = np.exp(sc - mx)
     den = np.sum(p, axis=-1, keepdims=True)
+    if round_p and dt != "f32" and dt != "f64":
+        p = to_compute(round_to(p.astype(np.float32), dt), dt).astype(np.float64)
     out = np.matmul(p, vf) / np.where(den > 0, den, 1.0)
     out = np.where(den > 0, out, 0.0)
     return round_to(out.astype(np.float32) if dt != "f64" else out, dt)

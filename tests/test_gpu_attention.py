@@ -30,7 +30,9 @@ pytestmark = [
     pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
 ]
 
-TOL = {torch.float32: (1e-4, 1e-4), torch.float16: (2.5e-2, 2.5e-2), torch.bfloat16: (2.5e-2, 2.5e-2)}
+# 16-bit data: the north-star bound, against the oracle with P rounded to
+# the dtype before P @ V (as the reference's kernel and this one do)
+TOL = {torch.float32: (1e-4, 1e-4), torch.float16: (1.6e-2, 1.6e-2), torch.bfloat16: (1.6e-2, 1.6e-2)}
 sdpa = ntops_amd.torch.scaled_dot_product_attention
 
 
@@ -40,7 +42,8 @@ def oracle(q, k, v, mask=None, causal=0, scale=None):
     if mask is not None:
         m = to_np(mask)
         mdt = DT_NAME[mask.dtype]
-    return from_np(O.scaled_dot_product_attention(to_np(q), to_np(k), to_np(v), dt, m, mdt, causal, scale), dt)
+    return from_np(O.scaled_dot_product_attention(to_np(q), to_np(k), to_np(v), dt, m, mdt, causal, scale,
+                                                  round_p=True), dt)
 
 
 def cases():
@@ -138,6 +141,29 @@ def test_sdpa_head_dim_tail_on_matrix_cores(d, causal):
     got = sdpa(q.cuda(), k.cuda(), v.cuda(), attn_mask=m.cuda())
     assert _lib.last_kernel().startswith(f"sdpa_fwd d{dk}"), _lib.last_kernel()
     assert_close(got, oracle(q, k, v, m), *TOL[torch.bfloat16], f"d {d} masked")
+
+
+@pytest.mark.parametrize("sq", (1, 256))
+def test_sdpa_rounds_p_before_pv(sq):
+    """P enters P @ V rounded to bf16 while the denominator sums it
+    unrounded: one key scores 0, 255 score ln(p1) with p1 just below the bf16
+    midpoint above 0.25, all values 1 -> (1 + 255 * 0.25) / (1 + 255 * p1)
+    = 0.99615 -> 0.99609375 (summing unrounded P everywhere, or rounded P
+    everywhere, gives 1).  sq = 1: the masked-path kernel; 256: the flash
+    kernel."""
+    D, n = 64, 255
+    p1 = 0.25 + 2.0 ** -10 * 0.999
+    scale = float(-math.log(p1))
+    q = torch.zeros(1, 2, sq, D)
+    q[..., 0] = 1.0
+    k = torch.zeros(1, 2, n + 1, D)
+    k[0, :, 1:, 0] = -1.0
+    v = torch.ones(1, 2, n + 1, D)
+    got = sdpa(q.bfloat16().cuda(), k.bfloat16().cuda(), v.bfloat16().cuda(), scale=scale)
+    assert _lib.last_kernel().startswith("sdpa_flash" if sq > 128 else "sdpa_fwd"), _lib.last_kernel()
+    assert (got.float() == 0.99609375).all(), got.float().unique()
+    exp = oracle(q.bfloat16(), k.bfloat16(), v.bfloat16(), None, 0, scale)
+    assert torch.equal(got.cpu(), exp)
 
 
 def test_sdpa_argument_checks():

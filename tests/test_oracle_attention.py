@@ -116,3 +116,58 @@ def _m_masked_row_nan(q, k, v, dt, mask=None, mask_dt=None, causal=0, scale=None
 @pytest.mark.parametrize("mutant", (_m_gqa_modulo, _m_causal_strict, _m_no_scale, _m_masked_row_nan))
 def test_planted_mistakes_are_caught(mutant):
     assert not pin_sdpa(mutant)
+
+
+def pin_round_p(f):
+    """round_p: the probabilities of P @ V rounded to the dtype, the
+    denominator summing them unrounded.  One key scores 0 and n keys score
+    s < 0, every value row is 1: the exact output is (1 + n round(e^s)) /
+    (1 + n e^s).  With e^s just below the bf16 midpoint above 0.25 (rounded
+    down by almost half a step, 0.39 % relative) that is 1 - 0.39 % ->
+    0.99609375 after the output's rounding, where ignoring round_p, or
+    summing the rounded probabilities in the denominator too, gives exactly
+    1."""
+    D, n = 8, 255
+    # e^s = p1 just below 0.25 + 2^-10, the midpoint above 0.25 in bf16: it
+    # rounds down to 0.25 (0.39 % relative); s = -1 * scale with scale = -ln p1
+    p1 = 0.25 + 2.0 ** -10 * 0.999
+    scale = -np.log(p1)
+    q = np.zeros((1, 1, 1, D), np.float32)
+    q[..., 0] = 1.0
+    k = np.zeros((1, 1, n + 1, D), np.float32)
+    k[0, 0, 1:, 0] = -1.0
+    v = np.ones((1, 1, n + 1, D), np.float32)
+    qb, kb, vb = (O.round_to(a, "bf16") for a in (q, k, v))
+    p1r = float(O.to_compute(O.round_to(np.float32(p1), "bf16"), "bf16"))
+    exp = (1.0 + n * p1r) / (1.0 + n * p1)
+    want = O.to_compute(O.round_to(np.full((1, 1, 1, D), exp, np.float32), "bf16"), "bf16")
+    got = O.to_compute(f(qb, kb, vb, "bf16", scale=scale, round_p=True), "bf16")
+    ok = bool(np.array_equal(got, want)) and bool(np.all(want < 1.0))
+    # fp32 data: round_p changes nothing
+    rng = np.random.default_rng(3)
+    a, b, c = (rng.standard_normal((1, 2, 5, D)).astype(np.float32) for _ in range(3))
+    ok &= np.array_equal(f(a, b, c, "f32", round_p=True), f(a, b, c, "f32"))
+    return ok
+
+
+def test_round_p_closed_form():
+    assert pin_round_p(O.scaled_dot_product_attention)
+
+
+def _m_round_p_ignored(q, k, v, dt, mask=None, mask_dt=None, causal=0, scale=None, round_p=False):
+    return O.scaled_dot_product_attention(q, k, v, dt, mask, mask_dt, causal, scale)
+
+
+def _m_round_p_denominator_too(q, k, v, dt, mask=None, mask_dt=None, causal=0, scale=None, round_p=False):
+    # the denominator summing the rounded probabilities: sum(round(p)) v / sum(round(p))
+    qf, kf, vf = (O.to_compute(a, dt).astype(np.float64) for a in (q, k, v))
+    s = qf @ kf.swapaxes(-1, -2) * (1.0 / np.sqrt(qf.shape[-1]) if scale is None else scale)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    if round_p:
+        p = O.to_compute(O.round_to(p.astype(np.float32), dt), dt).astype(np.float64)
+    return O.round_to(((p @ vf) / p.sum(-1, keepdims=True)).astype(np.float32), dt)
+
+
+@pytest.mark.parametrize("mutant", (_m_round_p_ignored, _m_round_p_denominator_too))
+def test_round_p_planted_mistakes_are_caught(mutant):
+    assert not pin_round_p(mutant)
