@@ -468,6 +468,21 @@ def make_workloads():
                       "hbm", 2 * CN_ * 4, 1, copy_build, copy_step, copy_cpu, "f32"))
     W[-1].yardstick = (lambda s: s["y"].copy_(s["x"]), "torch Tensor.copy_ (device-to-device), eager")
 
+    # the same copy at half the size (64 MiB each way): the ceiling of the
+    # bf16 (8192, 4096) elementwise workloads, whose launches are this short
+    cp2_shape = _lib.i64_array((CN_ // 2,))
+
+    def copy_half_build(i):
+        x = torch.randn(CN_ // 2, device="cuda", generator=_gen(90 + i))
+        return {"x": x, "y": torch.empty_like(x)}
+
+    def copy_half_step(s):
+        check(lib.ntops_cast(_lib.F32, _lib.F32, 1, cp2_shape, s["x"].data_ptr(), cp_st, s["y"].data_ptr(), cp_st,
+                             stream()), "copy")
+
+    W.append(Workload("copy_half", "streaming copy fp32 64 MiB -> 64 MiB (ntops_cast): the ceiling at half size",
+                      "GB/s", "hbm", CN_ * 4, 1, copy_half_build, copy_half_step, None, "f32"))
+
     # matrix-core rate probe: full-chip bf16 MFMAs on register operands, the
     # measured ceiling of the matrix-bound kernels
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -910,11 +925,13 @@ def time_yardstick(fn, build, steps, replays, settle_ms=0.0):
 
 
 def cpu_threads():
+    """Host threads for the CPU baseline: every CPU this process may run on
+    (its affinity mask), as the baseline's recipe asks."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+    return max(1, n)
 
 
 def cpu_model():
@@ -939,7 +956,8 @@ def time_cpu(w):
         ts.append(time.perf_counter() - t0)
     sec = statistics.median(ts)
     rate = work / sec / (1e12 if w.unit == "TFLOP/s" else 1e9)
-    return {"value": round(rate, 3), "unit": w.unit, "cores": torch.get_num_threads(), "kind": "reference",
+    return {"value": round(rate, 3), "unit": w.unit, "cores": torch.get_num_threads(), "affinity_cpus": cpu_threads(),
+            "kind": "reference",
             "sample": f"{sample}; PyTorch {torch.__version__} CPU op, median of {reps} after 1 warmup, "
                       f"{cpu_model()}"}
 
