@@ -782,9 +782,10 @@ def make_workloads():
     W[-1].bytes = 4 * AB * AH * AS * AD * 2
 
     def sdpa_torch(s):
-        # flash / memory-efficient backends only: without them torch falls
-        # back to its math path, whose bf16 batched products over transposed
-        # views have faulted the GPU; with them it raises instead
+        # flash / memory-efficient backends only, a precaution: torch's math
+        # backend would compute Q K^T as a bf16 batched product over a
+        # transposed view, a call documented to fault MI355X GPUs under this
+        # torch / ROCm build; restricted, torch raises instead of falling back
         from torch.nn.attention import SDPBackend, sdpa_kernel
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             F.scaled_dot_product_attention(s["q"], s["k"], s["v"], is_causal=True)
