@@ -209,6 +209,10 @@ NTOPS_API int ntops_cast(int src_dtype, int dst_dtype, int ndim, const int64_t* 
  * of cols contiguous elements of w_dtype (dtype or F32) w_row_stride apart --
  * 0 for one weight row shared by every row (the usual case; a non-zero
  * stride, a weight that differs per row, runs a slower looped kernel).
+ * Any width and row offset: when x and y rows sit at the same offset within
+ * 16 bytes the row is read once (register-resident, split into head /
+ * 16-byte packs / tail, or staged in VGPRs + LDS up to 146944 16-bit /
+ * 73472 fp32 elements); other layouts and wider rows run looped kernels.
  * dtype in {F32, F16, BF16}. */
 NTOPS_API int ntops_rms_norm(int dtype, int64_t rows, int64_t cols,
                    const void* x, int64_t x_row_stride,
@@ -274,7 +278,8 @@ NTOPS_API int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_t
  * (j <= i + Skv - Sq); mask and causal are exclusive.  dtype in {F32, F16,
  * BF16}; fp32 accumulation, the probabilities rounded to dtype for the
  * product with v (16-bit dtypes).  A row with every key masked yields 0.
- * D <= 256. */
+ * D <= 256; 16-bit data with D a multiple of 8 up to 128 and unit-stride
+ * rows runs on the matrix cores, anything else on a generic fp32 kernel. */
 NTOPS_API int ntops_sdpa(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv,
                int64_t D, const void* q, const int64_t* q_strides,
                const void* k, const int64_t* k_strides,
@@ -288,7 +293,9 @@ NTOPS_API int ntops_sdpa(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t 
  * over rows x cols with the conventions of ntops_rms_norm (weight of dtype or
  * F32, may be NULL; fp32 accumulation; one rounding).  Element for element
  * equal to ntops_binary(ADD) followed by ntops_rms_norm, in one pass (reads
- * x and residual once, writes residual_out and y once).  y may alias x and
+ * x and residual once, writes residual_out and y once) when the four
+ * operands' rows sit at one offset within 16 bytes and fit the one-pass
+ * kernels; otherwise it runs exactly those two calls.  y may alias x and
  * residual_out may alias residual; y and residual_out must differ. */
 NTOPS_API int ntops_add_rms_norm(int dtype, int64_t rows, int64_t cols,
                const void* x, int64_t x_row_stride,
