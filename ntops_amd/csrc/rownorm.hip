@@ -593,7 +593,9 @@ template <typename W>
 __host__ __device__ inline int64_t odd_param_bytes(int64_t cols) {
   return (cols * static_cast<int64_t>(sizeof(W)) + 15) / 16 * 16;
 }
-constexpr int64_t kOddLdsMax = 64 * 1024;
+// Their most staged-parameter LDS: under the 64 KiB a launch may take without
+// raising its limit, with room for the kernels' static reduction scratch.
+constexpr int64_t kOddLdsMax = 60 * 1024;
 
 template <typename T, typename W, int CHUNKS, int WPR>
 __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_rms_odd(

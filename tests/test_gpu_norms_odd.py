@@ -136,3 +136,20 @@ def test_rms_norm_odd_config_width():
     assert_close(got, exp, 1.6e-2, 1.6e-2, "rms_norm (16384, 4100)")
     mism = (got.view(torch.int16) != exp.view(torch.int16)).float().mean().item()
     assert mism < 1e-3, f"bit mismatch fraction {mism}"
+
+
+@pytest.mark.parametrize("cols", (7676, 7684))
+def test_layer_norm_odd_width_at_the_staging_limit(cols):
+    """bf16 rows with fp32 weight and bias staged in LDS: 7676 columns take
+    the head / pack / tail kernel at its 60 KiB staging limit (2 x 30704
+    bytes), 7684 the looped kernel just past it; both against the oracle."""
+    g = torch.Generator().manual_seed(cols)
+    x = torch.randn(33, cols, generator=g).bfloat16()
+    w = 1 + 0.05 * torch.randn(cols, generator=g)
+    b = 0.05 * torch.randn(cols, generator=g)
+    got = ntops_amd.torch.layer_norm(x.cuda(), (cols,), w.cuda(), b.cuda(), 1e-5)
+    exp = from_np(O.layer_norm(to_np(x), "bf16", cols, w.numpy(), b.numpy(), 1e-5, wb_dt="f32"), "bf16")
+    assert_close(got, exp, 1.6e-2, 1.6e-2, f"layer_norm {cols}")
+    got = ntops_amd.torch.rms_norm(x.cuda(), (cols,), w.cuda(), 1e-6)
+    exp = from_np(O.rms_norm(to_np(x), "bf16", cols, w.numpy(), 1e-6, w_dt="f32"), "bf16")
+    assert_close(got, exp, 1.6e-2, 1.6e-2, f"rms_norm {cols}")
