@@ -215,7 +215,8 @@ __global__ __launch_bounds__(256, 2) void k_flash_fwd(AttnArgs a, int nqb, int t
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   int bh, qb;
-  attn_block(blockIdx.x, total, nqb, bh, qb);
+  if (block_id() >= total) return;  // the tail of a 2-D grid (the whole block)
+  attn_block(static_cast<int>(block_id()), total, nqb, bh, qb);
   const int b = bh / a.Hq, h = bh - b * a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
   const int q0 = qb * BM;
@@ -867,7 +868,8 @@ __global__ __launch_bounds__(512, 1) void k_flash_attn(AttnArgs a, int nqb) {
 template <typename T>
 __global__ __launch_bounds__(64) void k_attn_generic(AttnArgs a) {
   const int lane = threadIdx.x;
-  const int64_t row = blockIdx.x;  // (b, h, q) linear
+  const int64_t row = block_id();  // (b, h, q) linear; blocks_2d grid
+  if (row >= static_cast<int64_t>(a.B) * a.Hq * a.Sq) return;  // the tail of the grid (the whole block)
   const int q = static_cast<int>(row % a.Sq);
   const int64_t bh = row / a.Sq;
   const int h = static_cast<int>(bh % a.Hq);
@@ -984,7 +986,7 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
       const uintptr_t mp = reinterpret_cast<uintptr_t>(a.mask);
       const int mm = a.mask_dtype < 0 ? 0
                      : (a.ms[2] % 4 == 0 && a.ms[1] % 4 == 0 && a.ms[0] % 4 == 0 && mp % (4 * esz) == 0) ? 1 : 2;
-      const dim3 grid(static_cast<unsigned>(total)), block(256);
+      const dim3 grid = blocks_2d(total), block(256);
       note_kernel("sdpa_fwd d%d mask%d es%d", a.D > 64 ? 128 : 64, mm, esz);
 #define NTOPS_FWD(DD, MM, ES) hipLaunchKernelGGL((k_flash_fwd<T, DD, MM, ES>), grid, block, 0, st, a, nqb, static_cast<int>(total))
 #define NTOPS_FWD_D(DD)                         \
@@ -1008,7 +1010,7 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.Hq * a.Sq;
   if (rows > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many rows");
   note_kernel("sdpa_generic");
-  hipLaunchKernelGGL((k_attn_generic<T>), dim3(static_cast<unsigned>(rows)), dim3(64), 0, st, a);
+  hipLaunchKernelGGL((k_attn_generic<T>), blocks_2d(rows), dim3(64), 0, st, a);
   return check_launch("sdpa");
 }
 

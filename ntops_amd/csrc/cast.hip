@@ -14,7 +14,7 @@ constexpr int kPerThread = 8;
 
 template <typename S, typename D>
 __global__ __launch_bounds__(kThreads) void k_cast_dense(const S* x, D* y, int64_t n) {
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kPerThread) + threadIdx.x;
+  const int64_t base = block_id() * (kThreads * kPerThread) + threadIdx.x;  // blocks_2d grid
   S r[kPerThread];
 #pragma unroll
   for (int u = 0; u < kPerThread; ++u) {
@@ -35,7 +35,7 @@ template <typename S, typename D>
 __global__ __launch_bounds__(kThreads) void k_cast_pack(const S* x, D* y, int64_t npack, int64_t n) {
   static_assert(sizeof(S) == sizeof(D), "same-size element types");
   constexpr int V = Pack16<S>::N;
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t p = block_id() * kThreads + threadIdx.x;  // blocks_2d grid
   if (p < npack) {
     const Pack16<S> r = load16_nt(x + p * V);
     Pack16<D> o;
@@ -43,7 +43,7 @@ __global__ __launch_bounds__(kThreads) void k_cast_pack(const S* x, D* y, int64_
     for (int i = 0; i < V; ++i) o.v[i] = convert<D>(r.v[i]);
     store16_nt(y + p * V, o);
   }
-  if (blockIdx.x == 0) {
+  if (block_id() == 0) {
     const int64_t i = npack * V + threadIdx.x;
     if (threadIdx.x < V && i < n) y[i] = convert<D>(x[i]);
   }
@@ -78,13 +78,13 @@ int launch_cast(int ndim, const int64_t* shape, const void* xv, const int64_t* x
       constexpr int V = 16 / sizeof(S);
       const int64_t npack = n / V;
       const int64_t blocks = std::max<int64_t>(1, ceil_div(npack, static_cast<int64_t>(kThreads)));
-      hipLaunchKernelGGL((k_cast_pack<S, D>), dim3(blocks), dim3(kThreads), 0, st, x, y, npack, n);
+      hipLaunchKernelGGL((k_cast_pack<S, D>), blocks_2d(blocks), dim3(kThreads), 0, st, x, y, npack, n);
       return check_launch("ntops_cast");
     }
   }
   if (dense) {
     const int64_t blocks = ceil_div(n, static_cast<int64_t>(kThreads) * kPerThread);
-    hipLaunchKernelGGL((k_cast_dense<S, D>), dim3(blocks), dim3(kThreads), 0, st, x, y, n);
+    hipLaunchKernelGGL((k_cast_dense<S, D>), blocks_2d(blocks), dim3(kThreads), 0, st, x, y, n);
   } else {
     int64_t blocks = ceil_div(n, kThreads);
     if (blocks > 65536) blocks = 65536;

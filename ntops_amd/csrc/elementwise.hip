@@ -692,7 +692,7 @@ template <typename T, typename O, typename F>
 __global__ __launch_bounds__(kThreads) void k_unary_dense(const T* x, O* y, int64_t npack,
                                                           int64_t n, F f) {
   constexpr int V = Pack16<T>::N;
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t p = block_id() * kThreads + threadIdx.x;  // blocks_2d grid
   if (p < npack) {
     const Pack16<T> r = load16_nt(x + p * V);
     O o[V];
@@ -700,7 +700,7 @@ __global__ __launch_bounds__(kThreads) void k_unary_dense(const T* x, O* y, int6
     for (int i = 0; i < V; ++i) o[i] = f(r.v[i]);
     store_out<O, V>(y + p * V, o);
   }
-  if (blockIdx.x == 0) {
+  if (block_id() == 0) {
     const int64_t i = npack * V + threadIdx.x;
     if (threadIdx.x < V && i < n) y[i] = f(x[i]);
   }
@@ -721,7 +721,7 @@ template <typename T, typename O, typename F>
 __global__ __launch_bounds__(kThreads) void k_binary_dense(const T* a, const T* b, O* y,
                                                            int64_t npack, int64_t n, F f) {
   constexpr int V = Pack16<T>::N;
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t p = block_id() * kThreads + threadIdx.x;  // blocks_2d grid
   if (p < npack) {
     const Pack16<T> ra = load16_nt(a + p * V);
     const Pack16<T> rb = load16_nt(b + p * V);
@@ -730,7 +730,7 @@ __global__ __launch_bounds__(kThreads) void k_binary_dense(const T* a, const T* 
     for (int i = 0; i < V; ++i) o[i] = f(ra.v[i], rb.v[i]);
     store_out<O, V>(y + p * V, o);
   }
-  if (blockIdx.x == 0) {
+  if (block_id() == 0) {
     const int64_t i = npack * V + threadIdx.x;
     if (threadIdx.x < V && i < n) y[i] = f(a[i], b[i]);
   }
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(kThreads) void k_binary_scalar_dense(const T* a, S 
                                                                   int64_t npack, int64_t n, F f) {
   constexpr int V = Pack16<T>::N;
   const auto bs = f.scalar_b(braw);
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t p = block_id() * kThreads + threadIdx.x;  // blocks_2d grid
   if (p < npack) {
     const Pack16<T> ra = load16_nt(a + p * V);
     O o[V];
@@ -749,7 +749,7 @@ __global__ __launch_bounds__(kThreads) void k_binary_scalar_dense(const T* a, S 
     for (int i = 0; i < V; ++i) o[i] = f.with_scalar(ra.v[i], bs);
     store_out<O, V>(y + p * V, o);
   }
-  if (blockIdx.x == 0) {
+  if (block_id() == 0) {
     const int64_t i = npack * V + threadIdx.x;
     if (threadIdx.x < V && i < n) y[i] = f.with_scalar(a[i], bs);
   }
@@ -785,7 +785,7 @@ __global__ __launch_bounds__(kThreads) void k_clamp_dense(const T* x, const T* l
                                                           T lo_s, T hi_s, T* y, int64_t npack,
                                                           int64_t n) {
   constexpr int V = Pack16<T>::N;
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t p = block_id() * kThreads + threadIdx.x;  // blocks_2d grid
   if (p < npack) {
     const Pack16<T> rx = load16_nt(x + p * V);
     Pack16<T> rl, rh;
@@ -796,7 +796,7 @@ __global__ __launch_bounds__(kThreads) void k_clamp_dense(const T* x, const T* l
     for (int i = 0; i < V; ++i) o[i] = clamp_value(rx.v[i], LO_T ? rl.v[i] : lo_s, HI_T ? rh.v[i] : hi_s);
     store_out<T, V>(y + p * V, o);
   }
-  if (blockIdx.x == 0) {
+  if (block_id() == 0) {
     const int64_t i = npack * V + threadIdx.x;
     if (threadIdx.x < V && i < n) y[i] = clamp_value(x[i], LO_T ? lo[i] : lo_s, HI_T ? hi[i] : hi_s);
   }
@@ -858,7 +858,7 @@ int launch_unary(const F& f, int ndim, const int64_t* shape, const void* xv, con
   O* y = static_cast<O*>(yv);
   if (space_is_dense(sp) && aligned16(x) && out_aligned<O, V>(y)) {
     const int64_t npack = n / V;
-    hipLaunchKernelGGL((k_unary_dense<T, O, F>), dim3(dense_blocks(npack)), dim3(kThreads), 0, st,
+    hipLaunchKernelGGL((k_unary_dense<T, O, F>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0, st,
                        x, y, npack, n, f);
   } else if (fits_int32(sp, n)) {
     hipLaunchKernelGGL((k_unary_strided<T, O, F, int32_t>), dim3(strided_blocks(n)),
@@ -898,7 +898,7 @@ int launch_binary(const F& f, int ndim, const int64_t* shape, const void* av, co
     if (n == 0) return NTOPS_OK;
     if (space_is_dense(sp) && aligned16(a) && out_aligned<O, V>(y)) {
       const int64_t npack = n / V;
-      hipLaunchKernelGGL((k_binary_scalar_dense<T, O, F, S>), dim3(dense_blocks(npack)),
+      hipLaunchKernelGGL((k_binary_scalar_dense<T, O, F, S>), blocks_2d(dense_blocks(npack)),
                          dim3(kThreads), 0, st, a, braw, y, npack, n, f);
     } else if (fits_int32(sp, n)) {
       hipLaunchKernelGGL((k_binary_scalar_strided<T, O, F, S, int32_t>), dim3(strided_blocks(n)),
@@ -918,7 +918,7 @@ int launch_binary(const F& f, int ndim, const int64_t* shape, const void* av, co
   if (n == 0) return NTOPS_OK;
   if (space_is_dense(sp) && aligned16(a) && aligned16(b) && out_aligned<O, V>(y)) {
     const int64_t npack = n / V;
-    hipLaunchKernelGGL((k_binary_dense<T, O, F>), dim3(dense_blocks(npack)), dim3(kThreads), 0, st,
+    hipLaunchKernelGGL((k_binary_dense<T, O, F>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0, st,
                        a, b, y, npack, n, f);
   } else if (fits_int32(sp, n)) {
     hipLaunchKernelGGL((k_binary_strided<T, O, F, int32_t>), dim3(strided_blocks(n)),
@@ -951,7 +951,7 @@ int launch_clamp_t(int ndim, const int64_t* shape, const T* x, const int64_t* xs
             (!LO_T || sp.stride[1][0] == 1) && (!HI_T || sp.stride[2][0] == 1);
   if (dense) {
     const int64_t npack = n / Pack16<T>::N;
-    hipLaunchKernelGGL((k_clamp_dense<T, LO_T, HI_T>), dim3(dense_blocks(npack)), dim3(kThreads),
+    hipLaunchKernelGGL((k_clamp_dense<T, LO_T, HI_T>), blocks_2d(dense_blocks(npack)), dim3(kThreads),
                        0, st, x, lo, hi, lo_s, hi_s, y, npack, n);
   } else if (fits_int32(sp, n)) {
     hipLaunchKernelGGL((k_clamp_strided<T, LO_T, HI_T, int32_t>), dim3(strided_blocks(n)),

@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void k_rope_half_vec(const T* sn, const T* cs,
   constexpr int V = Pack16<T>::N;
   const I half = static_cast<I>(a.D / 2);
   const I ppr = half / V;  // packs per half row
-  const I it = static_cast<I>(blockIdx.x) * 256 + threadIdx.x;
+  const I it = static_cast<I>(block_id()) * 256 + threadIdx.x;  // blocks_2d grid
   if (it >= items) return;
   auto body = [&](const RopeTensor& d, I li) {
     const I j = li % ppr;
@@ -130,7 +130,7 @@ template <typename T, typename I>
 __global__ __launch_bounds__(256) void k_rope_inter_vec(const T* sn, const T* cs, RopeArgs a, I items0, I items) {
   constexpr int V = Pack16<T>::N;
   const I ppr = static_cast<I>(a.D / V);
-  const I it = static_cast<I>(blockIdx.x) * 256 + threadIdx.x;
+  const I it = static_cast<I>(block_id()) * 256 + threadIdx.x;  // blocks_2d grid
   if (it >= items) return;
   auto body = [&](const RopeTensor& d, I li) {
     const I j = li % ppr;
@@ -241,21 +241,21 @@ int run_rope(const RopeArgs& a, const void* sv, const void* cv, int interleaved,
   if (half_vec || inter_vec) {
     const int64_t per_row = half_vec ? a.D / 2 / V : a.D / V;
     const int64_t items0 = rows0 * per_row, items = rows * per_row;
-    const unsigned grid = static_cast<unsigned>(ceil_div(items, 256));
+    const dim3 grid = blocks_2d(ceil_div(items, 256));
     if (items < 0x7fffffffLL) {
       using I = uint32_t;
       if (half_vec)
-        hipLaunchKernelGGL((k_rope_half_vec<T, I>), dim3(grid), dim3(256), 0, st, sn, cs, a, static_cast<I>(items0),
+        hipLaunchKernelGGL((k_rope_half_vec<T, I>), grid, dim3(256), 0, st, sn, cs, a, static_cast<I>(items0),
                            static_cast<I>(items));
       else
-        hipLaunchKernelGGL((k_rope_inter_vec<T, I>), dim3(grid), dim3(256), 0, st, sn, cs, a, static_cast<I>(items0),
+        hipLaunchKernelGGL((k_rope_inter_vec<T, I>), grid, dim3(256), 0, st, sn, cs, a, static_cast<I>(items0),
                            static_cast<I>(items));
     } else {
       using I = int64_t;
       if (half_vec)
-        hipLaunchKernelGGL((k_rope_half_vec<T, I>), dim3(grid), dim3(256), 0, st, sn, cs, a, items0, items);
+        hipLaunchKernelGGL((k_rope_half_vec<T, I>), grid, dim3(256), 0, st, sn, cs, a, items0, items);
       else
-        hipLaunchKernelGGL((k_rope_inter_vec<T, I>), dim3(grid), dim3(256), 0, st, sn, cs, a, items0, items);
+        hipLaunchKernelGGL((k_rope_inter_vec<T, I>), grid, dim3(256), 0, st, sn, cs, a, items0, items);
     }
     return check_launch("rope");
   }

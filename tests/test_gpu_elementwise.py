@@ -237,3 +237,26 @@ def test_empty_and_zero_dim():
     s = torch.tensor(1.5)
     assert_close(ntops_amd.torch.exp(s.cuda()), torch.exp(s), 1e-6, 1e-6, "0-d")
     assert_close(ntops_amd.torch.add(s.cuda(), s.cuda(), alpha=2), s + 2 * s, 1e-6, 1e-6, "0-d add")
+
+
+def test_dense_kernels_past_65536_blocks():
+    """2^28 + 11 bf16 elements: 2^25 16-byte packs, 131072 blocks of 256
+    threads -- a two-row 2-D grid (one dispatch dimension counts work-items
+    in 32 bits) -- and an 11-element tail.  silu against the oracle on the
+    head, the packs around the grid-row boundary (pack 2^24) and the tail;
+    add and the native copy bit for bit."""
+    n = (1 << 28) + 11
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(n, device="cuda", generator=g).bfloat16()
+    y = ntops_amd.torch.silu(x)
+    b = (1 << 24) * 8  # first element of grid row 1
+    for lo, hi in ((0, 4096), (b - 4096, b + 4096), (n - 4096, n)):
+        exp = from_np(O.silu(to_np(x[lo:hi].cpu()), "bf16"), "bf16")
+        assert_close(y[lo:hi], exp, *TOL_ELEMENTWISE["bf16"], f"silu [{lo}, {hi})")
+    z = ntops_amd.torch.add(x, y)
+    assert torch.equal(z, x + y)
+    del y, z
+    c = torch.empty_like(x)
+    from ntops_amd.torch.utils import _cast_into
+    _cast_into(x, c)
+    assert torch.equal(c, x)

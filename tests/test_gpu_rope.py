@@ -92,3 +92,18 @@ def test_rope_config_full_size():
         for b in range(4):
             exp = from_np(O.rotary_position_embedding(to_np(t[b : b + 1]), to_np(s), to_np(c), "bf16", False), "bf16")
             assert_equal(got[b : b + 1], exp, f"rope config {name} batch {b}")
+
+
+def test_rope_past_65536_blocks():
+    """bf16 (9, 8192, 32, 128): 18.9M items of one 16-byte pack pair, 73728
+    blocks on a 2-D grid; the first batch's first and the last batch's last
+    1024 positions against the oracle, bit for bit."""
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(9, 8192, 32, 128, device="cuda", generator=g).bfloat16()
+    s, c = tables(8192, 128, torch.bfloat16, True)
+    got = ntops_amd.torch.rotary_position_embedding(x, s.cuda(), c.cuda(), interleaved=False)
+    for b, p0 in ((0, 0), (8, 7168)):  # first and last 1024 positions
+        xs = x[b:b + 1, p0:p0 + 1024].cpu()
+        exp = from_np(O.rotary_position_embedding(to_np(xs), to_np(s[p0:p0 + 1024]), to_np(c[p0:p0 + 1024]), "bf16",
+                                                  False), "bf16")
+        assert_equal(got[b:b + 1, p0:p0 + 1024], exp, f"batch {b}")
