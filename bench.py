@@ -254,8 +254,12 @@ KERNEL_OF = {
     "div": "k_binary_dense",
     "eq": "k_binary_dense",
     "clamp": "k_clamp_dense",
+    "copy_half": "k_cast_pack",
     "rms_norm": "k_rms_vec",
     "layer_norm": "k_ln_vec",
+    "rms_norm_odd": "k_rms_odd",
+    "rms_norm_wide": "k_rms_wide",
+    "softmax_wide": "k_softmax_wide",
     "softmax": "k_softmax_vec",
     "rope": "k_rope_half_vec",
     "rope_qk": "k_rope_half_vec",
