@@ -355,9 +355,14 @@ __global__ __launch_bounds__(256) void k_ln_loop(const T* x, int64_t xs, const W
 }
 
 // ------------------------------------------------------------ wide rows --
-// Rows of more than 8192 packs (rowwide.h): the row is read once into VGPRs
-// and LDS, each pass reads it there; the weight and bias are read at their
-// use.  Row = block.
+// Parameter packs fetched ahead of their use in the wide kernels' output
+// pass (rms_norm: the weight; layer_norm: weight and bias, twice the VGPRs).
+constexpr int kWideRmsPrefetch = 2, kWideLnPrefetch = 1;
+
+// Rows of more than 8192 packs (rowwide.h): one block per CU walking rows;
+// a row is read once into VGPRs and LDS (the next one loading during the
+// output pass of the current one), each pass reads it there; the weight and
+// bias are read at their use.
 template <typename T, typename W>
 __global__ __launch_bounds__(kWideThreads) void k_rms_wide(const T* __restrict__ x, int64_t xs,
                                                            const W* __restrict__ w, T* __restrict__ y,
@@ -365,39 +370,41 @@ __global__ __launch_bounds__(kWideThreads) void k_rms_wide(const T* __restrict__
   constexpr int V = Pack16<T>::N;
   __shared__ float red[kWideWaves];
   extern __shared__ __attribute__((aligned(16))) char wsm[];
-  const int64_t row = block_id();
-  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
+  int64_t row = blockIdx.x;
+  if (row >= rows) return;
   const int npk = cols / V, t = threadIdx.x;
-  WideRow<T> d;
-  wide_load(d, x + row * xs, npk, wsm);
+  const __amdgpu_buffer_rsrc_t wr = param_rsrc<V>(w, npk);
+  // the sum of squares of a row, accumulated as its packs land
   float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < kWideRegChunks; ++c)
-#pragma unroll
-    for (int i = 0; i < V; ++i) ss = fmaf(to_f(d.r[c].v[i]), to_f(d.r[c].v[i]), ss);
-  for (int q = t; q < d.nl; q += kWideThreads) {
-    const Pack16<T> v = wide_lds_pack(d, q);
+  auto visit = [&](const Pack16<T>& v) {
 #pragma unroll
     for (int i = 0; i < V; ++i) ss = fmaf(to_f(v.v[i]), to_f(v.v[i]), ss);
-  }
-  ss = wide_reduce(ss, red, [](float a, float b) { return a + b; });
-  const float rstd = 1.0f / __fsqrt_rn(ss / static_cast<float>(cols) + eps);
-  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
-  const __amdgpu_buffer_rsrc_t wr = param_rsrc<V>(w, npk);
-  auto emit = [&](const Pack16<T>& v, int pk) {
-    ParamPack<W, V> wq;
-    wq.load(wr, pk);
-    Pack16<T> o;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float wv = w != nullptr ? wq.get(i) : 1.0f;
-      o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(v.v[i]), rstd), wv));
-    }
-    buffer_store16_nt(out, pk * 16u, o);
   };
+  WideRow<T> d;
+  wide_load(d, x + row * xs, npk, wsm, visit);
+  for (; row < rows; row += gridDim.x) {
+    const float tot = wide_reduce(ss, red, [](float a, float b) { return a + b; });
+    ss = 0.f;
+    const float rstd = 1.0f / __fsqrt_rn(tot / static_cast<float>(cols) + eps);
+    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
+    auto fetch = [&](int pk) {
+      ParamPack<W, V> wq;
+      wq.load(wr, pk);
+      return wq;
+    };
+    auto emit = [&](const Pack16<T>& v, int pk, const ParamPack<W, V>& wq) {
+      Pack16<T> o;
 #pragma unroll
-  for (int c = 0; c < kWideRegChunks; ++c) emit(d.r[c], c * kWideThreads + t);
-  for (int q = t; q < d.nl; q += kWideThreads) emit(wide_lds_pack(d, q), kWideRegPacks + q);
+      for (int i = 0; i < V; ++i) {
+        const float wv = w != nullptr ? wq.get(i) : 1.0f;
+        o.v[i] = static_cast<T>(mul_nc(mul_nc(to_f(v.v[i]), rstd), wv));
+      }
+      buffer_store16_nt(out, pk * 16u, o);
+    };
+    const bool more = row + gridDim.x < rows;
+    wide_emit_and_load<kWideRmsPrefetch>(d, more, x + (more ? row + gridDim.x : row) * xs, npk, fetch, emit,
+                                         visit);
+  }
 }
 
 template <typename T, typename W>
@@ -408,65 +415,73 @@ __global__ __launch_bounds__(kWideThreads) void k_ln_wide(const T* __restrict__ 
   constexpr int V = Pack16<T>::N;
   __shared__ float red[kWideWaves];
   extern __shared__ __attribute__((aligned(16))) char wsm[];
-  const int64_t row = block_id();
-  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
+  int64_t row = blockIdx.x;
+  if (row >= rows) return;
   const int npk = cols / V, t = threadIdx.x;
-  WideRow<T> d;
-  wide_load(d, x + row * xs, npk, wsm);
-  // register packs past the row end hold zeros: they add nothing to the sum
-  float s = 0.f;
-#pragma unroll
-  for (int c = 0; c < kWideRegChunks; ++c)
-#pragma unroll
-    for (int i = 0; i < V; ++i) s += to_f(d.r[c].v[i]);
-  for (int q = t; q < d.nl; q += kWideThreads) {
-    const Pack16<T> v = wide_lds_pack(d, q);
-#pragma unroll
-    for (int i = 0; i < V; ++i) s += to_f(v.v[i]);
-  }
-  const auto sum = [](float a, float b) { return a + b; };
-  const float mean = wide_reduce(s, red, sum) / static_cast<float>(cols);
-  float q2 = 0.f;
-#pragma unroll
-  for (int c = 0; c < kWideRegChunks; ++c) {
-    float qc = 0.f;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float dv = to_f(d.r[c].v[i]) - mean;
-      qc = fmaf(dv, dv, qc);
-    }
-    q2 += c * kWideThreads + t < npk ? qc : 0.f;
-  }
-  for (int q = t; q < d.nl; q += kWideThreads) {
-    const Pack16<T> v = wide_lds_pack(d, q);
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float dv = to_f(v.v[i]) - mean;
-      q2 = fmaf(dv, dv, q2);
-    }
-  }
-  const float var = wide_reduce(q2, red, sum) * (1.0f / static_cast<float>(cols));
-  const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
-  const float shift = -rstd * mean;
-  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
   const __amdgpu_buffer_rsrc_t wr = param_rsrc<V>(w, npk);
   const __amdgpu_buffer_rsrc_t br = param_rsrc<V>(b, npk);
-  auto emit = [&](const Pack16<T>& v, int pk) {
-    ParamPack<W, V> wq, bq;
-    wq.load(wr, pk);
-    bq.load(br, pk);
-    Pack16<T> o;
+  // the sum of a row, accumulated as its packs land
+  float s = 0.f;
+  auto visit = [&](const Pack16<T>& v) {
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float wv = w != nullptr ? wq.get(i) : 1.0f;
-      const float bv = b != nullptr ? bq.get(i) : 0.0f;
-      o.v[i] = static_cast<T>(fmaf(fmaf(to_f(v.v[i]), rstd, shift), wv, bv));
-    }
-    buffer_store16_nt(out, pk * 16u, o);
+    for (int i = 0; i < V; ++i) s += to_f(v.v[i]);
   };
+  WideRow<T> d;
+  wide_load(d, x + row * xs, npk, wsm, visit);
+  for (; row < rows; row += gridDim.x) {
+    const auto sum = [](float a, float b) { return a + b; };
+    const float mean = wide_reduce(s, red, sum) / static_cast<float>(cols);
+    s = 0.f;
+    wide_launder(d);
+    float q2 = 0.f;
 #pragma unroll
-  for (int c = 0; c < kWideRegChunks; ++c) emit(d.r[c], c * kWideThreads + t);
-  for (int q = t; q < d.nl; q += kWideThreads) emit(wide_lds_pack(d, q), kWideRegPacks + q);
+    for (int c = 0; c < kWideRegChunks; ++c) {
+      float qc = 0.f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float dv = to_f(d.r[c].v[i]) - mean;
+        qc = fmaf(dv, dv, qc);
+      }
+      q2 += c * kWideThreads + t < npk ? qc : 0.f;
+    }
+    for (int q = t; q < d.nl; q += kWideThreads) {
+      const Pack16<T> v = wide_lds_pack(d, q);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float dv = to_f(v.v[i]) - mean;
+        q2 = fmaf(dv, dv, q2);
+      }
+    }
+    const float var = wide_reduce(q2, red, sum) * (1.0f / static_cast<float>(cols));
+    wide_launder(d);
+    const float rstd = 1.0f / __fsqrt_rn(fmaxf(var, 0.f) + eps);
+    const float shift = -rstd * mean;
+    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
+    struct WB {
+      ParamPack<W, V> w, b;
+    };
+    auto fetch = [&](int pk) {
+      WB p;
+      p.w.load(wr, pk);
+      p.b.load(br, pk);
+      return p;
+    };
+    auto emit = [&](const Pack16<T>& v, int pk, const WB& p) {
+      const ParamPack<W, V>& wq = p.w;
+      const ParamPack<W, V>& bq = p.b;
+      Pack16<T> o;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float wv = w != nullptr ? wq.get(i) : 1.0f;
+        const float bv = b != nullptr ? bq.get(i) : 0.0f;
+        o.v[i] = static_cast<T>(fmaf(fmaf(to_f(v.v[i]), rstd, shift), wv, bv));
+      }
+      buffer_store16_nt(out, pk * 16u, o);
+    };
+    const bool more = row + gridDim.x < rows;
+    wide_emit_and_load<kWideLnPrefetch>(d, more, x + (more ? row + gridDim.x : row) * xs, npk, fetch, emit,
+                                        visit);
+  }
 }
 
 // ------------------------------------------- rows that are not 16-byte runs --
@@ -772,7 +787,7 @@ int run_rms(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* 
       wide_row_fits(cols / V)) {
     static bool lds_set = false;
     if (int e = wide_lds_attr(k_rms_wide<T, W>, lds_set)) return e;
-    hipLaunchKernelGGL((k_rms_wide<T, W>), blocks_2d(rows), dim3(kWideThreads), wide_lds_bytes(cols / V), st, x, xs,
+    hipLaunchKernelGGL((k_rms_wide<T, W>), dim3(wide_grid(rows)), dim3(kWideThreads), wide_lds_bytes(cols / V), st, x, xs,
                        w, y, ys, rows, static_cast<int>(cols), feps);
     return check_launch("rms_norm");
   }
@@ -824,7 +839,7 @@ int run_ln(int64_t rows, int64_t cols, const void* xv, int64_t xs, const void* w
       wrs == 0 && wide_row_fits(cols / V)) {
     static bool lds_set = false;
     if (int e = wide_lds_attr(k_ln_wide<T, W>, lds_set)) return e;
-    hipLaunchKernelGGL((k_ln_wide<T, W>), blocks_2d(rows), dim3(kWideThreads), wide_lds_bytes(cols / V), st, x, xs, w,
+    hipLaunchKernelGGL((k_ln_wide<T, W>), dim3(wide_grid(rows)), dim3(kWideThreads), wide_lds_bytes(cols / V), st, x, xs, w,
                        b, y, ys, rows, static_cast<int>(cols), feps);
     return check_launch("layer_norm");
   }

@@ -136,8 +136,9 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_softmax_vec(
   }
 }
 
-// Rows of more than 8192 packs (rowwide.h): one block per row, the row read
-// once into VGPRs and LDS; three passes over it there -- the row max, the
+// Rows of more than 8192 packs (rowwide.h): one block per CU walking rows,
+// each read once into VGPRs and LDS (the next one loading during the output
+// pass of the current one); three passes over it there -- the row max, the
 // sum of exp(x - max), the outputs exp(x - max) / sum (the exponential
 // evaluated again rather than kept: the registers hold the row itself).
 template <typename T>
@@ -147,49 +148,51 @@ __global__ __launch_bounds__(kWideThreads) void k_softmax_wide(const T* __restri
   constexpr int V = Pack16<T>::N;
   __shared__ float red[kWideWaves];
   extern __shared__ __attribute__((aligned(16))) char wsm[];
-  const int64_t row = block_id();
-  if (row >= rows) return;  // the tail of a 2-D grid (the whole block)
+  int64_t row = blockIdx.x;
+  if (row >= rows) return;
   const int npk = cols / V, t = threadIdx.x;
-  WideRow<T> d;
-  wide_load(d, x + row * xs, npk, wsm);
   const float ninf = -__builtin_huge_valf();
-  float m = ninf;
+  // the max of a row, taken as its packs land (every register pack of a
+  // wide row lies inside it)
+  float mx = ninf;
+  auto visit = [&](const Pack16<T>& v) {
 #pragma unroll
-  for (int c = 0; c < kWideRegChunks; ++c)
-    if (c * kWideThreads + t < npk)
-#pragma unroll
-      for (int i = 0; i < V; ++i) m = cmax(m, static_cast<float>(d.r[c].v[i]));
-  for (int q = t; q < d.nl; q += kWideThreads) {
-    const Pack16<T> v = wide_lds_pack(d, q);
-#pragma unroll
-    for (int i = 0; i < V; ++i) m = cmax(m, static_cast<float>(v.v[i]));
-  }
-  m = wide_reduce(m, red, [](float a, float b) { return cmax(a, b); });
-  float s = 0.f;
-#pragma unroll
-  for (int c = 0; c < kWideRegChunks; ++c) {
-    float sc = 0.f;
-#pragma unroll
-    for (int i = 0; i < V; ++i) sc += row_exp(static_cast<float>(d.r[c].v[i]) - m);
-    s += c * kWideThreads + t < npk ? sc : 0.f;
-  }
-  for (int q = t; q < d.nl; q += kWideThreads) {
-    const Pack16<T> v = wide_lds_pack(d, q);
-#pragma unroll
-    for (int i = 0; i < V; ++i) s += row_exp(static_cast<float>(v.v[i]) - m);
-  }
-  s = wide_reduce(s, red, [](float a, float b) { return a + b; });
-  const float inv = 1.0f / s;
-  const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
-  auto emit = [&](const Pack16<T>& v, int pk) {
-    Pack16<T> o;
-#pragma unroll
-    for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(row_exp(static_cast<float>(v.v[i]) - m) * inv);
-    buffer_store16_nt(out, pk * 16u, o);
+    for (int i = 0; i < V; ++i) mx = cmax(mx, static_cast<float>(v.v[i]));
   };
+  WideRow<T> d;
+  wide_load(d, x + row * xs, npk, wsm, visit);
+  for (; row < rows; row += gridDim.x) {
+    const float m = wide_reduce(mx, red, [](float a, float b) { return cmax(a, b); });
+    mx = ninf;
+    wide_launder(d);
+    float s = 0.f;
 #pragma unroll
-  for (int c = 0; c < kWideRegChunks; ++c) emit(d.r[c], c * kWideThreads + t);
-  for (int q = t; q < d.nl; q += kWideThreads) emit(wide_lds_pack(d, q), kWideRegPacks + q);
+    for (int c = 0; c < kWideRegChunks; ++c) {
+      float sc = 0.f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) sc += row_exp(static_cast<float>(d.r[c].v[i]) - m);
+      s += c * kWideThreads + t < npk ? sc : 0.f;
+    }
+    for (int q = t; q < d.nl; q += kWideThreads) {
+      const Pack16<T> v = wide_lds_pack(d, q);
+#pragma unroll
+      for (int i = 0; i < V; ++i) s += row_exp(static_cast<float>(v.v[i]) - m);
+    }
+    s = wide_reduce(s, red, [](float a, float b) { return a + b; });
+    wide_launder(d);
+    const float inv = 1.0f / s;
+    const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
+    struct None {};
+    auto fetch = [](int) { return None{}; };
+    auto emit = [&](const Pack16<T>& v, int pk, None) {
+      Pack16<T> o;
+#pragma unroll
+      for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(row_exp(static_cast<float>(v.v[i]) - m) * inv);
+      buffer_store16_nt(out, pk * 16u, o);
+    };
+    const bool more = row + gridDim.x < rows;
+    wide_emit_and_load<0>(d, more, x + (more ? row + gridDim.x : row) * xs, npk, fetch, emit, visit);
+  }
 }
 
 // One block per row, any element stride, input converted to the output dtype
@@ -326,7 +329,7 @@ int run_softmax(int64_t outer, int64_t dim, int64_t inner, const void* xv, const
             aligned16(y) && wide_row_fits(dim / V) && outer <= 0x7fffffffLL) {
           static bool lds_set = false;
           if (int e = wide_lds_attr(k_softmax_wide<To>, lds_set)) return e;
-          hipLaunchKernelGGL((k_softmax_wide<To>), blocks_2d(outer), dim3(kWideThreads), wide_lds_bytes(dim / V), st,
+          hipLaunchKernelGGL((k_softmax_wide<To>), dim3(wide_grid(outer)), dim3(kWideThreads), wide_lds_bytes(dim / V), st,
                              x, xs[0], y, ys[0], outer, static_cast<int>(dim));
           return check_launch("softmax");
         }

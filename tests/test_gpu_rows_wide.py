@@ -1,12 +1,15 @@
 """GPU parity: rows wider than the register-resident shapes (more than 8192
-16-byte packs), which one 1024-thread block per row reads once into VGPRs
+16-byte packs), which 1024-thread blocks (one per CU, each walking rows and
+loading its next row while it writes the current one) read once into VGPRs
 and LDS (rms_norm, layer_norm, softmax), against the oracle.
 
 Widths: just past the register budget (one staged pack), the 131072-element
 bf16 row, the widest staged row, and one element-pack past it (the looped
 kernels), in bf16, fp16 and fp32, with and without parameters; softmax
 also with -inf runs and a fully masked row; and the bf16 (512, 131072)
-shape on sampled rows plus its row-sum property on every row."""
+shape on sampled rows plus its row-sum property on every row; every row of
+a batch that makes each block walk two or three rows, with a partly filled
+last staged run."""
 
 import numpy as np
 import pytest
@@ -93,3 +96,25 @@ def test_wide_rows_config_512_131072():
     assert_close(s[rows], exp, 1.6e-2, 1.6e-2, "softmax (512, 131072)")
     tot = s.float().sum(-1)
     assert torch.allclose(tot, torch.ones_like(tot), atol=2e-2)
+
+
+def test_wide_rows_walked_by_each_block():
+    """549 rows (2-3 per block on a 256-CU part) of 8292 packs (100 staged:
+    one whole and one partial LDS run): every row against the oracle, so a
+    row loaded into the wrong place or a run left over from the previous row
+    fails."""
+    rows, cols = 549, (REG_PACKS + 100) * 8
+    g = torch.Generator().manual_seed(549)
+    x = (torch.randn(rows, cols, generator=g) * (1 + torch.arange(rows) % 7).unsqueeze(1)).bfloat16()
+    w = (1 + 0.05 * torch.randn(cols, generator=g)).bfloat16()
+    b = (0.05 * torch.randn(cols, generator=g)).bfloat16()
+    xg = x.cuda()
+    xn = to_np(x)
+    rtol, atol = TOL_REDUCTION["bf16"]
+    got = T.rms_norm(xg, (cols,), w.cuda(), 1e-6)
+    assert_close(got, from_np(O.rms_norm(xn, "bf16", cols, to_np(w), 1e-6), "bf16"), rtol, atol, "rms_norm walk")
+    got = T.layer_norm(xg, (cols,), w.cuda(), b.cuda(), 1e-5)
+    exp = from_np(O.layer_norm(xn, "bf16", cols, to_np(w), to_np(b), 1e-5), "bf16")
+    assert_close(got, exp, rtol, atol, "layer_norm walk")
+    got = T.softmax(xg, -1)
+    assert_close(got, from_np(O.softmax(xn, -1, "bf16"), "bf16"), rtol, atol, "softmax walk")
