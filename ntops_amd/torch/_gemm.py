@@ -41,6 +41,48 @@ def _padded_depth(a, b, k):
     return (k + unit - 1) // unit * unit
 
 
+def _kernel_layout(t, unit, other_major=True):
+    """True when operand t (A as (m, k), B as (k, n)) is in a layout the
+    matrix-core kernels read: its last axis with unit stride and rows of a
+    multiple of `unit` elements (A K-major, B N-major), or, when other_major,
+    its first axis with unit stride and columns of a multiple of `unit`
+    elements (A M-major, which also needs M % unit == 0; B K-major); a
+    contiguous axis whose length is not a multiple of `unit` is fine too (the
+    padded paths below copy it); and a 16-byte aligned start and batch
+    stride."""
+    r, c = t.shape[-2], t.shape[-1]
+    if t.data_ptr() % 16 or not (t.dim() == 2 or t.shape[0] == 1 or t.stride(0) % unit == 0):
+        return False
+    if t.stride(-1) == 1:
+        return t.stride(-2) % unit == 0 or c % unit != 0 or r == 1
+    if other_major and t.stride(-2) == 1:
+        return t.stride(-1) % unit == 0 or r % unit != 0 or c == 1
+    return False
+
+
+def _layout_copies(a, b):
+    """A and B as the matrix-core kernels can read them: an operand in
+    neither of their layouts (an M-major A whose M is not a multiple of 8,
+    an fp32 A that is not K-major, an operand with no unit-stride axis, a
+    start that is not 16-byte aligned) is copied into a fresh row-major
+    tensor by the native cast kernel, so the product leaves the generic
+    kernel.  Products too small to matter keep the operands as they are."""
+    unit = 4 if a.dtype == torch.float32 else 8
+    m, k, n = a.shape[-2], a.shape[-1], b.shape[-1]
+    if m <= unit or n <= unit or k == 0:
+        return a, b
+    m_major_ok = a.dtype != torch.float32 and m % unit == 0
+    if not _kernel_layout(a, unit, other_major=m_major_ok):
+        ac = torch.empty(a.shape, dtype=a.dtype, device=a.device)
+        _cast_into(a, ac)
+        a = ac
+    if not _kernel_layout(b, unit):
+        bc = torch.empty(b.shape, dtype=b.dtype, device=b.device)
+        _cast_into(b, bc)
+        b = bc
+    return a, b
+
+
 def _pad_last_two(t, rows, cols):
     """A new tensor of t's batch shape x (rows, cols) holding t in its leading
     corner and zeros elsewhere (copies and fills by the native cast kernel)."""
@@ -66,6 +108,8 @@ def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, what="ntops_amd.mm"):
                 f"{what}: expected all operands to have dtype {a.dtype}, got {t.dtype}"
             )
     dev = _lib.require_cuda(a, b, out, c)
+    with _DeviceGuard(dev):
+        a, b = _layout_copies(a, b)
     k = a.shape[-1]
     kp = _padded_depth(a, b, k)
     if kp is not None:

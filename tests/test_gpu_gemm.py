@@ -45,6 +45,9 @@ def expected16(m, n, k, layout, batch=1):
     rounded up to 8 columns by the wrapper, B copied N-major)."""
     if m == 1:  # a transposed (1, k) view keeps the row-major strides
         layout = "N" + layout[1]
+    if layout[0] == "T" and m % 8 and m > 8 and n > 8 and k > 0:
+        # an M-major A with M % 8 != 0 is copied row-major by the wrapper
+        layout = "N" + layout[1]
     if k > 8 and k % 8 and (layout[0] == "N" or layout[1] == "T") and n > 0:
         # the wrapper zero-extends K to a multiple of 8, both operands copied
         # into fresh row-major tensors
@@ -209,6 +212,64 @@ def test_mm_odd_k(m, n, k, dtype, layout):
     if dtype != torch.float32:
         assert _lib.last_kernel().startswith(expected16(m, n, k, layout)), _lib.last_kernel()
     check(got[rows], a[rows], b, dtype, what=f"mm odd k {layout}")
+
+
+# Operands in neither layout the matrix-core kernels read (an M-major A
+# whose M is not a multiple of 8, fp32 A that is not K-major, views with no
+# unit-stride axis or a start that is not 16-byte aligned) are copied
+# row-major by the wrapper; the product leaves the generic kernel.
+ODD_M = [(300, 256, 512), (1001, 1024, 768), (40, 512, 520), (2050, 4096, 1024)]
+
+
+@pytest.mark.parametrize("layout", ("TN", "TT"))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("m, n, k", ODD_M)
+def test_mm_m_major_odd_m(m, n, k, dtype, layout):
+    g = torch.Generator().manual_seed(7 * m + n + k)
+    a = (0.1 * torch.randn(m, k, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(k, n, generator=g)).to(dtype)
+    ag = a.t().contiguous().cuda().t()
+    bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
+    rows = tile_rows(m) if m > 1024 else list(range(m))
+    got = ntops_amd.torch.mm(ag, bg)
+    assert not _lib.last_kernel().startswith("gemm_generic"), _lib.last_kernel()
+    if dtype != torch.float32:
+        assert _lib.last_kernel().startswith(expected16(m, n, k, layout)), _lib.last_kernel()
+    check(got[rows], a[rows], b, dtype, what=f"mm m-major odd m {layout}")
+    bias = (0.1 * torch.randn(n, generator=g)).to(dtype)
+    got = ntops_amd.torch.addmm(bias.cuda(), ag, bg, beta=0.5, alpha=2.0)
+    assert not _lib.last_kernel().startswith("gemm_generic"), _lib.last_kernel()
+    check(got[rows], a[rows], b, dtype, c=bias.expand(len(rows), n), alpha=2.0, beta=0.5,
+          what=f"addmm m-major odd m {layout}")
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float32))
+def test_mm_operands_without_a_kernel_layout(dtype):
+    g = torch.Generator().manual_seed(11)
+    big_a = (0.1 * torch.randn(600, 1100, generator=g)).to(dtype)
+    big_b = (0.1 * torch.randn(520, 1040, generator=g)).to(dtype)
+    odd_rows = big_a[:, :513].contiguous()
+    views = {  # (A, B) as views of the tensors on each side
+        "no unit stride": lambda x, y, z: (x[:300, :1024:2], y[:512, ::2]),
+        "misaligned start": lambda x, y, z: (x[:300, 1:513], y[1:513, 3:515]),
+        "row stride not a multiple of 8": lambda x, y, z: (z[:300, :512], y[:512, :513]),
+    }
+    dev = (big_a.cuda(), big_b.cuda(), odd_rows.cuda())
+    for what, view in views.items():
+        a, b = view(big_a, big_b, odd_rows)
+        got = ntops_amd.torch.mm(*view(*dev))
+        assert not _lib.last_kernel().startswith("gemm_generic"), (what, _lib.last_kernel())
+        check(got, a, b, dtype, what=f"mm {what}")
+
+
+def test_bmm_m_major_odd_m():
+    g = torch.Generator().manual_seed(13)
+    a = (0.1 * torch.randn(3, 264, 203, generator=g)).bfloat16()  # (batch, k, m): A = a^T is M-major
+    b = (0.1 * torch.randn(3, 264, 256, generator=g)).bfloat16()
+    got = ntops_amd.torch.bmm(a.cuda().transpose(1, 2), b.cuda())
+    assert not _lib.last_kernel().startswith("gemm_generic"), _lib.last_kernel()
+    for i in range(3):
+        check(got[i], a[i].t(), b[i], torch.bfloat16, what="bmm m-major odd m")
 
 
 def test_bmm_odd_n():
