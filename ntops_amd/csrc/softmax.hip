@@ -138,47 +138,55 @@ __global__ __launch_bounds__(RowShape<WPR>::kThreads) void k_softmax_vec(
 
 // Rows of more than 8192 packs (rowwide.h): one block per CU walking rows,
 // each read once into VGPRs and LDS (the next one loading during the output
-// pass of the current one); three passes over it there -- the row max, the
-// sum of exp(x - max), the outputs exp(x - max) / sum (the exponential
-// evaluated again rather than kept: the registers hold the row itself).
+// pass of the current one); two passes over it there -- (max, sum of
+// exp(x - max)) merged pack by pack as the packs land, then the outputs
+// exp(x - max) / sum (the exponential evaluated again rather than kept: the
+// registers hold the row itself).
 template <typename T>
 __global__ __launch_bounds__(kWideThreads) void k_softmax_wide(const T* __restrict__ x, int64_t xs,
                                                                T* __restrict__ y, int64_t ys, int64_t rows,
                                                                int cols) {
   constexpr int V = Pack16<T>::N;
-  __shared__ float red[kWideWaves];
+  __shared__ float red_m[kWideWaves], red_s[kWideWaves];
   extern __shared__ __attribute__((aligned(16))) char wsm[];
   int64_t row = blockIdx.x;
   if (row >= rows) return;
-  const int npk = cols / V, t = threadIdx.x;
+  const int npk = cols / V;
   const float ninf = -__builtin_huge_valf();
-  // the max of a row, taken as its packs land (every register pack of a
-  // wide row lies inside it)
-  float mx = ninf;
+  // this thread's (max, sum of exp(x - max)) of a row, merged pack by pack
+  // as the packs land (every register pack of a wide row lies inside it)
+  float mx = ninf, sx = 0.f;
   auto visit = [&](const Pack16<T>& v) {
+    float f[V];
+    float pm = ninf;
 #pragma unroll
-    for (int i = 0; i < V; ++i) mx = cmax(mx, static_cast<float>(v.v[i]));
+    for (int i = 0; i < V; ++i) {
+      f[i] = static_cast<float>(v.v[i]);
+      pm = cmax(pm, f[i]);
+    }
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) ps += row_exp(f[i] - pm);
+    merge_max_sum(mx, sx, pm, ps);
   };
   WideRow<T> d;
   wide_load(d, x + row * xs, npk, wsm, visit);
   for (; row < rows; row += gridDim.x) {
-    const float m = wide_reduce(mx, red, [](float a, float b) { return cmax(a, b); });
+    // row summary: the wave's lanes, then the block's waves
+    float m = mx, s = sx;
+    wave_reduce2(m, s, [](float& a, float& b, float a2, float b2) { merge_max_sum(a, b, a2, b2); });
+    __syncthreads();  // the previous row's summaries have been read
+    if ((threadIdx.x & 63) == 0) {
+      red_m[threadIdx.x >> 6] = m;
+      red_s[threadIdx.x >> 6] = s;
+    }
+    __syncthreads();
+    m = red_m[0];
+    s = red_s[0];
+#pragma unroll
+    for (int w = 1; w < kWideWaves; ++w) merge_max_sum(m, s, red_m[w], red_s[w]);
     mx = ninf;
-    wide_launder(d);
-    float s = 0.f;
-#pragma unroll
-    for (int c = 0; c < kWideRegChunks; ++c) {
-      float sc = 0.f;
-#pragma unroll
-      for (int i = 0; i < V; ++i) sc += row_exp(static_cast<float>(d.r[c].v[i]) - m);
-      s += c * kWideThreads + t < npk ? sc : 0.f;
-    }
-    for (int q = t; q < d.nl; q += kWideThreads) {
-      const Pack16<T> v = wide_lds_pack(d, q);
-#pragma unroll
-      for (int i = 0; i < V; ++i) s += row_exp(static_cast<float>(v.v[i]) - m);
-    }
-    s = wide_reduce(s, red, [](float a, float b) { return a + b; });
+    sx = 0.f;
     wide_launder(d);
     const float inv = 1.0f / s;
     const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
