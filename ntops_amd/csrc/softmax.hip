@@ -189,13 +189,24 @@ __global__ __launch_bounds__(kWideThreads) void k_softmax_wide(const T* __restri
     sx = 0.f;
     wide_launder(d);
     const float inv = 1.0f / s;
+    // 16-bit outputs: exp(x - m) / s = 2^(x log2 e - (m log2 e + log2 s)), one
+    // fma and one exponential per element (the fp32 result's relative error,
+    // ~|x - m| * 2^-23, is far below the output's rounding)
+    constexpr float kLog2e = 1.44269504088896340736f;
+    const float c = fmaf(m, kLog2e, __builtin_amdgcn_logf(s));
     const __amdgpu_buffer_rsrc_t out = buffer_rsrc(y + row * ys, npk * 16u);
     struct None {};
     auto fetch = [](int) { return None{}; };
     auto emit = [&](const Pack16<T>& v, int pk, None) {
       Pack16<T> o;
 #pragma unroll
-      for (int i = 0; i < V; ++i) o.v[i] = static_cast<T>(row_exp(static_cast<float>(v.v[i]) - m) * inv);
+      for (int i = 0; i < V; ++i) {
+        const float xv = static_cast<float>(v.v[i]);
+        if constexpr (sizeof(T) == 2)
+          o.v[i] = static_cast<T>(__builtin_amdgcn_exp2f(fmaf(xv, kLog2e, -c)));
+        else
+          o.v[i] = static_cast<T>(row_exp(xv - m) * inv);
+      }
       buffer_store16_nt(out, pk * 16u, o);
     };
     const bool more = row + gridDim.x < rows;
