@@ -35,6 +35,11 @@
  *   ntops_gemm        <- src/ntops/torch/{mm,bmm,addmm}.py:7-18,
  *                        kernels/mm.py:54-65, kernels/bmm.py:8-43,
  *                        kernels/addmm.py:64-67
+ *   ntops_gemm_ws     <- the same interface as ntops_gemm, plus a caller-owned
+ *                        workspace that lets products whose tiles do not fill
+ *                        the chip split K (no ntops counterpart: Triton's
+ *                        autotuner picks smaller tiles instead)
+ *   ntops_gemm_workspace <- no ntops counterpart; sizes that workspace
  *   ntops_conv2d      <- src/ntops/torch/conv2d.py:8-53, kernels/conv2d.py:12-104
  *   ntops_add_rms_norm <- no ntops counterpart: the composition
  *                        rms_norm(x + residual) (torch/add.py:7-15 then
@@ -266,6 +271,24 @@ NTOPS_API int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_t
                const void* C, const int64_t* c_strides,
                double alpha, double beta,
                void* out, const int64_t* out_strides, void* stream);
+
+/* ntops_gemm with a caller-owned workspace (16-byte aligned device memory;
+ * NULL or too small: the product runs as ntops_gemm).  bf16 / fp16 products
+ * (batch 1) whose 128 x 128 tiles do not fill the GPU and whose K is long
+ * split K over up to 16 slices: fp32 partial products into the workspace,
+ * then their sum in slice order, so the result is deterministic (it differs
+ * from ntops_gemm's only by the fp32 summation order). */
+NTOPS_API int ntops_gemm_ws(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+               const void* A, const int64_t* a_strides,
+               const void* B, const int64_t* b_strides,
+               const void* C, const int64_t* c_strides,
+               double alpha, double beta,
+               void* out, const int64_t* out_strides,
+               void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of workspace ntops_gemm_ws uses for this problem on the current
+ * device (0: it would not split K). */
+NTOPS_API int64_t ntops_gemm_workspace(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K);
 
 /* ---- attention ---------------------------------------------------------- */
 /* out = softmax(q k^T * scale + mask) v for q (B, Hq, Sq, D), k and v

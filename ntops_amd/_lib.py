@@ -107,6 +107,12 @@ _SIGNATURES = {
         _i,
         [_i, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _d, _vp, _c_i64p, _vp],
     ),
+    "ntops_gemm_ws": (
+        _i,
+        [_i, _i64, _i64, _i64, _i64, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _d, _vp, _c_i64p, _vp, _i64,
+         _vp],
+    ),
+    "ntops_gemm_workspace": (_i64, [_i, _i64, _i64, _i64, _i64]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -66,6 +66,13 @@ struct GemmArgs {
   int use_c;
   int c_mode;  // epilogue's C access (kCNone / kCStrided / kCVec4 / kCRow), set by set_c_mode
   int staged;  // out is 16-byte aligned with unit column stride and N % 8 == 0
+  // Split-K (the SPLITK instantiation): block row blockIdx.y takes k in
+  // [blockIdx.y * kchunk, min(K, (blockIdx.y + 1) * kchunk)) and writes its
+  // fp32 partial tile to part + blockIdx.y * part_stride (rows of N).
+  float* part;          // the workspace (null: no split-K)
+  int64_t part_bytes;   // its size
+  int64_t part_stride;  // M * N
+  int kchunk;
   // Implicit convolution operand (used only by the CONV instantiation): B's
   // k-row kg = (c * R + r) * S + s starts at element
   // s * cv_per_s + c * cv_per_c + r * cv_per_r of the batch's B buffer, and
@@ -469,8 +476,9 @@ constexpr bool kStreamOutPanel = true;
 // kt + STAGES - 1 are issued right after the barrier that opens tile kt, so
 // an operand fetch that misses L2 has STAGES - 1 tiles of MFMA work to land.
 template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN,
-          int CONV = 0>
+          int CONV = 0, bool SPLITK = false>
 __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
+  static_assert(!SPLITK || CONV == 0, "split-K takes plain operands");
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
   constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
@@ -516,10 +524,13 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
     lb.init(B + n0, g.sb_k, (static_cast<int64_t>(g.K - 1) * g.sb_k + n_valid) * 2, wave, lane);
 
   const uint32_t smem_addr = lds_addr(smem);
+  // this block's k range (split-K: one slice of K per block row)
+  const int k_lo = SPLITK ? static_cast<int>(blockIdx.y) * g.kchunk : 0;
+  const int k_len = SPLITK ? min(g.K - k_lo, g.kchunk) : g.K;
   auto issue = [&](int stage, int k0) {
     const uint32_t base = smem_addr + static_cast<uint32_t>(stage * kStage);
-    la.issue(base, k0, m_valid, g.K);
-    lb.issue(base + kATile, k0, n_valid, g.K, &g);
+    la.issue(base, k_lo + k0, m_valid, g.K);
+    lb.issue(base + kATile, k_lo + k0, n_valid, g.K, &g);
   };
 
   f32x16 acc[TM][TN];
@@ -530,7 +541,7 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int ktiles = (g.K + BK - 1) / BK;
+  const int ktiles = (k_len + BK - 1) / BK;
   constexpr int KS = BK / 16;
   // Ping-pong: the block's waves form two groups with one wave per SIMD in
   // each (waves are placed round-robin over the 4 SIMDs).  In every phase one
@@ -596,9 +607,30 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
   for (; k < ktiles; ++k) tile(k, std::false_type{});
   if (grp == 0) block_barrier();
 
+  const int mw = m0 + wm * WTM, nw = n0 + wn * WTN;
+  if constexpr (SPLITK) {
+    // the fp32 partial tile: lane l holds row (l & 31) and 4 consecutive
+    // columns per (i, j, q), one 16-byte store each (N % 4 == 0, so the 4
+    // columns are all in or all out)
+    float* P = g.part + static_cast<int64_t>(blockIdx.y) * g.part_stride;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = mw + i * 32 + (lane & 31);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = nw + j * 32 + q * 8 + (lane >> 5) * 4;
+          if (EVEN || (m < g.M && n < g.N)) {
+            const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            *reinterpret_cast<f32x4*>(P + static_cast<int64_t>(m) * g.N + n) = v;
+          }
+        }
+    }
+    return;
+  }
   T* D = static_cast<T*>(g.D) + bat * g.sd_b;
   const T* Cp = g.use_c ? static_cast<const T*>(g.C) + bat * g.sc_b : nullptr;
-  const int mw = m0 + wm * WTM, nw = n0 + wn * WTN;
   char* ep = smem + wave * (WTM * WTN * 2);
   auto store = [&](auto cm_tag) {
     constexpr int CM = decltype(cm_tag)::value;
@@ -783,6 +815,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_panel(GemmArgs g, int seg) {
 // read as zero (buffer offsets past the extent).
 // Requires A K-major, K % 8 == 0; M/N-major B also N % 8 == 0.
 constexpr int kSkinnyMaxM = 64;
+// Rows up to which K-major products take the skinny kernel: past 32 its
+// blocks' re-reads of A (every block reads all of it) cost more than the
+// tile kernels' idle matrix rows (M = 64, N = 128256, K = 4096: 410 against
+// 245-275 µs on the 256 x 256 tiles) -- unless the 128 x 128 tiles would not
+// fill the GPU (and the product does not split K).
+constexpr int kSkinnyRouteM = 32;
+// Rows above which a product with a workspace takes the split-K tiles
+// instead of the skinny kernel (whose blocks each re-read all of A).
+constexpr int kSplitKMinM = 16;
 // Widest column slice (in 16-column groups) for MB 16-row blocks of A: the
 // partial-sum exchange (4 * J * MB KiB of LDS) stays within 32 KiB.
 constexpr int kSkinnyMaxJ(int mb) { return mb <= 2 ? 4 : 2; }
@@ -1306,6 +1347,44 @@ __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
   }
 }
 
+// ---- split-K reduction -----------------------------------------------------
+// out = alpha * (sum of the S fp32 partial tiles, in slice order) + beta * C,
+// rounded once; a thread owns 4 consecutive columns of one row (the
+// partials' 16-byte runs).  Fixed order, so the result does not depend on
+// which slice finished first.
+template <typename T, int CM>
+__global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int S) {
+  const int n4 = g.N / 4;
+  const int64_t id = block_id() * 256 + threadIdx.x;
+  if (id >= static_cast<int64_t>(g.M) * n4) return;
+  const int m = static_cast<int>(id / n4), n = static_cast<int>(id - static_cast<int64_t>(m) * n4) * 4;
+  const float* P = g.part + static_cast<int64_t>(m) * g.N + n;
+  f32x4 sum = *reinterpret_cast<const f32x4*>(P);
+  for (int z = 1; z < S; ++z) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(P + z * g.part_stride);
+    sum.x += v.x;
+    sum.y += v.y;
+    sum.z += v.z;
+    sum.w += v.w;
+  }
+  float c[4];
+  c_values<T, CM>(g, static_cast<const T*>(g.C), m, n, true, c);
+  T o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float v = g.alpha * sum[e];
+    if constexpr (CM != kCNone) v += c[e];
+    o[e] = static_cast<T>(v);
+  }
+  T* D = static_cast<T*>(g.D) + static_cast<int64_t>(m) * g.sd_m;
+  if (g.sd_n == 1 && (reinterpret_cast<uintptr_t>(D + n) & 7u) == 0) {
+    *reinterpret_cast<u32x2*>(D + n) = __builtin_bit_cast(u32x2, o);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) D[static_cast<int64_t>(n + e) * g.sd_n] = o[e];
+  }
+}
+
 // ---- host dispatch ---------------------------------------------------------
 template <typename T, int BM, int BN, int WM, int WN, int BK, int STAGES, bool AK, bool BKM, bool EVEN,
           int CONV = 0>
@@ -1388,6 +1467,63 @@ int launch_panel(const GemmArgs& g, hipStream_t st) {
   return check_launch("gemm");
 }
 
+// 128 x 128 tiles of the product that leave a quarter of the CUs idle.
+bool few_tiles128(int64_t M, int64_t N, int64_t batch) {
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+  return tiles * 4 <= static_cast<int64_t>(cu_count_cached()) * 3;
+}
+
+// Split-K for products whose 128 x 128 tiles do not fill the chip (few rows
+// times few columns, long K: decode- and prefill-sized linear layers): the
+// tiles times S slices of K make at most two blocks per CU (one round), each
+// slice at least 512 deep.  1 = no split.
+int splitk_slices(int64_t M, int64_t N, int64_t K, int* kchunk) {
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  const int64_t cus = cu_count_cached();
+  if (K < 1024 || !few_tiles128(M, N, 1)) return 1;
+  int64_t S = 2 * cus / tiles;  // whole rounds of two blocks per CU
+  S = std::min<int64_t>(std::min<int64_t>(S, K / 512), 16);
+  if (S < 2) return 1;
+  const int64_t chunk = ((K + S - 1) / S + 31) / 32 * 32;
+  *kchunk = static_cast<int>(chunk);
+  return static_cast<int>((K + chunk - 1) / chunk);
+}
+
+template <typename T, bool AK, bool BKM, bool EVEN>
+int launch_splitk_part(const GemmArgs& g, int S, hipStream_t st) {
+  constexpr int kLds = 4 * (128 + 128) * 32 * 2;
+  auto kern = k_gemm_mfma<T, 128, 128, 2, 2, 32, 4, AK, BKM, EVEN, 0, true>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLds) != hipSuccess)
+      return set_error(NTOPS_ERR_HIP, "gemm: cannot reserve %d bytes of LDS", kLds);
+    attr_set = true;
+  }
+  const int64_t tiles = static_cast<int64_t>((g.M + 127) / 128) * ((g.N + 127) / 128);
+  note_kernel("gemm_mfma 128x128 s4 %s %s %s splitk%d", AK ? "A:K" : "A:M", BKM ? "B:K" : "B:N",
+              EVEN ? "even" : "ragged", S);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(S)), dim3(256), kLds, st, g);
+  return check_launch("gemm");
+}
+
+// The S partial products into the workspace, then their ordered sum (with
+// alpha, beta * C and the one rounding) into out.
+template <typename T, bool AK, bool BKM>
+int launch_splitk(GemmArgs g, int S, hipStream_t st) {
+  const bool even = g.M % 128 == 0 && g.N % 128 == 0 && g.K % 32 == 0;
+  const int rc = even ? launch_splitk_part<T, AK, BKM, true>(g, S, st) : launch_splitk_part<T, AK, BKM, false>(g, S, st);
+  if (rc != NTOPS_OK) return rc;
+  const dim3 grid = blocks_2d(ceil_div(static_cast<int64_t>(g.M) * (g.N / 4), 256));
+  switch (g.use_c ? g.c_mode : kCNone) {
+    case kCNone: hipLaunchKernelGGL((k_gemm_splitk_reduce<T, kCNone>), grid, dim3(256), 0, st, g, S); break;
+    case kCVec4: hipLaunchKernelGGL((k_gemm_splitk_reduce<T, kCVec4>), grid, dim3(256), 0, st, g, S); break;
+    case kCRow: hipLaunchKernelGGL((k_gemm_splitk_reduce<T, kCRow>), grid, dim3(256), 0, st, g, S); break;
+    default: hipLaunchKernelGGL((k_gemm_splitk_reduce<T, kCStrided>), grid, dim3(256), 0, st, g, S); break;
+  }
+  return check_launch("gemm");
+}
+
 template <typename T, bool AK, bool BKM>
 int pick_tile(const GemmArgs& g, hipStream_t st) {
   if (g.K <= kPanelK && g.M % 128 == 0 && g.N % 128 == 0 && g.staged &&
@@ -1432,7 +1568,18 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     // K == 0 goes to the generic kernel, which never touches A or B (they may
     // be null, and an empty M/N-major operand has no valid buffer extent).
     if (g.K > 0 && (a_k || a_m) && (b_k || b_n) && d_ok && batch_ok && fits && al(g.A) && al(g.B)) {
-      if (a_k && g.M <= kSkinnyMaxM && g.batch <= 65535)
+      int kchunk = 0;
+      const int S = (g.part != nullptr && g.batch == 1 && g.M > kSplitKMinM) ? splitk_slices(g.M, g.N, g.K, &kchunk) : 1;
+      if (S > 1 && static_cast<int64_t>(S) * g.M * g.N * 4 <= g.part_bytes) {
+        g.kchunk = kchunk;
+        g.part_stride = static_cast<int64_t>(g.M) * g.N;
+        if (a_k && b_n) return launch_splitk<T, true, false>(g, S, st);
+        if (a_k && b_k) return launch_splitk<T, true, true>(g, S, st);
+        if (a_m && b_n) return launch_splitk<T, false, false>(g, S, st);
+        return launch_splitk<T, false, true>(g, S, st);
+      }
+      if (a_k && g.M <= kSkinnyMaxM && g.batch <= 65535 &&
+          (g.M <= kSkinnyRouteM || few_tiles128(g.M, g.N, g.batch)))
         return b_k ? launch_skinny<T, true>(g, st) : launch_skinny<T, false>(g, st);
       if (a_k && b_n) return pick_tile<T, true, false>(g, st);
       if (a_k && b_k) return pick_tile<T, true, true>(g, st);
@@ -1609,11 +1756,10 @@ namespace {
 
 using namespace ntops;
 
-extern "C" int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
-                          const void* A, const int64_t* a_strides, const void* B,
-                          const int64_t* b_strides, const void* C, const int64_t* c_strides,
-                          double alpha, double beta, void* out, const int64_t* out_strides,
-                          void* stream) {
+static int gemm_entry(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
+                      const int64_t* a_strides, const void* B, const int64_t* b_strides, const void* C,
+                      const int64_t* c_strides, double alpha, double beta, void* out, const int64_t* out_strides,
+                      void* workspace, int64_t workspace_bytes, void* stream) {
   if (batch < 0 || M < 0 || N < 0 || K < 0) return set_error(NTOPS_ERR_INVALID, "gemm: negative size");
   if (batch > 0x7fffffffLL || M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
     return set_error(NTOPS_ERR_UNSUPPORTED, "gemm: size exceeds int32");
@@ -1621,7 +1767,7 @@ extern "C" int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_
   if (out == nullptr || out_strides == nullptr || a_strides == nullptr || b_strides == nullptr)
     return set_error(NTOPS_ERR_INVALID, "gemm: null pointer");
   if (K > 0 && (A == nullptr || B == nullptr)) return set_error(NTOPS_ERR_INVALID, "gemm: null operand");
-  GemmArgs g;
+  GemmArgs g{};
   g.A = A;
   g.B = B;
   g.D = out;
@@ -1655,9 +1801,40 @@ extern "C" int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_
     g.sc_b = g.sc_m = g.sc_n = 0;
   }
   set_c_mode(g);
+  // the workspace serves split-K only when 16-byte aligned
+  if (workspace != nullptr && workspace_bytes > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
+    g.part = static_cast<float*>(workspace);
+    g.part_bytes = workspace_bytes;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   return dispatch_float16_32(dtype, "gemm", [&](auto tag) {
     using T = decltype(tag);
     return run_gemm<T>(g, st);
   });
+}
+
+extern "C" int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
+                          const int64_t* a_strides, const void* B, const int64_t* b_strides, const void* C,
+                          const int64_t* c_strides, double alpha, double beta, void* out,
+                          const int64_t* out_strides, void* stream) {
+  return gemm_entry(dtype, batch, M, N, K, A, a_strides, B, b_strides, C, c_strides, alpha, beta, out, out_strides,
+                    nullptr, 0, stream);
+}
+
+extern "C" int ntops_gemm_ws(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
+                             const int64_t* a_strides, const void* B, const int64_t* b_strides, const void* C,
+                             const int64_t* c_strides, double alpha, double beta, void* out,
+                             const int64_t* out_strides, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (workspace_bytes < 0) return set_error(NTOPS_ERR_INVALID, "gemm: negative workspace size");
+  return gemm_entry(dtype, batch, M, N, K, A, a_strides, B, b_strides, C, c_strides, alpha, beta, out, out_strides,
+                    workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t ntops_gemm_workspace(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K) {
+  if ((dtype != NTOPS_BF16 && dtype != NTOPS_F16) || batch != 1 || M <= kSplitKMinM || N <= 0 || K <= 0 ||
+      M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
+    return 0;
+  int kchunk = 0;
+  const int S = splitk_slices(M, N, K, &kchunk);
+  return S > 1 ? static_cast<int64_t>(S) * M * N * 4 : 0;
 }

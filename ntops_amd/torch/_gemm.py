@@ -146,9 +146,14 @@ def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, what="ntops_amd.mm"):
     m, k = a.shape[-2], a.shape[-1]
     n = b.shape[-1]
     lib = _lib.load()
+    dt = _lib.dtype_code(a.dtype)
     with _DeviceGuard(dev):
-        rc = lib.ntops_gemm(
-            _lib.dtype_code(a.dtype),
+        # products that would not fill the GPU split K through a workspace
+        # (fp32 partial products, summed in a fixed order)
+        ws_bytes = lib.ntops_gemm_workspace(dt, batch, m, n, k)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+        rc = lib.ntops_gemm_ws(
+            dt,
             batch,
             m,
             n,
@@ -163,6 +168,8 @@ def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, what="ntops_amd.mm"):
             float(beta),
             out.data_ptr(),
             _lib.i64_array(_strides3(out)),
+            ws.data_ptr() if ws is not None else None,
+            ws_bytes,
             _lib.stream_of(out),
         )
     _lib.check(rc, what)

@@ -42,7 +42,8 @@ def expected16(m, n, k, layout, batch=1):
     aligned) operands in `layout` ("N" = row-major, "T" = transposed view):
     the matrix-core kernels need one unit-stride axis per operand with 8-element
     multiples, and an output with N % 4 == 0 (an N that would break either is
-    rounded up to 8 columns by the wrapper, B copied N-major)."""
+    rounded up to 8 columns by the wrapper, B copied N-major); products whose
+    tiles would not fill the GPU split K."""
     if m == 1:  # a transposed (1, k) view keeps the row-major strides
         layout = "N" + layout[1]
     if layout[0] == "T" and m % 8 and m > 8 and n > 8 and k > 0:
@@ -62,7 +63,11 @@ def expected16(m, n, k, layout, batch=1):
     b_k = layout[1] == "T" and k % 8 == 0
     if k == 0 or not (a_k or a_m) or not (b_k or b_n) or n % 4:
         return "gemm_generic"
-    if a_k and m <= 64:
+    if batch == 1 and _lib.load().ntops_gemm_workspace(_lib.dtype_code(torch.bfloat16), 1, m, n, k) > 0:
+        return "gemm_mfma 128x128 "  # split K through the wrapper's workspace
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    few_tiles = -(-m // 128) * -(-n // 128) * batch * 4 <= cus * 3
+    if a_k and (m <= 32 or (m <= 64 and few_tiles)):
         return "gemm_skinny "
     if k <= 128 and m % 128 == 0 and n % 128 == 0:
         return "gemm_panel "
@@ -270,6 +275,66 @@ def test_bmm_m_major_odd_m():
     assert not _lib.last_kernel().startswith("gemm_generic"), _lib.last_kernel()
     for i in range(3):
         check(got[i], a[i].t(), b[i], torch.bfloat16, what="bmm m-major odd m")
+
+
+# Products whose 128 x 128 tiles do not fill the GPU (few rows, long K:
+# decode- and prefill-sized linear layers) split K through the wrappers'
+# workspace: fp32 partial products summed in a fixed order.
+SPLIT_K = [(64, 4096, 4096), (128, 14336, 4096), (100, 1000, 8200), (48, 4096, 14336), (256, 1024, 2048),
+           (17, 2048, 4096)]
+
+
+@pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+@pytest.mark.parametrize("m, n, k", SPLIT_K)
+def test_mm_split_k(m, n, k, dtype, layout):
+    g = torch.Generator().manual_seed(m + 5 * n + k)
+    a = (0.1 * torch.randn(m, k, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(k, n, generator=g)).to(dtype)
+    ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
+    bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
+    splits = _lib.load().ntops_gemm_workspace(_lib.dtype_code(dtype), 1, m, n, k) > 0
+    got = ntops_amd.torch.mm(ag, bg)
+    kern = _lib.last_kernel()
+    assert ("splitk" in kern) == splits, kern
+    check(got, a, b, dtype, what=f"mm split-k {layout} [{kern}]")
+    again = ntops_amd.torch.mm(ag, bg)
+    assert torch.equal(got, again), "split-K result depends on the run"
+    bias = (0.1 * torch.randn(n, generator=g)).to(dtype)
+    got = ntops_amd.torch.addmm(bias.cuda(), ag, bg, beta=0.5, alpha=2.0)
+    check(got, a, b, dtype, c=bias.expand(m, n), alpha=2.0, beta=0.5, what=f"addmm split-k {layout}")
+    cfull = (0.1 * torch.randn(m, n, generator=g)).to(dtype)
+    got = ntops_amd.torch.addmm(cfull.cuda(), ag, bg, beta=-1.5, alpha=0.5)
+    check(got, a, b, dtype, c=cfull, alpha=0.5, beta=-1.5, what=f"addmm split-k full C {layout}")
+
+
+def test_gemm_split_k_through_the_c_abi():
+    """ntops_gemm_ws with the workspace ntops_gemm_workspace asks for, with a
+    workspace one byte short (then it runs unsplit), and with none; strided
+    output rows."""
+    lib = _lib.load()
+    m, n, k = 96, 2048, 6144
+    g = torch.Generator().manual_seed(3)
+    a = (0.1 * torch.randn(m, k, generator=g)).bfloat16()
+    b = (0.1 * torch.randn(k, n, generator=g)).bfloat16()
+    ag, bg = a.cuda(), b.cuda()
+    need = lib.ntops_gemm_workspace(_lib.dtype_code(torch.bfloat16), 1, m, n, k)
+    assert need > 0
+    outs = []
+    for size, expect in ((need, True), (need - 1, False), (0, False)):
+        big = torch.zeros(m, n + 64, dtype=torch.bfloat16, device="cuda")
+        out = big[:, 32:32 + n]
+        ws = torch.empty(max(size, 1), dtype=torch.uint8, device="cuda")
+        rc = lib.ntops_gemm_ws(_lib.dtype_code(torch.bfloat16), 1, m, n, k,
+                               ag.data_ptr(), _lib.i64_array((0, k, 1)), bg.data_ptr(), _lib.i64_array((0, n, 1)),
+                               None, None, 1.0, 0.0, out.data_ptr(), _lib.i64_array((0, n + 64, 1)),
+                               ws.data_ptr() if size else None, size, _lib.stream_of(out))
+        _lib.check(rc, "ntops_gemm_ws")
+        assert ("splitk" in _lib.last_kernel()) == expect, _lib.last_kernel()
+        torch.cuda.synchronize()
+        assert big[:, :32].abs().sum() == 0 and big[:, 32 + n:].abs().sum() == 0
+        check(out, a, b, torch.bfloat16, what=f"ntops_gemm_ws {size}")
+        outs.append(out.clone())
 
 
 def test_bmm_odd_n():
