@@ -63,10 +63,11 @@ def expected16(m, n, k, layout, batch=1):
     b_k = layout[1] == "T" and k % 8 == 0
     if k == 0 or not (a_k or a_m) or not (b_k or b_n) or n % 4:
         return "gemm_generic"
-    if batch == 1 and _lib.load().ntops_gemm_workspace(_lib.dtype_code(torch.bfloat16), 1, m, n, k) > 0:
-        return "gemm_mfma 128x128 "  # split K through the wrapper's workspace
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    few_tiles = -(-m // 128) * -(-n // 128) * batch * 4 <= cus * 3
+    tiles = -(-m // 128) * -(-n // 128) * batch
+    few_tiles = tiles * 4 <= cus * 3
+    if batch == 1 and (m > 16 or not a_k) and k >= 1024 and few_tiles and min(2 * cus // tiles, k // 512) >= 2:
+        return "gemm_mfma 128x128 "  # split K through the wrapper's workspace
     if a_k and (m <= 32 or (m <= 64 and few_tiles)):
         return "gemm_skinny "
     if k <= 128 and m % 128 == 0 and n % 128 == 0:
@@ -277,11 +278,12 @@ def test_bmm_m_major_odd_m():
         check(got[i], a[i].t(), b[i], torch.bfloat16, what="bmm m-major odd m")
 
 
-# Products whose 128 x 128 tiles do not fill the GPU (few rows, long K:
-# decode- and prefill-sized linear layers) split K through the wrappers'
-# workspace: fp32 partial products summed in a fixed order.
+# Products whose 128 x 128 tiles (or, up to 16 rows, skinny column slices)
+# do not fill the GPU (few rows, long K: decode- and prefill-sized linear
+# layers) split K through the wrappers' workspace: fp32 partial products
+# summed in a fixed order.
 SPLIT_K = [(64, 4096, 4096), (128, 14336, 4096), (100, 1000, 8200), (48, 4096, 14336), (256, 1024, 2048),
-           (17, 2048, 4096)]
+           (17, 2048, 4096), (1, 4096, 14336), (16, 4096, 14336), (8, 14336, 4096), (3, 1000, 8200)]
 
 
 @pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
@@ -293,7 +295,10 @@ def test_mm_split_k(m, n, k, dtype, layout):
     b = (0.1 * torch.randn(k, n, generator=g)).to(dtype)
     ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
     bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
-    splits = _lib.load().ntops_gemm_workspace(_lib.dtype_code(dtype), 1, m, n, k) > 0
+    # (an M-major A of 2-7 rows keeps its layout and takes the generic kernel;
+    # a transposed (1, k) view is K-major)
+    splits = _lib.load().ntops_gemm_workspace(_lib.dtype_code(dtype), 1, m, n, k) > 0 and not (
+        layout[0] == "T" and 1 < m < 8)
     got = ntops_amd.torch.mm(ag, bg)
     kern = _lib.last_kernel()
     assert ("splitk" in kern) == splits, kern
