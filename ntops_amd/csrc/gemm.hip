@@ -838,7 +838,7 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-template <typename T, bool BKM, int MB, int J, int NW, bool SPLIT = false>
+template <typename T, bool BKM, int MB, int J, int NW>
 __global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmArgs g) {
   constexpr int U = MB + J <= 3 ? 8 : 4, NB = 16 * J;
   __shared__ float red[NW][J][MB][4][64];
@@ -853,10 +853,6 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmArgs g) {
   const int bat = blockIdx.y;
   const int nv = min(NB, g.N - n0);
   const int r16 = lane & 15, kq = (lane >> 4) * 8;
-  // this block's k range (split: slice blockIdx.z of kchunk; k past it reads
-  // as zero)
-  const int k_lo = SPLIT ? static_cast<int>(blockIdx.z) * g.kchunk : 0;
-  const int k_hi = SPLIT ? min(g.K, k_lo + g.kchunk) : g.K;
 
   const uint16_t* A = static_cast<const uint16_t*>(g.A) + bat * g.sa_b;
   const uint16_t* B = static_cast<const uint16_t*>(g.B) + bat * g.sb_b;
@@ -895,21 +891,21 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmArgs g) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[j][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int s0 = wave; k_lo + s0 * 32 < k_hi; s0 += NW * U) {
+  for (int s0 = wave; s0 * 32 < g.K; s0 += NW * U) {
     u32x4 bq[U][J], aq[U][MB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k0 = k_lo + (s0 + NW * u) * 32;
+      const int k0 = (s0 + NW * u) * 32;
 #pragma unroll
       for (int j = 0; j < J; ++j) {
-        const bool b_ok = b_col_ok[j] && k0 + b_krow[j] < k_hi;
+        const bool b_ok = b_col_ok[j] && k0 + b_krow[j] < g.K;
         bq[u][j] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                        rb, b_ok ? b_off[j] + static_cast<uint32_t>(k0) * b_kstep : kOOB, 0, 0));
       }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const bool a_ok = mb * 16 + r16 < g.M && k0 + kq < k_hi;
+        const bool a_ok = mb * 16 + r16 < g.M && k0 + kq < g.K;
         aq[u][mb] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, a_ok ? a_off[mb] + k0 * 2u : kOOB, 0, 0));
       }
@@ -968,11 +964,6 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmArgs g) {
         float v = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) v += red[w][j][mb][r][lane];
-        if constexpr (SPLIT) {
-          // the slice's fp32 partial (alpha, C and the rounding come with the sum)
-          g.part[blockIdx.z * g.part_stride + static_cast<int64_t>(m) * g.N + n] = v;
-          continue;
-        }
         v *= g.alpha;
         if (Cp != nullptr) v += g.beta * static_cast<float>(Cp[m * g.sc_m + n * g.sc_n]);
         D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = static_cast<T>(v);
@@ -1008,52 +999,10 @@ int skinny_j(int64_t M, int64_t N, int64_t batch) {
   return 1;
 }
 
-// K slices for a skinny product of at most 16 rows (batch 1) whose column
-// slices give fewer than four blocks per CU: up to 8, each at least 2048
-// deep (a block keeps 4 waves x 8 steps of 32 k in flight).  1 = no split.
-int skinny_slices(int64_t M, int64_t N, int64_t K, int* kchunk) {
-  if (M > 16 || K < 4096) return 1;
-  const int64_t blocks = (N + 16 * skinny_j(M, N, 1) - 1) / (16 * skinny_j(M, N, 1));
-  int64_t S = 4 * static_cast<int64_t>(cu_count_cached()) / blocks;
-  S = std::min<int64_t>(std::min<int64_t>(S, K / 2048), 8);
-  if (S < 2) return 1;
-  const int64_t chunk = ((K + S - 1) / S + 31) / 32 * 32;
-  *kchunk = static_cast<int>(chunk);
-  return static_cast<int>((K + chunk - 1) / chunk);
-}
-
-template <typename T>
-int launch_splitk_reduce(const GemmArgs& g, int S, hipStream_t st);
-
-// A skinny product of at most 16 rows split over S slices of K: fp32
-// partials into the workspace, then their ordered sum.
-template <typename T, bool BKM>
-int launch_skinny_split(GemmArgs g, int S, int kchunk, hipStream_t st) {
-  const int j = skinny_j(g.M, g.N, 1);
-  g.kchunk = kchunk;
-  g.part_stride = static_cast<int64_t>(g.M) * g.N;
-  note_kernel("gemm_skinny m16 n%d %s splitk%d", 16 * j, BKM ? "B:K" : "B:N", S);
-  const dim3 grid(static_cast<unsigned>((g.N + 16 * j - 1) / (16 * j)), 1, static_cast<unsigned>(S));
-  if (j == 4)
-    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 1, 4, 4, true>), grid, dim3(256), 0, st, g);
-  else if (j == 2)
-    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 1, 2, 4, true>), grid, dim3(256), 0, st, g);
-  else
-    hipLaunchKernelGGL((k_gemm_skinny<T, BKM, 1, 1, 4, true>), grid, dim3(256), 0, st, g);
-  if (int rc = check_launch("gemm")) return rc;
-  return launch_splitk_reduce<T>(g, S, st);
-}
-
 template <typename T, bool BKM>
 int launch_skinny(const GemmArgs& g, hipStream_t st) {
   const int mb = (g.M + 15) / 16;
   const int j = skinny_j(g.M, g.N, g.batch);
-  if (g.part != nullptr && g.batch == 1) {
-    int kchunk = 0;
-    const int S = skinny_slices(g.M, g.N, g.K, &kchunk);
-    if (S > 1 && static_cast<int64_t>(S) * g.M * g.N * 4 <= g.part_bytes)
-      return launch_skinny_split<T, BKM>(g, S, kchunk, st);
-  }
   if (mb == 1) return launch_skinny_mb<T, BKM, 1>(g, st, j);
   if (mb == 2) return launch_skinny_mb<T, BKM, 2>(g, st, j);
   if (mb == 3) return launch_skinny_mb<T, BKM, 3>(g, st, j);
@@ -1626,8 +1575,7 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     // be null, and an empty M/N-major operand has no valid buffer extent).
     if (g.K > 0 && (a_k || a_m) && (b_k || b_n) && d_ok && batch_ok && fits && al(g.A) && al(g.B)) {
       int kchunk = 0;
-      // (up to kSplitKMinM rows a K-major A takes the skinny kernel, which
-      // splits K itself)
+      // (up to kSplitKMinM rows a K-major A takes the skinny kernel)
       const int S = (g.part != nullptr && g.batch == 1 && (g.M > kSplitKMinM || !a_k))
                         ? splitk_slices(g.M, g.N, g.K, &kchunk)
                         : 1;
@@ -1895,8 +1843,9 @@ extern "C" int64_t ntops_gemm_workspace(int dtype, int64_t batch, int64_t M, int
   if ((dtype != NTOPS_BF16 && dtype != NTOPS_F16) || batch != 1 || M <= 0 || N <= 0 || K <= 0 ||
       M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
     return 0;
-  // the larger of the two splits (which one runs depends on A's layout)
+  // (a K-major A of up to kSplitKMinM rows takes the skinny kernel instead
+  // and leaves the workspace unused)
   int kchunk = 0;
-  const int S = std::max(splitk_slices(M, N, K, &kchunk), M <= kSplitKMinM ? skinny_slices(M, N, K, &kchunk) : 1);
+  const int S = splitk_slices(M, N, K, &kchunk);
   return S > 1 ? static_cast<int64_t>(S) * M * N * 4 : 0;
 }

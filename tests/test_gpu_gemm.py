@@ -278,10 +278,10 @@ def test_bmm_m_major_odd_m():
         check(got[i], a[i].t(), b[i], torch.bfloat16, what="bmm m-major odd m")
 
 
-# Products whose 128 x 128 tiles (or, up to 16 rows, skinny column slices)
-# do not fill the GPU (few rows, long K: decode- and prefill-sized linear
-# layers) split K through the wrappers' workspace: fp32 partial products
-# summed in a fixed order.
+# Products whose 128 x 128 tiles do not fill the GPU (few rows, long K:
+# decode- and prefill-sized linear layers) split K through the wrappers'
+# workspace: fp32 partial products summed in a fixed order.  Up to 16 rows
+# a K-major A keeps the skinny kernel.
 SPLIT_K = [(64, 4096, 4096), (128, 14336, 4096), (100, 1000, 8200), (48, 4096, 14336), (256, 1024, 2048),
            (17, 2048, 4096), (1, 4096, 14336), (16, 4096, 14336), (8, 14336, 4096), (3, 1000, 8200)]
 
@@ -295,10 +295,11 @@ def test_mm_split_k(m, n, k, dtype, layout):
     b = (0.1 * torch.randn(k, n, generator=g)).to(dtype)
     ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
     bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
-    # (an M-major A of 2-7 rows keeps its layout and takes the generic kernel;
-    # a transposed (1, k) view is K-major)
-    splits = _lib.load().ntops_gemm_workspace(_lib.dtype_code(dtype), 1, m, n, k) > 0 and not (
-        layout[0] == "T" and 1 < m < 8)
+    # (a K-major A of at most 16 rows takes the skinny kernel, an M-major A of
+    # 2-7 rows the generic one; a transposed (1, k) view is K-major)
+    a_kmajor = layout[0] == "N" or m == 1
+    splits = (_lib.load().ntops_gemm_workspace(_lib.dtype_code(dtype), 1, m, n, k) > 0
+              and (m > 16 or not a_kmajor) and not (layout[0] == "T" and 1 < m < 8))
     got = ntops_amd.torch.mm(ag, bg)
     kern = _lib.last_kernel()
     assert ("splitk" in kern) == splits, kern
