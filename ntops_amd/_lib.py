@@ -139,8 +139,8 @@ def load():
 
 
 def i64_array(values):
-    values = tuple(int(v) for v in values)
-    return (ctypes.c_int64 * max(len(values), 1))(*values)
+    """The sizes or strides `values` (Python ints) as an int64_t[] argument."""
+    return (ctypes.c_int64 * (len(values) or 1))(*values)
 
 
 def dtype_code(dtype):
@@ -150,7 +150,14 @@ def dtype_code(dtype):
         raise TypeError(f"ntops_amd: unsupported dtype {dtype}") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(tensor):
+    """torch's current HIP stream on tensor's device (the raw handle; torch's
+    Stream object costs microseconds of host time per call to build)."""
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(tensor.device.index))
     return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
 
 

@@ -61,6 +61,28 @@ def _get_matmul_input_precision():
 # --------------------------------------------------------------- helpers --
 
 
+_get_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+
+
+def _broadcast_shape(a, b):
+    """torch.broadcast_shapes(a, b) for two concrete shapes, without its
+    symbolic-shape machinery (tens of microseconds of host time per call)."""
+    if a == b:
+        return a
+    n = max(len(a), len(b))
+    pa = (1,) * (n - len(a)) + tuple(a)
+    pb = (1,) * (n - len(b)) + tuple(b)
+    out = []
+    for x, y in zip(pa, pb):
+        if x != y and x != 1 and y != 1:
+            raise RuntimeError(
+                f"shape mismatch: objects cannot be broadcast to a single shape.  Mismatch is between "
+                f"{tuple(a)} and {tuple(b)}"
+            )
+        out.append(y if x == 1 else x)
+    return torch.Size(out)
+
+
 class _DeviceGuard:
     """Makes `device` current for the duration of a library call."""
 
@@ -70,7 +92,7 @@ class _DeviceGuard:
 
     def __enter__(self):
         idx = self.device.index if self.device.index is not None else 0
-        cur = torch.cuda.current_device()
+        cur = _get_device()
         if cur != idx:
             self.prev = cur
             torch.cuda.set_device(idx)
@@ -112,6 +134,11 @@ def _to_dtype(t, dtype):
     return _cast_into(t, out)
 
 
+def _expand_to(t, shape):
+    """t broadcast to `shape` (t itself when it already has that shape)."""
+    return t if t.shape == shape else t.expand(shape)
+
+
 def _contiguous(t):
     """A row-major copy of t made by the native copy kernel (t if already)."""
     if t.is_contiguous():
@@ -130,10 +157,18 @@ def _norm_param(param, input, nd, dtype, per_row=False):
     broadcasting inside the normalized dims), else a contiguous copy of all
     rows and row stride cols (always so with per_row).  Returns (tensor,
     row_stride); (None, 0) for an empty input."""
-    pe = param.expand_as(input)
     if input.numel() == 0:
+        param.expand_as(input)  # raises for a shape that does not broadcast
         return None, 0
     lead = input.dim() - nd
+    if (
+        not per_row
+        and param.dtype == dtype
+        and param.shape == input.shape[lead:]
+        and param.is_contiguous()
+    ):
+        return param, 0  # the usual case: one contiguous row of the normalized dims
+    pe = param.expand_as(input)
     if not per_row and all(pe.shape[i] == 1 or pe.stride(i) == 0 for i in range(lead)):
         row = pe[(0,) * lead] if lead else pe
         return _contiguous(_to_dtype(row, dtype)), 0
@@ -214,7 +249,7 @@ def _launch2(entry, op, dtype, shape, a, other, other_is_tensor, res, what, alph
     `dtype` broadcast to `shape`, or a Python number)."""
     lib = _lib.load()
     if other_is_tensor:
-        b = other.expand(shape)
+        b = other if other.shape == shape else other.expand(shape)
         b_ptr, b_strides, b_f, b_i = b.data_ptr(), _strides(b), 0.0, 0
     else:
         b_ptr, b_strides = None, None
@@ -238,10 +273,10 @@ def _binary(op, input, other, alpha, out, what, compute_dtype=None):
     if compute_dtype is not None:
         result_dtype = compute_dtype(result_dtype)
     dev = _lib.require_cuda(input, other if other_is_tensor else None)
-    shape = torch.broadcast_shapes(input.shape, other.shape) if other_is_tensor else input.shape
+    shape = _broadcast_shape(input.shape, other.shape) if other_is_tensor else input.shape
     target, res = _prepare_out(out, shape, result_dtype, dev, like=input)
 
-    a = _to_dtype(input, result_dtype).expand(shape)
+    a = _expand_to(_to_dtype(input, result_dtype), shape)
     is_float = result_dtype.is_floating_point
     if alpha is None:
         alpha_f, alpha_i = 1.0, 1
@@ -267,9 +302,9 @@ def _compare(op, input, other, out, what):
     bool, like torch (the reference writes into a tensor of input's dtype)."""
     other, other_is_tensor, common = _split_other(input, other, what)
     dev = _lib.require_cuda(input, other if other_is_tensor else None)
-    shape = torch.broadcast_shapes(input.shape, other.shape) if other_is_tensor else input.shape
+    shape = _broadcast_shape(input.shape, other.shape) if other_is_tensor else input.shape
     target, res = _prepare_out(out, shape, torch.bool, dev)
-    a = _to_dtype(input, common).expand(shape)
+    a = _expand_to(_to_dtype(input, common), shape)
     with _DeviceGuard(dev):
         b = _to_dtype(other, common) if other_is_tensor else other
         _launch2("compare", op, common, shape, a, b, other_is_tensor, res, what)

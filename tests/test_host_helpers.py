@@ -1,0 +1,57 @@
+"""CPU checks of the torch wrappers' host-side helpers that replace torch
+utilities on the launch path (they run on every call, so they avoid
+torch's slower general forms): two-shape broadcasting and the int64 array
+argument of the C ABI."""
+
+import ctypes
+
+import pytest
+import torch
+
+from ntops_amd import _lib
+from ntops_amd.torch.utils import _broadcast_shape, _expand_to
+
+
+@pytest.mark.parametrize(
+    "a, b",
+    [
+        ((16, 64), (16, 64)),
+        ((16, 64), (64,)),
+        ((64,), (16, 64)),
+        ((4, 1, 8), (3, 1)),
+        ((1,), (2, 3, 4)),
+        ((), (5, 6)),
+        ((5, 6), ()),
+        ((0, 3), (1, 3)),
+        ((2, 1, 0), (7, 1)),
+        ((1, 1), (1,)),
+    ],
+)
+def test_broadcast_shape_matches_torch(a, b):
+    got = _broadcast_shape(torch.Size(a), torch.Size(b))
+    assert isinstance(got, torch.Size)
+    assert got == torch.broadcast_shapes(a, b)
+
+
+@pytest.mark.parametrize("a, b", [((16, 64), (16, 63)), ((3,), (4,)), ((2, 3), (3, 2)), ((0,), (2,))])
+def test_broadcast_shape_rejects_like_torch(a, b):
+    with pytest.raises(RuntimeError):
+        torch.broadcast_shapes(a, b)
+    with pytest.raises(RuntimeError, match="cannot be broadcast"):
+        _broadcast_shape(torch.Size(a), torch.Size(b))
+
+
+def test_expand_to_keeps_equal_shapes_and_broadcasts_others():
+    t = torch.arange(6.0).reshape(2, 3)
+    assert _expand_to(t, torch.Size((2, 3))) is t
+    e = _expand_to(torch.arange(3.0), torch.Size((2, 3)))
+    assert e.shape == (2, 3) and e.stride() == (0, 1)
+    assert torch.equal(e, torch.arange(3.0).expand(2, 3))
+
+
+def test_i64_array_holds_the_values():
+    for values in ((), (7,), torch.Size([4, 4096]), (-3, 2**40, 0)):
+        arr = _lib.i64_array(values)
+        assert isinstance(arr, ctypes.Array)
+        assert list(arr)[: len(values)] == list(values)
+        assert len(arr) == max(len(values), 1)
