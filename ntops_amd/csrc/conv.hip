@@ -32,11 +32,14 @@
 //  * GEMM path (when C * R * S and K are large enough to feed the matrix
 //    cores): the input of a chunk of images is unfolded into a caller-owned
 //    workspace col[n][c * R * S + r * S + s][p * Q + q] (k-rows padded to a
-//    multiple of 8 pixels), then ntops_gemm computes, per image,
-//    out_n = W (K x CRS) . col_n (CRS x PQ) + bias, with W shared across the
+//    multiple of 8 pixels; CRS padded to KP, a multiple of 8, with zero
+//    rows), then ntops_gemm computes, per image,
+//    out_n = W (K x KP) . col_n (KP x PQ) + bias, with W shared across the
 //    batch (batch stride 0) and the bias as a C operand broadcast along the
-//    pixels (strides 0, 1, 0).  bf16 / fp16 run on MFMA, fp32 on the IEEE
-//    FMA GEMM.
+//    pixels (strides 0, 1, 0).  W is read in place when its rows are KP
+//    contiguous elements at 16-byte alignment, else copied into the
+//    workspace as K x KP with zero columns past CRS (e.g. a 3-channel 7 x 7
+//    stem, CRS = 147).  bf16 / fp16 run on MFMA, fp32 on the IEEE FMA GEMM.
 //  * direct path (small channel counts, any strides): one thread per output
 //    element, fp32 accumulation.
 #include <atomic>
@@ -51,7 +54,7 @@ namespace {
 // its own copy at its own address for the life of the process; host code
 // reaches it only through conv_scratch(), never through the symbol's name
 // (which on the host is a stand-in, not a device address).  Every byte a call
-// reads is written by the same call's shift / unfold kernel first, so no
+// reads is written by the same call first (its shift / unfold / copy kernels, or the zero fill of the pad rows), so no
 // clearing is needed; calls that overlap on one GPU share it and race.
 constexpr int64_t kConvScratchBytes = NTOPS_CONV2D_NOALLOC_MAX_SCRATCH;
 static __device__ __align__(256) char scratch[kConvScratchBytes];
@@ -140,7 +143,7 @@ __global__ __launch_bounds__(256) void k_conv_direct(ConvArgs a, int64_t total) 
 // ld elements (pixels PQ .. ld - 1 are zero).  One thread per 8 pixels of one
 // (b, kg) row: a 16-byte (or 32-byte for fp32) run of the output row.
 template <typename T>
-__global__ __launch_bounds__(256) void k_im2col(ConvArgs a, T* col, int n0, int nb, int64_t ld) {
+__global__ __launch_bounds__(256) void k_im2col(ConvArgs a, T* col, int n0, int nb, int64_t ld, int64_t kp) {
   const int crs = a.C * a.R * a.S;
   const int64_t chunks = ld / 8;
   const int64_t total = static_cast<int64_t>(nb) * crs * chunks;
@@ -169,7 +172,7 @@ __global__ __launch_bounds__(256) void k_im2col(ConvArgs a, T* col, int n0, int 
       }
       v[e] = val;
     }
-    T* dst = col + row * ld + pq0;
+    T* dst = col + (static_cast<int64_t>(b) * kp + kg) * ld + pq0;
     if constexpr (sizeof(T) == 2) {
       *reinterpret_cast<u32x4*>(dst) = __builtin_bit_cast(u32x4, v);
     } else {
@@ -181,25 +184,31 @@ __global__ __launch_bounds__(256) void k_im2col(ConvArgs a, T* col, int n0, int 
   }
 }
 
-// Stages x[n][c] (H x W elements) into LDS: 16-byte loads when the rows are
-// contiguous, 16-byte aligned runs of a multiple of 8 elements, else one
-// element per load.
+// Stages rows row0 .. row0 + nrows - 1 of x[n][c] (W elements each) into
+// LDS: 16-byte loads when the rows are contiguous, 16-byte aligned runs of a
+// multiple of 8 elements, else one element per load.
 template <typename T>
-__device__ __forceinline__ void stage_plane(const ConvArgs& a, const T* xc, T* plane) {
+__device__ __forceinline__ void stage_rows(const ConvArgs& a, const T* xc, T* plane, int row0, int nrows) {
   constexpr int V = 16 / sizeof(T);
-  const int hw = a.H * a.W;
+  xc += static_cast<int64_t>(row0) * a.xs[2];
   if (a.xs[3] == 1 && a.W % V == 0 && a.xs[2] % V == 0 && (reinterpret_cast<uintptr_t>(xc) & 15u) == 0) {
     const int wv = a.W / V;
-    for (int i = threadIdx.x; i < a.H * wv; i += blockDim.x) {
+    for (int i = threadIdx.x; i < nrows * wv; i += blockDim.x) {
       const int ih = i / wv, c8 = i - (i / wv) * wv;
       *reinterpret_cast<u32x4*>(plane + ih * a.W + c8 * V) = *reinterpret_cast<const u32x4*>(xc + ih * a.xs[2] + c8 * V);
     }
   } else {
-    for (int i = threadIdx.x; i < hw; i += blockDim.x) {
+    for (int i = threadIdx.x; i < nrows * a.W; i += blockDim.x) {
       const int ih = i / a.W, iw = i - (i / a.W) * a.W;
       plane[i] = xc[ih * a.xs[2] + iw * a.xs[3]];
     }
   }
+}
+
+// The whole H x W plane x[n][c].
+template <typename T>
+__device__ __forceinline__ void stage_plane(const ConvArgs& a, const T* xc, T* plane) {
+  stage_rows<T>(a, xc, plane, 0, a.H);
 }
 
 // Same output as k_im2col, one workgroup per (image, channel): the input
@@ -211,7 +220,8 @@ __device__ __forceinline__ void stage_plane(const ConvArgs& a, const T* xc, T* p
 constexpr int kPlaneLds = 64 * 1024;
 
 template <typename T>
-__global__ __launch_bounds__(256) void k_im2col_plane(ConvArgs a, T* col, int n0, int nb, int64_t ld) {
+__global__ __launch_bounds__(256) void k_im2col_plane(ConvArgs a, T* col, int n0, int nb, int64_t ld,
+                                                      int64_t kp) {
   extern __shared__ __attribute__((aligned(16))) char sm[];  // H * W elements
   T* plane = reinterpret_cast<T*>(sm);
   const int64_t id = block_id();  // (image, channel) plane; blocks_2d grid
@@ -223,7 +233,7 @@ __global__ __launch_bounds__(256) void k_im2col_plane(ConvArgs a, T* col, int n0
   const int rs = a.R * a.S;
   const int pq = a.P * a.Q;
   const int nch = static_cast<int>(ld / 8);
-  T* dst0 = col + (static_cast<int64_t>(b) * a.C * rs + static_cast<int64_t>(c) * rs) * ld;
+  T* dst0 = col + (static_cast<int64_t>(b) * kp + static_cast<int64_t>(c) * rs) * ld;
   for (int j = threadIdx.x; j < nch; j += blockDim.x) {
     // the 8 pixels of run j: output (p, q) computed once, then reused for
     // every tap
@@ -263,6 +273,86 @@ __global__ __launch_bounds__(256) void k_im2col_plane(ConvArgs a, T* col, int n0
       }
     }
   }
+}
+
+// Same output as k_im2col for planes too large for k_im2col_plane's LDS: one
+// workgroup per (image, channel, band of kBandRuns 8-pixel runs of the
+// unfolded row); it stages only the input rows its band's output rows read
+// (kBandRuns * 8 pixels = a few output rows, so a 3-channel 224 x 224 stem
+// with stride 2 and a 7 x 7 kernel stages 17 rows, 7.4 KiB), then writes
+// every tap's 16-byte runs from LDS -- lane l of the block on run l % 64,
+// taps l / 64, l / 64 + 4, ... -- so neighbouring lanes store neighbouring
+// runs.  The launch reserves band_lds_rows(a) rows of W elements.
+constexpr int kBandRuns = 64;
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_im2col_band(ConvArgs a, T* col, int n0, int nb, int64_t ld, int64_t kp,
+                                                     int nbands) {
+  extern __shared__ __attribute__((aligned(16))) char sm[];
+  T* band = reinterpret_cast<T*>(sm);
+  const int64_t id = block_id();  // ((image, channel), band); blocks_2d grid
+  if (id >= static_cast<int64_t>(nb) * a.C * nbands) return;  // the tail of the grid (the whole block)
+  const int64_t plane_id = id / nbands;
+  const int bi = static_cast<int>(id - plane_id * nbands);
+  const int b = static_cast<int>(plane_id / a.C);
+  const int c = static_cast<int>(plane_id - static_cast<int64_t>(b) * a.C);
+  const int pq = a.P * a.Q;
+  const int nch = static_cast<int>(ld / 8);
+  const int j0 = bi * kBandRuns;
+  const int j1 = min(nch, j0 + kBandRuns);
+  // output rows of the band's pixels, and the input rows they read
+  const int p_lo = (8 * j0) / a.Q;
+  const int p_hi = (min(8 * j1, pq) - 1) / a.Q;
+  const int ih0 = max(0, p_lo * a.sh - a.ph);
+  const int ih1 = min(a.H - 1, p_hi * a.sh - a.ph + (a.R - 1) * a.dh);
+  if (ih1 >= ih0)
+    stage_rows<T>(a, static_cast<const T*>(a.x) + (n0 + b) * a.xs[0] + c * a.xs[1], band, ih0, ih1 - ih0 + 1);
+  __syncthreads();
+  const int rs = a.R * a.S;
+  T* dst0 = col + (static_cast<int64_t>(b) * kp + static_cast<int64_t>(c) * rs) * ld;
+  const int j = j0 + (threadIdx.x & (kBandRuns - 1));
+  if (j >= j1) return;
+  int p = (8 * j) / a.Q;
+  int q = 8 * j - p * a.Q;
+  int hbase[8], wbase[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const bool in = 8 * j + e < pq;
+    hbase[e] = in ? p * a.sh - a.ph : -0x40000000;  // out-of-range pixels never land in the band
+    wbase[e] = q * a.sw - a.pw;
+    if (++q == a.Q) {
+      q = 0;
+      ++p;
+    }
+  }
+  for (int t = threadIdx.x / kBandRuns; t < rs; t += 256 / kBandRuns) {
+    const int r = t / a.S, sx = t - r * a.S;
+    T v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int ih = hbase[e] + r * a.dh;
+      const int iw = wbase[e] + sx * a.dw;
+      const bool ok = static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
+                      static_cast<unsigned>(iw) < static_cast<unsigned>(a.W);
+      v[e] = ok ? band[(ih - ih0) * a.W + iw] : static_cast<T>(0.f);
+    }
+    T* dst = dst0 + static_cast<int64_t>(t) * ld + 8 * j;
+    if constexpr (sizeof(T) == 2) {
+      *reinterpret_cast<u32x4*>(dst) = __builtin_bit_cast(u32x4, v);
+    } else {
+      reinterpret_cast<u32x4*>(dst)[0] = u32x4{__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                                               __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
+      reinterpret_cast<u32x4*>(dst)[1] = u32x4{__builtin_bit_cast(uint32_t, v[4]), __builtin_bit_cast(uint32_t, v[5]),
+                                               __builtin_bit_cast(uint32_t, v[6]), __builtin_bit_cast(uint32_t, v[7])};
+    }
+  }
+}
+
+// Input rows a band of k_im2col_band may stage: its kBandRuns * 8 pixels
+// span at most (kBandRuns * 8 - 1) / Q + 2 output rows.
+int64_t band_lds_rows(const ConvArgs& a) {
+  const int64_t prow = (kBandRuns * 8 - 1) / a.Q + 2;
+  return std::min<int64_t>(a.H, (prow - 1) * a.sh + static_cast<int64_t>(a.R - 1) * a.dh + 1);
 }
 
 // xs[b][s][c][row][q] for images n0 .. n0 + nb - 1 (stride-1 convolutions):
@@ -485,6 +575,44 @@ __global__ __launch_bounds__(256) void k_conv_weights_cl(ConvArgs a, T* wt) {
     conv_weight_pack(a, wt, i);
 }
 
+// Rows crs .. kp - 1 of each of nb unfolded images (the zero rows that pad
+// the GEMM's reduction depth to a multiple of 8), one 16-byte chunk per
+// thread per step (rows of ld elements are whole 16-byte chunks).
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_col_zero_rows(T* col, int64_t nb, int64_t crs, int64_t kp, int64_t ld) {
+  const int64_t per_row = ld * static_cast<int64_t>(sizeof(T)) / 16;
+  const int64_t per_img = (kp - crs) * per_row;
+  const int64_t total = nb * per_img;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t b = i / per_img, rem = i - b * per_img;
+    char* row0 = reinterpret_cast<char*>(col + (b * kp + crs) * ld);
+    *reinterpret_cast<u32x4*>(row0 + rem * 16) = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// W (any strides) as a row-major K x kp matrix whose columns crs .. kp - 1
+// are zero: the GEMM's A operand when the weight rows cannot be read in
+// place.
+template <typename T>
+__global__ __launch_bounds__(256) void k_conv_weights_rows(ConvArgs a, T* wp, int64_t kp) {
+  const int rs = a.R * a.S;
+  const int64_t crs = static_cast<int64_t>(a.C) * rs;
+  const int64_t total = static_cast<int64_t>(a.K) * kp;
+  const T* w = static_cast<const T*>(a.w);
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t k = i / kp, j = i - k * kp;
+    T v = static_cast<T>(0.f);
+    if (j < crs) {
+      const int c = static_cast<int>(j / rs), t = static_cast<int>(j - static_cast<int64_t>(c) * rs);
+      const int r = t / a.S, sx = t - r * a.S;
+      v = w[k * a.ws[0] + c * a.ws[1] + r * a.ws[2] + sx * a.ws[3]];
+    }
+    wp[i] = v;
+  }
+}
+
 unsigned grid_for(int64_t work, int per_block) {
   int64_t g = (work + per_block - 1) / per_block;
   if (g > 65536) g = 65536;  // grid-stride loops cover the rest
@@ -494,23 +622,35 @@ unsigned grid_for(int64_t work, int per_block) {
 // Pixels per unfolded row (a multiple of 8, so rows stay 16-byte aligned).
 int64_t col_ld(const ConvArgs& a) { return (static_cast<int64_t>(a.P) * a.Q + 7) / 8 * 8; }
 
+// Unfolded rows per image: C R S padded to a multiple of 8 (the GEMM's
+// K-major operand needs 16-byte rows); the pad rows are zero.
+int64_t col_rows(const ConvArgs& a) { return (static_cast<int64_t>(a.C) * a.R * a.S + 7) / 8 * 8; }
+
+// Whether W can be the GEMM's A operand in place: rows of C R S contiguous
+// elements, a row stride of a multiple of 8 elements, 16-byte aligned.
+bool w_rows_ok(const ConvArgs& a) {
+  return a.ws[3] == 1 && a.ws[2] == a.S && a.ws[1] == static_cast<int64_t>(a.R) * a.S && a.ws[0] % 8 == 0 &&
+         (reinterpret_cast<uintptr_t>(a.w) & 15u) == 0;
+}
+
+// Whether the unfold path copies W into the workspace (K x col_rows, zero
+// columns past C R S).
+bool unfold_stages_w(const ConvArgs& a) {
+  return col_rows(a) != static_cast<int64_t>(a.C) * a.R * a.S || !w_rows_ok(a);
+}
+
 // Whether the GEMM path applies: enough reduction depth, output channels and
-// output pixels to feed the matrix cores, unit-stride weight rows of a
-// multiple of 8 elements, and pixel planes of the output that are
-// contiguous.
+// output pixels to feed the matrix cores, and pixel planes of the output
+// that are contiguous.
 bool use_gemm(const ConvArgs& a, int dt) {
   const int64_t crs = static_cast<int64_t>(a.C) * a.R * a.S;
   const int64_t pq = static_cast<int64_t>(a.P) * a.Q;
-  const bool w_rows = a.ws[3] == 1 && a.ws[2] == a.S && a.ws[1] == static_cast<int64_t>(a.R) * a.S &&
-                      a.ws[0] % 8 == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15u) == 0;
   const bool out_plane = a.os[3] == 1 && a.os[2] == a.Q;
-  return dt != NTOPS_F64 && crs >= 64 && crs % 8 == 0 && a.K >= 32 && pq >= 16 && w_rows && out_plane &&
-         crs * col_ld(a) <= 0x7fffffffLL;
+  return dt != NTOPS_F64 && crs >= 64 && a.K >= 32 && pq >= 16 && out_plane &&
+         col_rows(a) * col_ld(a) <= 0x7fffffffLL;
 }
 
-int64_t col_bytes_per_image(const ConvArgs& a, int dt) {
-  return static_cast<int64_t>(a.C) * a.R * a.S * col_ld(a) * dtype_size(dt);
-}
+int64_t col_bytes_per_image(const ConvArgs& a, int dt) { return col_rows(a) * col_ld(a) * dtype_size(dt); }
 
 // Output planes whose pixel count is not a multiple of 8 are computed at
 // the unfold's padded width (the matrix-core GEMM's N-major operand and
@@ -525,7 +665,8 @@ int64_t padded_out_bytes_per_image(const ConvArgs& a, int dt) {
 int64_t shift_rows(const ConvArgs& a) { return static_cast<int64_t>(a.P) + static_cast<int64_t>(a.R - 1) * a.dh; }
 
 // Whether the implicit GEMM applies (on top of use_gemm): stride 1, 16-bit
-// data, output rows of a multiple of 8 pixels, operands inside the 2 GiB
+// data, output rows of a multiple of 8 pixels, W readable in place with
+// C R S a multiple of 8, operands inside the 2 GiB
 // buffer range, and an output whose channel and image strides are multiples
 // of 4 elements at an 8-byte aligned address (the epilogue's store width);
 // anything else takes the unfold + GEMM path.
@@ -533,8 +674,9 @@ bool use_implicit(const ConvArgs& a, int dt) {
   const int64_t elems = static_cast<int64_t>(a.S) * a.C * shift_rows(a) * a.Q;
   const int64_t crs = static_cast<int64_t>(a.C) * a.R * a.S;
   const bool out_ok = a.os[1] % 4 == 0 && a.os[0] % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 7u) == 0;
-  return (dt == NTOPS_BF16 || dt == NTOPS_F16) && a.sh == 1 && a.sw == 1 && a.Q % 8 == 0 &&
-         elems * 2 < (int64_t(1) << 31) && (256 * a.ws[0] + crs) * 2 < (int64_t(1) << 31) && out_ok;
+  return (dt == NTOPS_BF16 || dt == NTOPS_F16) && a.sh == 1 && a.sw == 1 && a.Q % 8 == 0 && crs % 8 == 0 &&
+         w_rows_ok(a) && elems * 2 < (int64_t(1) << 31) && (256 * a.ws[0] + crs) * 2 < (int64_t(1) << 31) &&
+         out_ok;
 }
 
 // Rows and pixels per row of the channels-last padded copy.
@@ -574,10 +716,13 @@ int64_t ws_bytes_per_image(const ConvArgs& a, int dt) {
 }
 
 // Workspace bytes the chosen GEMM path needs once per call, ahead of the
-// images' (the channels-last path's reordered weights, rounded up to 256).
+// images' (the channels-last path's reordered weights, or the unfold path's
+// K x col_rows copy of W; rounded up to 256).
 int64_t ws_bytes_fixed(const ConvArgs& a, int dt) {
-  if (!use_channels_last(a, dt)) return 0;
-  return (static_cast<int64_t>(a.K) * a.C * a.R * a.S * dtype_size(dt) + 255) / 256 * 256;
+  if (use_channels_last(a, dt))
+    return (static_cast<int64_t>(a.K) * a.C * a.R * a.S * dtype_size(dt) + 255) / 256 * 256;
+  if (use_implicit(a, dt) || !unfold_stages_w(a)) return 0;
+  return (static_cast<int64_t>(a.K) * col_rows(a) * dtype_size(dt) + 255) / 256 * 256;
 }
 
 int fill_args(ConvArgs& a, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
@@ -750,35 +895,60 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
     }
     return NTOPS_OK;
   }
-  // GEMM path, in chunks of images that fit the workspace
+  // GEMM path, in chunks of images that fit the workspace: [W copy (if
+  // staged)][unfolded images][padded output planes (if P Q % 8 != 0)]
   const int64_t ld = col_ld(a);
-  const int64_t nb_max = std::min<int64_t>(N, workspace_bytes / per_image);
-  const int64_t a_str[3] = {0, w_strides[0], 1};
-  const int64_t b_str[3] = {crs * ld, ld, 1};
+  const int64_t kp = col_rows(a);
+  const bool stage_w = unfold_stages_w(a);
+  void* col = static_cast<char*>(workspace) + fixed;
+  const int64_t nb_max = std::min<int64_t>(N, (workspace_bytes - fixed) / per_image);
+  const void* wa = stage_w ? workspace : w;
+  const int64_t a_str[3] = {0, stage_w ? kp : w_strides[0], 1};
+  const int64_t b_str[3] = {kp * ld, ld, 1};
   const int64_t c_str[3] = {0, bias_stride, 0};
   const int64_t d_str[3] = {out_strides[0], out_strides[1], 1};
   const int es = dtype_size(dtype);
   // planes of P Q % 8 != 0 pixels: the GEMM writes rows of ld pixels into
   // the workspace after the unfold, then k_conv_rows_out copies them out
   const bool padded = padded_out_bytes_per_image(a, dtype) > 0;
-  void* staged = static_cast<char*>(workspace) + nb_max * crs * ld * es;
+  void* staged = static_cast<char*>(col) + nb_max * kp * ld * es;
   const int64_t s_str[3] = {K * ld, ld, 1};
+  if (stage_w || kp != crs) {
+    // the W copy, and the zero pad rows of every image slot of a chunk
+    // (the unfold never writes them)
+    rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
+      using T = decltype(tag);
+      if (stage_w)
+        hipLaunchKernelGGL(k_conv_weights_rows<T>, dim3(grid_for(K * kp, 256)), dim3(256), 0, st, a,
+                           static_cast<T*>(workspace), kp);
+      if (kp != crs)
+        hipLaunchKernelGGL(k_conv_col_zero_rows<T>, dim3(grid_for(nb_max * (kp - crs) * ld * es / 16, 256)),
+                           dim3(256), 0, st, static_cast<T*>(col), nb_max, crs, kp, ld);
+      return check_launch("conv2d");
+    });
+    if (rc != NTOPS_OK) return rc;
+  }
   for (int64_t n0 = 0; n0 < N; n0 += nb_max) {
     const int64_t nb = std::min(nb_max, N - n0);
     rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {
       using T = decltype(tag);
+      const int64_t band_bytes = band_lds_rows(a) * W * static_cast<int64_t>(sizeof(T));
+      const int nbands = static_cast<int>((ld / 8 + kBandRuns - 1) / kBandRuns);
       if (static_cast<int64_t>(H) * W * static_cast<int64_t>(sizeof(T)) <= kPlaneLds)
         hipLaunchKernelGGL(k_im2col_plane<T>, blocks_2d(nb * C), dim3(256),
-                           static_cast<unsigned>(H * W * sizeof(T)), st, a, static_cast<T*>(workspace),
-                           static_cast<int>(n0), static_cast<int>(nb), ld);
+                           static_cast<unsigned>(H * W * sizeof(T)), st, a, static_cast<T*>(col),
+                           static_cast<int>(n0), static_cast<int>(nb), ld, kp);
+      else if (band_bytes <= kPlaneLds)
+        hipLaunchKernelGGL(k_im2col_band<T>, blocks_2d(nb * C * nbands), dim3(256), static_cast<unsigned>(band_bytes),
+                           st, a, static_cast<T*>(col), static_cast<int>(n0), static_cast<int>(nb), ld, kp, nbands);
       else
         hipLaunchKernelGGL(k_im2col<T>, dim3(grid_for(nb * crs * (ld / 8), 256)), dim3(256), 0, st, a,
-                           static_cast<T*>(workspace), static_cast<int>(n0), static_cast<int>(nb), ld);
+                           static_cast<T*>(col), static_cast<int>(n0), static_cast<int>(nb), ld, kp);
       return check_launch("conv2d");
     });
     if (rc != NTOPS_OK) return rc;
     void* dst = static_cast<char*>(out) + n0 * out_strides[0] * es;
-    rc = ntops_gemm(dtype, nb, K, padded ? ld : P * Q, crs, w, a_str, workspace, b_str, bias,
+    rc = ntops_gemm(dtype, nb, K, padded ? ld : P * Q, kp, wa, a_str, col, b_str, bias,
                     bias ? c_str : nullptr, 1.0, bias ? 1.0 : 0.0, padded ? staged : dst, padded ? s_str : d_str,
                     stream);
     if (rc != NTOPS_OK) return rc;

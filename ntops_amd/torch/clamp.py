@@ -1,14 +1,22 @@
 """clamp -- mirror of src/ntops/torch/clamp.py:7-15 (math: kernels/clamp.py:9).
 
 min / max may each be None, a Python number or a tensor (broadcast), like
-torch.clamp; the result dtype, shape and argument checks are torch's (read
-from a shape-only evaluation on the meta device).  Number bounds are rounded
+torch.clamp; the result dtype, shape and argument checks are torch's.  Number bounds are rounded
 to the result dtype; a NaN in the input or a bound propagates."""
 
 import torch
 
 from ntops_amd import _lib
-from ntops_amd.torch.utils import _DeviceGuard, _cast_into, _is_number, _prepare_out, _strides, _to_dtype
+from ntops_amd.torch.utils import (
+    _broadcast_shape,
+    _DeviceGuard,
+    _cast_into,
+    _expand_to,
+    _is_number,
+    _prepare_out,
+    _strides,
+    _to_dtype,
+)
 
 
 def _as_bound(v):
@@ -17,8 +25,27 @@ def _as_bound(v):
     return v
 
 
-def _meta(v):
-    return v.to("meta") if isinstance(v, torch.Tensor) else v
+def _proxy(v):
+    """A one-element CPU tensor standing in for tensor v in torch's type
+    promotion (same dtype, zero-dim or not like v), or v itself."""
+    if isinstance(v, torch.Tensor):
+        return torch.zeros((1,) * v.dim(), dtype=v.dtype)
+    return v
+
+
+def _result(input, lo, hi):
+    """torch.clamp's result dtype and shape, with its argument errors, at a
+    few microseconds of host time: number bounds on a floating tensor keep
+    its dtype and shape; otherwise torch.clamp decides on one-element CPU
+    stand-ins (the dtype) and the shapes broadcast (the shape)."""
+    if input.dtype.is_floating_point and not any(isinstance(v, torch.Tensor) for v in (lo, hi)):
+        return input.dtype, input.shape
+    dtype = torch.clamp(_proxy(input), _proxy(lo), _proxy(hi)).dtype
+    shape = input.shape
+    for v in (lo, hi):
+        if isinstance(v, torch.Tensor):
+            shape = _broadcast_shape(shape, v.shape)
+    return dtype, shape
 
 
 def clamp(input, min=None, max=None, *, out=None):
@@ -28,17 +55,16 @@ def clamp(input, min=None, max=None, *, out=None):
     for v in (lo, hi):
         if v is not None and not isinstance(v, torch.Tensor) and not _is_number(v):
             raise TypeError(f"ntops_amd.clamp: unsupported bound {type(v)}")
-    probe = torch.clamp(_meta(input), _meta(lo), _meta(hi))
-    dtype, shape = probe.dtype, probe.shape
+    dtype, shape = _result(input, lo, hi)
     dev = _lib.require_cuda(input, *(v for v in (lo, hi) if isinstance(v, torch.Tensor)))
     target, res = _prepare_out(out, shape, dtype, dev, like=input)
-    x = _to_dtype(input, dtype).expand(shape)
+    x = _expand_to(_to_dtype(input, dtype), shape)
 
     def bound(v):
         if v is None:
             return None, None, 0.0, 0, 0
         if isinstance(v, torch.Tensor):
-            t = _to_dtype(v, dtype).expand(shape)
+            t = _expand_to(_to_dtype(v, dtype), shape)
             return t, t.data_ptr(), 0.0, 0, 1
         return None, None, float(v), int(v) if not isinstance(v, float) else 0, 1
 

@@ -73,17 +73,25 @@ GEMM_CASES = [
     (8, 64, 4, 4, 64, 3, 3, 1, 1, 1, True),
     (4, 64, 6, 6, 96, 3, 3, 1, 1, 1, False),
     (4, 48, 5, 5, 64, 3, 3, 1, 1, 1, True),
+    # C R S not a multiple of 8: unfold into KP = C R S rounded up to 8 rows
+    # (zero pad rows) against a zero-padded K x KP copy of W -- a 3-channel
+    # 7 x 7 stride-2 stem (147 -> 152), 5 x 5 over 5 channels (125 -> 128),
+    # and 3 x 3 over 9 channels (81 -> 88) on an 11 x 13 plane (also padded
+    # output rows)
+    (2, 3, 64, 64, 64, 7, 7, 2, 3, 1, True),
+    (2, 5, 20, 20, 32, 5, 5, 1, 2, 1, False),
+    (3, 9, 11, 13, 40, 3, 3, 1, 1, 1, True),
 ]
 
 
-def expected_path(dtype, c, p, q, stride):
+def expected_path(dtype, c, p, q, stride, crs):
     """Kernel family of the GEMM paths: the channels-last implicit GEMM for
     16-bit data with C % 32 == 0 and P * Q % 4 == 0, the implicit GEMM over
     shifted planes for the rest of the 16-bit stride-1 problems with
-    Q % 8 == 0, otherwise unfold + GEMM."""
+    Q % 8 == 0 and C R S % 8 == 0, otherwise unfold + GEMM."""
     if dtype != torch.float32 and c % 32 == 0 and (p * q) % 4 == 0:
         return " conv_cl"
-    if dtype != torch.float32 and pair(stride) == (1, 1) and q % 8 == 0:
+    if dtype != torch.float32 and pair(stride) == (1, 1) and q % 8 == 0 and crs % 8 == 0:
         return " conv"
     return ""
 
@@ -105,7 +113,7 @@ def test_conv2d_gemm_path(case, dtype):
     got = conv2d(x.cuda(), wt.cuda(), bias=None if b is None else b.cuda(), stride=stride, padding=padding,
                  dilation=dilation)
     kern = _lib.last_kernel()
-    want = expected_path(dtype, c, P, Q, stride)
+    want = expected_path(dtype, c, P, Q, stride, c * r * s)
     assert kern.startswith("gemm_") and (kern.endswith(want) if want else not kern.endswith("conv") and
                                          not kern.endswith("conv_cl")), kern
     exp = oracle(x, wt, b, stride, padding, dilation)
@@ -202,7 +210,9 @@ def test_conv2d_layouts_and_forms(dtype):
         xc = x.cuda().to(memory_format=torch.channels_last)
         assert not xc.is_contiguous()
         assert_close(conv2d(xc, wt.cuda(), padding=1), oracle(x, wt, None, 1, 1, 1), *tol, "channels-last")
-        # a sliced (non-contiguous) weight runs the direct kernel
+        # a sliced (non-contiguous) weight: the direct kernel for 3
+        # channels, a K x C R S copy in the workspace for the unfold path
+        # for 64
         wbig = torch.randn(k, c, 3, 5, generator=g).to(dtype)
         ws = wbig[:, :, :, 1:4]
         assert_close(conv2d(x.cuda(), wbig.cuda()[:, :, :, 1:4], stride=2), oracle(x, ws.contiguous(), None, 2, 0, 1),
@@ -278,3 +288,69 @@ def test_conv2d_output_views_the_implicit_gemm_cannot_store(form):
     _lib.check(rc, f"conv2d into a {form} output")
     assert _lib.last_kernel().startswith("gemm_") and not _lib.last_kernel().endswith(" conv")
     assert_close(out, oracle(x, wt, b, 1, 1, 1), 1.6e-2, 1.6e-2, form)
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float32))
+def test_conv2d_padded_depth_weight_copies(dtype):
+    """The unfold path with W copied into the workspace (zero columns past
+    C R S): weights whose rows are not C R S contiguous elements (a slice,
+    an odd row stride from a wider allocation) and C R S % 8 != 0, with and
+    without bias, against the oracle; the second call reuses a workspace
+    whose pad rows held other data."""
+    g = torch.Generator().manual_seed(21)
+    tol = TOL[dtype] if dtype != torch.float32 else (2e-5, 2e-5)
+    x = torch.randn(2, 3, 40, 36, generator=g).to(dtype)
+    wfull = (torch.randn(64, 3, 7, 9, generator=g) / 12).to(dtype)
+    wsl = wfull[:, :, :, 1:8]  # (64, 3, 7, 7), rows of 147 elements at stride 189
+    b = torch.randn(64, generator=g).to(dtype)
+    got = conv2d(x.cuda(), wfull.cuda()[:, :, :, 1:8], bias=b.cuda(), stride=2, padding=3)
+    assert _lib.last_kernel().startswith("gemm_"), _lib.last_kernel()
+    assert_close(got, oracle(x, wsl.contiguous(), b, 2, 3, 1), *tol, "sliced 7 x 7 weight")
+    # through the C ABI, one workspace for both calls: call 1 (C R S = 588,
+    # 592 rows) fills the workspace with its W copy and unfold rows, call 2
+    # (C R S = 147, 152 rows) must see zeros in its pad rows, which lie over
+    # call 1's data
+    lib = _lib.load()
+    st = lambda t: _lib.i64_array(t.stride())  # noqa: E731
+    dt = _lib.dtype_code(dtype)
+    x1 = torch.randn(2, 12, 40, 36, generator=g).to(dtype).cuda()
+    w1 = (torch.randn(64, 12, 7, 7, generator=g) / 24).to(dtype).cuda()
+    w2 = wsl.contiguous().cuda()
+    outs = []
+    geo1 = (2, 12, 40, 36, 64, 7, 7, 20, 18, 2, 2, 3, 3, 1, 1)
+    geo2 = (2, 3, 40, 36, 64, 7, 7, 20, 18, 2, 2, 3, 3, 1, 1)
+    o1 = torch.empty(2, 64, 20, 18, dtype=dtype, device="cuda")
+    o2 = torch.empty_like(o1)
+    need = max(lib.ntops_conv2d_workspace(dt, *geo1, st(w1), st(o1)), lib.ntops_conv2d_workspace(dt, *geo2, st(w2), st(o2)))
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    for geo, xx, ww, oo in ((geo1, x1, w1, o1), (geo2, x.cuda(), w2, o2)):
+        rc = lib.ntops_conv2d(dt, *geo, xx.data_ptr(), st(xx), ww.data_ptr(), st(ww), None, 0, oo.data_ptr(), st(oo),
+                              ws.data_ptr(), need, _lib.stream_of(oo))
+        _lib.check(rc, "conv2d")
+        assert _lib.last_kernel().startswith("gemm_"), _lib.last_kernel()
+        outs.append(oo)
+    torch.cuda.synchronize()
+    assert_close(outs[0], oracle(x1.cpu(), w1.cpu(), None, 2, 3, 1), *tol, "C R S = 588")
+    assert_close(outs[1], oracle(x, wsl.contiguous(), None, 2, 3, 1), *tol, "C R S = 147 after 588")
+
+
+@pytest.mark.parametrize(
+    "dtype, n, c, h, w, k, r, stride, pad, dil",
+    [
+        # input planes past the 64 KiB that k_im2col_plane stages whole: the
+        # unfold stages a band of input rows per (image, channel, 512 pixels)
+        (torch.bfloat16, 2, 3, 192, 192, 64, 7, 2, 3, 1),  # stem: C R S = 147 -> 152 rows
+        (torch.float32, 1, 4, 130, 130, 32, 5, 1, 2, 2),  # dilated, 126 x 126 plane (padded out rows)
+        (torch.bfloat16, 1, 8, 200, 180, 32, 3, 1, 1, 1),  # Q % 8 != 0 keeps it off the shifted planes
+    ],
+)
+def test_conv2d_band_unfold(dtype, n, c, h, w, k, r, stride, pad, dil):
+    g = torch.Generator().manual_seed(c * 100 + h)
+    x = torch.randn(n, c, h, w, generator=g).to(dtype)
+    wt = (torch.randn(k, c, r, r, generator=g) / (c * r * r) ** 0.5).to(dtype)
+    b = torch.randn(k, generator=g).to(dtype)
+    got = conv2d(x.cuda(), wt.cuda(), bias=b.cuda(), stride=stride, padding=pad, dilation=dil)
+    assert _lib.last_kernel().startswith("gemm_"), _lib.last_kernel()
+    tol = TOL[dtype] if dtype != torch.float32 else (2e-5, 2e-5)
+    assert_close(got, oracle(x, wt, b, stride, pad, dil), *tol, "band unfold")

@@ -55,3 +55,39 @@ def test_i64_array_holds_the_values():
         assert isinstance(arr, ctypes.Array)
         assert list(arr)[: len(values)] == list(values)
         assert len(arr) == max(len(values), 1)
+
+
+_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.float64, torch.int32, torch.int64, torch.uint8,
+           torch.bool)
+
+
+def _bounds():
+    yield None
+    yield 2
+    yield -1.5
+    yield True
+    for dt in (torch.float32, torch.bfloat16, torch.int64, torch.int16):
+        yield torch.ones((), dtype=dt)  # zero-dim tensor
+        yield torch.ones(3, dtype=dt)  # broadcasts along the last dim
+        yield torch.ones(2, 1, dtype=dt)  # broadcasts along the first dim
+
+
+@pytest.mark.parametrize("dtype", _DTYPES)
+def test_clamp_result_matches_torch(dtype):
+    """The wrappers' clamp result dtype / shape (and the combinations torch
+    refuses) against torch.clamp evaluated on CPU tensors of the same
+    shapes."""
+    from ntops_amd.torch.clamp import _result
+
+    x = torch.zeros(2, 3, dtype=dtype)
+    for lo in _bounds():
+        for hi in _bounds():
+            if lo is None and hi is None:
+                continue
+            try:
+                ref = torch.clamp(x, lo, hi)
+            except (RuntimeError, TypeError):
+                with pytest.raises((RuntimeError, TypeError)):
+                    _result(x, lo, hi)
+                continue
+            assert _result(x, lo, hi) == (ref.dtype, ref.shape), (dtype, lo, hi)
