@@ -296,9 +296,13 @@ __device__ __forceinline__ void strided_offsets(const KSpace<NOPS, I>& sp, I lin
   }
 }
 
-// Host: merges adjacent dims that are contiguous with respect to every
-// operand, drops size-1 dims.  Returns false if ndim exceeds the limit after
-// merging.  numel is written to *numel.
+// Host: drops size-1 dims, orders the rest by the last operand's (the
+// output's) strides, largest outermost -- an elementwise result does not
+// depend on the order in which elements are visited, and this order makes a
+// permuted dense layout (a transposed view and the empty_like output that
+// follows it) one dense run -- then merges adjacent dims that are
+// contiguous with respect to every operand.  Returns false if ndim exceeds
+// the limit after merging.  numel is written to *numel.
 template <int NOPS>
 bool build_space(int ndim, const int64_t* shape, const int64_t* const strides[NOPS],
                  StridedSpace<NOPS>* sp, int64_t* numel) {
@@ -314,6 +318,20 @@ bool build_space(int ndim, const int64_t* shape, const int64_t* const strides[NO
     ++n;
   }
   *numel = total;
+  // stable insertion sort by |output stride|, descending
+  auto key = [](int64_t v) { return v < 0 ? -v : v; };
+  for (int i = 1; i < n; ++i) {
+    for (int j = i; j > 0 && key(st[NOPS - 1][j - 1]) < key(st[NOPS - 1][j]); --j) {
+      const int64_t t = shp[j];
+      shp[j] = shp[j - 1];
+      shp[j - 1] = t;
+      for (int k = 0; k < NOPS; ++k) {
+        const int64_t u = st[k][j];
+        st[k][j] = st[k][j - 1];
+        st[k][j - 1] = u;
+      }
+    }
+  }
   // merge from the innermost side
   int m = 0;
   int64_t oshp[64];

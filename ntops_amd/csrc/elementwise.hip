@@ -16,11 +16,15 @@
 // compute in fp32 and round once; add's alpha is rounded to the tensor dtype
 // and applied with a fused multiply-add).
 //
-// Two launch shapes:
+// Three launch shapes:
 //  * dense: every operand is one contiguous, aligned run.  Each thread moves
 //    one 16-byte pack of every input (V elements) and writes the V results
 //    with one store (16 bytes, or V bytes for a bool result); packs of a
 //    block are consecutive 4 KiB runs (fully coalesced).
+//  * rows: two merged dims whose inner dim is unit-stride for every operand
+//    and a whole number of packs, with any outer strides (0 included: a row
+//    broadcast such as a bias, or row views of a wider tensor); one pack per
+//    thread as in the dense shape, the row and pack from one division.
 //  * strided: any strides (0 = broadcast) over up to 8 merged dims, 32-bit
 //    index math whenever every offset fits.
 // The output element type is the functor's result type (bool for the
@@ -706,6 +710,51 @@ __global__ __launch_bounds__(kThreads) void k_unary_dense(const T* x, O* y, int6
   }
 }
 
+// Rows shape: pack p is pack p % ppr of row p / ppr; operand k's row r
+// starts at r * s0[k] (a multiple of the pack width).
+template <typename T, typename O, typename F, typename I>
+__global__ __launch_bounds__(kThreads) void k_unary_rows(const T* x, O* y, I xs0, I ys0, I ppr, I npack, F f) {
+  constexpr int V = Pack16<T>::N;
+  const I p = static_cast<I>(block_id()) * kThreads + threadIdx.x;  // blocks_2d grid
+  if (p >= npack) return;
+  const I r = p / ppr, c = (p - r * ppr) * V;
+  const Pack16<T> v = load16_nt(x + r * xs0 + c);
+  O o[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) o[i] = f(v.v[i]);
+  store_out<O, V>(y + r * ys0 + c, o);
+}
+
+template <typename T, typename O, typename F, typename I>
+__global__ __launch_bounds__(kThreads) void k_binary_rows(const T* a, const T* b, O* y, I as0, I bs0, I ys0, I ppr,
+                                                          I npack, F f) {
+  constexpr int V = Pack16<T>::N;
+  const I p = static_cast<I>(block_id()) * kThreads + threadIdx.x;  // blocks_2d grid
+  if (p >= npack) return;
+  const I r = p / ppr, c = (p - r * ppr) * V;
+  const Pack16<T> va = load16_nt(a + r * as0 + c);
+  const Pack16<T> vb = load16_nt(b + r * bs0 + c);
+  O o[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) o[i] = f(va.v[i], vb.v[i]);
+  store_out<O, V>(y + r * ys0 + c, o);
+}
+
+template <typename T, typename O, typename F, typename S, typename I>
+__global__ __launch_bounds__(kThreads) void k_binary_scalar_rows(const T* a, S braw, O* y, I as0, I ys0, I ppr,
+                                                                 I npack, F f) {
+  constexpr int V = Pack16<T>::N;
+  const auto bs = f.scalar_b(braw);
+  const I p = static_cast<I>(block_id()) * kThreads + threadIdx.x;  // blocks_2d grid
+  if (p >= npack) return;
+  const I r = p / ppr, c = (p - r * ppr) * V;
+  const Pack16<T> va = load16_nt(a + r * as0 + c);
+  O o[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) o[i] = f.with_scalar(va.v[i], bs);
+  store_out<O, V>(y + r * ys0 + c, o);
+}
+
 template <typename T, typename O, typename F, typename I>
 __global__ __launch_bounds__(kThreads) void k_unary_strided(KSpace<2, I> sp, const T* x, O* y,
                                                             I n, F f) {
@@ -826,6 +875,24 @@ inline unsigned strided_blocks(int64_t n) {
   return static_cast<unsigned>(b < 1 ? 1 : b);
 }
 
+// Whether the rows shape applies: two dims, the inner one unit-stride for
+// every operand and a whole number of V-element packs, outer strides
+// multiples of V (every row starts on a pack boundary).
+template <int NOPS>
+bool space_is_rows(const StridedSpace<NOPS>& sp, int V) {
+  if (sp.ndim != 2 || sp.shape[1] % V != 0) return false;
+  for (int k = 0; k < NOPS; ++k)
+    if (sp.stride[k][1] != 1 || sp.stride[k][0] % V != 0) return false;
+  return true;
+}
+
+// Rows-shape operands: (npack, packs per row, outer strides) with the index
+// type the launch uses (32-bit when every offset and pack index fits).
+template <int NOPS>
+bool rows_fit_int32(const StridedSpace<NOPS>& sp, int64_t n) {
+  return fits_int32(sp, n) && n < (int64_t(1) << 31);
+}
+
 template <int NOPS>
 bool space_is_dense(const StridedSpace<NOPS>& sp) {
   if (sp.ndim == 0) return true;
@@ -860,6 +927,15 @@ int launch_unary(const F& f, int ndim, const int64_t* shape, const void* xv, con
     const int64_t npack = n / V;
     hipLaunchKernelGGL((k_unary_dense<T, O, F>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0, st,
                        x, y, npack, n, f);
+  } else if (space_is_rows(sp, V) && aligned16(x) && out_aligned<O, V>(y)) {
+    const int64_t npack = n / V, ppr = sp.shape[1] / V;
+    if (rows_fit_int32(sp, n))
+      hipLaunchKernelGGL((k_unary_rows<T, O, F, int32_t>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0, st, x,
+                         y, static_cast<int32_t>(sp.stride[0][0]), static_cast<int32_t>(sp.stride[1][0]),
+                         static_cast<int32_t>(ppr), static_cast<int32_t>(npack), f);
+    else
+      hipLaunchKernelGGL((k_unary_rows<T, O, F, int64_t>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0, st, x,
+                         y, sp.stride[0][0], sp.stride[1][0], ppr, npack, f);
   } else if (fits_int32(sp, n)) {
     hipLaunchKernelGGL((k_unary_strided<T, O, F, int32_t>), dim3(strided_blocks(n)),
                        dim3(kThreads), 0, st, to_kspace<2, int32_t>(sp), x, y,
@@ -900,6 +976,16 @@ int launch_binary(const F& f, int ndim, const int64_t* shape, const void* av, co
       const int64_t npack = n / V;
       hipLaunchKernelGGL((k_binary_scalar_dense<T, O, F, S>), blocks_2d(dense_blocks(npack)),
                          dim3(kThreads), 0, st, a, braw, y, npack, n, f);
+    } else if (space_is_rows(sp, V) && aligned16(a) && out_aligned<O, V>(y)) {
+      const int64_t npack = n / V, ppr = sp.shape[1] / V;
+      if (rows_fit_int32(sp, n))
+        hipLaunchKernelGGL((k_binary_scalar_rows<T, O, F, S, int32_t>), blocks_2d(dense_blocks(npack)), dim3(kThreads),
+                           0, st, a, braw, y, static_cast<int32_t>(sp.stride[0][0]),
+                           static_cast<int32_t>(sp.stride[1][0]), static_cast<int32_t>(ppr),
+                           static_cast<int32_t>(npack), f);
+      else
+        hipLaunchKernelGGL((k_binary_scalar_rows<T, O, F, S, int64_t>), blocks_2d(dense_blocks(npack)), dim3(kThreads),
+                           0, st, a, braw, y, sp.stride[0][0], sp.stride[1][0], ppr, npack, f);
     } else if (fits_int32(sp, n)) {
       hipLaunchKernelGGL((k_binary_scalar_strided<T, O, F, S, int32_t>), dim3(strided_blocks(n)),
                          dim3(kThreads), 0, st, to_kspace<2, int32_t>(sp), a, braw, y,
@@ -920,6 +1006,16 @@ int launch_binary(const F& f, int ndim, const int64_t* shape, const void* av, co
     const int64_t npack = n / V;
     hipLaunchKernelGGL((k_binary_dense<T, O, F>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0, st,
                        a, b, y, npack, n, f);
+  } else if (space_is_rows(sp, V) && aligned16(a) && aligned16(b) && out_aligned<O, V>(y)) {
+    const int64_t npack = n / V, ppr = sp.shape[1] / V;
+    if (rows_fit_int32(sp, n))
+      hipLaunchKernelGGL((k_binary_rows<T, O, F, int32_t>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0, st, a,
+                         b, y, static_cast<int32_t>(sp.stride[0][0]), static_cast<int32_t>(sp.stride[1][0]),
+                         static_cast<int32_t>(sp.stride[2][0]), static_cast<int32_t>(ppr),
+                         static_cast<int32_t>(npack), f);
+    else
+      hipLaunchKernelGGL((k_binary_rows<T, O, F, int64_t>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0, st, a,
+                         b, y, sp.stride[0][0], sp.stride[1][0], sp.stride[2][0], ppr, npack, f);
   } else if (fits_int32(sp, n)) {
     hipLaunchKernelGGL((k_binary_strided<T, O, F, int32_t>), dim3(strided_blocks(n)),
                        dim3(kThreads), 0, st, to_kspace<3, int32_t>(sp), a, b, y,

@@ -260,3 +260,60 @@ def test_dense_kernels_past_65536_blocks():
     from ntops_amd.torch.utils import _cast_into
     _cast_into(x, c)
     assert torch.equal(c, x)
+
+
+@pytest.mark.parametrize("dtype", FLOATS)
+def test_rows_shape_broadcast_rows_and_row_views(dtype):
+    """Two merged dims with a unit-stride inner dim of whole packs and any
+    outer strides (the rows launch shape): a bias row broadcast over rows,
+    row views of a wider tensor, a bool result, a scalar operand -- bit for
+    bit against torch on the CPU (single rounding of each result)."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(300, 1024, generator=g).to(dtype)
+    bias = torch.randn(1024, generator=g).to(dtype)
+    xg, bg = x.cuda(), bias.cuda()
+    assert_equal(ntops_amd.torch.add(xg, bg), x + bias, "add row broadcast")
+    assert_equal(ntops_amd.torch.mul(bg, xg), bias * x, "mul row broadcast (first operand)")
+    assert_equal(ntops_amd.torch.eq(xg, bg), x == bias, "eq row broadcast")
+    v, vg = x[:, 256:768], xg[:, 256:768]
+    assert_equal(ntops_amd.torch.add(vg, xg[:, :512]), v + x[:, :512], "add row views")
+    assert_equal(ntops_amd.torch.mul(vg, 0.375), v * 0.375, "mul scalar row view")
+    assert_equal(ntops_amd.torch.gt(vg, 0.25), v > 0.25, "gt scalar row view")
+    dt = DT_NAME[dtype]
+    assert_close(ntops_amd.torch.silu(vg), from_np(O.silu(to_np(v), dt), dt), *TOL_ELEMENTWISE[dt], "silu row view")
+    i = torch.randint(-(1 << 30), 1 << 30, (77, 512), generator=g, dtype=torch.int32)
+    assert_equal(ntops_amd.torch.bitwise_and(i.cuda(), i[3].cuda()), i & i[3], "bitwise_and row broadcast")
+
+
+def test_permuted_dense_layouts_run_dense():
+    """A transposed / permuted dense operand whose output follows its layout
+    (empty_like) is one dense run once the dims are ordered by the output's
+    strides: results bit for bit, output strides those of the input."""
+    g = torch.Generator().manual_seed(6)
+    a = torch.randn(4, 96, 40, generator=g).bfloat16()
+    b = torch.randn(4, 96, 40, generator=g).bfloat16()
+    ap, bp = a.permute(2, 0, 1), b.permute(2, 0, 1)
+    got = ntops_amd.torch.add(ap.cuda(), bp.cuda())
+    assert got.stride() == ap.stride()
+    assert_equal(got, ap + bp, "add permuted")
+    got = ntops_amd.torch.mul(ap.cuda(), bp.contiguous().cuda())  # same values, row-major layout
+    assert_equal(got, ap * bp, "mul permuted x other layout")
+    dt = "bf16"
+    got = ntops_amd.torch.silu(a.transpose(0, 2).cuda())
+    assert got.stride() == a.transpose(0, 2).stride()
+    assert_close(got, from_np(O.silu(to_np(a.transpose(0, 2)), dt), dt), *TOL_ELEMENTWISE[dt], "silu transposed")
+
+
+def test_rows_shape_past_2_31_elements():
+    """The rows shape with 64-bit indices: a bias row added to 524289 rows of
+    4096 bf16 elements (2^31 + 4096), checked bit for bit against torch's
+    own add on the first rows, the rows around element 2^31 and the last."""
+    rows, cols = (1 << 31) // 4096 + 1, 4096
+    g = torch.Generator(device="cuda").manual_seed(8)
+    x = torch.randn(rows, cols, device="cuda", generator=g).bfloat16()
+    bias = torch.randn(cols, device="cuda", generator=g).bfloat16()
+    y = ntops_amd.torch.add(x, bias)
+    mid = (1 << 31) // cols
+    for lo, hi in ((0, 4), (mid - 2, mid + 1), (rows - 3, rows)):
+        assert torch.equal(y[lo:hi], x[lo:hi] + bias), (lo, hi)
+    del x, y
