@@ -9,6 +9,32 @@ from ntops_amd import _lib
 from ntops_amd.torch.utils import _DeviceGuard, _contiguous
 
 
+def _merged_stride(shape, stride, lo, hi):
+    """The one stride that walks dims lo .. hi - 1 of a view as a single
+    dim (size-1 dims ignored; 1 when all are size 1), or None when they do
+    not merge."""
+    dims = [d for d in range(lo, hi) if shape[d] != 1]
+    if not dims:
+        return 1
+    for a, b in zip(dims, dims[1:]):
+        if stride[a] != stride[b] * shape[b]:
+            return None
+    return stride[dims[-1]]
+
+
+def _view_strides(input, dim):
+    """(outer, dim, inner) element strides of `input` seen as
+    (outer, size, inner) around `dim`, when the leading and the trailing dims
+    each merge into one; else None (the input is then copied row-major).
+    Row views of a wider tensor run in place this way."""
+    shape, stride = input.shape, input.stride()
+    s_outer = _merged_stride(shape, stride, 0, dim)
+    s_inner = _merged_stride(shape, stride, dim + 1, input.dim())
+    if s_outer is None or s_inner is None:
+        return None
+    return (s_outer, stride[dim], s_inner)
+
+
 def softmax(input, dim, dtype=None):
     tensor_dtype = dtype if dtype is not None else input.dtype
     if tensor_dtype not in (torch.float32, torch.float16, torch.bfloat16, torch.float64):
@@ -30,9 +56,13 @@ def softmax(input, dim, dtype=None):
         inner = math.prod(input.shape[dim + 1 :])
 
     dev = _lib.require_cuda(input)
-    x = _contiguous(input)
-    output = torch.empty(input.shape, dtype=tensor_dtype, device=input.device)
     strides = (size * inner, inner, 1)
+    x_strides = _view_strides(input, dim) if ndim > 0 else strides
+    x = input
+    if x_strides is None:
+        x = _contiguous(input)
+        x_strides = strides
+    output = torch.empty(input.shape, dtype=tensor_dtype, device=input.device)
 
     lib = _lib.load()
     with _DeviceGuard(dev):
@@ -43,7 +73,7 @@ def softmax(input, dim, dtype=None):
             size,
             inner,
             x.data_ptr(),
-            _lib.i64_array(strides),
+            _lib.i64_array(x_strides),
             output.data_ptr(),
             _lib.i64_array(strides),
             _lib.stream_of(output),

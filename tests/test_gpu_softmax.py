@@ -95,6 +95,40 @@ def test_softmax_noncontiguous():
         assert_close(got, exp, 1.6e-2, 1.6e-2, f"permuted dim {dim}")
 
 
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float32))
+def test_softmax_views_read_in_place(dtype):
+    """Views whose leading and trailing dims each merge into one stride run
+    in place, without a row-major copy: row views of a wider tensor (the
+    register-resident, looped and wide-row kernels), a middle dim of a
+    transposed tensor, an expanded (stride-0) row, a sliced batch."""
+    g = torch.Generator().manual_seed(11)
+    dt = DT_NAME[dtype]
+    tol = TOL_REDUCTION[dt]
+    big = (torch.randn(64, 1024 + 160, generator=g) * 2).to(dtype)
+    bg = big.cuda()
+    for lo, w in ((0, 128), (8, 1024), (160, 1024), (3, 77)):
+        got = ntops_amd.torch.softmax(bg[:, lo:lo + w], -1)
+        exp = from_np(O.softmax(to_np(big[:, lo:lo + w].contiguous()), -1, dt), dt)
+        assert_close(got, exp, *tol, f"row view [{lo}, {lo + w})")
+    wide = (torch.randn(3, 70000 + 64, generator=g)).to(dtype)
+    got = ntops_amd.torch.softmax(wide.cuda()[:, 64:], -1)
+    exp = from_np(O.softmax(to_np(wide[:, 64:].contiguous()), -1, dt), dt)
+    assert_close(got, exp, *tol, "wide row view")
+    z = torch.randn(8, 16, 40, generator=g).to(dtype)
+    zt = z.transpose(0, 1)  # (16, 8, 40): dim 1 has stride 640, outer stride 40
+    got = ntops_amd.torch.softmax(zt.cuda(), 1)
+    exp = from_np(O.softmax(to_np(zt.contiguous()), 1, dt), dt)
+    assert_close(got, exp, *tol, "transposed middle dim")
+    row = torch.randn(1, 256, generator=g).to(dtype)
+    got = ntops_amd.torch.softmax(row.cuda().expand(5, 256), -1)
+    exp = from_np(O.softmax(to_np(row.expand(5, 256).contiguous()), -1, dt), dt)
+    assert_close(got, exp, *tol, "expanded row")
+    b = torch.randn(6, 4, 96, generator=g).to(dtype)
+    got = ntops_amd.torch.softmax(b.cuda()[1::2], -1)
+    exp = from_np(O.softmax(to_np(b[1::2].contiguous()), -1, dt), dt)
+    assert_close(got, exp, *tol, "sliced batch")
+
+
 def test_softmax_config_full_size():
     """bf16 (4, 32, 2048, 2048) scores ~N(0,1)/sqrt(128), -inf above the
     diagonal, softmax over the last dim."""
