@@ -15,7 +15,7 @@ import math
 import torch
 
 from ntops_amd import _lib
-from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _norm_param
+from ntops_amd.torch.utils import _DeviceGuard, _norm_param, _rows_of
 
 
 def add_rms_norm(input, residual, normalized_shape, weight=None, eps=None, *, inplace=False):
@@ -42,9 +42,11 @@ def add_rms_norm(input, residual, normalized_shape, weight=None, eps=None, *, in
         if input.data_ptr() == residual.data_ptr():
             raise RuntimeError("add_rms_norm: inplace needs distinct input and residual")
         x, res, output, new_residual = input, residual, input, residual
+        x_rs = r_rs = cols
     else:
-        x, res = _contiguous(input), _contiguous(residual)
-        output, new_residual = torch.empty_like(x), torch.empty_like(x)
+        (x, x_rs), (res, r_rs) = _rows_of(input, nd), _rows_of(residual, nd)
+        output = torch.empty(input.shape, dtype=input.dtype, device=input.device)
+        new_residual = torch.empty(input.shape, dtype=input.dtype, device=input.device)
 
     w_ptr, w_rs, w_code = None, 0, _lib.dtype_code(input.dtype)
     if weight is not None:
@@ -56,7 +58,7 @@ def add_rms_norm(input, residual, normalized_shape, weight=None, eps=None, *, in
     lib = _lib.load()
     with _DeviceGuard(dev):
         rc = lib.ntops_add_rms_norm(
-            _lib.dtype_code(input.dtype), rows, cols, x.data_ptr(), cols, res.data_ptr(), cols, w_ptr, w_rs, w_code,
+            _lib.dtype_code(input.dtype), rows, cols, x.data_ptr(), x_rs, res.data_ptr(), r_rs, w_ptr, w_rs, w_code,
             float(eps), output.data_ptr(), cols, new_residual.data_ptr(), cols, _lib.stream_of(output))
     _lib.check(rc, "ntops_amd.add_rms_norm")
     return output, new_residual

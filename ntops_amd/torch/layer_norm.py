@@ -6,7 +6,7 @@ import math
 import torch
 
 from ntops_amd import _lib
-from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _norm_param
+from ntops_amd.torch.utils import _DeviceGuard, _norm_param, _rows_of
 
 
 def layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
@@ -25,8 +25,8 @@ def layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
     dev = _lib.require_cuda(input, weight, bias)
     cols = math.prod(normalized_shape)
     rows = input.numel() // cols if cols else 0
-    x = _contiguous(input)
-    output = torch.empty_like(x)
+    x, x_rs = _rows_of(input, nd)
+    output = torch.empty(input.shape, dtype=input.dtype, device=input.device)
 
     # weight and bias share one dtype (the input's, or fp32 for both) and
     # one row stride: each is expanded like the reference's
@@ -49,7 +49,7 @@ def layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
             rows,
             cols,
             x.data_ptr(),
-            cols,
+            x_rs,
             weight.data_ptr() if weight is not None else None,
             bias.data_ptr() if bias is not None else None,
             wb_rs,

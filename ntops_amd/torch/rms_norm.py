@@ -14,7 +14,7 @@ import math
 import torch
 
 from ntops_amd import _lib
-from ntops_amd.torch.utils import _DeviceGuard, _contiguous, _norm_param
+from ntops_amd.torch.utils import _DeviceGuard, _norm_param, _rows_of
 
 
 def rms_norm(input, normalized_shape, weight=None, eps=None):
@@ -36,8 +36,8 @@ def rms_norm(input, normalized_shape, weight=None, eps=None):
     dev = _lib.require_cuda(input, weight)
     cols = math.prod(normalized_shape)
     rows = input.numel() // cols if cols else 0
-    x = _contiguous(input)
-    output = torch.empty_like(x)
+    x, x_rs = _rows_of(input, nd)
+    output = torch.empty(input.shape, dtype=input.dtype, device=input.device)
 
     w_ptr, w_rs, w_code = None, 0, _lib.dtype_code(input.dtype)
     if weight is not None:
@@ -53,7 +53,7 @@ def rms_norm(input, normalized_shape, weight=None, eps=None):
             rows,
             cols,
             x.data_ptr(),
-            cols,
+            x_rs,
             w_ptr,
             w_rs,
             w_code,

@@ -147,6 +147,38 @@ def _contiguous(t):
     return _cast_into(t, out)
 
 
+def _rows_of(t, nd):
+    """(rows tensor, row stride) for a norm over t's last nd dims: t itself
+    when those dims are one contiguous run per row, the leading dims walk
+    the rows with a single stride, and every row starts at the same offset
+    within 16 bytes as the matching row of a row-major output (row views of
+    a wider tensor read in place, on the kernels a row-major copy would
+    take), else a row-major copy made by the native copy kernel (row
+    stride = the row length)."""
+    shape, stride = t.shape, t.stride()
+    lead = t.dim() - nd
+    cols = 1
+    for n in shape[lead:]:
+        cols *= n
+    expect = 1
+    for d in range(t.dim() - 1, lead - 1, -1):
+        if shape[d] != 1 and stride[d] != expect:
+            return _contiguous(t), cols
+        expect *= shape[d]
+    dims = [d for d in range(lead) if shape[d] != 1]
+    if t.data_ptr() % 16:
+        return _contiguous(t), cols
+    if not dims:
+        return t, cols
+    for a, b in zip(dims, dims[1:]):
+        if stride[a] != stride[b] * shape[b]:
+            return _contiguous(t), cols
+    rs = stride[dims[-1]]
+    if ((rs - cols) * t.element_size()) % 16:
+        return _contiguous(t), cols
+    return t, rs
+
+
 def _norm_param(param, input, nd, dtype, per_row=False):
     """A norm's weight or bias as the reference passes it to its kernel,
     `param.expand_as(input)` (src/ntops/torch/rms_norm.py:17-18,

@@ -158,6 +158,31 @@ def test_rms_norm_odd_width_row_views(cols, dtype):
         assert_close(got, exp, rtol, atol, f"rms_norm row views offset {lo}")
 
 
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float32))
+@pytest.mark.parametrize("cols, lo, width", ((4096, 256, 8192), (1024, 8, 1152), (100000, 64, 100064), (1000, 24, 1032)))
+def test_norms_on_row_views_in_place(cols, lo, width, dtype):
+    """Row views of a wider tensor whose rows start 16-byte aligned like a
+    row-major output's run in place (row stride passed to the kernels):
+    rms_norm, layer_norm and add_rms_norm equal, bit for bit, the same call
+    on a row-major copy of the view, and match the oracle."""
+    g = torch.Generator().manual_seed(cols + lo)
+    big = torch.randn(19, width, generator=g).to(dtype)
+    res_big = torch.randn(19, width, generator=g).to(dtype)
+    w = (1 + 0.02 * torch.randn(cols, generator=g)).to(dtype)
+    b = (0.02 * torch.randn(cols, generator=g)).to(dtype)
+    v, r = big.cuda()[:, lo:lo + cols], res_big.cuda()[:, lo:lo + cols]
+    vc, rc = v.contiguous(), r.contiguous()
+    T = ntops_amd.torch
+    assert torch.equal(T.rms_norm(v, (cols,), w.cuda(), 1e-6), T.rms_norm(vc, (cols,), w.cuda(), 1e-6))
+    assert torch.equal(T.layer_norm(v, (cols,), w.cuda(), b.cuda()), T.layer_norm(vc, (cols,), w.cuda(), b.cuda()))
+    o1, n1 = T.add_rms_norm(v, r, (cols,), w.cuda(), 1e-6)
+    o2, n2 = T.add_rms_norm(vc, rc, (cols,), w.cuda(), 1e-6)
+    assert torch.equal(o1, o2) and torch.equal(n1, n2)
+    dt = DT_NAME[dtype]
+    exp = from_np(O.rms_norm(to_np(big[:, lo:lo + cols].contiguous()), dt, cols, to_np(w), 1e-6), dt)
+    assert_close(T.rms_norm(v, (cols,), w.cuda(), 1e-6), exp, *TOL_REDUCTION[dt], "rms_norm row view")
+
+
 def test_norm_noncontiguous_input_and_fp32_weight():
     x = torch.randn(64, 96).bfloat16()
     xg = x.cuda().t()  # (96, 64) non-contiguous

@@ -91,3 +91,36 @@ def test_clamp_result_matches_torch(dtype):
                     _result(x, lo, hi)
                 continue
             assert _result(x, lo, hi) == (ref.dtype, ref.shape), (dtype, lo, hi)
+
+
+def test_rows_of_reads_row_views_in_place():
+    """Norm inputs: row views whose rows start 16-byte aligned like a
+    row-major output's are passed with their row stride; other layouts are
+    copied row-major (here on the CPU the copy is torch's, the rule is the
+    same)."""
+    import ntops_amd.torch.utils as U
+
+    copied = []
+    real = U._contiguous
+    U._contiguous = lambda t: copied.append(t.shape) or t.contiguous()
+    try:
+        base = torch.zeros(64, 1024, dtype=torch.bfloat16)
+        t, rs = U._rows_of(base[:, :512], 1)
+        assert rs == 1024 and t.data_ptr() == base.data_ptr() and not copied
+        t, rs = U._rows_of(base.view(8, 8, 1024)[:, :, 128:640], 1)  # leading dims merge
+        assert rs == 1024 and not copied
+        t, rs = U._rows_of(base.view(8, 8, 1024)[:, :4, :], 1)  # leading dims do not merge
+        assert rs == 1024 and copied and t.is_contiguous()
+        copied.clear()
+        t, rs = U._rows_of(base[:, 1:513], 1)  # rows at a 2-byte offset
+        assert rs == 512 and copied
+        copied.clear()
+        t, rs = U._rows_of(base[:, :100], 1)  # (1024 - 100) * 2 bytes is not a multiple of 16
+        assert rs == 100 and copied
+        copied.clear()
+        t, rs = U._rows_of(base.view(64, 16, 64)[:, :, :], 2)  # two normalized dims, contiguous
+        assert rs == 1024 and not copied
+        t, rs = U._rows_of(base.view(64, 16, 64).transpose(1, 2), 2)  # normalized dims not one run
+        assert rs == 1024 and copied
+    finally:
+        U._contiguous = real
