@@ -921,6 +921,241 @@ __global__ __launch_bounds__(64) void k_attn_generic(AttnArgs a) {
   }
 }
 
+// ---- fp32 attention on the matrix cores --------------------------------------
+// IEEE fp32 products (v_mfma_f32_16x16x4_f32) with fp32 accumulation and the
+// online-softmax recurrence in fp32.  Work item: (batch, head, 128 query
+// rows), 8 waves of 16 rows.  The scores are computed transposed,
+// S^T = K Q^T (keys x queries): lane l's accumulator r holds key
+// 4 (l >> 4) + r of a 16-key block for query l & 15.  That is the B operand
+// of O^T += V^T P^T for MFMA step r when the keys of step r are taken as
+// 4 (l >> 4) + r (a sum over keys does not depend on their order), so P
+// never leaves the registers; and every accumulator of a lane belongs to
+// one query, so the rescale of O is per lane while the row max and sum
+// combine the four lanes l & 15 + 16 g.  The head dim is walked as
+// d = 16 t + 4 g + e (g = l >> 4, e = MFMA step of a 4-step group) in both
+// products, so a lane reads 4 consecutive floats per 4 MFMAs.  K (32 keys x
+// DP) and V^T (DP x 32 keys) tiles are double-buffered in LDS, each tile's
+// global loads issued into registers before the previous tile's products
+// and stored after them (one barrier per tile).  Keys past Skv, past the
+// causal bound, and head-dim columns past D read as zero / are masked.
+constexpr int kF32K = 32;  // keys per tile
+
+template <int DP>
+constexpr int f32_attn_lds_bytes() {
+  return 2 * (kF32K * (DP + 4) + DP * (kF32K + 4)) * 4;
+}
+
+// NW waves, each with RG blocks of 16 query rows (the K and V fragments read
+// from LDS serve all RG of them).
+template <int DP, int NW, int RG>
+__global__ __launch_bounds__(64 * NW) void k_flash_f32(AttnArgs a, int nqb) {
+  constexpr int QB = 16 * NW * RG;  // query rows per block
+  constexpr int KP = DP + 4;        // floats per K row in LDS
+  constexpr int VP = kF32K + 4;     // floats per V^T row in LDS
+  constexpr int kKTile = kF32K * KP, kBuf = kKTile + DP * VP;
+  constexpr int kThreads = 64 * NW;
+  constexpr int kF4 = kF32K * DP / 4;                   // float4 per operand and tile
+  constexpr int kLd = (kF4 + kThreads - 1) / kThreads;  // per thread
+  static_assert(kF4 % kThreads == 0 || kThreads % kF4 == 0, "tile must split evenly over the block");
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t item = block_id();  // (batch, head, query block); blocks_2d grid
+  const int64_t nbh = static_cast<int64_t>(a.B) * a.Hq;
+  if (item >= nbh * nqb) return;  // the tail of the grid (the whole block)
+  // causal: longest query blocks first over the whole grid (the blocks run
+  // 4 .. S / 32 key tiles; dealing them longest first keeps the last
+  // round from being one long block); otherwise the query blocks of a head
+  // run together
+  int qb;
+  int64_t bh;
+  if (a.causal) {
+    qb = nqb - 1 - static_cast<int>(item / nbh);
+    bh = item % nbh;
+  } else {
+    qb = static_cast<int>(item % nqb);
+    bh = item / nqb;
+  }
+  const int h = static_cast<int>(bh % a.Hq);
+  const int b = static_cast<int>(bh / a.Hq);
+  const int hk = h / (a.Hq / a.Hkv);
+  const float* Q = static_cast<const float*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const float* K = static_cast<const float*>(a.k) + b * a.ks[0] + hk * a.ks[1];
+  const float* V = static_cast<const float*>(a.v) + b * a.vs[0] + hk * a.vs[1];
+  const int q_wave = qb * QB + wave * 16 * RG;  // this wave's first query
+  const int dt = a.D;
+  int qrow[RG];
+  f32x4 qf[RG][DP / 16];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    qrow[rg] = q_wave + 16 * rg + r16;
+#pragma unroll
+    for (int t = 0; t < DP / 16; ++t) {
+      const int d = 16 * t + 4 * g;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (qrow[rg] < a.Sq && d < dt) v = *reinterpret_cast<const f32x4*>(Q + qrow[rg] * a.qs[2] + d);
+      qf[rg][t] = v * a.scale_log2;
+    }
+  }
+  const int off = a.causal == 2 ? a.Skv - a.Sq : 0;
+  int kv_end = a.Skv;
+  if (a.causal) kv_end = max(0, min(a.Skv, qb * QB + QB - 1 + off + 1));
+  const int ntiles = (kv_end + kF32K - 1) / kF32K;
+  f32x4 kst[kLd], vst[kLd];
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < kLd; ++j) {
+      const int f = threadIdx.x + kThreads * j;
+      const int key = t * kF32K + f / (DP / 4), d = 4 * (f % (DP / 4));
+      const bool ok = f < kF4 && key < kv_end && d < dt;
+      f32x4 kz = {0.f, 0.f, 0.f, 0.f}, vz = {0.f, 0.f, 0.f, 0.f};
+      if (ok) {
+        kz = *reinterpret_cast<const f32x4*>(K + key * a.ks[2] + d);
+        vz = *reinterpret_cast<const f32x4*>(V + key * a.vs[2] + d);
+      }
+      kst[j] = kz;
+      vst[j] = vz;
+    }
+  };
+  auto store_tile = [&](int buf) {
+    float* kt = sm + buf * kBuf;
+    float* vt = kt + kKTile;
+#pragma unroll
+    for (int j = 0; j < kLd; ++j) {
+      const int f = threadIdx.x + kThreads * j;
+      if (f >= kF4) break;
+      const int kl = f / (DP / 4), d = 4 * (f % (DP / 4));
+      *reinterpret_cast<f32x4*>(kt + kl * KP + d) = kst[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vt[(d + e) * VP + kl] = vst[j][e];
+    }
+  };
+  int64_t mrow[RG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) mrow[rg] = b * a.ms[0] + h * a.ms[1] + static_cast<int64_t>(qrow[rg]) * a.ms[2];
+  f32x4 o[RG][DP / 16];
+  float m[RG], l[RG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    m[rg] = neg_inf();
+    l[rg] = 0.f;
+#pragma unroll
+    for (int i = 0; i < DP / 16; ++i) o[rg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  // the last key this wave's rows attend to (causal): tiles past it are
+  // loaded and stored for the block but not computed
+  const int wave_end = a.causal ? min(kv_end, q_wave + 16 * RG - 1 + off + 1) : kv_end;
+  for (int t = 0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) load_tile(t + 1);
+    const float* kt = sm + (t & 1) * kBuf;
+    const float* vt = kt + kKTile;
+    if (t * kF32K < wave_end) {  // wave-uniform
+      f32x4 sc[RG][2];
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) sc[rg][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int tt = 0; tt < DP / 16; ++tt)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + (kb * 16 + r16) * KP + 16 * tt + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg)
+              sc[rg][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[e], qf[rg][tt][e], sc[rg][kb], 0, 0, 0);
+        }
+      // mask, then the online softmax of each of this lane's queries
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) {
+        float mx = neg_inf();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = t * kF32K + kb * 16 + 4 * g + r;
+            float v = sc[rg][kb][r];
+            if (a.mask_dtype >= 0 && key < a.Skv && qrow[rg] < a.Sq) v += mask_log2(a, mrow[rg] + key * a.ms[3]);
+            if (key >= a.Skv || (a.causal && key > qrow[rg] + off)) v = neg_inf();
+            sc[rg][kb][r] = v;
+            mx = fmaxf(mx, v);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m[rg], mx);
+        const float m_use = m_new == neg_inf() ? 0.f : m_new;
+        const float alpha = fast_exp2(m[rg] - m_use);
+        float ps = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = fast_exp2(sc[rg][kb][r] - m_use);
+            sc[rg][kb][r] = p;
+            ps += p;
+          }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        l[rg] = l[rg] * alpha + ps;
+        m[rg] = m_new;
+#pragma unroll
+        for (int i = 0; i < DP / 16; ++i) o[rg][i] *= alpha;
+      }
+#pragma unroll
+      for (int i = 0; i < DP / 16; ++i)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const f32x4 vf = *reinterpret_cast<const f32x4*>(vt + (16 * i + r16) * VP + kb * 16 + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg)
+              o[rg][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[e], sc[rg][kb][e], o[rg][i], 0, 0, 0);
+        }
+    }
+    if (t + 1 < ntiles) store_tile((t + 1) & 1);  // read last in tile t - 1, before the barrier that ended it
+    __syncthreads();
+  }
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    if (qrow[rg] >= a.Sq) continue;
+    const float inv = l[rg] > 0.f ? 1.f / l[rg] : 0.f;  // fully masked rows give 0
+    float* O = static_cast<float*>(a.o) + b * a.os[0] + h * a.os[1] + static_cast<int64_t>(qrow[rg]) * a.os[2];
+#pragma unroll
+    for (int i = 0; i < DP / 16; ++i) {
+      const int d = 16 * i + 4 * g;
+      if (d < dt) *reinterpret_cast<f32x4*>(O + d) = o[rg][i] * inv;
+    }
+  }
+}
+
+template <int DP, int NW, int RG>
+int launch_flash_f32(const AttnArgs& a, hipStream_t st) {
+  constexpr int kLds = f32_attn_lds_bytes<DP>();
+  auto kern = k_flash_f32<DP, NW, RG>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, kLds) !=
+        hipSuccess)
+      return set_error(NTOPS_ERR_HIP, "sdpa: cannot reserve %d bytes of LDS", kLds);
+    attr_set = true;
+  }
+  constexpr int QB = 16 * NW * RG;
+  const int nqb = (a.Sq + QB - 1) / QB;
+  const int64_t total = static_cast<int64_t>(nqb) * a.Hq * a.B;
+  if (total > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "sdpa: too many blocks");
+  note_kernel("sdpa_f32 d%d", DP);
+  hipLaunchKernelGGL(kern, blocks_2d(total), dim3(64 * NW), kLds, st, a, nqb);
+  return check_launch("sdpa");
+}
+
 template <typename T, int D, bool CAUSAL, bool TAIL>
 int launch_flash_attn(const AttnArgs& a, hipStream_t st) {
   constexpr int kLds = kFaStages * 2 * 64 * D * 2;
@@ -1005,6 +1240,19 @@ int run_attention(const AttnArgs& a, hipStream_t st) {
 #undef NTOPS_FWD_D
 #undef NTOPS_FWD
       return check_launch("sdpa");
+    }
+  }
+  if constexpr (std::is_same<T, float>::value) {
+    // fp32 on the matrix cores: head dims up to 128 in multiples of 4,
+    // unit-stride head dims with 16-byte aligned rows
+    const auto unit4 = [&](const int64_t* s) { return s[3] == 1 && s[2] % 4 == 0 && s[1] % 4 == 0 && s[0] % 4 == 0; };
+    if (a.D % 4 == 0 && a.D <= 128 && unit4(a.qs) && unit4(a.ks) && unit4(a.vs) && unit4(a.os) && aligned16(a.q) &&
+        aligned16(a.k) && aligned16(a.v) && aligned16(a.o)) {
+      // 8 waves of one 16-row block each measured fastest: two blocks per
+      // wave (4 or 8 waves) need 190-400 registers and ran 2-45 % slower
+      if (a.D <= 32) return launch_flash_f32<32, 8, 1>(a, st);
+      if (a.D <= 64) return launch_flash_f32<64, 8, 1>(a, st);
+      return launch_flash_f32<128, 8, 1>(a, st);
     }
   }
   const int64_t rows = static_cast<int64_t>(a.B) * a.Hq * a.Sq;

@@ -305,3 +305,38 @@ def test_sdpa_lower_right_chained_zero_tile_items():
         exp = oracle(q[bi:bi + 1, h0:h0 + 4], k[bi:bi + 1, h0 // 4:h0 // 4 + 1], v[bi:bi + 1, h0 // 4:h0 // 4 + 1],
                      None, 2)
         assert_close(got[bi:bi + 1, h0:h0 + 4], exp, *TOL[dtype], f"batch {bi} heads {h0}..{h0 + 3}")
+
+
+@pytest.mark.parametrize("d", (4, 36, 64, 100, 128))
+def test_sdpa_f32_matrix_core_kernel(d):
+    """fp32 attention on the matrix-core kernel (IEEE fp32 products, fp32
+    accumulation): head dims in multiples of 4 up to 128, causal in both
+    corners over many query blocks (dealt longest first), GQA, an additive
+    float mask with a scale, against the oracle at the fp32 tolerance."""
+    g = torch.Generator().manual_seed(100 + d)
+    rt = lambda *s: torch.randn(*s, generator=g)  # noqa: E731
+    for (sq, skv, causal) in ((700, 700, 1), (300, 650, 2), (650, 300, 2), (257, 33, 0)):
+        q, k, v = rt(2, 8, sq, d), rt(2, 4, skv, d), rt(2, 4, skv, d)
+        variant = CausalVariant.LOWER_RIGHT if causal == 2 else None
+        got = sdpa(q.cuda(), k.cuda(), v.cuda(), is_causal=causal > 0, enable_gqa=True, causal_variant=variant)
+        assert _lib.last_kernel() == f"sdpa_f32 d{32 if d <= 32 else 64 if d <= 64 else 128}", _lib.last_kernel()
+        assert_close(got, oracle(q, k, v, None, causal), *TOL[torch.float32], f"d {d} sq {sq} skv {skv} causal {causal}")
+    q, k, v = rt(1, 4, 100, d), rt(1, 4, 90, d), rt(1, 4, 90, d)
+    m = rt(1, 4, 100, 90) * 2
+    got = sdpa(q.cuda(), k.cuda(), v.cuda(), attn_mask=m.cuda(), scale=0.3)
+    assert_close(got, oracle(q, k, v, m, 0, 0.3), *TOL[torch.float32], f"d {d} float mask")
+
+
+def test_sdpa_f32_generic_fallbacks():
+    """A head dim past 128 takes the generic kernel; a strided head dim is
+    laid out by the wrapper and runs on the matrix cores."""
+    g = torch.Generator().manual_seed(7)
+    rt = lambda *s: torch.randn(*s, generator=g)  # noqa: E731
+    q, k, v = rt(1, 2, 50, 132), rt(1, 2, 60, 132), rt(1, 2, 60, 132)
+    got = sdpa(q.cuda(), k.cuda(), v.cuda(), is_causal=True)
+    assert _lib.last_kernel() == "sdpa_generic"
+    assert_close(got, oracle(q, k, v, None, 1), *TOL[torch.float32], "d 132")
+    qs = rt(1, 2, 50, 64 * 2)[..., ::2]  # head-dim stride 2 (the wrapper lays it out for the kernels)
+    got = sdpa(qs.cuda(), k[..., :64].cuda(), v[..., :64].cuda())
+    assert_close(got, oracle(qs.contiguous(), k[..., :64].contiguous(), v[..., :64].contiguous()), *TOL[torch.float32],
+                 "strided head dim")
