@@ -492,22 +492,35 @@ struct DivF<MODE, T, true> {
 };
 // Integer trunc / floor division in int64; division by zero gives 0 (torch's
 // CPU kernel raises), b = -1 negates with wraparound.
+// Types of up to 32 bits divide in 32-bit arithmetic (exact for every
+// value they hold once b = 0 and b = -1 are taken out; a 64-bit division is
+// a long software sequence on the GPU), int64 and wider scalars in 64-bit.
 template <int MODE, typename T>
 struct DivF<MODE, T, false> {
-  __device__ __forceinline__ static int64_t apply(int64_t a, int64_t b) {
+  template <typename I>
+  __device__ __forceinline__ static I apply(I a, I b) {
+    using U = typename std::make_unsigned<I>::type;
     if (b == 0) return 0;
-    if (b == -1) return static_cast<int64_t>(static_cast<uint64_t>(0) - static_cast<uint64_t>(a));
-    int64_t q = a / b;
+    if (b == -1) return static_cast<I>(static_cast<U>(0) - static_cast<U>(a));
+    I q = a / b;
     if constexpr (MODE == 2)
       if ((a % b != 0) && ((a < 0) != (b < 0))) q -= 1;
     return q;
   }
   __device__ __forceinline__ T operator()(T a, T b) const {
-    return static_cast<T>(apply(static_cast<int64_t>(a), static_cast<int64_t>(b)));
+    if constexpr (sizeof(T) <= 4)
+      return static_cast<T>(apply<int32_t>(static_cast<int32_t>(a), static_cast<int32_t>(b)));
+    else
+      return static_cast<T>(apply<int64_t>(static_cast<int64_t>(a), static_cast<int64_t>(b)));
   }
-  __device__ __forceinline__ int64_t scalar_b(int64_t b) const { return b; }
+  // A Python-number divisor is first converted to T with wraparound, as
+  // torch does (uint8 by -7 divides by 249).
+  __device__ __forceinline__ int64_t scalar_b(int64_t b) const { return static_cast<int64_t>(static_cast<T>(b)); }
   __device__ __forceinline__ T with_scalar(T a, int64_t b) const {
-    return static_cast<T>(apply(static_cast<int64_t>(a), b));
+    if constexpr (sizeof(T) <= 4)
+      return static_cast<T>(apply<int32_t>(static_cast<int32_t>(a), static_cast<int32_t>(b)));
+    else
+      return static_cast<T>(apply<int64_t>(static_cast<int64_t>(a), b));
   }
 };
 
@@ -707,6 +720,29 @@ __global__ __launch_bounds__(kThreads) void k_unary_dense(const T* x, O* y, int6
   if (block_id() == 0) {
     const int64_t i = npack * V + threadIdx.x;
     if (threadIdx.x < V && i < n) y[i] = f(x[i]);
+  }
+}
+
+// One operand broadcast from a single element in memory (a 0-dim GPU
+// tensor), the other and the output dense: the element is read once per
+// thread, the dense operand in packs.  A_BCAST: the broadcast operand is a.
+template <typename T, typename O, typename F, bool A_BCAST>
+__global__ __launch_bounds__(kThreads) void k_binary_bcast_dense(const T* a, const T* b, O* y, int64_t npack,
+                                                                 int64_t n, F f) {
+  constexpr int V = Pack16<T>::N;
+  const T* d = A_BCAST ? b : a;
+  const T sv = A_BCAST ? a[0] : b[0];
+  const int64_t p = block_id() * kThreads + threadIdx.x;  // blocks_2d grid
+  if (p < npack) {
+    const Pack16<T> r = load16_nt(d + p * V);
+    O o[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) o[i] = A_BCAST ? f(sv, r.v[i]) : f(r.v[i], sv);
+    store_out<O, V>(y + p * V, o);
+  }
+  if (block_id() == 0) {
+    const int64_t i = npack * V + threadIdx.x;
+    if (threadIdx.x < V && i < n) y[i] = A_BCAST ? f(sv, d[i]) : f(d[i], sv);
   }
 }
 
@@ -1006,6 +1042,17 @@ int launch_binary(const F& f, int ndim, const int64_t* shape, const void* av, co
     const int64_t npack = n / V;
     hipLaunchKernelGGL((k_binary_dense<T, O, F>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0, st,
                        a, b, y, npack, n, f);
+  } else if (sp.ndim == 1 && sp.stride[2][0] == 1 && (sp.stride[0][0] == 0) != (sp.stride[1][0] == 0) &&
+             (sp.stride[0][0] == 1 || sp.stride[1][0] == 1) && out_aligned<O, V>(y) &&
+             aligned16(sp.stride[0][0] == 0 ? b : a)) {
+    // one operand a single element broadcast over a dense run
+    const int64_t npack = n / V;
+    if (sp.stride[0][0] == 0)
+      hipLaunchKernelGGL((k_binary_bcast_dense<T, O, F, true>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0,
+                         st, a, b, y, npack, n, f);
+    else
+      hipLaunchKernelGGL((k_binary_bcast_dense<T, O, F, false>), blocks_2d(dense_blocks(npack)), dim3(kThreads), 0,
+                         st, a, b, y, npack, n, f);
   } else if (space_is_rows(sp, V) && aligned16(a) && aligned16(b) && out_aligned<O, V>(y)) {
     const int64_t npack = n / V, ppr = sp.shape[1] / V;
     if (rows_fit_int32(sp, n))

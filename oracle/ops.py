@@ -387,6 +387,10 @@ def div(a, b, dt, rounding_mode=None):
         return round_to(q, dt)
     if dt == "bool" or rounding_mode is None:
         raise ValueError("div: integer true division promotes to float first")
+    if _is_number(b):
+        # a Python-number divisor is converted to dt with wrap-around first
+        # (torch: uint8 // -7 divides by 249)
+        b = _int_wrap(np.asarray(int(b), dtype=np.int64), dt)
     return _int_wrap(_int_divide(a, b, rounding_mode == "floor"), dt)
 
 

@@ -356,3 +356,43 @@ def test_div_floor_exact_remainder_cases():
     ab, bb = torch.from_numpy(a).bfloat16(), torch.from_numpy(b).bfloat16()
     got = T.div(ab.cuda(), bb.cuda(), rounding_mode="floor")
     same(got, ora(lambda x, y, d: O.div(x, y, d, "floor"), to_np(ab), to_np(bb), dt="bf16"), "floor hard cases bf16")
+
+
+@pytest.mark.parametrize("dtype", (torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8))
+@pytest.mark.parametrize("rounding_mode", ("trunc", "floor"))
+def test_div_integer_extremes(dtype, rounding_mode):
+    """Integer division at the type's extremes (the 32-bit arithmetic used
+    for types up to 32 bits, 64-bit for int64): min / -1 wraps, every sign
+    combination, |b| > |a|, tensor and number divisors (a number past the
+    32-bit range takes the 64-bit form), against torch on the CPU."""
+    info = torch.iinfo(dtype)
+    vals = sorted(v for v in {info.min, info.min + 1, -7, -3, -1, 0, 1, 2, 3, 7, info.max - 1, info.max}
+                  if info.min <= v <= info.max)
+    a = torch.tensor(vals, dtype=dtype).repeat_interleave(len(vals))
+    b = torch.tensor(vals, dtype=dtype).repeat(len(vals))
+    # min / -1 wraps to min; torch's CPU kernel traps on it for int32 / int64
+    wrap = (a == info.min) & (b == -1)
+    got_wrap = T.div(a[wrap].cuda(), b[wrap].cuda(), rounding_mode=rounding_mode)
+    assert (got_wrap.cpu() == info.min).all()
+    keep = (b != 0) & ~wrap
+    a, b = a[keep], b[keep]
+    got = T.div(a.cuda(), b.cuda(), rounding_mode=rounding_mode)
+    same(got, torch.div(a, b, rounding_mode=rounding_mode), f"div {rounding_mode} {dtype} extremes")
+    for num in (3, -7, info.max) + ((2**40,) if dtype == torch.int64 else ()):
+        got = T.div(a.cuda(), num, rounding_mode=rounding_mode)
+        same(got, torch.div(a, num, rounding_mode=rounding_mode), f"div {rounding_mode} {dtype} by {num}")
+
+
+def test_binary_zero_dim_gpu_operand():
+    """A 0-dim GPU tensor operand (broadcast from one element in memory) on
+    either side of a non-commutative op, bit for bit against torch."""
+    x = torch.randn(1000, 77).bfloat16()
+    s = torch.tensor(0.37).bfloat16()
+    xg, sg = x.cuda(), s.cuda()
+    same(T.sub(xg, sg), x - s, "x - s")
+    same(T.sub(sg, xg), s - x, "s - x")
+    same(T.div(sg, xg), s / x, "s / x")
+    same(T.mul(xg.t(), sg), x.t() * s, "transposed x * s")
+    i = torch.randint(-100, 100, (4096,), dtype=torch.int32)
+    d = torch.tensor(7, dtype=torch.int32)
+    same(T.div(i.cuda(), d.cuda(), rounding_mode="floor"), torch.div(i, d, rounding_mode="floor"), "int floor by 0-dim")

@@ -390,3 +390,17 @@ def _m_isinf_pos_only(x, dt):
 ])
 def test_planted_mistakes_are_caught(name, mutant):
     assert not PINS[name](mutant), f"a planted mistake in {name} went unnoticed"
+
+
+def test_oracle_int_div_number_wraps_to_dtype():
+    """An integer tensor divided by a Python number: the number is converted
+    to the tensor's dtype with wrap-around first, as torch's CPU kernel does
+    (uint8 // -7 divides by 249, int8 // 300 by 44)."""
+    for dt, vals, num in (("u8", [0, 5, 200, 255], -7), ("u8", [0, 5, 200, 255], 300), ("i8", [-100, 5, 100], 300),
+                          ("i8", [-100, 5, 100], -300), ("i32", [-7, 7, 2**31 - 1], 3)):
+        tdt = {"u8": torch.uint8, "i8": torch.int8, "i32": torch.int32}[dt]
+        a = torch.tensor(vals, dtype=tdt)
+        for mode in ("trunc", "floor"):
+            exp = torch.div(a, num, rounding_mode=mode).numpy()
+            got = O.div(a.numpy(), num, dt, mode)
+            np.testing.assert_array_equal(got, exp, err_msg=f"{dt} {vals} // {num} {mode}")
