@@ -18,6 +18,9 @@
  *                        (kernels/<op>.py application)
  *   ntops_binary      <- src/ntops/torch/{add,mul,bitwise_and,bitwise_or}.py:7-15,
  *                        {sub,div,pow}.py:7-15
+ *   ntops_binary_cvt  <- no ntops counterpart (ntops requires equal dtypes):
+ *                        torch's promotion of mixed operand dtypes to fp32
+ *                        (cast, then the op) fused into the elementwise pass
  *   ntops_compare     <- src/ntops/torch/{eq,ne,gt,ge,lt,le}.py:7-15
  *   ntops_classify    <- src/ntops/torch/{isinf,isnan}.py:7-14
  *   ntops_clamp       <- src/ntops/torch/clamp.py:7-15
@@ -160,6 +163,15 @@ NTOPS_API int ntops_binary(int op, int dtype, int ndim, const int64_t* shape,
                  const void* b, const int64_t* b_strides,
                  double b_f, int64_t b_i, double alpha_f, int64_t alpha_i,
                  void* out, const int64_t* out_strides, void* stream);
+
+/* out (F32) = op(a, b) over n dense elements whose operand dtypes differ
+ * from the fp32 result (a_dtype, b_dtype in {F32, F16, BF16, I32}; dtype
+ * must be F32): each operand is converted to fp32 on load and the fp32 op
+ * of ntops_binary applied, so the result equals casting both first and
+ * calling ntops_binary on F32 -- in one pass.  op in {ADD, SUB, MUL, DIV};
+ * alpha_f as for ntops_binary.  a, b and out must be 16-byte aligned. */
+NTOPS_API int ntops_binary_cvt(int op, int a_dtype, int b_dtype, int dtype, int64_t n,
+                 const void* a, const void* b, double alpha_f, void* out, void* stream);
 
 enum ntops_compare_op {
   NTOPS_CMP_EQ = 1, /* a == b   eq.py:9 */

@@ -54,6 +54,7 @@ _SIGNATURES = {
         _i,
         [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _i64, _d, _i64, _vp, _c_i64p, _vp],
     ),
+    "ntops_binary_cvt": (_i, [_i, _i, _i, _i, _i64, _vp, _vp, _d, _vp, _vp]),
     "ntops_compare": (
         _i,
         [_i, _i, _i, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _d, _i64, _vp, _c_i64p, _vp],

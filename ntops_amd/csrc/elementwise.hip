@@ -901,6 +901,75 @@ __global__ __launch_bounds__(kThreads) void k_clamp_strided(KSpace<4, I> sp, con
   }
 }
 
+// Mixed operand dtypes with an fp32 result (torch's promotion of, e.g., a
+// bf16 tensor and an fp32 tensor, or int32 true division): both operands
+// dense, converted to fp32 on load (exact for 16-bit floats; int32 rounds
+// to nearest even, as torch's cast does) and combined by the fp32 functor,
+// so the result equals casting first and then running the fp32 op.  Eight
+// elements per thread: one or two 16-byte loads per operand, two 16-byte
+// stores.
+template <typename Ta, typename Tb, typename F>
+__global__ __launch_bounds__(kThreads) void k_binary_cvt(const Ta* a, const Tb* b, float* y, int64_t n8, int64_t n,
+                                                         F f) {
+  const int64_t p = block_id() * kThreads + threadIdx.x;  // blocks_2d grid
+  auto ld8 = [](auto* src, int64_t i, float (&v)[8]) {
+    using S = typename std::remove_const<typename std::remove_pointer<decltype(src)>::type>::type;
+    if constexpr (sizeof(S) == 2) {
+      const Pack16<S> r = load16_nt(src + i);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(r.v[e]);
+    } else {
+      const Pack16<S> r0 = load16_nt(src + i), r1 = load16_nt(src + i + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = static_cast<float>(r0.v[e]);
+        v[e + 4] = static_cast<float>(r1.v[e]);
+      }
+    }
+  };
+  if (p < n8) {
+    float va[8], vb[8];
+    ld8(a, p * 8, va);
+    ld8(b, p * 8, vb);
+    float o0[4], o1[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o0[e] = f(va[e], vb[e]);
+      o1[e] = f(va[e + 4], vb[e + 4]);
+    }
+    store_out<float, 4>(y + p * 8, o0);
+    store_out<float, 4>(y + p * 8 + 4, o1);
+  }
+  if (block_id() == 0) {
+    const int64_t i = n8 * 8 + threadIdx.x;
+    if (threadIdx.x < 8 && i < n) y[i] = f(static_cast<float>(a[i]), static_cast<float>(b[i]));
+  }
+}
+
+template <typename F>
+int launch_binary_cvt(const F& f, int a_dtype, int b_dtype, int64_t n, const void* a, const void* b, void* y,
+                      hipStream_t st, const char* what) {
+  auto cvt_type = [&](int dt, const char* w, auto&& fn) -> int {
+    switch (dt) {
+      case NTOPS_F32: return fn(float{});
+      case NTOPS_F16: return fn(_Float16{});
+      case NTOPS_BF16: return fn(__bf16{});
+      case NTOPS_I32: return fn(int32_t{});
+      default: return set_error(NTOPS_ERR_UNSUPPORTED, "%s: unsupported operand dtype %d", w, dt);
+    }
+  };
+  return cvt_type(a_dtype, what, [&](auto ta) {
+    using Ta = decltype(ta);
+    return cvt_type(b_dtype, what, [&](auto tb) {
+      using Tb = decltype(tb);
+      const int64_t n8 = n / 8;
+      hipLaunchKernelGGL((k_binary_cvt<Ta, Tb, F>), blocks_2d(ceil_div(n8 > 0 ? n8 : 1, int64_t{kThreads})), dim3(kThreads), 0, st,
+                         static_cast<const Ta*>(a), static_cast<const Tb*>(b), static_cast<float*>(y), n8, n, f);
+      return check_launch(what);
+    });
+  });
+}
+
 // ------------------------------------------------------------ launchers --
 inline int64_t dense_blocks(int64_t npack) {
   return ceil_div(npack > 0 ? npack : 1, static_cast<int64_t>(kThreads));
@@ -1283,6 +1352,32 @@ extern "C" int ntops_binary(int op, int dtype, int ndim, const int64_t* shape, c
       });
     default:
       return set_error(NTOPS_ERR_UNSUPPORTED, "%s: unknown op %d", what, op);
+  }
+}
+
+extern "C" int ntops_binary_cvt(int op, int a_dtype, int b_dtype, int dtype, int64_t n, const void* a,
+                                const void* b, double alpha_f, void* out, void* stream) {
+  const char* what = "ntops_binary_cvt";
+  if (n < 0) return set_error(NTOPS_ERR_INVALID, "%s: negative size", what);
+  if (n == 0) return NTOPS_OK;
+  if (a == nullptr || b == nullptr || out == nullptr) return set_error(NTOPS_ERR_INVALID, "%s: null pointer", what);
+  if (dtype != NTOPS_F32) return set_error(NTOPS_ERR_UNSUPPORTED, "%s: the result must be fp32", what);
+  if (!aligned16(a) || !aligned16(b) || !aligned16(out))
+    return set_error(NTOPS_ERR_INVALID, "%s: operands must be 16-byte aligned", what);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (op) {
+    case NTOPS_BINARY_ADD:
+    case NTOPS_BINARY_SUB: {
+      AddF<float> f;
+      f.alpha = op == NTOPS_BINARY_SUB ? -alpha_f : alpha_f;
+      return launch_binary_cvt(f, a_dtype, b_dtype, n, a, b, out, st, what);
+    }
+    case NTOPS_BINARY_MUL:
+      return launch_binary_cvt(MulF<float>{}, a_dtype, b_dtype, n, a, b, out, st, what);
+    case NTOPS_BINARY_DIV:
+      return launch_binary_cvt(DivF<0, float>{}, a_dtype, b_dtype, n, a, b, out, st, what);
+    default:
+      return set_error(NTOPS_ERR_UNSUPPORTED, "%s: unsupported op %d", what, op);
   }
 }
 

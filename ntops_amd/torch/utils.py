@@ -296,6 +296,11 @@ def _launch2(entry, op, dtype, shape, a, other, other_is_tensor, res, what, alph
     _lib.check(rc, what)
 
 
+# ops and operand dtypes of ntops_binary_cvt (mixed dtypes, fp32 result)
+_CVT_OPS = (_lib.BINARY_ADD, _lib.BINARY_SUB, _lib.BINARY_MUL, _lib.BINARY_DIV)
+_CVT_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.int32)
+
+
 def _binary(op, input, other, alpha, out, what, compute_dtype=None):
     """Shared body of the binary arithmetic ops (add, sub, mul, div, pow,
     bitwise_and / or) with torch's promotion (torch.result_type) and
@@ -308,7 +313,6 @@ def _binary(op, input, other, alpha, out, what, compute_dtype=None):
     shape = _broadcast_shape(input.shape, other.shape) if other_is_tensor else input.shape
     target, res = _prepare_out(out, shape, result_dtype, dev, like=input)
 
-    a = _expand_to(_to_dtype(input, result_dtype), shape)
     is_float = result_dtype.is_floating_point
     if alpha is None:
         alpha_f, alpha_i = 1.0, 1
@@ -322,8 +326,32 @@ def _binary(op, input, other, alpha, out, what, compute_dtype=None):
         alpha_f, alpha_i = _scalar_parts(alpha)
 
     with _DeviceGuard(dev):
-        b = _to_dtype(other, result_dtype) if other_is_tensor else other
-        _launch2("binary", op, result_dtype, shape, a, b, other_is_tensor, res, what, (alpha_f, alpha_i))
+        if (
+            other_is_tensor
+            and result_dtype == torch.float32
+            and op in _CVT_OPS
+            and (input.dtype != result_dtype or other.dtype != result_dtype)
+            and input.dtype in _CVT_DTYPES
+            and other.dtype in _CVT_DTYPES
+            and input.shape == shape
+            and other.shape == shape
+            and input.is_contiguous()
+            and other.is_contiguous()
+            and res.is_contiguous()
+            and input.data_ptr() % 16 == 0
+            and other.data_ptr() % 16 == 0
+            and res.data_ptr() % 16 == 0
+        ):
+            # mixed operand dtypes promoted to fp32: the conversion fused into
+            # the elementwise pass instead of a cast kernel per operand
+            rc = _lib.load().ntops_binary_cvt(
+                op, _lib.dtype_code(input.dtype), _lib.dtype_code(other.dtype), _lib.F32, res.numel(),
+                input.data_ptr(), other.data_ptr(), alpha_f, res.data_ptr(), _lib.stream_of(res))
+            _lib.check(rc, what)
+        else:
+            a = _expand_to(_to_dtype(input, result_dtype), shape)
+            b = _to_dtype(other, result_dtype) if other_is_tensor else other
+            _launch2("binary", op, result_dtype, shape, a, b, other_is_tensor, res, what, (alpha_f, alpha_i))
         if res is not target:
             _cast_into(res, target)
     return target

@@ -317,3 +317,31 @@ def test_rows_shape_past_2_31_elements():
     for lo, hi in ((0, 4), (mid - 2, mid + 1), (rows - 3, rows)):
         assert torch.equal(y[lo:hi], x[lo:hi] + bias), (lo, hi)
     del x, y
+
+
+def test_mixed_dtype_operands_fused_conversion():
+    """Operands of different dtypes promoted to an fp32 result take one pass
+    (the conversion fused into the kernel): equal, bit for bit, to torch on
+    the CPU (cast, then the fp32 op), incl. alpha, an int32 true division,
+    and the 8-element tail."""
+    g = torch.Generator().manual_seed(12)
+    n = 4096 * 33 + 5
+    a16 = torch.randn(n, generator=g).bfloat16()
+    h16 = torch.randn(n, generator=g).half()
+    f32 = torch.randn(n, generator=g)
+    i32 = torch.randint(-1000, 1000, (n,), generator=g, dtype=torch.int32)
+    j32 = torch.randint(1, 50, (n,), generator=g, dtype=torch.int32)
+    cases = [
+        ("add bf16 + f32", lambda T_: T_.add(a16c, f32c), lambda: a16 + f32),
+        ("add f32 + f16, alpha", lambda T_: T_.add(f32c, h16c, alpha=0.3), lambda: torch.add(f32, h16, alpha=0.3)),
+        ("sub f16 - f32, alpha", lambda T_: T_.sub(h16c, f32c, alpha=1.7), lambda: torch.sub(h16, f32, alpha=1.7)),
+        ("mul i32 * f32", lambda T_: T_.mul(i32c, f32c), lambda: i32 * f32),
+        ("div i32 / i32", lambda T_: T_.div(i32c, j32c), lambda: i32 / j32),
+        ("div bf16 / f32", lambda T_: T_.div(a16c, f32c), lambda: a16 / f32),
+    ]
+    a16c, h16c, f32c, i32c, j32c = (t.cuda() for t in (a16, h16, f32, i32, j32))
+    for name, ours, ref in cases:
+        got = ours(ntops_amd.torch)
+        exp = ref()
+        assert got.dtype == exp.dtype == torch.float32, name
+        assert_equal(got, exp, name)
