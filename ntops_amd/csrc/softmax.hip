@@ -11,8 +11,11 @@
 //   vector path -- row held in VGPRs (rowcommon.h), one HBM read and one HBM
 //   write per element;
 //   looped path -- any stride or dtype pair, one 256-thread block per row.
-// inner > 1: one thread per (outer, inner) column walking dim_size; adjacent
-//   threads touch adjacent inner elements, so every pass is coalesced.
+// inner > 1: a 256-thread block takes CW adjacent (outer, inner) columns
+//   and splits dim_size over 256 / CW row slices (adjacent threads touch
+//   adjacent inner elements, so every pass is coalesced); the slices' maxima
+//   and sums combine through LDS in a fixed order, CW chosen so that the
+//   grid has at least two blocks per CU where it can.
 #include "dispatch.h"
 #include "rowcommon.h"
 #include "rowwide.h"
@@ -295,27 +298,47 @@ __global__ __launch_bounds__(256) void k_softmax_loop_v(const T* x, int64_t xs0,
   for (int64_t j = tail + t; j < cols; j += 256) yr[j] = convert<T>(ex(static_cast<C>(xr[j]) - m) * inv);
 }
 
-// One thread per (outer, inner) column.
-template <typename Ti, typename To, typename C>
+// Block = CW columns x (256 / CW) row slices; block b takes columns
+// [b % tiles_per_outer * CW, + CW) of outer index b / tiles_per_outer.  Each
+// pass (max, sum of exp(x - max), outputs) walks the slice's rows; the
+// per-slice maxima and sums are combined in slice order through LDS.
+template <typename Ti, typename To, typename C, int CW>
 __global__ __launch_bounds__(256) void k_softmax_col(const Ti* x, int64_t xs0, int64_t xs1,
                                                      int64_t xs2, To* y, int64_t ys0,
                                                      int64_t ys1, int64_t ys2, int64_t outer,
                                                      int64_t dim, int64_t inner) {
-  const int64_t cols_total = outer * inner;
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < cols_total;
-       t += static_cast<int64_t>(gridDim.x) * 256) {
-    const int64_t o = t / inner;
-    const int64_t in = t - o * inner;
-    const Ti* xc = x + o * xs0 + in * xs2;
-    To* yc = y + o * ys0 + in * ys2;
-    C m = -__builtin_huge_val();
-    for (int64_t j = 0; j < dim; ++j) m = cmax(m, static_cast<C>(convert<To>(xc[j * xs1])));
-    C s = 0;
-    for (int64_t j = 0; j < dim; ++j) s += ex(static_cast<C>(convert<To>(xc[j * xs1])) - m);
-    const C inv = C(1) / s;
-    for (int64_t j = 0; j < dim; ++j)
-      yc[j * ys1] = convert<To>(ex(static_cast<C>(convert<To>(xc[j * xs1])) - m) * inv);
-  }
+  constexpr int RS = 256 / CW;
+  __shared__ C red[RS][CW];
+  const int64_t tiles = (inner + CW - 1) / CW;
+  const int64_t b = block_id();  // blocks_2d grid
+  if (b >= outer * tiles) return;  // the tail of the grid (the whole block)
+  const int64_t o = b / tiles;
+  const int tx = threadIdx.x % CW, ty = threadIdx.x / CW;
+  const int64_t in = (b - o * tiles) * CW + tx;
+  const bool ok = in < inner;
+  const Ti* xc = x + o * xs0 + (ok ? in : 0) * xs2;
+  To* yc = y + o * ys0 + (ok ? in : 0) * ys2;
+  auto val = [&](int64_t j) { return static_cast<C>(convert<To>(xc[j * xs1])); };
+  C m = -__builtin_huge_val();
+  if (ok)
+    for (int64_t j = ty; j < dim; j += RS) m = cmax(m, val(j));
+  red[ty][tx] = m;
+  __syncthreads();
+  m = red[0][tx];
+#pragma unroll
+  for (int k = 1; k < RS; ++k) m = cmax(m, red[k][tx]);
+  __syncthreads();
+  C s = 0;
+  if (ok)
+    for (int64_t j = ty; j < dim; j += RS) s += ex(val(j) - m);
+  red[ty][tx] = s;
+  __syncthreads();
+  s = red[0][tx];
+#pragma unroll
+  for (int k = 1; k < RS; ++k) s += red[k][tx];
+  if (!ok) return;
+  const C inv = C(1) / s;
+  for (int64_t j = ty; j < dim; j += RS) yc[j * ys1] = convert<To>(ex(val(j) - m) * inv);
 }
 
 template <typename Ti, typename To>
@@ -364,10 +387,22 @@ int run_softmax(int64_t outer, int64_t dim, int64_t inner, const void* xv, const
                        y, ys[0], ys[1], outer, dim);
     return check_launch("softmax");
   }
-  int64_t blocks = ceil_div(outer * inner, 256);
-  if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL((k_softmax_col<Ti, To, C>), dim3(blocks), dim3(256), 0, st, x, xs[0], xs[1],
-                     xs[2], y, ys[0], ys[1], ys[2], outer, dim, inner);
+  // the widest column tile (coalescing) that still gives two blocks per CU
+  const int64_t want = 2 * static_cast<int64_t>(cu_count_cached());
+  auto blocks_for = [&](int cw) { return outer * ((inner + cw - 1) / cw); };
+  const int cw = blocks_for(64) >= want ? 64 : blocks_for(32) >= want ? 32 : blocks_for(16) >= want ? 16 : 8;
+#define NTOPS_SM_COL(CW)                                                                              \
+  hipLaunchKernelGGL((k_softmax_col<Ti, To, C, CW>), blocks_2d(blocks_for(CW)), dim3(256), 0, st, x, xs[0], \
+                     xs[1], xs[2], y, ys[0], ys[1], ys[2], outer, dim, inner)
+  if (cw == 64)
+    NTOPS_SM_COL(64);
+  else if (cw == 32)
+    NTOPS_SM_COL(32);
+  else if (cw == 16)
+    NTOPS_SM_COL(16);
+  else
+    NTOPS_SM_COL(8);
+#undef NTOPS_SM_COL
   return check_launch("softmax");
 }
 

@@ -163,3 +163,25 @@ def test_softmax_many_rows(cols):
     x = (torch.randn(200003, cols, generator=torch.Generator().manual_seed(cols)) * 3).bfloat16()
     got = ntops_amd.torch.softmax(x.cuda(), -1)
     assert_close(got, from_np(O.softmax(to_np(x), -1, "bf16"), "bf16"), *TOL_REDUCTION["bf16"], "softmax")
+
+
+@pytest.mark.parametrize("shape, dim, dtype", [
+    ((32, 2048, 128), 1, torch.bfloat16),
+    ((4096, 1024), 0, torch.bfloat16),
+    ((3, 517, 1000), 1, torch.float32),
+    ((2, 3, 300, 7), 2, torch.float16),
+    ((64, 40, 640), 1, torch.bfloat16),
+])
+def test_softmax_middle_dims(shape, dim, dtype):
+    """Softmax over a dim with inner elements after it: column tiles of 8-64
+    columns with the dim split over row slices (every tile width the grid
+    size selects), against the oracle."""
+    g = torch.Generator().manual_seed(sum(shape) + dim)
+    x = (torch.randn(shape, generator=g) * 2).to(dtype)
+    dt = DT_NAME[dtype]
+    got = ntops_amd.torch.softmax(x.cuda(), dim)
+    exp = from_np(O.softmax(to_np(x), dim, dt), dt)
+    assert_close(got, exp, *TOL_REDUCTION[dt], f"softmax {shape} dim {dim}")
+    got = ntops_amd.torch.softmax(x.cuda(), dim, dtype=torch.float32)
+    exp = from_np(O.softmax(to_np(x), dim, dt, out_dt="f32"), "f32")
+    assert_close(got, exp, *TOL_REDUCTION["f32"], f"softmax {shape} dim {dim} -> f32")
