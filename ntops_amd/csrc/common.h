@@ -157,6 +157,18 @@ __device__ __forceinline__ void store16_nt(T* p, const Pack16<T>& v) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
+// The same resource with its address and size read from the first active
+// lane.  Where the compiler cannot prove `base` / `bytes` uniform it keeps the
+// resource in VGPRs and wraps every buffer access in a readfirstlane loop (a
+// branch per load, which also splits the schedule around it); this form tells
+// it they are uniform.  Only for values that really are wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc_uniform(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo), 0,
+                                           static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)), 0x00020000);
+}
 constexpr int kBufNT = 2;  // cache-policy bit: nontemporal (streamed once)
 template <typename T>
 __device__ __forceinline__ Pack16<T> buffer_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {

@@ -42,8 +42,8 @@
 // (fp32: v_mfma_f32_16x16x4_f32).
 // Short-K path (K <= 128, M and N multiples of 128): a persistent kernel
 // built around the output stream.
-// fp32 tile path (K-major A): v_mfma_f32_16x16x4_f32 wave tiles, operands
-// from L2 per wave.
+// fp32 tile path (K-major A): v_mfma_f32_16x16x4_f32 wave tiles of 64 x 64,
+// 32-deep K tiles shared by the block through two LDS buffers.
 // Generic path (any other strides): 64x64 LDS-tiled FMA kernel with fp32
 // accumulation (IEEE; gfx950 has no reduced-precision fp32 MFMA input).
 #include "gemm.h"
@@ -1168,128 +1168,176 @@ int launch_skinny_f32(const GemmArgs& g, hipStream_t st) {
 }
 
 // ---- fp32 tile kernel -------------------------------------------------------
-// fp32 products on v_mfma_f32_16x16x4_f32 without shared LDS tiles: each wave owns a
-// 64 x 64 output tile (4 x 4 MFMA tiles, 64 accumulator registers) and loads
-// its operands straight from global memory (L2) into the MFMA layout, 16 k
-// per step.  A (K-major) comes as one 16-byte load per lane and 16-row block
-// holding k0 + 4 (l >> 4) + e, e = 0..3; element e feeds MFMA e of the
-// step.  B matches that k order: K-major B the same way; an M/N-major B as
-// 16-byte row pieces (4 k-rows x 64 columns per instruction) staged in a
-// per-wave LDS tile with padded rows and read back per column.  Each loaded
-// fragment serves four MFMAs, so a step moves 8 KiB per 64 MFMAs and the
-// kernel needs no barriers.  Blocks of 2 x 2 waves cover 128 x 128 and are ordered like the
-// bf16 tiles.  Out-of-range rows, columns and k read as zero.
-template <bool BKM>
-__global__ __launch_bounds__(256) void k_gemm_f32_tile(GemmArgs g) {
-  constexpr int TM = 4, TN = 4, U = 2;
-  constexpr int kTrRow = 68;  // floats per k-row of the M/N-major B tile (64 + 4: conflict-free reads)
-  __shared__ __attribute__((aligned(16))) float trs[BKM ? 1 : 4][16 * kTrRow];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tm_count = (g.M + 127) / 128, tn_count = (g.N + 127) / 128;
+// fp32 products on v_mfma_f32_16x16x4_f32 (IEEE fp32 products, fp32
+// accumulation).  A block of WM x 2 waves (WM = 1, 2, 4) covers (64 WM) x 128 outputs, each
+// wave a 64 x 64 tile (4 x 4 MFMA tiles).  K advances in 32-deep tiles of A
+// and B shared through two LDS buffers: each thread loads its 16-byte chunks
+// of the next tile into registers before the current tile's MFMAs and writes
+// them to the other buffer after the first half of them.  Within a tile the
+// fragments of the second 16-k step are read while the first step's MFMAs
+// run, and those of the next tile's first step after the tile's one barrier,
+// while the second step's run.  Lane l of a 16-k step holds 4 consecutive k,
+// 4 (l >> 4) + e, of its row (A) or column (B), and element e feeds MFMA e:
+// one 16-byte LDS read per fragment for K-major tiles.
+// LDS layouts: a K-major tile is [row][32 k], 16-byte chunk c of row r at
+// slot c ^ ((r >> 1) & 7), so the 16 rows a read covers hit all 64 banks;
+// an N-major B tile is [32 k][128 + 4 n] (padded rows put the four k-rows a
+// column read covers in different banks), read per element.
+// Out-of-range rows, columns and k read as zero (buffer resources).
+template <bool BKM, int WM>
+__global__ __launch_bounds__(128 * WM) void k_gemm_f32_lds(GemmArgs g) {
+  constexpr int T = 128 * WM, BM = 64 * WM, BN = 128, BK = 32;
+  constexpr int kBRow = BN + 4;                         // floats per k-row of an N-major B tile
+  constexpr int A_CH = BM * 8 / T, B_CH = BN * 8 / T;  // 16-byte chunks per thread per tile
+  constexpr int A_FL = BM * BK, B_FL = BKM ? BN * BK : BK * kBRow;
+  __shared__ __attribute__((aligned(16))) float lds[2][A_FL + B_FL];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tm_count = (g.M + BM - 1) / BM, tn_count = (g.N + BN - 1) / BN;
   int bat, tmi, tni;
   tile_of(blockIdx.x, gridDim.x, tm_count, tn_count, bat, tmi, tni);
-  const int m0 = tmi * 128 + (wave >> 1) * 64, n0 = tni * 128 + (wave & 1) * 64;
-  const int mv = max(0, min(64, g.M - m0)), nv = max(0, min(64, g.N - n0));
-  const int r16 = lane & 15, kq = (lane >> 4) * 4;
+  const int bm0 = tmi * BM, bn0 = tni * BN;
+  const int mv = max(0, min(BM, g.M - bm0)), nv = max(0, min(BN, g.N - bn0));
   const float* A = static_cast<const float*>(g.A) + bat * g.sa_b;
   const float* B = static_cast<const float*>(g.B) + bat * g.sb_b;
-  const __amdgpu_buffer_rsrc_t ra =
-      buffer_rsrc(A + static_cast<int64_t>(m0) * g.sa_m,
-                  mv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(mv - 1) * g.sa_m + g.K) * 4) : 0u);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc_uniform(
+      A + static_cast<int64_t>(bm0) * g.sa_m,
+      mv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(mv - 1) * g.sa_m + g.K) * 4) : 0u);
   const __amdgpu_buffer_rsrc_t rb =
-      BKM ? buffer_rsrc(B + static_cast<int64_t>(n0) * g.sb_n,
-                        nv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(nv - 1) * g.sb_n + g.K) * 4) : 0u)
-          : buffer_rsrc(B + n0, nv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(g.K - 1) * g.sb_k + nv) * 4) : 0u);
-  uint32_t a_off[TM];
-  bool a_ok[TM];
+      BKM ? buffer_rsrc_uniform(B + static_cast<int64_t>(bn0) * g.sb_n,
+                                nv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(nv - 1) * g.sb_n + g.K) * 4) : 0u)
+          : buffer_rsrc_uniform(B + bn0,
+                                nv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(g.K - 1) * g.sb_k + nv) * 4) : 0u);
+  // Loader slots.  K-major chunk q: row q / 8, k 4 (q % 8) .. + 3 of the tile;
+  // N-major B chunk q: k-row q / 32, columns 4 (q % 32) .. + 3.
+  uint32_t a_off[A_CH], a_lds[A_CH];
+  int a_k[A_CH];
+  bool a_ok[A_CH];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    a_off[i] = static_cast<uint32_t>(((16 * i + r16) * g.sa_m + kq) * 4);
-    a_ok[i] = 16 * i + r16 < mv;
+  for (int i = 0; i < A_CH; ++i) {
+    const int q = tid + i * T, r = q >> 3, c = q & 7;
+    a_off[i] = static_cast<uint32_t>((r * g.sa_m + 4 * c) * 4);
+    a_ok[i] = r < mv;
+    a_k[i] = 4 * c;
+    a_lds[i] = r * BK + 4 * (c ^ ((r >> 1) & 7));
   }
-  uint32_t b_off[TN];
-  bool b_ok[TN];
+  uint32_t b_off[B_CH], b_lds[B_CH];
+  int b_k[B_CH];
+  bool b_ok[B_CH];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    // M/N-major: load j covers k-rows 4 j + (l >> 4), columns 4 (l & 15) .. + 3
-    b_off[j] = BKM ? static_cast<uint32_t>(((16 * j + r16) * g.sb_n + kq) * 4)
-                   : static_cast<uint32_t>(((4 * j + (lane >> 4)) * g.sb_k + 4 * r16) * 4);
-    b_ok[j] = BKM ? 16 * j + r16 < nv : 4 * r16 < nv;
+  for (int i = 0; i < B_CH; ++i) {
+    const int q = tid + i * T;
+    if constexpr (BKM) {
+      const int r = q >> 3, c = q & 7;
+      b_off[i] = static_cast<uint32_t>((r * g.sb_n + 4 * c) * 4);
+      b_ok[i] = r < nv;
+      b_k[i] = 4 * c;
+      b_lds[i] = A_FL + r * BK + 4 * (c ^ ((r >> 1) & 7));
+    } else {
+      const int kr = q >> 5, c = q & 31;
+      b_off[i] = static_cast<uint32_t>((kr * g.sb_k + 4 * c) * 4);
+      b_ok[i] = 4 * c < nv;
+      b_k[i] = kr;
+      b_lds[i] = A_FL + kr * kBRow + 4 * c;
+    }
   }
   const uint32_t b_kstep = BKM ? 4u : static_cast<uint32_t>(g.sb_k * 4);  // bytes per k
-
-  f32x4 acc[TM][TN];
+  f32x4 qa[A_CH], qb[B_CH];
+  auto gload = [&](int k0) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < A_CH; ++i)
+      qa[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            ra, a_ok[i] && k0 + a_k[i] < g.K ? a_off[i] + k0 * 4u : kOOB, 0, 0));
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int k0 = 0; k0 < g.K; k0 += 16 * U) {
-    f32x4 aq[U][TM], bq[U][TN];
+    for (int i = 0; i < B_CH; ++i)
+      qb[i] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     rb, b_ok[i] && k0 + b_k[i] < g.K ? b_off[i] + static_cast<uint32_t>(k0) * b_kstep : kOOB, 0, 0));
+  };
+  auto lstore = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = k0 + 16 * u;
-      const bool k_ok = k + kq < g.K;
+    for (int i = 0; i < A_CH; ++i) *reinterpret_cast<f32x4*>(&lds[buf][a_lds[i]]) = qa[i];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        aq[u][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                 ra, a_ok[i] && k_ok ? a_off[i] + k * 4u : kOOB, 0, 0));
+    for (int i = 0; i < B_CH; ++i) *reinterpret_cast<f32x4*>(&lds[buf][b_lds[i]]) = qb[i];
+  };
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int r16 = lane & 15, kg = lane >> 4;
+  // fragments of 16-k step s (0 or 1) of the tile in `la`
+  auto fread = [&](const float* la, int s, f32x4 (&a)[4], f32x4 (&b)[4]) {
+    const int c = 4 * s + kg;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        if constexpr (BKM) {
-          bq[u][j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   rb, b_ok[j] && k_ok ? b_off[j] + k * 4u : kOOB, 0, 0));
-        } else {
-          const bool ok = b_ok[j] && k + 4 * j + (lane >> 4) < g.K;
-          bq[u][j] = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                         rb, ok ? b_off[j] + static_cast<uint32_t>(k) * b_kstep : kOOB, 0, 0));
-        }
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int r = wm + 16 * i + r16;
+      a[i] = *reinterpret_cast<const f32x4*>(&la[r * BK + 4 * (c ^ ((r >> 1) & 7))]);
     }
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      f32x4 bf[TN];
+    for (int j = 0; j < 4; ++j) {
       if constexpr (BKM) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bf[j] = bq[u][j];
+        const int r = wn + 16 * j + r16;
+        b[j] = *reinterpret_cast<const f32x4*>(&la[A_FL + r * BK + 4 * (c ^ ((r >> 1) & 7))]);
       } else {
-        // Stage the step's 16 x 64 tile (row-major, padded rows) and read
-        // column l & 15 of k-rows 4 (l >> 4) + e back for each 16-column group.
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          *reinterpret_cast<f32x4*>(&trs[wave][(4 * j + (lane >> 4)) * kTrRow + 4 * r16]) = bq[u][j];
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bf[j][e] = trs[wave][(kq + e) * kTrRow + 16 * j + r16];
+        for (int e = 0; e < 4; ++e) b[j][e] = la[A_FL + (16 * s + 4 * kg + e) * kBRow + wn + 16 * j + r16];
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[u][i][e], bf[j][e], acc[i][j], 0, 0, 0);
     }
+  };
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const f32x4 (&a)[4], const f32x4 (&b)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
+  };
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  f32x4 fa0[4], fb0[4], fa1[4], fb1[4];
+  fread(lds[0], 0, fa0, fb0);
+  int buf = 0;
+  for (int k0 = 0; k0 < g.K; k0 += BK) {
+    const bool more = k0 + BK < g.K;
+    if (more) gload(k0 + BK);
+    fread(lds[buf], 1, fa1, fb1);
+    mma(fa0, fb0);
+    // The other buffer's last reads (the previous tile's second step) were
+    // made before the previous barrier: it is free to refill.
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+    if (more) fread(lds[buf ^ 1], 0, fa0, fb0);
+    mma(fa1, fb1);
+    buf ^= 1;
   }
   float* D = static_cast<float*>(g.D) + bat * g.sd_b;
   const float* Cp = g.use_c ? static_cast<const float*>(g.C) + bat * g.sc_b : nullptr;
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 16 * i + (lane >> 4) * 4 + r, n = n0 + 16 * j + r16;
+        const int m = bm0 + wm + 16 * i + kg * 4 + r, n = bn0 + wn + 16 * j + r16;
         if (m < g.M && n < g.N) {
           float v = g.alpha * acc[i][j][r];
           if (Cp != nullptr) v += g.beta * Cp[m * g.sc_m + n * g.sc_n];
           D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = v;
         }
       }
+}
+
+template <bool BKM, int WM>
+int launch_f32_lds(const GemmArgs& g, hipStream_t st) {
+  const int64_t tiles = static_cast<int64_t>((g.M + 64 * WM - 1) / (64 * WM)) * ((g.N + 127) / 128) * g.batch;
+  if (tiles > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "gemm: too many tiles");
+  note_kernel("gemm_f32_lds m%d %s", 64 * WM, BKM ? "B:K" : "B:N");
+  hipLaunchKernelGGL((k_gemm_f32_lds<BKM, WM>), dim3(static_cast<unsigned>(tiles)), dim3(128 * WM), 0, st, g);
+  return check_launch("gemm");
 }
 
 // ---- generic kernel (any dtype among F32/F16/BF16, any strides) -------------
@@ -1608,19 +1656,21 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     if (g.K > 0 && g.M <= kSkinnyMaxM && a_k && (b_k || b_n) && batch_ok && fits && aligned16(g.A) &&
         aligned16(g.B))
       return b_k ? launch_skinny_f32<true>(g, st) : launch_skinny_f32<false>(g, st);
-    // Larger fp32 products: the LDS-free MFMA tile kernel.
+    // Larger fp32 products: the LDS-tiled MFMA kernel.  256-row blocks (8
+    // waves) for an N-major B when they give two blocks per CU (a few percent
+    // faster there; 128-row blocks are faster for a K-major B), 128-row blocks
+    // when those fill every CU, else 64-row blocks (twice the blocks).
     const bool b_n4 = g.sb_n == 1 && g.sb_k % 4 == 0 && g.N % 4 == 0 && !b_k;
-    const bool fits_t = (128 * g.sa_m + g.K) * 4 < lim &&
+    const bool fits_t = (256 * g.sa_m + g.K) * 4 < lim &&
                         (b_k ? (128 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 128)) * 4 < lim;
-    const int64_t tiles = static_cast<int64_t>((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
     if (g.K > 0 && a_k && (b_k || b_n4) && fits_t && aligned16(g.A) && aligned16(g.B) &&
-        (g.batch == 1 || (g.sa_b % 4 == 0 && g.sb_b % 4 == 0)) && tiles <= 0x7fffffffLL) {
-      note_kernel("gemm_f32_tile %s", b_k ? "B:K" : "B:N");
-      if (b_k)
-        hipLaunchKernelGGL((k_gemm_f32_tile<true>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, g);
-      else
-        hipLaunchKernelGGL((k_gemm_f32_tile<false>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, g);
-      return check_launch("gemm");
+        (g.batch == 1 || (g.sa_b % 4 == 0 && g.sb_b % 4 == 0))) {
+      const int64_t cus = cu_count_cached() > 0 ? cu_count_cached() : 256;
+      const int64_t cols = (g.N + 127) / 128 * g.batch;
+      if (!b_k && (g.M + 255) / 256 * cols >= 2 * cus) return launch_f32_lds<false, 4>(g, st);
+      if ((g.M + 127) / 128 * cols >= cus)
+        return b_k ? launch_f32_lds<true, 2>(g, st) : launch_f32_lds<false, 2>(g, st);
+      return b_k ? launch_f32_lds<true, 1>(g, st) : launch_f32_lds<false, 1>(g, st);
     }
   }
   const int64_t tiles = static_cast<int64_t>((g.M + 63) / 64) * ((g.N + 63) / 64) * g.batch;

@@ -367,16 +367,49 @@ def test_mm_small_m_f32(m, n, k, layout):
 
 
 @pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
-@pytest.mark.parametrize("m, n, k", [(256, 512, 128), (300, 200, 72), (1000, 1024, 640), (130, 1000, 4), (65, 129, 1028)])
+@pytest.mark.parametrize("m, n, k", [(256, 512, 128), (300, 200, 72), (1000, 1024, 640), (130, 1000, 4), (65, 129, 1028),
+                                     (1100, 260, 132), (1024, 384, 36), (2048, 132, 2052)])
 def test_mm_f32_tiles(m, n, k, layout):
-    """fp32 beyond the skinny rows: the LDS-free fp32 MFMA tile kernel
-    (K-major A; B either way), partial 64 x 64 wave tiles at every edge."""
+    """fp32 beyond the skinny rows: the LDS-tiled fp32 MFMA kernel (K-major
+    A; B either way), partial tiles at every edge, K tails of 4-28."""
     a = torch.randn(m, k)
     b = torch.randn(k, n)
     ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
     bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
     got = ntops_amd.torch.mm(ag, bg)
+    # (a K-major B whose N is not a multiple of 4 is copied N-major by the wrapper, padded to whole rows)
+    bl = "B:K" if layout[1] == "T" and n % 4 == 0 else "B:N"
+    assert _lib.last_kernel() == f"gemm_f32_lds m{f32_block_rows(m, n, 1, bl)} {bl}"
     check(got, a, b, torch.float32, what=f"mm f32 tiles {layout}")
+
+
+def f32_block_rows(m, n, batch, bl):
+    """Rows per block the fp32 tile kernel is launched with: 256 for an
+    N-major B when that gives two blocks per CU, 128 when 128-row blocks
+    fill every CU, else 64."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    cols = -(-n // 128) * batch
+    if bl == "B:N" and -(-m // 256) * cols >= 2 * cus:
+        return 256
+    return 128 if -(-m // 128) * cols >= cus else 64
+
+
+@pytest.mark.parametrize("m, n, k, bt", [(4096, 4096, 36, False), (4096, 4096, 36, True), (2048, 2048, 100, False),
+                                         (2048, 2048, 100, True), (200, 300, 68, False), (200, 300, 68, True)])
+def test_mm_f32_tiles_exact_sums(m, n, k, bt):
+    """Small-integer operands: every product and partial sum is exact in
+    fp32, so every output of each block shape (64 / 128 / 256 rows) must
+    equal the integer product (catches a lost, doubled or misplaced k chunk,
+    row or column)."""
+    g = torch.Generator().manual_seed(5)
+    a = torch.randint(-8, 9, (m, k), generator=g).float()
+    b = torch.randint(-8, 9, (k, n), generator=g).float()
+    bg = b.cuda() if not bt else b.t().contiguous().cuda().t()
+    got = ntops_amd.torch.mm(a.cuda(), bg)
+    bl = "B:K" if bt else "B:N"
+    assert _lib.last_kernel() == f"gemm_f32_lds m{f32_block_rows(m, n, 1, bl)} {bl}"
+    exp = (a.double() @ b.double()).float()
+    assert torch.equal(got.cpu(), exp)
 
 
 def test_addmm_and_bmm_f32_tiles():
@@ -390,6 +423,11 @@ def test_addmm_and_bmm_f32_tiles():
     b = torch.randn(3, 64, 260)
     got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
     assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), 1e-5, 1e-5 * 8, "bmm f32 tiles")
+    a = torch.randn(3, 1030, 64)
+    b = torch.randn(3, 64, 260)
+    got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
+    assert _lib.last_kernel() == f"gemm_f32_lds m{f32_block_rows(1030, 260, 3, 'B:N')} B:N"
+    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), 1e-5, 1e-5 * 8, "bmm f32 batched tiles")
 
 
 def test_addmm_and_bmm_small_m():
