@@ -1184,7 +1184,10 @@ int launch_skinny_f32(const GemmArgs& g, hipStream_t st) {
 // an N-major B tile is [32 k][128 + 4 n] (padded rows put the four k-rows a
 // column read covers in different banks), read per element.
 // Out-of-range rows, columns and k read as zero (buffer resources).
-template <bool BKM, int WM>
+// SPLITK: block row blockIdx.y takes k in [blockIdx.y * kchunk, + kchunk)
+// (kchunk a multiple of 32) and writes its raw fp32 partial tile to
+// part + blockIdx.y * part_stride (rows of N).
+template <bool BKM, int WM, bool SPLITK = false>
 __global__ __launch_bounds__(128 * WM) void k_gemm_f32_lds(GemmArgs g) {
   constexpr int T = 128 * WM, BM = 64 * WM, BN = 128, BK = 32;
   constexpr int kBRow = BN + 4;                         // floats per k-row of an N-major B tile
@@ -1242,17 +1245,19 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_f32_lds(GemmArgs g) {
     }
   }
   const uint32_t b_kstep = BKM ? 4u : static_cast<uint32_t>(g.sb_k * 4);  // bytes per k
+  const int kbeg = SPLITK ? static_cast<int>(blockIdx.y) * g.kchunk : 0;
+  const int kend = SPLITK ? min(g.K, kbeg + g.kchunk) : g.K;
   f32x4 qa[A_CH], qb[B_CH];
   auto gload = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < A_CH; ++i)
       qa[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            ra, a_ok[i] && k0 + a_k[i] < g.K ? a_off[i] + k0 * 4u : kOOB, 0, 0));
+                                            ra, a_ok[i] && k0 + a_k[i] < kend ? a_off[i] + k0 * 4u : kOOB, 0, 0));
 #pragma unroll
     for (int i = 0; i < B_CH; ++i)
       qb[i] = __builtin_bit_cast(
           f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                     rb, b_ok[i] && k0 + b_k[i] < g.K ? b_off[i] + static_cast<uint32_t>(k0) * b_kstep : kOOB, 0, 0));
+                     rb, b_ok[i] && k0 + b_k[i] < kend ? b_off[i] + static_cast<uint32_t>(k0) * b_kstep : kOOB, 0, 0));
   };
   auto lstore = [&](int buf) {
 #pragma unroll
@@ -1295,14 +1300,14 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_f32_lds(GemmArgs g) {
         for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
   };
-  gload(0);
+  gload(kbeg);
   lstore(0);
   __syncthreads();
   f32x4 fa0[4], fb0[4], fa1[4], fb1[4];
   fread(lds[0], 0, fa0, fb0);
   int buf = 0;
-  for (int k0 = 0; k0 < g.K; k0 += BK) {
-    const bool more = k0 + BK < g.K;
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    const bool more = k0 + BK < kend;
     if (more) gload(k0 + BK);
     fread(lds[buf], 1, fa1, fb1);
     mma(fa0, fb0);
@@ -1324,9 +1329,13 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_f32_lds(GemmArgs g) {
       for (int r = 0; r < 4; ++r) {
         const int m = bm0 + wm + 16 * i + kg * 4 + r, n = bn0 + wn + 16 * j + r16;
         if (m < g.M && n < g.N) {
-          float v = g.alpha * acc[i][j][r];
-          if (Cp != nullptr) v += g.beta * Cp[m * g.sc_m + n * g.sc_n];
-          D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = v;
+          if constexpr (SPLITK) {
+            g.part[blockIdx.y * g.part_stride + static_cast<int64_t>(m) * g.N + n] = acc[i][j][r];
+          } else {
+            float v = g.alpha * acc[i][j][r];
+            if (Cp != nullptr) v += g.beta * Cp[m * g.sc_m + n * g.sc_n];
+            D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = v;
+          }
         }
       }
 }
@@ -1426,8 +1435,12 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int S) {
     o[e] = static_cast<T>(v);
   }
   T* D = static_cast<T*>(g.D) + static_cast<int64_t>(m) * g.sd_m;
-  if (g.sd_n == 1 && (reinterpret_cast<uintptr_t>(D + n) & 7u) == 0) {
-    *reinterpret_cast<u32x2*>(D + n) = __builtin_bit_cast(u32x2, o);
+  constexpr uintptr_t kAlign = 4 * sizeof(T) - 1;
+  if (g.sd_n == 1 && (reinterpret_cast<uintptr_t>(D + n) & kAlign) == 0) {
+    if constexpr (sizeof(T) == 2)
+      *reinterpret_cast<u32x2*>(D + n) = __builtin_bit_cast(u32x2, o);
+    else
+      *reinterpret_cast<u32x4*>(D + n) = __builtin_bit_cast(u32x4, o);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e) D[static_cast<int64_t>(n + e) * g.sd_n] = o[e];
@@ -1550,6 +1563,33 @@ int splitk_slices(int64_t M, int64_t N, int64_t K, int* kchunk) {
   return static_cast<int>((K + chunk - 1) / chunk);
 }
 
+// fp32 split over K for products whose 128 x 128 tiles leave CUs idle:
+// up to two blocks per CU, slices of at least 128 k (an fp32 k-step costs
+// eight times a 16-bit one on the matrix cores, so shorter slices than the
+// 16-bit path's 512 still pay for their partial tile).
+int splitk_slices_f32(int64_t M, int64_t N, int64_t K, int* kchunk) {
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  const int64_t cus = cu_count_cached() > 0 ? cu_count_cached() : 256;
+  if (tiles >= cus || M <= kSkinnyMaxM || N % 4 != 0) return 1;
+  int64_t S = std::min<int64_t>(std::min<int64_t>(2 * cus / tiles, K / 128), 16);
+  if (S < 2) return 1;
+  const int64_t chunk = ((K + S - 1) / S + 31) / 32 * 32;
+  *kchunk = static_cast<int>(chunk);
+  return static_cast<int>((K + chunk - 1) / chunk);
+}
+
+template <bool BKM>
+int launch_f32_splitk(GemmArgs g, int S, hipStream_t st) {
+  const int64_t tiles = static_cast<int64_t>((g.M + 127) / 128) * ((g.N + 127) / 128);
+  note_kernel("gemm_f32_lds m128 %s splitk%d", BKM ? "B:K" : "B:N", S);
+  hipLaunchKernelGGL((k_gemm_f32_lds<BKM, 2, true>), dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(S)),
+                     dim3(256), 0, st, g);
+  const int rc = check_launch("gemm");
+  if (rc != NTOPS_OK) return rc;
+  if (g.c_mode == kCVec4) g.c_mode = kCStrided;  // (kCVec4 reads four 16-bit values)
+  return launch_splitk_reduce<float>(g, S, st);
+}
+
 template <typename T, bool AK, bool BKM, bool EVEN>
 int launch_splitk_part(const GemmArgs& g, int S, hipStream_t st) {
   constexpr int kLds = 4 * (128 + 128) * 32 * 2;
@@ -1665,6 +1705,13 @@ int run_gemm(GemmArgs g, hipStream_t st) {
                         (b_k ? (128 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 128)) * 4 < lim;
     if (g.K > 0 && a_k && (b_k || b_n4) && fits_t && aligned16(g.A) && aligned16(g.B) &&
         (g.batch == 1 || (g.sa_b % 4 == 0 && g.sb_b % 4 == 0))) {
+      int kchunk = 0;
+      const int S = (g.part != nullptr && g.batch == 1) ? splitk_slices_f32(g.M, g.N, g.K, &kchunk) : 1;
+      if (S > 1 && static_cast<int64_t>(S) * g.M * g.N * 4 <= g.part_bytes) {
+        g.kchunk = kchunk;
+        g.part_stride = static_cast<int64_t>(g.M) * g.N;
+        return b_k ? launch_f32_splitk<true>(g, S, st) : launch_f32_splitk<false>(g, S, st);
+      }
       const int64_t cus = cu_count_cached() > 0 ? cu_count_cached() : 256;
       const int64_t cols = (g.N + 127) / 128 * g.batch;
       if (!b_k && (g.M + 255) / 256 * cols >= 2 * cus) return launch_f32_lds<false, 4>(g, st);
@@ -1890,9 +1937,14 @@ extern "C" int ntops_gemm_ws(int dtype, int64_t batch, int64_t M, int64_t N, int
 }
 
 extern "C" int64_t ntops_gemm_workspace(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K) {
-  if ((dtype != NTOPS_BF16 && dtype != NTOPS_F16) || batch != 1 || M <= 0 || N <= 0 || K <= 0 ||
-      M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
+  if ((dtype != NTOPS_BF16 && dtype != NTOPS_F16 && dtype != NTOPS_F32) || batch != 1 || M <= 0 || N <= 0 ||
+      K <= 0 || M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
     return 0;
+  if (dtype == NTOPS_F32) {
+    int kchunk = 0;
+    const int S = splitk_slices_f32(M, N, K, &kchunk);
+    return S > 1 ? static_cast<int64_t>(S) * M * N * 4 : 0;
+  }
   // (a K-major A of up to kSplitKMinM rows takes the skinny kernel instead
   // and leaves the workspace unused)
   int kchunk = 0;

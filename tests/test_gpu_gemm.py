@@ -287,7 +287,7 @@ SPLIT_K = [(64, 4096, 4096), (128, 14336, 4096), (100, 1000, 8200), (48, 4096, 1
 
 
 @pytest.mark.parametrize("layout", ("NN", "NT", "TN"))
-@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
 @pytest.mark.parametrize("m, n, k", SPLIT_K)
 def test_mm_split_k(m, n, k, dtype, layout):
     g = torch.Generator().manual_seed(m + 5 * n + k)
@@ -296,7 +296,9 @@ def test_mm_split_k(m, n, k, dtype, layout):
     ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
     bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
     # (a K-major A of at most 16 rows takes the skinny kernel, an M-major A of
-    # 2-7 rows the generic one; a transposed (1, k) view is K-major)
+    # 2-7 rows the generic one; a transposed (1, k) view is K-major; fp32
+    # splits only past the fp32 skinny kernel's 64 rows, where the workspace
+    # query returns 0)
     a_kmajor = layout[0] == "N" or m == 1
     splits = (_lib.load().ntops_gemm_workspace(_lib.dtype_code(dtype), 1, m, n, k) > 0
               and (m > 16 or not a_kmajor) and not (layout[0] == "T" and 1 < m < 8))
@@ -377,10 +379,20 @@ def test_mm_f32_tiles(m, n, k, layout):
     ag = a.cuda() if layout[0] == "N" else a.t().contiguous().cuda().t()
     bg = b.cuda() if layout[1] == "N" else b.t().contiguous().cuda().t()
     got = ntops_amd.torch.mm(ag, bg)
-    # (a K-major B whose N is not a multiple of 4 is copied N-major by the wrapper, padded to whole rows)
-    bl = "B:K" if layout[1] == "T" and n % 4 == 0 else "B:N"
-    assert _lib.last_kernel() == f"gemm_f32_lds m{f32_block_rows(m, n, 1, bl)} {bl}"
+    assert _lib.last_kernel().startswith(f32_expected_kernel(m, n, k, layout[1] == "T"))
     check(got, a, b, torch.float32, what=f"mm f32 tiles {layout}")
+
+
+def f32_expected_kernel(m, n, k, b_kmajor):
+    """The fp32 tile kernel a 2-D product takes.  A K-major B whose N is not a
+    multiple of 4 is copied N-major by the wrapper into rows padded to a
+    multiple of 4; products whose tiles leave CUs idle split K when the
+    workspace query says so."""
+    bl = "B:K" if b_kmajor and n % 4 == 0 else "B:N"
+    np_ = -(-n // 4) * 4
+    if _lib.load().ntops_gemm_workspace(_lib.dtype_code(torch.float32), 1, m, np_, k) > 0:
+        return f"gemm_f32_lds m128 {bl} splitk"
+    return f"gemm_f32_lds m{f32_block_rows(m, np_, 1, bl)} {bl}"
 
 
 def f32_block_rows(m, n, batch, bl):
@@ -395,19 +407,19 @@ def f32_block_rows(m, n, batch, bl):
 
 
 @pytest.mark.parametrize("m, n, k, bt", [(4096, 4096, 36, False), (4096, 4096, 36, True), (2048, 2048, 100, False),
-                                         (2048, 2048, 100, True), (200, 300, 68, False), (200, 300, 68, True)])
+                                         (2048, 2048, 100, True), (200, 300, 68, False), (200, 300, 68, True),
+                                         (512, 1024, 1000, False), (512, 1024, 1000, True)])
 def test_mm_f32_tiles_exact_sums(m, n, k, bt):
     """Small-integer operands: every product and partial sum is exact in
-    fp32, so every output of each block shape (64 / 128 / 256 rows) must
-    equal the integer product (catches a lost, doubled or misplaced k chunk,
-    row or column)."""
+    fp32, so every output of each block shape (64 / 128 / 256 rows, and K
+    split in slices of 160) must equal the integer product (catches a lost,
+    doubled or misplaced k chunk, slice, row or column)."""
     g = torch.Generator().manual_seed(5)
     a = torch.randint(-8, 9, (m, k), generator=g).float()
     b = torch.randint(-8, 9, (k, n), generator=g).float()
     bg = b.cuda() if not bt else b.t().contiguous().cuda().t()
     got = ntops_amd.torch.mm(a.cuda(), bg)
-    bl = "B:K" if bt else "B:N"
-    assert _lib.last_kernel() == f"gemm_f32_lds m{f32_block_rows(m, n, 1, bl)} {bl}"
+    assert _lib.last_kernel().startswith(f32_expected_kernel(m, n, k, bt))
     exp = (a.double() @ b.double()).float()
     assert torch.equal(got.cpu(), exp)
 
