@@ -285,11 +285,12 @@ NTOPS_API int ntops_gemm(int dtype, int64_t batch, int64_t M, int64_t N, int64_t
                void* out, const int64_t* out_strides, void* stream);
 
 /* ntops_gemm with a caller-owned workspace (16-byte aligned device memory;
- * NULL or too small: the product runs as ntops_gemm).  bf16 / fp16 / fp32
- * products (batch 1) whose 128 x 128 tiles do not fill the GPU and whose K is
- * long enough split K over up to 16 slices: fp32 partial products into the
- * workspace, then their sum in slice order, so the result is deterministic
- * (it differs from ntops_gemm's only by the fp32 summation order). */
+ * NULL or too small: the product runs as ntops_gemm).  Products whose
+ * 128 x 128 tiles do not fill the GPU and whose K is long enough (bf16 /
+ * fp16: batch 1; fp32: any batch) split K over up to 16 slices: fp32 partial
+ * products into the workspace, then their sum in slice order, so the result
+ * is deterministic (it differs from ntops_gemm's only by the fp32 summation
+ * order). */
 NTOPS_API int ntops_gemm_ws(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
                const void* A, const int64_t* a_strides,
                const void* B, const int64_t* b_strides,

@@ -708,6 +708,18 @@ bool use_channels_last(const ConvArgs& a, int dt) {
          crs <= 0x7fffffffLL && pq <= 0x7fffffffLL;
 }
 
+// Workspace bytes after the unfold path's images through which its fp32
+// GEMM over nb images splits K (what ntops_gemm_workspace asks for; 0 for
+// 16-bit data and the implicit paths): a batch of per-image products with
+// few output channels and pixels fills few tiles otherwise.
+int64_t split_bytes(const ConvArgs& a, int dt, int64_t nb) {
+  if (dt != NTOPS_F32 || use_channels_last(a, dt) || use_implicit(a, dt)) return 0;
+  const int64_t pq = static_cast<int64_t>(a.P) * a.Q;
+  const int64_t cols = padded_out_bytes_per_image(a, dt) > 0 ? col_ld(a) : pq;
+  const int64_t w = ntops_gemm_workspace(dt, nb, a.K, cols, col_rows(a));
+  return w > 0 ? (w + 511) / 256 * 256 : 0;  // (room to start it 256-aligned)
+}
+
 // Workspace bytes per image of the chosen GEMM path.
 int64_t ws_bytes_per_image(const ConvArgs& a, int dt) {
   if (use_channels_last(a, dt)) return cl_rows(a) * cl_cols(a) * a.C * dtype_size(dt);
@@ -768,7 +780,7 @@ extern "C" int64_t ntops_conv2d_workspace(int dtype, int64_t N, int64_t C, int64
   a.w = nullptr;  // alignment is checked again on the call
   a.out = nullptr;
   if (!use_gemm(a, dtype)) return 0;
-  return ws_bytes_fixed(a, dtype) + ws_bytes_per_image(a, dtype) * N;
+  return ws_bytes_fixed(a, dtype) + ws_bytes_per_image(a, dtype) * N + split_bytes(a, dtype, N);
 }
 
 extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R,
@@ -948,9 +960,12 @@ extern "C" int ntops_conv2d(int dtype, int64_t N, int64_t C, int64_t H, int64_t 
     });
     if (rc != NTOPS_OK) return rc;
     void* dst = static_cast<char*>(out) + n0 * out_strides[0] * es;
-    rc = ntops_gemm(dtype, nb, K, padded ? ld : P * Q, kp, wa, a_str, col, b_str, bias,
-                    bias ? c_str : nullptr, 1.0, bias ? 1.0 : 0.0, padded ? staged : dst, padded ? s_str : d_str,
-                    stream);
+    // what the chunk leaves of the workspace serves the GEMM's split over K
+    const int64_t used = (fixed + nb_max * per_image + 255) / 256 * 256;
+    void* part = used < workspace_bytes ? static_cast<char*>(workspace) + used : nullptr;
+    rc = ntops_gemm_ws(dtype, nb, K, padded ? ld : P * Q, kp, wa, a_str, col, b_str, bias, bias ? c_str : nullptr,
+                       1.0, bias ? 1.0 : 0.0, padded ? staged : dst, padded ? s_str : d_str, part,
+                       part ? workspace_bytes - used : 0, stream);
     if (rc != NTOPS_OK) return rc;
     if (padded) {
       rc = dispatch_float16_32(dtype, "conv2d", [&](auto tag) {

@@ -199,6 +199,40 @@ def test_conv2d_workspace_chunks():
     assert_close(full, oracle(x.cpu(), wt.cpu(), b.cpu(), 1, 1, 1), 1.6e-2, 1.6e-2, "one chunk")
 
 
+@pytest.mark.parametrize("n, c, h, k, stride", [(8, 256, 14, 256, 1), (6, 128, 28, 128, 2), (3, 96, 20, 96, 1)])
+def test_conv2d_f32_split_k(n, c, h, k, stride):
+    """fp32 unfold + GEMM with few output tiles: the batched GEMM splits K
+    through the rest of the workspace (padded output planes included), and
+    equals the oracle; with a workspace that holds the images but not the
+    partial products it runs unsplit and agrees to fp32 summation order."""
+    g = torch.Generator().manual_seed(n + c + k)
+    x = torch.randn(n, c, h, h, generator=g)
+    wt = torch.randn(k, c, 3, 3, generator=g) / (9 * c) ** 0.5
+    b = torch.randn(k, generator=g)
+    got = conv2d(x.cuda(), wt.cuda(), bias=b.cuda(), stride=stride, padding=1)
+    assert _lib.last_kernel().startswith("gemm_f32_lds m128 B:N splitk"), _lib.last_kernel()
+    assert_close(got, oracle(x, wt, b, stride, 1, 1), 2e-5, 2e-5, "conv2d f32 split-K")
+    lib = _lib.load()
+    p = (h + 2 - 3) // stride + 1
+    geo = (n, c, h, h, k, 3, 3, p, p, stride, stride, 1, 1, 1, 1)
+    st = lambda t: _lib.i64_array(t.stride())  # noqa: E731
+    total = lib.ntops_conv2d_workspace(_lib.dtype_code(torch.float32), *geo, st(wt), st(got))
+    one = lib.ntops_conv2d_workspace(_lib.dtype_code(torch.float32), 1, *geo[1:], st(wt), st(got))
+    assert total > 0 and one > 0
+    # the images' bytes without the split's: total less the partial products (and their alignment room)
+    split = lib.ntops_gemm_workspace(_lib.dtype_code(torch.float32), n, k, -(-p * p // 8) * 8, c * 9)
+    assert split > 0
+    images = total - (split + 511) // 256 * 256
+    ws = torch.empty(images, dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(got)
+    xg, wg, bg = x.cuda(), wt.cuda(), b.cuda()
+    rc = lib.ntops_conv2d(_lib.dtype_code(torch.float32), *geo, xg.data_ptr(), st(xg), wg.data_ptr(), st(wg),
+                          bg.data_ptr(), 1, out.data_ptr(), st(out), ws.data_ptr(), images, _lib.stream_of(out))
+    _lib.check(rc, "conv2d")
+    assert "splitk" not in _lib.last_kernel(), _lib.last_kernel()
+    assert_close(out, got, 2e-5, 2e-5, "unsplit against split")
+
+
 @pytest.mark.parametrize("dtype", (torch.float32, torch.bfloat16))
 def test_conv2d_layouts_and_forms(dtype):
     g = torch.Generator().manual_seed(3)

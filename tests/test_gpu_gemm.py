@@ -397,13 +397,13 @@ def f32_expected_kernel(m, n, k, b_kmajor):
 
 def f32_block_rows(m, n, batch, bl):
     """Rows per block the fp32 tile kernel is launched with: 256 for an
-    N-major B when that gives two blocks per CU, 128 when 128-row blocks
-    fill every CU, else 64."""
+    N-major B of more than 128 rows when that gives two blocks per CU, 128 when 128-row blocks
+    fill every CU (and there are more than 64 rows), else 64."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     cols = -(-n // 128) * batch
-    if bl == "B:N" and -(-m // 256) * cols >= 2 * cus:
+    if bl == "B:N" and m > 128 and -(-m // 256) * cols >= 2 * cus:
         return 256
-    return 128 if -(-m // 128) * cols >= cus else 64
+    return 128 if m > 64 and -(-m // 128) * cols >= cus else 64
 
 
 @pytest.mark.parametrize("m, n, k, bt", [(4096, 4096, 36, False), (4096, 4096, 36, True), (2048, 2048, 100, False),
@@ -440,6 +440,11 @@ def test_addmm_and_bmm_f32_tiles():
     got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
     assert _lib.last_kernel() == f"gemm_f32_lds m{f32_block_rows(1030, 260, 3, 'B:N')} B:N"
     assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), 1e-5, 1e-5 * 8, "bmm f32 batched tiles")
+    a = torch.randn(5, 40, 72)  # a batch of few-row products: the skinny kernel
+    b = torch.randn(5, 72, 200)
+    got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
+    assert _lib.last_kernel().startswith("gemm_skinny_f32 "), _lib.last_kernel()
+    assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), 1e-5, 1e-5 * 9, "bmm f32 few rows")
 
 
 def test_addmm_and_bmm_small_m():
