@@ -365,8 +365,10 @@ NTOPS_API int ntops_rope_qk(int dtype, int64_t B, int64_t S, int64_t Hq, int64_t
  * unfold), in chunks of images; ntops_conv2d_workspace returns the bytes
  * that cover the whole batch in one chunk (0 when the problem runs without a
  * workspace): a per-call part plus a part per image, so its value for N = 1
- * is what one chunk of one image needs.  With less than that the direct
- * kernel runs. */
+ * is what one chunk of one image needs, and for fp32 on the unfold path room
+ * for the GEMM's partial products over K slices (used when what a chunk of
+ * images leaves of the workspace covers them; optional).  With less than the
+ * N = 1 value the direct kernel runs. */
 NTOPS_API int64_t ntops_conv2d_workspace(int dtype, int64_t N, int64_t C, int64_t H, int64_t W,
                int64_t K, int64_t R, int64_t S, int64_t P, int64_t Q,
                int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
