@@ -43,7 +43,8 @@
 // Short-K path (K <= 128, M and N multiples of 128): a persistent kernel
 // built around the output stream.
 // fp32 tile path (K-major A): v_mfma_f32_16x16x4_f32 wave tiles of 64 x 64,
-// 32-deep K tiles shared by the block through two LDS buffers.
+// 32-deep K tiles shared by the block through two LDS buffers, or (N-major B
+// filling the GPU) operands from L2 per wave.
 // Generic path (any other strides): 64x64 LDS-tiled FMA kernel with fp32
 // accumulation (IEEE; gfx950 has no reduced-precision fp32 MFMA input).
 #include "gemm.h"
@@ -1169,7 +1170,7 @@ int launch_skinny_f32(const GemmArgs& g, hipStream_t st) {
 
 // ---- fp32 tile kernel -------------------------------------------------------
 // fp32 products on v_mfma_f32_16x16x4_f32 (IEEE fp32 products, fp32
-// accumulation).  A block of WM x 2 waves (WM = 1, 2, 4) covers (64 WM) x 128 outputs, each
+// accumulation).  A block of WM x 2 waves (WM = 1 or 2) covers (64 WM) x 128 outputs, each
 // wave a 64 x 64 tile (4 x 4 MFMA tiles).  K advances in 32-deep tiles of A
 // and B shared through two LDS buffers: each thread loads its 16-byte chunks
 // of the next tile into registers before the current tile's MFMAs and writes
@@ -1336,6 +1337,109 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_f32_lds(GemmArgs g) {
             if (Cp != nullptr) v += g.beta * Cp[m * g.sc_m + n * g.sc_n];
             D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = v;
           }
+        }
+      }
+}
+
+// fp32 products with an N-major B, without shared LDS tiles: each wave owns
+// a 64 x 64 output tile and loads its operands straight from L2 (A as one
+// 16-byte load per lane and 16-row block holding k0 + 4 (l >> 4) + e, whose
+// element e feeds MFMA e; B as 16-byte row pieces, 4 k-rows x 64 columns per
+// instruction, staged in a per-wave LDS tile with padded rows and read back
+// per column).  The next 16-k step's operands are loaded before the current
+// step's MFMAs.  No barriers, four waves per SIMD; the k order is the LDS
+// kernel's, so the two give identical results.  Blocks of 2 x 2 waves cover
+// 128 x 128.
+__global__ __launch_bounds__(256, 3) void k_gemm_f32_reg(GemmArgs g) {
+  constexpr int TM = 4, TN = 4;
+  constexpr int kTrRow = 68;  // floats per k-row of the staged B tile (64 + 4: conflict-free reads)
+  __shared__ __attribute__((aligned(16))) float trs[4][16 * kTrRow];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tm_count = (g.M + 127) / 128, tn_count = (g.N + 127) / 128;
+  int bat, tmi, tni;
+  tile_of(blockIdx.x, gridDim.x, tm_count, tn_count, bat, tmi, tni);
+  const int m0 = tmi * 128 + (wave >> 1) * 64, n0 = tni * 128 + (wave & 1) * 64;
+  const int mv = max(0, min(64, g.M - m0)), nv = max(0, min(64, g.N - n0));
+  const int r16 = lane & 15, kq = (lane >> 4) * 4;
+  const float* A = static_cast<const float*>(g.A) + bat * g.sa_b;
+  const float* B = static_cast<const float*>(g.B) + bat * g.sb_b;
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc_uniform(
+      A + static_cast<int64_t>(m0) * g.sa_m,
+      mv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(mv - 1) * g.sa_m + g.K) * 4) : 0u);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc_uniform(
+      B + n0, nv > 0 ? static_cast<uint32_t>((static_cast<int64_t>(g.K - 1) * g.sb_k + nv) * 4) : 0u);
+  uint32_t a_off[TM];
+  bool a_ok[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    a_off[i] = static_cast<uint32_t>(((16 * i + r16) * g.sa_m + kq) * 4);
+    a_ok[i] = 16 * i + r16 < mv;
+  }
+  // load j covers k-rows 4 j + (l >> 4), columns 4 (l & 15) .. + 3
+  uint32_t b_off[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) b_off[j] = static_cast<uint32_t>(((4 * j + (lane >> 4)) * g.sb_k + 4 * r16) * 4);
+  const bool b_ok = 4 * r16 < nv;
+  const uint32_t b_kstep = static_cast<uint32_t>(g.sb_k * 4);  // bytes per k
+  auto load = [&](int k, f32x4 (&aq)[TM], f32x4 (&bq)[TN]) {
+    const bool k_ok = k + kq < g.K;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      aq[i] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, a_ok[i] && k_ok ? a_off[i] + k * 4u : kOOB, 0, 0));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const bool ok = b_ok && k + 4 * j + (lane >> 4) < g.K;
+      bq[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rb, ok ? b_off[j] + static_cast<uint32_t>(k) * b_kstep : kOOB, 0, 0));
+    }
+  };
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 aq[TM], bq[TN];
+  load(0, aq, bq);
+  for (int k0 = 0; k0 < g.K; k0 += 16) {
+    f32x4 an[TM], bn[TN];
+    load(k0 + 16, an, bn);  // past K every lane reads the out-of-range offset (zeros)
+    // Stage the step's 16 x 64 B tile (row-major, padded rows) and read
+    // column l & 15 of k-rows 4 (l >> 4) + e back for each 16-column group.
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      *reinterpret_cast<f32x4*>(&trs[wave][(4 * j + (lane >> 4)) * kTrRow + 4 * r16]) = bq[j];
+    f32x4 bf[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bf[j][e] = trs[wave][(kq + e) * kTrRow + 16 * j + r16];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[i][e], bf[j][e], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) aq[i] = an[i];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bq[j] = bn[j];
+  }
+  float* D = static_cast<float*>(g.D) + bat * g.sd_b;
+  const float* Cp = g.use_c ? static_cast<const float*>(g.C) + bat * g.sc_b : nullptr;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * i + (lane >> 4) * 4 + r, n = n0 + 16 * j + r16;
+        if (m < g.M && n < g.N) {
+          float v = g.alpha * acc[i][j][r];
+          if (Cp != nullptr) v += g.beta * Cp[m * g.sc_m + n * g.sc_n];
+          D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n) * g.sd_n] = v;
         }
       }
 }
@@ -1702,11 +1806,13 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     if (g.K > 0 && g.M <= kSkinnyMaxM && a_k && (b_k || b_n) && batch_ok && fits && aligned16(g.A) &&
         aligned16(g.B))
       return b_k ? launch_skinny_f32<true>(g, st) : launch_skinny_f32<false>(g, st);
-    // Larger fp32 products: the LDS-tiled MFMA kernel.  256-row blocks (8
-    // waves) for an N-major B of more than 128 rows when they give two blocks per CU (a few percent
-    // faster there; 128-row blocks are faster for a K-major B), 128-row blocks
-    // when those fill every CU and M > 64, else 64-row blocks (twice the
-    // blocks, none half empty).
+    // Larger fp32 products.  When 128 x 128 tiles fill every CU (and M > 64),
+    // the LDS-tiled kernel's 128-row blocks, except for an N-major B with
+    // three or more tiles per CU: the LDS-free kernel, whose four waves per
+    // SIMD then beat the LDS kernel's two by 4-8 % (with one tile per CU it
+    // is 12-23 % slower, and 3-5 % slower for a K-major B at any count).
+    // Fewer tiles: the LDS kernel's 64-row blocks (twice the blocks, none
+    // half empty).
     const bool b_n4 = g.sb_n == 1 && g.sb_k % 4 == 0 && g.N % 4 == 0 && !b_k;
     const bool fits_t = (256 * g.sa_m + g.K) * 4 < lim &&
                         (b_k ? (128 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 128)) * 4 < lim;
@@ -1720,10 +1826,14 @@ int run_gemm(GemmArgs g, hipStream_t st) {
         return b_k ? launch_f32_splitk<true>(g, S, st) : launch_f32_splitk<false>(g, S, st);
       }
       const int64_t cus = cu_count_cached() > 0 ? cu_count_cached() : 256;
-      const int64_t cols = (g.N + 127) / 128 * g.batch;
-      if (!b_k && g.M > 128 && (g.M + 255) / 256 * cols >= 2 * cus) return launch_f32_lds<false, 4>(g, st);
-      if (g.M > 64 && (g.M + 127) / 128 * cols >= cus)
-        return b_k ? launch_f32_lds<true, 2>(g, st) : launch_f32_lds<false, 2>(g, st);
+      const int64_t tiles = static_cast<int64_t>((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
+      if (g.M > 64 && tiles >= cus) {
+        if (b_k || tiles < 3 * cus) return b_k ? launch_f32_lds<true, 2>(g, st) : launch_f32_lds<false, 2>(g, st);
+        if (tiles > 0x7fffffffLL) return set_error(NTOPS_ERR_UNSUPPORTED, "gemm: too many tiles");
+        note_kernel("gemm_f32_reg B:N");
+        hipLaunchKernelGGL(k_gemm_f32_reg, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, g);
+        return check_launch("gemm");
+      }
       return b_k ? launch_f32_lds<true, 1>(g, st) : launch_f32_lds<false, 1>(g, st);
     }
   }

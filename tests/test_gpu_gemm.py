@@ -392,18 +392,19 @@ def f32_expected_kernel(m, n, k, b_kmajor):
     np_ = -(-n // 4) * 4
     if _lib.load().ntops_gemm_workspace(_lib.dtype_code(torch.float32), 1, m, np_, k) > 0:
         return f"gemm_f32_lds m128 {bl} splitk"
-    return f"gemm_f32_lds m{f32_block_rows(m, np_, 1, bl)} {bl}"
+    return f32_tile_kernel(m, np_, 1, bl)
 
 
-def f32_block_rows(m, n, batch, bl):
-    """Rows per block the fp32 tile kernel is launched with: 256 for an
-    N-major B of more than 128 rows when that gives two blocks per CU, 128 when 128-row blocks
-    fill every CU (and there are more than 64 rows), else 64."""
+def f32_tile_kernel(m, n, batch, bl):
+    """Unsplit fp32 tile kernel: when 128 x 128 tiles fill every CU (and
+    there are more than 64 rows) the LDS kernel's 128-row blocks, or the
+    LDS-free kernel for an N-major B with three or more tiles per CU; else
+    the LDS kernel's 64-row blocks."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    cols = -(-n // 128) * batch
-    if bl == "B:N" and m > 128 and -(-m // 256) * cols >= 2 * cus:
-        return 256
-    return 128 if m > 64 and -(-m // 128) * cols >= cus else 64
+    tiles = -(-m // 128) * -(-n // 128) * batch
+    if m > 64 and tiles >= cus:
+        return "gemm_f32_reg B:N" if bl == "B:N" and tiles >= 3 * cus else f"gemm_f32_lds m128 {bl}"
+    return f"gemm_f32_lds m64 {bl}"
 
 
 @pytest.mark.parametrize("m, n, k, bt", [(4096, 4096, 36, False), (4096, 4096, 36, True), (2048, 2048, 100, False),
@@ -411,9 +412,10 @@ def f32_block_rows(m, n, batch, bl):
                                          (512, 1024, 1000, False), (512, 1024, 1000, True)])
 def test_mm_f32_tiles_exact_sums(m, n, k, bt):
     """Small-integer operands: every product and partial sum is exact in
-    fp32, so every output of each block shape (64 / 128 / 256 rows, and K
-    split in slices of 160) must equal the integer product (catches a lost,
-    doubled or misplaced k chunk, slice, row or column)."""
+    fp32, so every output of each fp32 tile kernel (LDS blocks of 64 and 128
+    rows, the LDS-free kernel, K split in slices of 160) must equal the
+    integer product (catches a lost, doubled or misplaced k chunk, slice, row
+    or column)."""
     g = torch.Generator().manual_seed(5)
     a = torch.randint(-8, 9, (m, k), generator=g).float()
     b = torch.randint(-8, 9, (k, n), generator=g).float()
@@ -438,7 +440,7 @@ def test_addmm_and_bmm_f32_tiles():
     a = torch.randn(3, 1030, 64)
     b = torch.randn(3, 64, 260)
     got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
-    assert _lib.last_kernel() == f"gemm_f32_lds m{f32_block_rows(1030, 260, 3, 'B:N')} B:N"
+    assert _lib.last_kernel() == f32_tile_kernel(1030, 260, 3, "B:N")
     assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), 1e-5, 1e-5 * 8, "bmm f32 batched tiles")
     a = torch.randn(5, 40, 72)  # a batch of few-row products: the skinny kernel
     b = torch.randn(5, 72, 200)
