@@ -1673,12 +1673,13 @@ int splitk_slices(int64_t M, int64_t N, int64_t K, int* kchunk) {
 // fp32 split over K for products whose 128 x 128 tiles leave CUs idle:
 // up to two blocks per CU, slices of at least 128 k (an fp32 k-step costs
 // eight times a 16-bit one on the matrix cores, so shorter slices than the
-// 16-bit path's 512 still pay for their partial tile).
+// 16-bit path's 512 still pay for their partial tile); products with one to
+// two tiles per CU (one wave per SIMD) and K >= 1024 split in two.
 int splitk_slices_f32(int64_t M, int64_t N, int64_t K, int64_t batch, int* kchunk) {
   const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128) * batch;
   const int64_t cus = cu_count_cached() > 0 ? cu_count_cached() : 256;
-  if (tiles >= cus || M <= kSkinnyMaxM || N % 4 != 0) return 1;
-  int64_t S = std::min<int64_t>(std::min<int64_t>(2 * cus / tiles, K / 128), 16);
+  if (tiles >= 2 * cus || M <= kSkinnyMaxM || N % 4 != 0) return 1;
+  int64_t S = tiles >= cus ? (K >= 1024 ? 2 : 1) : std::min<int64_t>(std::min<int64_t>(2 * cus / tiles, K / 128), 16);
   if (S < 2) return 1;
   const int64_t chunk = ((K + S - 1) / S + 31) / 32 * 32;
   *kchunk = static_cast<int>(chunk);

@@ -442,6 +442,12 @@ def test_addmm_and_bmm_f32_tiles():
     got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
     assert _lib.last_kernel() == f32_tile_kernel(1030, 260, 3, "B:N")
     assert_close(got, from_np(O.gemm(to_np(a), to_np(b), "f32"), "f32"), 1e-5, 1e-5 * 8, "bmm f32 batched tiles")
+    g = torch.Generator().manual_seed(11)  # a batch filling the GPU three times over: the LDS-free kernel
+    a = torch.randint(-8, 9, (8, 1024, 68), generator=g).float()
+    b = torch.randint(-8, 9, (8, 68, 1536), generator=g).float()
+    got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
+    assert _lib.last_kernel() == f32_tile_kernel(1024, 1536, 8, "B:N")
+    assert torch.equal(got.cpu(), torch.bmm(a.double(), b.double()).float()), "bmm f32 exact sums"
     a = torch.randn(5, 40, 72)  # a batch of few-row products: the skinny kernel
     b = torch.randn(5, 72, 200)
     got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
