@@ -989,14 +989,19 @@ int launch_skinny_mb(const GemmArgs& g, hipStream_t st, int j) {
   return check_launch("gemm");
 }
 
-// Column-slice width 16 j: the widest that still gives every CU a block.
+// Column-slice width 16 j: the widest that still gives three quarters of
+// the CUs a block.  Wider slices read whole 128-byte lines of an N-major B
+// row (32 columns: half lines) and more columns per A fragment: N = 14336,
+// K = 4096 runs 25-26 us in 224 64-column blocks against 34-39 us in 448
+// 32-column ones (N-major B; K-major at 16 rows 28 against 31.5), while one
+// block per CU stays better than fewer (N = 4096: 256 16-column blocks).
 // (16-wave blocks splitting K finer for the few-block shapes, e.g.
 // 16 x 4096 x 14336, measured no faster than 4-wave ones.)
 int skinny_j(int64_t M, int64_t N, int64_t batch) {
   const int mb = static_cast<int>((M + 15) / 16);
   const int cus = cu_count_cached() > 0 ? cu_count_cached() : 256;
   for (int c : {4, 2})
-    if (c <= kSkinnyMaxJ(mb) && (N + 16 * c - 1) / (16 * c) * batch >= cus) return c;
+    if (c <= kSkinnyMaxJ(mb) && (N + 16 * c - 1) / (16 * c) * batch * 4 >= 3 * cus) return c;
   return 1;
 }
 
