@@ -1162,7 +1162,7 @@ int launch_skinny_f32(const GemmArgs& g, hipStream_t st) {
   const int cus = cu_count_cached() > 0 ? cu_count_cached() : 256;
   int j = 1;
   for (int c : {4, 2}) {
-    if (c <= kSkinnyMaxJ(mb) && static_cast<int64_t>((g.N + 16 * c - 1) / (16 * c)) * g.batch >= cus) {
+    if (c <= kSkinnyMaxJ(mb) && static_cast<int64_t>((g.N + 16 * c - 1) / (16 * c)) * g.batch * 4 >= 3 * cus) {
       j = c;
       break;
     }
@@ -1808,7 +1808,8 @@ int run_gemm(GemmArgs g, hipStream_t st) {
                       (b_k ? (16 * 64 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 64)) * 4 < lim;
     // (also for a batch of them: a convolution's 64-channel images of 3136
     // pixels measured 158 us here against 181 us in the tile kernel's 64-row
-    // blocks)
+    // blocks; and 33-64 rows split over K in 64-row blocks measured slower,
+    // 64 x 14336 x 4096 139 against 114 us, except at K = 14336)
     if (g.K > 0 && g.M <= kSkinnyMaxM && a_k && (b_k || b_n) && batch_ok && fits && aligned16(g.A) &&
         aligned16(g.B))
       return b_k ? launch_skinny_f32<true>(g, st) : launch_skinny_f32<false>(g, st);
