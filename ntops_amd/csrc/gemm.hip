@@ -67,6 +67,7 @@ struct GemmArgs {
   int use_c;
   int c_mode;  // epilogue's C access (kCNone / kCStrided / kCVec4 / kCRow), set by set_c_mode
   int staged;  // out is 16-byte aligned with unit column stride and N % 8 == 0
+  int ragged;  // out rows are not 8-byte aligned runs with unit column stride: element stores
   // Split-K (the SPLITK instantiation): block row blockIdx.y takes k in
   // [blockIdx.y * kchunk, min(K, (blockIdx.y + 1) * kchunk)) and writes its
   // fp32 partial tile to part + blockIdx.y * part_stride (rows of N).
@@ -451,7 +452,35 @@ __device__ __forceinline__ void store_tile_direct(const GemmArgs& g, const f32x1
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = nw + j * 32 + q * 8 + (lane >> 5) * 4;
-        // N % 4 == 0 on this path, so columns n .. n + 3 are all in or all out
+        if (g.ragged) {
+          // rows of any stride, N of any width: element stores, C read per element
+          if (m < g.M) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (n + e < g.N) {
+                float cv[4] = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (CM != kCNone)
+                  cv[e] = g.beta * static_cast<float>(Cp[m * g.sc_m + (n + e) * g.sc_n]);
+                D[static_cast<int64_t>(m) * g.sd_m + static_cast<int64_t>(n + e) * g.sd_n] =
+                    static_cast<T>(final_value<T, CM>(g, acc, cv, i, j, q, e));
+              }
+            }
+          }
+          continue;
+        }
+        if (!EVEN && m < g.M && n < g.N && n + 3 >= g.N) {
+          // the last, partial 4-column group of a row (N % 4 != 0)
+#pragma unroll
+          for (int e = 0; e < 3; ++e) {
+            if (n + e < g.N) {
+              float cv[4] = {0.f, 0.f, 0.f, 0.f};
+              if constexpr (CM != kCNone)
+                cv[e] = g.beta * static_cast<float>(Cp[m * g.sc_m + (n + e) * g.sc_n]);
+              D[static_cast<int64_t>(m) * g.sd_m + n + e] = static_cast<T>(final_value<T, CM>(g, acc, cv, i, j, q, e));
+            }
+          }
+          continue;
+        }
         if (EVEN || (m < g.M && n + 3 < g.N)) {
           float cv[4];
           c_values<T, CM>(g, Cp, m, n, true, cv);
@@ -1764,8 +1793,8 @@ int run_gemm(GemmArgs g, hipStream_t st) {
     const bool a_m = g.sa_m == 1 && g.sa_k % 8 == 0 && g.M % 8 == 0 && !a_k;
     const bool b_k = g.sb_k == 1 && g.sb_n % 8 == 0 && g.K % 8 == 0;
     const bool b_n = g.sb_n == 1 && g.sb_k % 8 == 0 && g.N % 8 == 0 && !b_k;
-    const bool d_ok = g.sd_n == 1 && g.sd_m % 4 == 0 && g.sd_b % 4 == 0 &&
-                      (reinterpret_cast<uintptr_t>(g.D) & 7u) == 0 && g.N % 4 == 0;
+    // (any output layout: 4-column runs at 8-byte aligned addresses are
+    // stored as such, anything else element by element -- g.ragged)
     const bool batch_ok = (g.batch == 1) || (g.sa_b % 8 == 0 && g.sb_b % 8 == 0);
     // Every operand byte offset inside a tile's buffer resource must stay
     // below 2 GiB (out-of-range chunks use offset 2^31).
@@ -1774,10 +1803,11 @@ int run_gemm(GemmArgs g, hipStream_t st) {
                       (b_k ? (256 * g.sb_n + g.K) : (static_cast<int64_t>(g.K) * g.sb_k + 256)) * 2 < lim;
     // K == 0 goes to the generic kernel, which never touches A or B (they may
     // be null, and an empty M/N-major operand has no valid buffer extent).
-    if (g.K > 0 && (a_k || a_m) && (b_k || b_n) && d_ok && batch_ok && fits && al(g.A) && al(g.B)) {
+    if (g.K > 0 && (a_k || a_m) && (b_k || b_n) && batch_ok && fits && al(g.A) && al(g.B)) {
       int kchunk = 0;
       // (up to kSplitKMinM rows a K-major A takes the skinny kernel)
-      const int S = (g.part != nullptr && g.batch == 1 && (g.M > kSplitKMinM || !a_k))
+      // (the reduce kernel sums 4-column groups: N % 4 == 0)
+      const int S = (g.part != nullptr && g.batch == 1 && g.N % 4 == 0 && (g.M > kSplitKMinM || !a_k))
                         ? splitk_slices(g.M, g.N, g.K, &kchunk)
                         : 1;
       if (S > 1 && static_cast<int64_t>(S) * g.M * g.N * 4 <= g.part_bytes) {
@@ -2017,6 +2047,10 @@ static int gemm_entry(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
   g.alpha = static_cast<float>(alpha);
   g.beta = static_cast<float>(beta);
   g.use_c = (C != nullptr && beta != 0.0) ? 1 : 0;
+  g.ragged = (out_strides[2] == 1 && out_strides[1] % 4 == 0 && (batch == 1 || out_strides[0] % 4 == 0) &&
+              (reinterpret_cast<uintptr_t>(out) & 7u) == 0)
+                 ? 0
+                 : 1;
   g.staged = (out_strides[2] == 1 && out_strides[1] % 8 == 0 && (batch == 1 || out_strides[0] % 8 == 0) &&
               N % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0)
                  ? 1

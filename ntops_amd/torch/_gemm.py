@@ -18,12 +18,13 @@ def _strides3(t):
 def _padded_width(a, b, n):
     """Column count to run the GEMM at when n columns would send it to the
     generic kernel (None otherwise): the matrix-core kernels load an N-major
-    B in 16-byte row pieces (16-bit: N % 8 == 0; fp32: N % 4 == 0) and store
-    4-column runs (N % 4 == 0)."""
+    B in 16-byte row pieces (16-bit: N % 8 == 0; fp32: N % 4 == 0).  A K-major
+    B has no such limit, and output rows of any width are stored element by
+    element."""
     unit = 4 if a.dtype == torch.float32 else 8
     if n <= unit or n % unit == 0 or a.shape[-1] == 0 or a.shape[-2] == 0:
         return None
-    if n % 4 == 0 and b.stride(-2) == 1 and b.stride(-1) != 1:  # K-major B: N is free
+    if b.stride(-2) == 1 and b.stride(-1) != 1:  # K-major B: N is free
         return None
     return (n + unit - 1) // unit * unit
 

@@ -53,20 +53,22 @@ def expected16(m, n, k, layout, batch=1):
         # the wrapper zero-extends K to a multiple of 8, both operands copied
         # into fresh row-major tensors
         k, layout = (k + 7) // 8 * 8, "NN"
-    if n > 8 and n % 8 and (n % 4 or layout[1] == "N") and k > 0:
+    if n > 8 and n % 8 and layout[1] == "N" and k > 0:
         # the wrapper runs the product at the width rounded up to 8 columns,
-        # B copied N-major
+        # B copied into rows of that width (a K-major B runs as it is: the
+        # kernels store rows of any width element by element)
         n, layout = (n + 7) // 8 * 8, layout[0] + "N"
     a_k = layout[0] == "N" and k % 8 == 0
     a_m = layout[0] == "T" and m % 8 == 0
     b_n = layout[1] == "N" and n % 8 == 0
     b_k = layout[1] == "T" and k % 8 == 0
-    if k == 0 or not (a_k or a_m) or not (b_k or b_n) or n % 4:
+    if k == 0 or not (a_k or a_m) or not (b_k or b_n):
         return "gemm_generic"
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     tiles = -(-m // 128) * -(-n // 128) * batch
     few_tiles = tiles * 4 <= cus * 3
-    if batch == 1 and (m > 16 or not a_k) and k >= 1024 and few_tiles and min(2 * cus // tiles, k // 512) >= 2:
+    if (batch == 1 and n % 4 == 0 and (m > 16 or not a_k) and k >= 1024 and few_tiles
+            and min(2 * cus // tiles, k // 512) >= 2):
         return "gemm_mfma 128x128 "  # split K through the wrapper's workspace
     if a_k and (m <= 32 or (m <= 64 and few_tiles)):
         return "gemm_skinny "
@@ -197,6 +199,42 @@ def test_mm_odd_n(m, n, k, dtype, layout):
     got = ntops_amd.torch.addmm(bias.cuda(), a.cuda(), bg, beta=0.5, alpha=2.0)
     check(got[rows], a[rows], b, dtype, c=bias.expand(len(rows), n), alpha=2.0, beta=0.5,
           what=f"addmm odd n {layout}")
+
+
+@pytest.mark.parametrize("form", ("odd_row_stride", "column_major"))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("m, n, k", [(300, 264, 256), (1024, 1000, 512), (40, 129, 520), (600, 50257, 64)])
+def test_gemm_ragged_output_through_the_c_abi(m, n, k, dtype, form):
+    """Outputs the 4-column vector stores cannot take (a row stride of an odd
+    element count at a 2-byte offset, a column-major view) and widths of any
+    N, with a K-major B (F.linear's weight) and a bias row: the matrix-core
+    kernels store them element by element; the bytes around the view stay
+    untouched."""
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(m + n + k)
+    a = (0.1 * torch.randn(m, k, generator=g)).to(dtype)
+    w = (0.1 * torch.randn(n, k, generator=g)).to(dtype)  # B = w.t(), K-major
+    bias = (0.1 * torch.randn(n, generator=g)).to(dtype)
+    ag, wg, biasg = a.cuda(), w.cuda(), bias.cuda()
+    if form == "odd_row_stride":
+        big = torch.zeros(m, n + 3, dtype=dtype, device="cuda")
+        out, ostr = big[:, 1:1 + n], (0, n + 3, 1)
+    else:
+        big = torch.zeros(n, m + 2, dtype=dtype, device="cuda")
+        out, ostr = big[:, :m].t(), (0, 1, m + 2)
+    rc = lib.ntops_gemm(_lib.dtype_code(dtype), 1, m, n, k, ag.data_ptr(), _lib.i64_array((0, k, 1)),
+                        wg.data_ptr(), _lib.i64_array((0, 1, k)), biasg.data_ptr(), _lib.i64_array((0, 0, 1)),
+                        2.0, 0.5, out.data_ptr(), _lib.i64_array(ostr), _lib.stream_of(out))
+    _lib.check(rc, "ntops_gemm ragged output")
+    assert not _lib.last_kernel().startswith("gemm_generic"), _lib.last_kernel()
+    torch.cuda.synchronize()
+    if form == "odd_row_stride":
+        assert big[:, 0].abs().sum() == 0 and big[:, 1 + n:].abs().sum() == 0
+    else:
+        assert big[:, m:].abs().sum() == 0
+    rows = tile_rows(m) if m > 512 else list(range(m))
+    check(out[rows], a[rows], w.t(), dtype, c=bias.expand(len(rows), n), alpha=2.0, beta=0.5,
+          what=f"ragged output {form}")
 
 
 # K not a multiple of 8 (or of 4): A's rows and B's columns zero-extended so
@@ -384,12 +422,12 @@ def test_mm_f32_tiles(m, n, k, layout):
 
 
 def f32_expected_kernel(m, n, k, b_kmajor):
-    """The fp32 tile kernel a 2-D product takes.  A K-major B whose N is not a
-    multiple of 4 is copied N-major by the wrapper into rows padded to a
-    multiple of 4; products whose tiles leave CUs idle split K when the
-    workspace query says so."""
-    bl = "B:K" if b_kmajor and n % 4 == 0 else "B:N"
-    np_ = -(-n // 4) * 4
+    """The fp32 tile kernel a 2-D product takes.  An N-major B whose N is not
+    a multiple of 4 is copied by the wrapper into rows padded to a multiple of
+    4 (a K-major B runs as it is); products whose tiles leave CUs idle split K
+    when the workspace query says so."""
+    bl = "B:K" if b_kmajor else "B:N"
+    np_ = n if b_kmajor else -(-n // 4) * 4
     if _lib.load().ntops_gemm_workspace(_lib.dtype_code(torch.float32), 1, m, np_, k) > 0:
         return f"gemm_f32_lds m128 {bl} splitk"
     return f32_tile_kernel(m, np_, 1, bl)
