@@ -1770,6 +1770,39 @@ int pick_tile(const GemmArgs& g, hipStream_t st) {
   if (big_tiles >= 240 && g.K > 256) {
     const bool even = g.M % 256 == 0 && g.N % 256 == 0 && g.K % kBK == 0;
     if (even) return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, AK, BKM, true>(g, st);
+    // M or N not a multiple of 256: the bounds-checked kernel runs a third
+    // slower than the even one over the whole product (bf16 8192 x 50264 x
+    // 768: 839 against 625 us at N = 50176), so the even kernel takes the
+    // 256-aligned interior and 128 x 128 ragged tiles the edge strips (right:
+    // all rows; bottom: the interior's columns).
+    const int m0 = g.M / 256 * 256, n0 = g.N / 256 * 256;
+    if (g.K % kBK == 0 && static_cast<int64_t>(m0 / 256) * (n0 / 256) * g.batch >= 240) {
+      const int64_t es = sizeof(T);
+      GemmArgs in = g;
+      in.M = m0;
+      in.N = n0;
+      int rc = launch_mfma<T, 256, 256, 2, 4, kBK, kStages, AK, BKM, true>(in, st);
+      if (rc == NTOPS_OK && n0 < g.N) {
+        GemmArgs r = g;
+        r.N = g.N - n0;
+        r.B = static_cast<const char*>(g.B) + n0 * g.sb_n * es;
+        r.D = static_cast<char*>(g.D) + n0 * g.sd_n * es;
+        if (g.use_c) r.C = static_cast<const char*>(g.C) + n0 * g.sc_n * es;
+        rc = launch_mfma<T, 128, 128, 2, 2, kBK, kStages, AK, BKM, false>(r, st);
+      }
+      if (rc == NTOPS_OK && m0 < g.M) {
+        GemmArgs b = g;
+        b.M = g.M - m0;
+        b.N = n0;
+        b.A = static_cast<const char*>(g.A) + m0 * g.sa_m * es;
+        b.D = static_cast<char*>(g.D) + m0 * g.sd_m * es;
+        if (g.use_c) b.C = static_cast<const char*>(g.C) + m0 * g.sc_m * es;
+        rc = launch_mfma<T, 128, 128, 2, 2, kBK, kStages, AK, BKM, false>(b, st);
+      }
+      if (rc == NTOPS_OK)
+        note_kernel("gemm_mfma 256x256 s4 %s %s even+edges", AK ? "A:K" : "A:M", BKM ? "B:K" : "B:N");
+      return rc;
+    }
     return launch_mfma<T, 256, 256, 2, 4, kBK, kStages, AK, BKM, false>(g, st);
   }
   const bool even = g.M % 128 == 0 && g.N % 128 == 0 && g.K % kBK == 0;

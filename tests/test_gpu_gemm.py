@@ -237,6 +237,31 @@ def test_gemm_ragged_output_through_the_c_abi(m, n, k, dtype, form):
           what=f"ragged output {form}")
 
 
+@pytest.mark.parametrize("m, n, k, b_kmajor", [(4100, 4200, 512, False), (4100, 4200, 512, True),
+                                              (4136, 4099, 320, True), (4096, 4360, 1024, False)])
+def test_mm_even_interior_and_edge_strips(m, n, k, b_kmajor):
+    """Large products whose M or N is not a multiple of 256: the even 256 x
+    256 kernel on the interior, ragged 128 x 128 tiles on the right and bottom
+    strips.  Small-integer operands make every fp32 sum exact, so each output
+    equals the double-precision product rounded once to bf16; an addmm with a
+    bias row is checked on sampled rows against the oracle."""
+    g = torch.Generator().manual_seed(m + n + k)
+    a = torch.randint(-8, 9, (m, k), generator=g).to(torch.bfloat16)
+    b = torch.randint(-8, 9, (k, n), generator=g).to(torch.bfloat16)
+    bg = b.cuda() if not b_kmajor else b.t().contiguous().cuda().t()
+    got = ntops_amd.torch.mm(a.cuda(), bg)
+    assert _lib.last_kernel().endswith("even+edges"), _lib.last_kernel()
+    exp = (a.double() @ b.double()).float().bfloat16()
+    assert torch.equal(got.cpu(), exp)
+    bias = (0.1 * torch.randn(n, generator=g)).bfloat16()
+    af, bf_ = (0.1 * torch.randn(m, k, generator=g)).bfloat16(), (0.1 * torch.randn(k, n, generator=g)).bfloat16()
+    bfg = bf_.cuda() if not b_kmajor else bf_.t().contiguous().cuda().t()
+    got = ntops_amd.torch.addmm(bias.cuda(), af.cuda(), bfg, beta=0.5, alpha=2.0)
+    rows = tile_rows(m)
+    check(got[rows], af[rows], bf_, torch.bfloat16, c=bias.expand(len(rows), n), alpha=2.0, beta=0.5,
+          what="addmm interior + edges")
+
+
 # K not a multiple of 8 (or of 4): A's rows and B's columns zero-extended so
 # the matrix cores take the product.
 ODD_K = [(300, 256, 100), (1000, 1024, 1001), (40, 512, 77), (2048, 2048, 4095)]
