@@ -68,6 +68,7 @@ struct GemmArgs {
   int c_mode;  // epilogue's C access (kCNone / kCStrided / kCVec4 / kCRow), set by set_c_mode
   int staged;  // out is 16-byte aligned with unit column stride and N % 8 == 0
   int ragged;  // out rows are not 8-byte aligned runs with unit column stride: element stores
+  int shifted;  // unit column stride, rows not 16-byte aligned: full-tile kernels store shifted 16-byte chunks
   // Split-K (the SPLITK instantiation): block row blockIdx.y takes k in
   // [blockIdx.y * kchunk, min(K, (blockIdx.y + 1) * kchunk)) and writes its
   // fp32 partial tile to part + blockIdx.y * part_stride (rows of N).
@@ -430,6 +431,83 @@ __device__ __forceinline__ void store_rows(const GemmArgs& g, const u32x4 (&rows
   }
 }
 
+// Staged rows of a 16-bit output whose rows start anywhere (2-byte aligned):
+// each wave-tile row segment is 64 columns = 128 bytes at byte address G0 with
+// s = G0 % 16.  Lane c of the row's 8 lanes (holding columns 8c .. 8c + 7)
+// writes the aligned 16-byte chunk that starts 16 (c + 1) - s bytes into the
+// segment (c < 7): the top s bytes of its own chunk and the low 16 - s of the
+// next lane's; lane 0 also writes the segment's first (16 - s) / 2 columns and
+// lane 7 its last s / 2, element by element.  Every store stays inside the
+// segment.  Full tiles only (EVEN): no column of a segment lies past N.
+template <typename T, int WTM, bool NT>
+__device__ __forceinline__ void store_rows_shifted(const GemmArgs& g, const u32x4 (&rows)[WTM / 8], T* D,
+                                                   int mw, int nw, int lane) {
+  static_assert(sizeof(T) == 2, "16-bit outputs");
+#pragma unroll
+  for (int r0 = 0; r0 < WTM; r0 += 8) {
+    const int r = r0 + (lane >> 3), c = lane & 7;
+    const u32x4 cur = rows[r0 / 8];
+    u32x4 nxt;
+    nxt.x = static_cast<uint32_t>(__shfl_down(static_cast<int>(cur.x), 1, 8));
+    nxt.y = static_cast<uint32_t>(__shfl_down(static_cast<int>(cur.y), 1, 8));
+    nxt.z = static_cast<uint32_t>(__shfl_down(static_cast<int>(cur.z), 1, 8));
+    nxt.w = static_cast<uint32_t>(__shfl_down(static_cast<int>(cur.w), 1, 8));
+    T* seg = D + static_cast<int64_t>(mw + r) * g.sd_m + nw;
+    const uint32_t s = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(seg)) & 15u;
+    if (s == 0) {
+      u32x4* dst = reinterpret_cast<u32x4*>(seg + 8 * c);
+      if constexpr (NT)
+        __builtin_nontemporal_store(cur, dst);
+      else
+        *dst = cur;
+      continue;
+    }
+    // (cur | nxt) >> 8 * (16 - s) bits, as 64-bit halves
+    const uint64_t x0 = cur.x | (static_cast<uint64_t>(cur.y) << 32), x1 = cur.z | (static_cast<uint64_t>(cur.w) << 32);
+    const uint64_t x2 = nxt.x | (static_cast<uint64_t>(nxt.y) << 32), x3 = nxt.z | (static_cast<uint64_t>(nxt.w) << 32);
+    const uint32_t sh = 8u * (16u - s);  // 16 .. 112 bits
+    uint64_t o0, o1;
+    if (sh < 64) {
+      o0 = (x0 >> sh) | (x1 << (64 - sh));
+      o1 = (x1 >> sh) | (x2 << (64 - sh));
+    } else if (sh == 64) {
+      o0 = x1;
+      o1 = x2;
+    } else {
+      const uint32_t k = sh - 64;
+      o0 = (x1 >> k) | (x2 << (64 - k));
+      o1 = (x2 >> k) | (x3 << (64 - k));
+    }
+    char* base = reinterpret_cast<char*>(seg) - s;  // the 16-byte aligned address below G0
+    if (c < 7) {
+      const u32x4 v = {static_cast<uint32_t>(o0), static_cast<uint32_t>(o0 >> 32), static_cast<uint32_t>(o1),
+                       static_cast<uint32_t>(o1 >> 32)};
+      u32x4* dst = reinterpret_cast<u32x4*>(base + 16 * (c + 1));
+      if constexpr (NT)
+        __builtin_nontemporal_store(v, dst);
+      else
+        *dst = v;
+    }
+    auto elem = [&](uint32_t e) -> uint16_t {
+      const uint32_t d = e < 2 ? cur.x : e < 4 ? cur.y : e < 6 ? cur.z : cur.w;
+      return static_cast<uint16_t>(d >> (16 * (e & 1)));
+    };
+    uint16_t* seg16 = reinterpret_cast<uint16_t*>(seg);
+    if (c == 0)
+      for (uint32_t e = 0; e < (16u - s) / 2; ++e) seg16[e] = elem(e);
+    if (c == 7)
+      for (uint32_t e = 8 - s / 2; e < 8; ++e) seg16[56 + e] = elem(e);
+  }
+}
+
+template <typename T, int CM, int TM, int TN, int WTM, int WTN, bool EVEN, bool NT>
+__device__ __forceinline__ void store_tile_shifted(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
+                                                   char* ep, T* D, const T* Cp, int mw, int nw, int lane) {
+  u32x4 rows[WTM / 8];
+  stage_tile<T, CM, TM, TN, WTM, WTN, EVEN>(g, acc, ep, Cp, mw, nw, lane, rows);
+  store_rows_shifted<T, WTM, NT>(g, rows, D, mw, nw, lane);
+}
+
 template <typename T, int CM, int TM, int TN, int WTM, int WTN, bool EVEN, bool NT>
 __device__ __forceinline__ void store_tile_staged(const GemmArgs& g, const f32x16 (&acc)[TM][TN],
                                                   char* ep, T* D, const T* Cp, int mw, int nw,
@@ -666,6 +744,8 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(GemmArgs g) {
     constexpr int CM = decltype(cm_tag)::value;
     if (g.staged)
       store_tile_staged<T, CM, TM, TN, WTM, WTN, EVEN, kStreamOutMfma>(g, acc, ep, D, Cp, mw, nw, lane);
+    else if (EVEN && WTN == 64 && g.shifted)
+      store_tile_shifted<T, CM, TM, TN, WTM, WTN, EVEN, kStreamOutMfma>(g, acc, ep, D, Cp, mw, nw, lane);
     else
       store_tile_direct<T, CM, TM, TN, EVEN>(g, acc, D, Cp, mw, nw, lane);
   };
@@ -2088,6 +2168,7 @@ static int gemm_entry(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
               N % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0)
                  ? 1
                  : 0;
+  g.shifted = (!g.staged && out_strides[2] == 1 && (reinterpret_cast<uintptr_t>(out) & 1u) == 0) ? 1 : 0;
   g.C = C;
   if (g.use_c) {
     if (c_strides == nullptr) return set_error(NTOPS_ERR_INVALID, "gemm: null C strides");

@@ -262,6 +262,45 @@ def test_mm_even_interior_and_edge_strips(m, n, k, b_kmajor):
           what="addmm interior + edges")
 
 
+@pytest.mark.parametrize("m, n, k", [(2048, 16387, 320), (4100, 8195, 512)])
+def test_mm_shifted_rows_exact(m, n, k):
+    """Odd N with a K-major B (F.linear's weight): output rows start at every
+    2-byte offset, so the full interior tiles store 16-byte chunks shifted to
+    aligned addresses (plus element stores at each row segment's two ends)
+    and the edge strips store element by element.  Small-integer operands:
+    every output equals the double-precision product rounded once to bf16."""
+    g = torch.Generator().manual_seed(m + n + k)
+    a = torch.randint(-8, 9, (m, k), generator=g).to(torch.bfloat16)
+    w = torch.randint(-8, 9, (n, k), generator=g).to(torch.bfloat16)
+    got = ntops_amd.torch.mm(a.cuda(), w.cuda().t())
+    assert _lib.last_kernel().endswith("even+edges"), _lib.last_kernel()
+    assert torch.equal(got.cpu(), (a.double() @ w.double().t()).float().bfloat16())
+
+
+def test_gemm_shifted_rows_full_tiles_through_the_c_abi():
+    """A row stride of an odd element count over full 256 x 256 tiles (the
+    even kernel alone) with a bias: shifted 16-byte stores everywhere; the
+    bytes between the rows stay untouched."""
+    lib = _lib.load()
+    m, n, k = 4096, 4096, 384
+    g = torch.Generator().manual_seed(17)
+    a = torch.randint(-8, 9, (m, k), generator=g).to(torch.bfloat16)
+    b = torch.randint(-8, 9, (k, n), generator=g).to(torch.bfloat16)
+    bias = torch.randint(-8, 9, (n,), generator=g).to(torch.bfloat16)
+    big = torch.zeros(m, n + 5, dtype=torch.bfloat16, device="cuda")
+    out = big[:, 1:1 + n]
+    ag, bg, biasg = a.cuda(), b.cuda(), bias.cuda()
+    rc = lib.ntops_gemm(_lib.dtype_code(torch.bfloat16), 1, m, n, k, ag.data_ptr(), _lib.i64_array((0, k, 1)),
+                        bg.data_ptr(), _lib.i64_array((0, n, 1)), biasg.data_ptr(), _lib.i64_array((0, 0, 1)),
+                        1.0, 1.0, out.data_ptr(), _lib.i64_array((0, n + 5, 1)), _lib.stream_of(out))
+    _lib.check(rc, "ntops_gemm shifted rows")
+    assert _lib.last_kernel().startswith("gemm_mfma 256x256 s4 A:K B:N even"), _lib.last_kernel()
+    torch.cuda.synchronize()
+    assert big[:, 0].abs().sum() == 0 and big[:, 1 + n:].abs().sum() == 0
+    exp = (a.double() @ b.double() + bias.double()).float().bfloat16()
+    assert torch.equal(out.cpu(), exp)
+
+
 # K not a multiple of 8 (or of 4): A's rows and B's columns zero-extended so
 # the matrix cores take the product.
 ODD_K = [(300, 256, 100), (1000, 1024, 1001), (40, 512, 77), (2048, 2048, 4095)]
