@@ -262,6 +262,18 @@ def test_mm_even_interior_and_edge_strips(m, n, k, b_kmajor):
           what="addmm interior + edges")
 
 
+def test_bmm_even_interior_and_edge_strips():
+    """A batch of products whose M and N are not multiples of 256: the
+    interior and both strips of every batch member (the strips offset inside
+    each member, the batch strides unchanged).  Exact small-integer sums."""
+    g = torch.Generator().manual_seed(23)
+    a = torch.randint(-8, 9, (4, 2100, 320), generator=g).to(torch.bfloat16)
+    b = torch.randint(-8, 9, (4, 320, 2060), generator=g).to(torch.bfloat16)
+    got = ntops_amd.torch.bmm(a.cuda(), b.cuda())
+    assert _lib.last_kernel().endswith("even+edges"), _lib.last_kernel()
+    assert torch.equal(got.cpu(), torch.bmm(a.double(), b.double()).float().bfloat16())
+
+
 @pytest.mark.parametrize("m, n, k", [(2048, 16387, 320), (4100, 8195, 512)])
 def test_mm_shifted_rows_exact(m, n, k):
     """Odd N with a K-major B (F.linear's weight): output rows start at every
