@@ -138,10 +138,16 @@ def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, what="ntops_amd.mm"):
                 else:
                     cp = torch.empty(out.shape[:-1] + (np_,), dtype=c.dtype, device=c.device)
                     _cast_into(c, cp[..., :n])
-            op = torch.empty(out.shape[:-1] + (np_,), dtype=out.dtype, device=out.device)
-        gemm(a, bp, op, cp, alpha, beta, what)
+            n0 = n // 256 * 256 if out.dtype != torch.float32 else 0
+            op = torch.empty(out.shape[:-1] + (np_ - n0,), dtype=out.dtype, device=out.device)
+        # 16-bit, n >= 256: the first n0 (a multiple of 256) columns straight
+        # into out (the kernels store rows that start anywhere), only the last
+        # np_ - n0 through the temporary; the interior is launched last
+        gemm(a, bp[..., n0:], op, None if cp is None else cp[..., n0:], alpha, beta, what)
+        if n0:
+            gemm(a, bp[..., :n0], out[..., :n0], None if c is None else c[..., :n0], alpha, beta, what)
         with _DeviceGuard(dev):
-            _cast_into(op[..., :n], out)
+            _cast_into(op[..., :n - n0], out[..., n0:])
         return out
     batch = a.shape[0] if a.dim() == 3 else 1
     m, k = a.shape[-2], a.shape[-1]
