@@ -138,11 +138,12 @@ def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, what="ntops_amd.mm"):
                 else:
                     cp = torch.empty(out.shape[:-1] + (np_,), dtype=c.dtype, device=c.device)
                     _cast_into(c, cp[..., :n])
-            n0 = n // 256 * 256 if out.dtype != torch.float32 else 0
+            # the first n0 columns go straight into out (the kernels store rows
+            # that start anywhere; 16-bit tiles take 256 columns at a time,
+            # fp32 ones 4), only the last np_ - n0 through the temporary; the
+            # interior is launched last
+            n0 = n // 256 * 256 if out.dtype != torch.float32 else n // 4 * 4
             op = torch.empty(out.shape[:-1] + (np_ - n0,), dtype=out.dtype, device=out.device)
-        # 16-bit, n >= 256: the first n0 (a multiple of 256) columns straight
-        # into out (the kernels store rows that start anywhere), only the last
-        # np_ - n0 through the temporary; the interior is launched last
         gemm(a, bp[..., n0:], op, None if cp is None else cp[..., n0:], alpha, beta, what)
         if n0:
             gemm(a, bp[..., :n0], out[..., :n0], None if c is None else c[..., :n0], alpha, beta, what)
